@@ -1,0 +1,309 @@
+/* mormot_ai_hip.h - the C-ABI of mormot.ai.infer.hip, the MI355X (gfx950)
+ * quantized-inference backend of the mormot2-ai native engine.
+ *
+ * Every entry point takes plain pointers, sizes and integers: no C++ or torch
+ * types cross this boundary. A Pascal unit binds them as `external` functions
+ * of libmormot_ai_hip.so (cdecl); ctypes binds them the same way.
+ *
+ * Conventions
+ * - status: every function returns 0 on success, else a negative IHIP_E_*
+ *   code or a positive hipError_t; ihip_last_error() gives the text of the
+ *   last failure of the calling thread (the EInferCuda message of
+ *   src/infer/mormot.ai.infer.cuda.pas:475-487).
+ * - device addresses are uint64_t (TCuDevicePtr of cuda.pas:137-175).
+ * - dtype codes are the ordinals of TInferDType
+ *   (src/infer/mormot.ai.infer.tensor.pas:47-62): the Pascal caller passes
+ *   ord(w.DType) unchanged.
+ * - one ihip_ctx is one device + one non-blocking stream; it may be used from
+ *   any thread, one at a time (cuda.pas:13-15): callers serialise, as
+ *   TInferCudaBackend.GpuLock does (backend.cuda.pas:102-104).
+ */
+#ifndef MORMOT_AI_HIP_H
+#define MORMOT_AI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- element and block types: TInferDType (tensor.pas:47-62) ---- */
+enum {
+  IHIP_F32 = 1,
+  IHIP_F16 = 2,
+  IHIP_BF16 = 3,
+  IHIP_Q8_0 = 8,
+  IHIP_Q4_0 = 9,
+  IHIP_Q4_K = 10,
+  IHIP_Q6_K = 11,
+  IHIP_Q5_0 = 12,
+  IHIP_MXFP4 = 13,
+  IHIP_Q5_1 = 14
+};
+
+/* ---- arithmetic of a Linear ----
+ * IHIP_MODE_F32: y = dequant(W) x in float, x in F32 - the contract of the
+ *   reference's GPU kernels (tools/cuda/linear.cu:1-6): within 1e-5 of the
+ *   double F32 Linear over InferRowToF32 weights.
+ * IHIP_MODE_Q8: the arithmetic of TInferCpuBackend.Linear
+ *   (src/infer/mormot.ai.infer.backend.cpu.pas:1409-1566): x quantized per row
+ *   to Q8_0 (32-value block types) or Q8_K (Q4_K/Q6_K), exact integer block
+ *   sums, the scales applied and summed in double; F32/BF16 weights summed in
+ *   double. Same bits as the CPU up to the order of a double sum. */
+enum { IHIP_MODE_F32 = 0, IHIP_MODE_Q8 = 1 };
+
+/* ---- status codes ---- */
+enum {
+  IHIP_OK = 0,
+  IHIP_E_ARG = -1,         /* an argument out of range (EInferCuda misuse) */
+  IHIP_E_NODEVICE = -2,    /* no HIP device / library */
+  IHIP_E_UNSUPPORTED = -3, /* this dtype/shape has no kernel: CPU fallback */
+  IHIP_E_NONFINITE = -4,   /* a NaN/Inf activation where Q8 refuses it */
+  IHIP_E_CAPTURE = -5,     /* not allowed while capturing, or capture misuse */
+  IHIP_E_NOMEM = -6        /* a fixed maximum size exceeded */
+};
+
+typedef struct ihip_ctx ihip_ctx;
+typedef struct ihip_model ihip_model;
+
+/* ======================================================================
+ * TInferCuda (src/infer/mormot.ai.infer.cuda.pas:179-254): device, stream,
+ * buffers, graphs
+ * ==================================================================== */
+
+/* number of usable gfx950 devices, 0 when none (TInferCuda.Available,
+ * cuda.pas:599-612) */
+int ihip_available(void);
+/* text of the last failure on this thread */
+const char* ihip_last_error(void);
+/* a context on device aDevice: loads the embedded gfx950 code object with
+ * hipModuleLoadData (TInferCuda.Create, cuda.pas:494-573) */
+int ihip_create(int device, ihip_ctx** out);
+void ihip_destroy(ihip_ctx* ctx);
+/* device name and total memory (cuda.pas:61-132 device queries) */
+int ihip_device_info(ihip_ctx* ctx, char* name, int name_len,
+                     uint64_t* total_mem, int* cus);
+
+/* device buffers (TInferCuBuffer, cuda.pas:137-175) */
+int ihip_alloc(ihip_ctx* ctx, uint64_t bytes, uint64_t* dev);
+int ihip_free(ihip_ctx* ctx, uint64_t dev);
+/* synchronous copies on the context's stream (Upload/Download) */
+int ihip_upload(ihip_ctx* ctx, uint64_t dev, const void* host, uint64_t bytes);
+int ihip_download(ihip_ctx* ctx, void* host, uint64_t dev, uint64_t bytes);
+/* enqueued copies (cuMemcpyHtoDAsync / DtoD, cuda.pas:614-673); the host
+ * memory must stay valid until the next synchronize */
+int ihip_upload_async(ihip_ctx* ctx, uint64_t dev, const void* host, uint64_t bytes);
+int ihip_copy_async(ihip_ctx* ctx, uint64_t dst, uint64_t src, uint64_t bytes);
+int ihip_synchronize(ihip_ctx* ctx);
+
+/* stream capture into a graph, instantiate or update, launch
+ * (TInferCuda.CaptureBegin/CaptureEnd/GraphLaunch, cuda.pas:675-771) */
+int ihip_capture_begin(ihip_ctx* ctx);
+int ihip_capture_end(ihip_ctx* ctx, int slot);
+int ihip_graph_launch(ihip_ctx* ctx, int slot);
+
+/* elapsed milliseconds between two points of the stream, measured with HIP
+ * events on that stream: ihip_event_record(ctx, i) marks point i (0..63) */
+int ihip_event_record(ihip_ctx* ctx, int index);
+int ihip_event_elapsed(ihip_ctx* ctx, int from, int to, float* ms);
+
+/* ======================================================================
+ * TInferCudaBackend (src/infer/mormot.ai.infer.backend.cuda.pas:51-148)
+ * ==================================================================== */
+
+/* bytes of aCount values of aType (InferTypeBytes, tensor.pas:280-294); 0 if
+ * aCount is no whole number of blocks */
+uint64_t ihip_type_bytes(int dtype, uint64_t count);
+
+/* the device copy of a weight, uploaded on first use and found again by
+ * (host address, dtype, bytes) (TInferCudaBackend.Weight, backend.cuda.pas:
+ * 414-449). The host data is [count, out, in] of dtype in GGUF layout; the
+ * device copy is repacked per matrix into the HIP layout (quants, then
+ * scales), of the same byte size: matrix m starts at dev + m * out * rowbytes,
+ * as in the host tensor. count > 1: the experts of a layer. */
+int ihip_weight(ihip_ctx* ctx, const void* host, int dtype, int64_t out,
+                int64_t in, int64_t count, uint64_t* dev);
+/* F32 side data (biases, norms) kept by host address, as Weight(.., idtF32) */
+int ihip_weight_f32(ihip_ctx* ctx, const float* host, int64_t count, uint64_t* dev);
+/* drop the device copy of every weight overlapping [from, to)
+ * (ForgetWeights, backend.cuda.pas:282-314); returns the new WeightEpoch */
+int ihip_forget_weights(ihip_ctx* ctx, const void* from, const void* to);
+int ihip_clear_weights(ihip_ctx* ctx);
+/* true when Linear of aType with aIn inputs runs on the device
+ * (GpuLinear, backend.cuda.pas:316-320) */
+int ihip_gpu_linear(int dtype, int64_t in);
+
+/* y[rows, out] = x[rows, in] * W^T + bias: W repacked at device address w
+ * (EnqueueLinearAt, backend.cuda.pas:354-379); bias a device address of
+ * [out] floats or 0; mode IHIP_MODE_F32 or IHIP_MODE_Q8; enqueued, no wait */
+int ihip_enqueue_linear_at(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
+                           int dtype, uint64_t w, int64_t out, uint64_t y,
+                           uint64_t bias, int mode);
+/* one token row through `slots` experts chosen on the device
+ * (EnqueueLinearIds, backend.cuda.pas:386-412): slot s reads expert ids[s]
+ * (int32 at a device address), its matrix at w + ids[s] * stride bytes
+ * (stride = out * rowbytes), x row s when x_per_slot else row 0, y row s;
+ * bias: device [experts, out] floats (row ids[s]) or 0 */
+int ihip_enqueue_linear_ids(ihip_ctx* ctx, uint64_t x, int64_t in, int dtype,
+                            uint64_t w, int64_t stride, int64_t out,
+                            uint64_t ids, int64_t slots, int x_per_slot,
+                            uint64_t y, uint64_t bias, int mode);
+/* the synchronous Linear of the backend on host buffers: x uploaded, the
+ * weight from the cache, y downloaded (TInferCudaBackend.Linear,
+ * backend.cuda.pas:469-515) */
+int ihip_linear(ihip_ctx* ctx, const float* x, int64_t rows, int64_t in,
+                const void* w, int dtype, int64_t out, const float* bias,
+                float* y, int mode);
+
+/* dequantize rows [row0, row0 + rows) of a repacked weight to F32
+ * (InferRowToF32, tensor.pas:467-602, on the device) */
+int ihip_enqueue_dequant(ihip_ctx* ctx, uint64_t w, int dtype, int64_t out,
+                         int64_t in, int64_t row0, int64_t rows, uint64_t y);
+
+/* ---- the operations of a layer (tools/cuda/ops.cu counterparts) ---- */
+
+/* activations of `rows` rows quantized for IHIP_MODE_Q8 into the device
+ * buffer xq (ihip_q8_bytes each): Q8_0 (k_quant 0) or Q8_K (k_quant 1) -
+ * InferQuantizeRowQ8_0 / InferQuantizeRowQ8_K (backend.cpu.pas:617-819).
+ * A non-finite value sets the int32 at `bad` (device address, may be 0) */
+uint64_t ihip_q8_bytes(int64_t in, int k_quant);
+int ihip_enqueue_quantize(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
+                          int k_quant, uint64_t xq, uint64_t bad);
+/* y = w * x / sqrt(mean x^2 + eps) per row (TInferCpuBackend.RmsNorm,
+ * backend.cpu.pas:1769-1795); y may be x */
+int ihip_enqueue_rmsnorm(ihip_ctx* ctx, uint64_t x, uint64_t w, uint64_t y,
+                         int64_t rows, int64_t cols, double eps);
+/* x += t, then y = rmsnorm(x) (addnorm, ops.cu:135-150) */
+int ihip_enqueue_addnorm(ihip_ctx* ctx, uint64_t x, uint64_t t, uint64_t w,
+                         uint64_t y, int64_t rows, int64_t cols, double eps);
+/* x += t */
+int ihip_enqueue_add(ihip_ctx* ctx, uint64_t x, uint64_t t, int64_t n);
+/* gate = silu(gate) * up, or the clamped gpt-oss form when limit > 0
+ * (TInferCpuBackend.SwiGlu, backend.cpu.pas:1797-1834) */
+int ihip_enqueue_swiglu(ihip_ctx* ctx, uint64_t gate, uint64_t up, int64_t n,
+                        float alpha, float limit);
+/* per row and head: RMSNorm of q/k heads (qn, kn device [head_dim] or 0),
+ * rotate_half RoPE from cs = [rows, hd/2] cos then [rows, hd/2] sin, q in
+ * place, k and v stored into the caches at row past + r
+ * (qkrope, ops.cu:211-314; CPU: decoder.pas:2625-2680); kv_f16 selects a
+ * half-float cache */
+int ihip_enqueue_qkrope(ihip_ctx* ctx, uint64_t q, uint64_t k, uint64_t v,
+                        uint64_t qn, uint64_t kn, uint64_t cs, uint64_t kc,
+                        uint64_t vc, int64_t rows, int64_t heads,
+                        int64_t kv_heads, int64_t head_dim, int64_t past,
+                        double eps, int kv_f16);
+/* causal GQA attention of `rows` new rows over the cache (window > 0: the
+ * last `window` keys; sinks: device [heads] or 0; scale 0: 1/sqrt(hd))
+ * (TInferCpuBackend.CausalAttention, backend.cpu.pas:1233-1380;
+ * attention + attnmerge, ops.cu:352-617) */
+int ihip_enqueue_attention(ihip_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc,
+                           uint64_t y, int64_t rows, int64_t heads,
+                           int64_t kv_heads, int64_t head_dim, int64_t past,
+                           int64_t window, uint64_t sinks, double scale,
+                           int kv_f16);
+/* the router of TDecoderModel.Route (decoder.pas:2901-2949) for one row of
+ * logits, on the device: ids and weights sorted by id (route, ops.cu:664-720) */
+int ihip_enqueue_route(ihip_ctx* ctx, uint64_t logits, int64_t experts,
+                       int64_t k, int norm_topk, uint64_t ids, uint64_t w);
+/* y = sum over slots in id order of w[s] * d[s] (moecombine, ops.cu:724-734) */
+int ihip_enqueue_moecombine(ihip_ctx* ctx, uint64_t d, uint64_t w, uint64_t y,
+                            int64_t k, int64_t n);
+/* x[r] = InferRowToF32(embed, ids[r]) for device ids (TDecoderModel.Embed,
+ * decoder.pas:2563-2580); embed is a repacked weight [vocab, hidden] */
+int ihip_enqueue_embed(ihip_ctx* ctx, uint64_t embed, int dtype, int64_t vocab,
+                       int64_t hidden, uint64_t ids, int64_t rows, uint64_t x);
+/* the first index of the maximum of n floats, NaN skipped, lowest id on a tie
+ * (InferArgMax, sampler.pas:123-160), written as int32 to `out` */
+int ihip_enqueue_argmax(ihip_ctx* ctx, uint64_t v, int64_t n, uint64_t out);
+
+/* ======================================================================
+ * TQwen3Cuda (src/infer/mormot.ai.infer.model.qwen3.cuda.pas:150-301):
+ * the whole decoder on the device, behind TDecoderDevice
+ * (src/infer/mormot.ai.infer.decoder.pas:907-928)
+ * ==================================================================== */
+
+/* one host tensor: data in the GGUF/safetensors layout of dtype, or NULL */
+typedef struct {
+  const void* data;
+  int32_t dtype;
+  int32_t reserved;
+} ihip_tensor;
+
+/* the weights of one layer (TDecoderLayer, decoder.pas:253-267) */
+typedef struct {
+  ihip_tensor input_norm;  /* [hidden] F32 */
+  ihip_tensor q, k, v, o;  /* [qw, h], [kvw, h], [kvw, h], [h, qw] */
+  ihip_tensor q_bias, k_bias, v_bias, o_bias; /* F32 or NULL (gpt-oss) */
+  ihip_tensor q_norm, k_norm; /* [head_dim] F32 or NULL (Qwen3) */
+  ihip_tensor sinks;       /* [heads] F32 or NULL (gpt-oss) */
+  ihip_tensor post_norm;   /* [hidden] F32: the pre-FFN norm */
+  ihip_tensor gate, up, down; /* dense FFN [ff, h], [ff, h], [h, ff] */
+  ihip_tensor router, router_bias; /* [experts, h] and [experts] */
+  ihip_tensor exp_gate, exp_up, exp_down; /* [E, fi, h], [E, fi, h], [E, h, fi] */
+  ihip_tensor exp_gate_bias, exp_up_bias, exp_down_bias; /* [E, fi], [E, fi], [E, h] */
+  int32_t window;          /* sliding window, 0 = full attention */
+  int32_t moe;             /* 1: the FFN is a mixture of experts */
+} ihip_layer_desc;
+
+/* the settings of TDecoderConfig (decoder.pas:158-225) that this path reads */
+typedef struct {
+  int32_t vocab, hidden, layers, heads, kv_heads, head_dim;
+  int32_t ffn, experts, experts_used, expert_ffn;
+  int32_t norm_topk, max_positions;
+  float rms_eps;
+  float swiglu_alpha, swiglu_limit;
+  float reserved0;
+  double rope_theta;
+  /* YaRN (decoder.pas:1759-1829): factor 0 = none */
+  double rope_factor, rope_beta_fast, rope_beta_slow;
+  int32_t rope_original, rope_truncate;
+  double rope_attention;
+  ihip_tensor embed, final_norm, head; /* head.data NULL: tied to embed */
+  const ihip_layer_desc* layer;        /* [layers] */
+} ihip_model_desc;
+
+/* the model on the device: every weight uploaded (UploadWeights,
+ * model.qwen3.cuda.pas:602-828); mode: the Linear arithmetic; kv_f16: a
+ * half-float KV cache (TQwen3Cuda.KvF16); the host tensors must outlive it */
+int ihip_model_create(ihip_ctx* ctx, const ihip_model_desc* desc, int mode,
+                      int kv_f16, int64_t max_tokens, ihip_model** out);
+void ihip_model_destroy(ihip_model* m);
+/* forget the cached tokens (TDecoderContext.Truncate(0)) */
+int ihip_model_reset(ihip_model* m);
+/* count tokens after the cached ones; logits [vocab] of the last one, or of
+ * every one when all_logits (TQwen3Cuda.Forward, model.qwen3.cuda.pas:1722) */
+int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count,
+                       float* logits, int all_logits);
+/* greedy decode (TDecoderModel.Greedy, decoder.pas:3390-3426): the prompt,
+ * then max_new ids by argmax; with the argmax on the device */
+int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n,
+                      int64_t max_new, int32_t* out_ids);
+/* the cos/sin table the model uploads for positions [first, first + rows):
+ * [rows, rope/2] cos then sin (TDecoderModel.Rotary, decoder.pas:2539-2561) */
+int ihip_model_rotary(const ihip_model_desc* desc, int64_t first, int64_t rows,
+                      float* cs);
+/* timings of the last greedy call: prefill and decode milliseconds */
+int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
+
+/* ======================================================================
+ * seeded synthetic weights, written on the host (the generators of
+ * tests/test.infer.fast.pas:144-260 generalised to every block type)
+ * ==================================================================== */
+
+/* blocks of dtype for a [rows, cols] matrix at dst: codes uniform over their
+ * bit range, scales uniform in [2^lo_exp2, 2^hi_exp2] (fp16, or E8M0 for
+ * MXFP4); threads: 0 = all cores */
+int ihip_synth_blocks(void* dst, int dtype, int64_t rows, int64_t cols,
+                      uint64_t seed, int lo_exp2, int hi_exp2, int threads);
+/* weights ~ N(0, sigma) in dtype: F32/BF16 rounded, Q8_0 by the GGUF
+ * writer's ties-away quantizer, Q4_K/Q6_K/MXFP4 by codes whose scales give
+ * that spread */
+int ihip_synth_normal(void* dst, int dtype, int64_t rows, int64_t cols,
+                      uint64_t seed, float sigma, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MORMOT_AI_HIP_H */

@@ -1,0 +1,224 @@
+/* model.c - TEST INFRASTRUCTURE ONLY (see oracle.h).
+ * The CPU decoder: TDecoderModel.ForwardPart (decoder.pas:3245-3369) with
+ * AttentionBlock (:2625-2702), DenseBlock/DenseFfn (:2866-2899), MoeBlock
+ * (:3037-3053) and Experts (:3092-3150) over TInferCpuBackend, and Greedy
+ * (:3390-3426). */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include "oracle.h"
+
+struct orc_model {
+  ihip_model_desc d;
+  ihip_layer_desc* layer;
+  int64_t max_tokens, length;
+  int kv_f16, threads;
+  float** keys;
+  float** values;
+};
+
+static uint64_t row_bytes(int t, int64_t cols)
+{
+  return (uint64_t)(cols / orc_block_values(t)) * orc_block_size(t);
+}
+
+int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, int threads,
+                     orc_model** out)
+{
+  orc_model* m = (orc_model*)calloc(1, sizeof(*m));
+  m->d = *d;
+  m->layer = (ihip_layer_desc*)malloc(d->layers * sizeof(ihip_layer_desc));
+  memcpy(m->layer, d->layer, d->layers * sizeof(ihip_layer_desc));
+  m->max_tokens = max_tokens;
+  m->kv_f16 = kv_f16;
+  m->threads = threads > 0 ? threads : 1;
+  int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
+  m->keys = (float**)calloc(d->layers, sizeof(float*));
+  m->values = (float**)calloc(d->layers, sizeof(float*));
+  for (int l = 0; l < d->layers; l++) {
+    m->keys[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
+    m->values[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
+  }
+  *out = m;
+  return 0;
+}
+
+void orc_model_destroy(orc_model* m)
+{
+  if (!m) return;
+  for (int l = 0; l < m->d.layers; l++) {
+    free(m->keys[l]);
+    free(m->values[l]);
+  }
+  free(m->keys);
+  free(m->values);
+  free(m->layer);
+  free(m);
+}
+
+static int lin(orc_model* m, const float* x, int64_t rows, int64_t in, ihip_tensor w,
+               uint64_t offset, int64_t out, const float* bias, float* y)
+{
+  return orc_linear(x, rows, in, (const uint8_t*)w.data + offset, w.dtype, out, bias, y,
+                    m->threads);
+}
+
+static void add(float* x, const float* t, int64_t n)
+{
+  for (int64_t i = 0; i < n; i++) x[i] = x[i] + t[i];
+}
+
+static float half_round(float v)
+{
+  return orc_half_to_single(orc_single_to_half(v));
+}
+
+int orc_model_forward(orc_model* m, const int32_t* ids, int64_t n, float* logits,
+                      int all_logits)
+{
+  const ihip_model_desc* d = &m->d;
+  int64_t h = d->hidden, hd = d->head_dim, qw = (int64_t)d->heads * hd,
+          kvw = (int64_t)d->kv_heads * hd, past = m->length, half = hd / 2;
+  int64_t f = d->ffn > d->expert_ffn ? d->ffn : d->expert_ffn;
+  int err = 0;
+  if (n <= 0 || past + n > m->max_tokens)
+    return IHIP_E_ARG;
+  for (int64_t i = 0; i < n; i++)
+    if (ids[i] < 0 || ids[i] >= d->vocab) return IHIP_E_ARG;
+  float* x = (float*)malloc(n * h * 4);
+  float* hh = (float*)malloc(n * h * 4);
+  float* tmp = (float*)malloc(n * h * 4);
+  float* q = (float*)malloc(n * qw * 4);
+  float* k = (float*)malloc(n * kvw * 4);
+  float* v = (float*)malloc(n * kvw * 4);
+  float* attn = (float*)malloc(n * qw * 4);
+  float* gate = (float*)malloc(n * (f > 0 ? f : 1) * 4);
+  float* up = (float*)malloc(n * (f > 0 ? f : 1) * 4);
+  float* cs = (float*)malloc(n * hd * 4);
+  int64_t E = d->experts > 0 ? d->experts : 1, K = d->experts_used > 0 ? d->experts_used : 1;
+  float* route = (float*)malloc(n * E * 4);
+  int32_t* chosen = (int32_t*)malloc(n * K * 4);
+  float* cw = (float*)malloc(n * K * 4);
+  float* gather = (float*)malloc(n * h * 4);
+  float* eout = (float*)malloc(n * h * 4);
+  int64_t* rowi = (int64_t*)malloc(n * sizeof(int64_t));
+  float* roww = (float*)malloc(n * 4);
+
+  orc_rotary(d, past, n, cs);
+  const float* cosv = cs;
+  const float* sinv = cs + n * half;
+  for (int64_t i = 0; i < n; i++)
+    orc_row_to_f32(d->embed.data, d->embed.dtype, ids[i], h, x + i * h);
+  for (int l = 0; l < d->layers && !err; l++) {
+    const ihip_layer_desc* L = &m->layer[l];
+    /* AttentionBlock */
+    orc_rmsnorm(x, n, h, (const float*)L->input_norm.data, d->rms_eps, hh);
+    err |= lin(m, hh, n, h, L->q, 0, qw, (const float*)L->q_bias.data, q);
+    err |= lin(m, hh, n, h, L->k, 0, kvw, (const float*)L->k_bias.data, k);
+    err |= lin(m, hh, n, h, L->v, 0, kvw, (const float*)L->v_bias.data, v);
+    if (L->q_norm.data) {
+      orc_rmsnorm(q, n * d->heads, hd, (const float*)L->q_norm.data, d->rms_eps, q);
+      orc_rmsnorm(k, n * d->kv_heads, hd, (const float*)L->k_norm.data, d->rms_eps, k);
+    }
+    orc_rope(q, n, d->heads, hd, cosv, sinv, hd);
+    orc_rope(k, n, d->kv_heads, hd, cosv, sinv, hd);
+    float* kc = m->keys[l] + past * kvw;
+    float* vc = m->values[l] + past * kvw;
+    for (int64_t i = 0; i < n * kvw; i++) {
+      kc[i] = m->kv_f16 ? half_round(k[i]) : k[i];
+      vc[i] = m->kv_f16 ? half_round(v[i]) : v[i];
+    }
+    orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads,
+                         attn, L->window, (const float*)L->sinks.data, 0);
+    err |= lin(m, attn, n, qw, L->o, 0, h, (const float*)L->o_bias.data, tmp);
+    add(x, tmp, n * h);
+    /* the feed-forward block */
+    orc_rmsnorm(x, n, h, (const float*)L->post_norm.data, d->rms_eps, hh);
+    if (!L->moe) {
+      err |= lin(m, hh, n, h, L->gate, 0, d->ffn, NULL, gate);
+      err |= lin(m, hh, n, h, L->up, 0, d->ffn, NULL, up);
+      orc_swiglu(gate, up, n * d->ffn, d->swiglu_alpha, d->swiglu_limit);
+      err |= lin(m, gate, n, d->ffn, L->down, 0, h, NULL, tmp);
+    } else {
+      int64_t fi = d->expert_ffn;
+      err |= lin(m, hh, n, h, L->router, 0, E, (const float*)L->router_bias.data, route);
+      for (int64_t r = 0; r < n; r++)
+        orc_route(route + r * E, E, K, d->norm_topk, chosen + r * K, cw + r * K);
+      memset(tmp, 0, n * h * 4);
+      uint64_t gb = row_bytes(L->exp_gate.dtype, h) * fi;
+      uint64_t db = row_bytes(L->exp_down.dtype, fi) * h;
+      for (int64_t e = 0; e < E; e++) {
+        int64_t cnt = 0;
+        for (int64_t r = 0; r < n; r++)
+          for (int64_t j = 0; j < K; j++)
+            if (chosen[r * K + j] == e) {
+              rowi[cnt] = r;
+              roww[cnt] = cw[r * K + j];
+              memcpy(gather + cnt * h, hh + r * h, h * 4);
+              cnt++;
+            }
+        if (cnt == 0) continue;
+        const float* bg = L->exp_gate_bias.data ? (const float*)L->exp_gate_bias.data + e * fi : NULL;
+        const float* bu = L->exp_up_bias.data ? (const float*)L->exp_up_bias.data + e * fi : NULL;
+        const float* bd = L->exp_down_bias.data ? (const float*)L->exp_down_bias.data + e * h : NULL;
+        err |= lin(m, gather, cnt, h, L->exp_gate, e * gb, fi, bg, gate);
+        err |= lin(m, gather, cnt, h, L->exp_up, e * gb, fi, bu, up);
+        orc_swiglu(gate, up, cnt * fi, d->swiglu_alpha, d->swiglu_limit);
+        err |= lin(m, gate, cnt, fi, L->exp_down, e * db, h, bd, eout);
+        for (int64_t c = 0; c < cnt; c++) {
+          float w = roww[c];
+          float* dst = tmp + rowi[c] * h;
+          const float* src = eout + c * h;
+          for (int64_t i = 0; i < h; i++) {
+            float p = w * src[i];
+            dst[i] = dst[i] + p;
+          }
+        }
+      }
+    }
+    add(x, tmp, n * h);
+  }
+  if (!err) {
+    m->length = past + n;
+    if (logits) {
+      orc_rmsnorm(x, n, h, (const float*)d->final_norm.data, d->rms_eps, hh);
+      ihip_tensor head = d->head.data ? d->head : d->embed;
+      if (all_logits)
+        err |= lin(m, hh, n, h, head, 0, d->vocab, NULL, logits);
+      else
+        err |= lin(m, hh + (n - 1) * h, 1, h, head, 0, d->vocab, NULL, logits);
+    }
+  }
+  free(x); free(hh); free(tmp); free(q); free(k); free(v); free(attn);
+  free(gate); free(up); free(cs); free(route); free(chosen); free(cw);
+  free(gather); free(eout); free(rowi); free(roww);
+  return err ? IHIP_E_ARG : 0;
+}
+
+static float margin(const float* lg, int64_t n, int64_t best)
+{
+  float second = -INFINITY;
+  for (int64_t i = 0; i < n; i++)
+    if (i != best && lg[i] > second) second = lg[i];
+  return lg[best] - second;
+}
+
+int orc_model_greedy(orc_model* m, const int32_t* prompt, int64_t n, int64_t max_new,
+                     int32_t* out_ids, float* margins)
+{
+  int64_t V = m->d.vocab;
+  float* lg = (float*)malloc(V * 4);
+  int err = orc_model_forward(m, prompt, n, lg, 0);
+  for (int64_t i = 0; i < max_new && !err; i++) {
+    int64_t next = orc_argmax(lg, V);
+    out_ids[i] = (int32_t)next;
+    if (margins) margins[i] = margin(lg, V, next);
+    int32_t id = (int32_t)next;
+    if (i + 1 < max_new)
+      err = orc_model_forward(m, &id, 1, lg, 0);
+    else
+      err = orc_model_forward(m, &id, 1, NULL, 0);
+  }
+  free(lg);
+  return err;
+}

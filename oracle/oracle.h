@@ -1,0 +1,115 @@
+/* oracle.h - TEST INFRASTRUCTURE ONLY.
+ *
+ * A CPU restatement in plain C of the reference's CPU arithmetic for the
+ * quantized-inference hot path (landrix/mormot2-ai, Object Pascal), used as
+ * the checker of the HIP backend. Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it; the product never does.
+ *
+ * Each function cites the reference file:line it follows (paths under
+ * src/infer/ of the reference). The reference itself cannot be compiled here
+ * (Object Pascal + mORMot2, no FPC/Delphi in the image), so oracle/_ref stays
+ * empty; parity is pinned by the reference's golden vectors
+ * (tests/data/infer-ref/{q8,q4,q5,q51,qk,mxfp4,ops}, copied as data into
+ * tests/golden/) and by the closed-form checks of tests/test_oracle*.py.
+ *
+ * Pinning status per function (see the tests named):
+ *   orc_half_to_single_bits, orc_single_to_half  - q8 half/x + half/bits vectors + all
+ *       65536 half patterns against numpy's IEEE conversion
+ *   orc_e8m0_half_bits                           - closed form 2^(e-128)
+ *   orc_row_to_f32                               - q8/q4/q5/q51/qk/mxfp4 dequant/y
+ *   orc_quantize_q8_0 (ties even / away)         - q8 quant/blocks, q4 q8ref/blocks
+ *   orc_quantize_q4_0                            - q4 quant/blocks
+ *   orc_quantize_q8_k                            - qk q8k/blocks
+ *   orc_linear (Q8 arithmetic)                   - linear/y of every format
+ *   orc_linear_f32                               - ops linear/y, brute force
+ *   orc_rmsnorm, orc_swiglu, orc_rope            - closed forms in numpy (float64)
+ *   orc_causal_attention                         - ops softmax/y + numpy float64
+ *   orc_route                                    - brute-force numpy softmax/top-k
+ *   orc_argmax                                   - numpy argmax + NaN/tie cases
+ *   orc_rotary                                   - numpy float32 step replay
+ *   orc_model_*                                  - composed of the above;
+ *       checked against a numpy float64 forward of a tiny model
+ */
+#ifndef ORACLE_H
+#define ORACLE_H
+
+#include <stdint.h>
+#include "../include/mormot_ai_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* tensor.pas:296-326 InferHalfToSingleBits; :328-377 InferSingleToHalf */
+uint32_t orc_half_to_single_bits(uint16_t h);
+float orc_half_to_single(uint16_t h);
+uint16_t orc_single_to_half(float f);
+/* tensor.pas:459-465 InferE8M0HalfBits */
+uint32_t orc_e8m0_half_bits(uint8_t e);
+/* tensor.pas:187-192 INFER_DTYPE_SIZE / INFER_DTYPE_BLOCK */
+int orc_block_size(int dtype);
+int orc_block_values(int dtype);
+/* tensor.pas:467-602 InferRowToF32: row `row` of [*, cols] */
+int orc_row_to_f32(const void* data, int dtype, int64_t row, int64_t cols,
+                   float* dst);
+
+/* backend.cpu.pas:634-699 QuantizeQ8_0: returns 0, or 1 + index of the first
+ * non-finite value */
+int64_t orc_quantize_q8_0(const float* x, int64_t n, void* blocks, int ties_away);
+/* backend.cpu.pas:703-756 InferQuantizeRowQ4_0 */
+int64_t orc_quantize_q4_0(const float* x, int64_t n, void* blocks);
+/* backend.cpu.pas:758-819 InferQuantizeRowQ8_K */
+int64_t orc_quantize_q8_k(const float* x, int64_t n, void* blocks);
+
+/* backend.cpu.pas:1472-1566 TInferCpuBackend.Linear: the quantized
+ * arithmetic for block types, the double F32 sum for F32; BF16 widened to
+ * F32 first (decoder.pas:2211-2221). threads > 1 splits the outputs, every
+ * output keeps its own sequential sum: the same bits at any thread count */
+int orc_linear(const float* x, int64_t rows, int64_t in, const void* w,
+               int dtype, int64_t out, const float* bias, float* y, int threads);
+/* the tier-2 oracle of test.infer.cuda.pas:815-831: F32 weights from
+ * InferRowToF32, the double Linear of backend.cpu.pas:1548-1565 */
+int orc_linear_f32(const float* x, int64_t rows, int64_t in, const void* w,
+                   int dtype, int64_t out, const float* bias, float* y, int threads);
+
+/* backend.cpu.pas:1769-1795 */
+void orc_rmsnorm(const float* x, int64_t rows, int64_t cols, const float* w,
+                 double eps, float* y);
+/* backend.cpu.pas:1797-1834 */
+void orc_swiglu(float* gate, const float* up, int64_t n, float alpha, float limit);
+/* backend.cpu.pas:1862-1888 */
+void orc_rope(float* x, int64_t rows, int64_t heads, int64_t head_dim,
+              const float* cos_, const float* sin_, int64_t rot_dim);
+/* backend.cpu.pas:1233-1380, the reference (double) branch of CausalRows */
+void orc_causal_attention(const float* q, int64_t rows, int64_t heads,
+                          int64_t head_dim, const float* keys, const float* values,
+                          int64_t past, int64_t kv_heads, float* y, int64_t window,
+                          const float* sinks, double scale);
+/* decoder.pas:2901-2949 TDecoderModel.Route (no expert scale, no tape) */
+void orc_route(const float* logits, int64_t experts, int64_t k, int norm_topk,
+               int32_t* chosen, float* weights);
+/* sampler.pas:123-160 InferArgMax */
+int64_t orc_argmax(const float* v, int64_t n);
+
+/* decoder.pas:1735-1750 + 1759-1829: the inverse frequencies (and YaRN) of a
+ * model; decoder.pas:2539-2561 Rotary: [rows, half] cos, then sin */
+int orc_rotary(const ihip_model_desc* d, int64_t first, int64_t rows, float* cs);
+
+/* the CPU decoder (decoder.pas:3245-3369 ForwardPart with TInferCpuBackend):
+ * kv_f16 != 0 rounds every cached key/value to half (the device's F16 cache
+ * restated, not a reference behaviour) */
+typedef struct orc_model orc_model;
+int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16,
+                     int threads, orc_model** out);
+void orc_model_destroy(orc_model* m);
+int orc_model_forward(orc_model* m, const int32_t* ids, int64_t count,
+                      float* logits, int all_logits);
+/* decoder.pas:3390-3426 Greedy; margins[i] = top1 - top2 logit of step i */
+int orc_model_greedy(orc_model* m, const int32_t* prompt, int64_t n,
+                     int64_t max_new, int32_t* out_ids, float* margins);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,194 @@
+"""ctypes binding of oracle/liboracle.so - the CPU checker (test
+infrastructure only: the product never loads it)."""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+
+F32, F16, BF16, Q8_0, Q4_0, Q4_K, Q6_K, Q5_0, MXFP4, Q5_1 = 1, 2, 3, 8, 9, 10, 11, 12, 13, 14
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q8_0: (32, 34), Q4_0: (32, 18),
+         Q4_K: (256, 144), Q6_K: (256, 210), Q5_0: (32, 22), MXFP4: (32, 17), Q5_1: (32, 24)}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            import subprocess
+            subprocess.check_call(["make", "-s", "-C", os.path.dirname(LIB_PATH)])
+        L = C.CDLL(LIB_PATH)
+        vp, i64, f32p = C.c_void_p, C.c_int64, C.POINTER(C.c_float)
+        L.orc_half_to_single_bits.restype = C.c_uint32
+        L.orc_half_to_single_bits.argtypes = [C.c_uint16]
+        L.orc_single_to_half.restype = C.c_uint16
+        L.orc_single_to_half.argtypes = [C.c_float]
+        L.orc_e8m0_half_bits.restype = C.c_uint32
+        L.orc_e8m0_half_bits.argtypes = [C.c_uint8]
+        L.orc_row_to_f32.argtypes = [vp, C.c_int, i64, i64, vp]
+        for n in ("orc_quantize_q4_0", "orc_quantize_q8_k"):
+            getattr(L, n).restype = i64
+            getattr(L, n).argtypes = [vp, i64, vp]
+        L.orc_quantize_q8_0.restype = i64
+        L.orc_quantize_q8_0.argtypes = [vp, i64, vp, C.c_int]
+        for n in ("orc_linear", "orc_linear_f32"):
+            getattr(L, n).argtypes = [vp, i64, i64, vp, C.c_int, i64, vp, vp, C.c_int]
+        L.orc_rmsnorm.argtypes = [vp, i64, i64, vp, C.c_double, vp]
+        L.orc_rmsnorm.restype = None
+        L.orc_swiglu.argtypes = [vp, vp, i64, C.c_float, C.c_float]
+        L.orc_swiglu.restype = None
+        L.orc_rope.argtypes = [vp, i64, i64, i64, vp, vp, i64]
+        L.orc_rope.restype = None
+        L.orc_causal_attention.argtypes = [vp, i64, i64, i64, vp, vp, i64, i64, vp, i64, vp,
+                                           C.c_double]
+        L.orc_causal_attention.restype = None
+        L.orc_route.argtypes = [vp, i64, i64, C.c_int, vp, vp]
+        L.orc_route.restype = None
+        L.orc_argmax.restype = i64
+        L.orc_argmax.argtypes = [vp, i64]
+        L.orc_rotary.argtypes = [vp, i64, i64, vp]
+        L.orc_model_create.argtypes = [vp, i64, C.c_int, C.c_int, C.POINTER(vp)]
+        L.orc_model_destroy.argtypes = [vp]
+        L.orc_model_destroy.restype = None
+        L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
+        L.orc_model_greedy.argtypes = [vp, vp, i64, i64, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def row_bytes(dtype, cols):
+    bv, bs = BLOCK[dtype]
+    return cols // bv * bs
+
+
+def dequant(w, dtype, rows, cols):
+    out = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        assert lib().orc_row_to_f32(_p(w), dtype, r, cols, out[r].ctypes.data) == 0
+    return out
+
+
+def quantize_q8_0(x, ties_away=False):
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.zeros(x.size // 32 * 34, np.uint8)
+    bad = lib().orc_quantize_q8_0(_p(x), x.size, _p(out), int(ties_away))
+    return out, bad
+
+
+def quantize_q4_0(x):
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.zeros(x.size // 32 * 18, np.uint8)
+    bad = lib().orc_quantize_q4_0(_p(x), x.size, _p(out))
+    return out, bad
+
+
+def quantize_q8_k(x):
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.zeros(x.size // 256 * 292, np.uint8)
+    bad = lib().orc_quantize_q8_k(_p(x), x.size, _p(out))
+    return out, bad
+
+
+def linear(x, w, dtype, out, bias=None, threads=8, f32=False):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, nin = x.shape
+    y = np.empty((rows, out), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    fn = lib().orc_linear_f32 if f32 else lib().orc_linear
+    rc = fn(_p(x), rows, nin, _p(w), dtype, out, _p(b), _p(y), threads)
+    if rc:
+        raise ValueError(f"oracle linear failed: {rc}")
+    return y
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), x.shape[0], x.shape[1], _p(np.ascontiguousarray(w, np.float32)),
+                      eps, _p(y))
+    return y
+
+
+def swiglu(g, u, alpha=1.0, limit=0.0):
+    g = np.array(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    lib().orc_swiglu(_p(g), _p(u), g.size, alpha, limit)
+    return g
+
+
+def rope(x, heads, hd, cos, sin, rot=0):
+    x = np.array(x, np.float32)
+    lib().orc_rope(_p(x), x.shape[0], heads, hd, _p(np.ascontiguousarray(cos, np.float32)),
+                   _p(np.ascontiguousarray(sin, np.float32)), rot)
+    return x
+
+
+def causal_attention(q, heads, hd, keys, values, past, kvh, window=0, sinks=None, scale=0.0):
+    q = np.ascontiguousarray(q, np.float32)
+    y = np.empty_like(q)
+    s = None if sinks is None else np.ascontiguousarray(sinks, np.float32)
+    lib().orc_causal_attention(_p(q), q.shape[0], heads, hd,
+                               _p(np.ascontiguousarray(keys, np.float32)),
+                               _p(np.ascontiguousarray(values, np.float32)),
+                               past, kvh, _p(y), window, _p(s), scale)
+    return y
+
+
+def route(logits, k, norm_topk=True):
+    lg = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().orc_route(_p(lg), lg.size, k, int(norm_topk), _p(ids), _p(w))
+    return ids, w
+
+
+def argmax(v):
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+class Model:
+    """The CPU decoder over a model description (mormot_ai_hip.ihip_model_desc)."""
+
+    def __init__(self, desc, max_tokens, kv_f16=False, threads=8):
+        self.desc = desc  # keeps the host tensors alive
+        h = C.c_void_p()
+        rc = lib().orc_model_create(C.addressof(desc.struct), max_tokens, int(kv_f16), threads,
+                                    C.byref(h))
+        if rc:
+            raise RuntimeError(rc)
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().orc_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def forward(self, ids, all_logits=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        V = self.desc.vocab
+        lg = np.empty((len(ids) if all_logits else 1, V), np.float32)
+        rc = lib().orc_model_forward(self.h, _p(ids), len(ids), _p(lg), int(all_logits))
+        if rc:
+            raise RuntimeError(rc)
+        return lg if all_logits else lg[0]
+
+    def greedy(self, prompt, max_new):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max_new, np.int32)
+        margins = np.empty(max_new, np.float32)
+        rc = lib().orc_model_greedy(self.h, _p(p), len(p), max_new, _p(out), _p(margins))
+        if rc:
+            raise RuntimeError(rc)
+        return out, margins
