@@ -124,6 +124,10 @@ uint64_t ihip_type_bytes(int dtype, uint64_t count);
  * as in the host tensor. count > 1: the experts of a layer. */
 int ihip_weight(ihip_ctx* ctx, const void* host, int dtype, int64_t out,
                 int64_t in, int64_t count, uint64_t* dev);
+/* the repack of ihip_weight on the host: [count, out, in] GGUF blocks into
+ * the HIP layout (inverse = 0), or back (inverse = 1); no device needed */
+int ihip_repack(const void* src, void* dst, int dtype, int64_t out, int64_t in,
+                int64_t count, int inverse);
 /* F32 side data (biases, norms) kept by host address, as Weight(.., idtF32) */
 int ihip_weight_f32(ihip_ctx* ctx, const float* host, int64_t count, uint64_t* dev);
 /* drop the device copy of every weight overlapping [from, to)
@@ -143,7 +147,8 @@ int ihip_enqueue_linear_at(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
 /* one token row through `slots` experts chosen on the device
  * (EnqueueLinearIds, backend.cuda.pas:386-412): slot s reads expert ids[s]
  * (int32 at a device address), its matrix at w + ids[s] * stride bytes
- * (stride = out * rowbytes), x row s when x_per_slot else row 0, y row s;
+ * (stride = out * rowbytes), x row s / x_per_slot (x_per_slot = 1: row s,
+ * k: the token of slot s when every token has k slots; 0: row 0), y row s;
  * bias: device [experts, out] floats (row ids[s]) or 0 */
 int ihip_enqueue_linear_ids(ihip_ctx* ctx, uint64_t x, int64_t in, int dtype,
                             uint64_t w, int64_t stride, int64_t out,

@@ -1,0 +1,670 @@
+// backend.cpp - TInferCudaBackend of the reference
+// (src/infer/mormot.ai.infer.backend.cuda.pas:51-517) for HIP: the weight
+// cache with its repack into the HIP layout, the Linear dispatch (GEMV kernel
+// per dtype, arithmetic and shape), and the enqueue wrappers of the layer
+// operations.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <thread>
+
+#include "internal.h"
+
+namespace ihip {
+
+// ---------------------------------------------------------------- repack
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// the value i (0..255) of a GGUF Q6_K super-block, 0..63 (Q6KValue + 32,
+// tensor.pas:419-439)
+static inline int q6_value(const uint8_t* b, int i)
+{
+  int n = i >> 7, l, h, r;
+  i &= 127;
+  l = i & 31;
+  h = (b[128 + 32 * n + l] >> (2 * (i >> 5))) & 3;
+  switch (i >> 5) {
+  case 0: r = b[64 * n + l] & 15; break;
+  case 1: r = b[64 * n + l + 32] & 15; break;
+  case 2: r = b[64 * n + l] >> 4; break;
+  default: r = b[64 * n + l + 32] >> 4; break;
+  }
+  return r | (h << 4);
+}
+
+// one row o of matrix m: GGUF blocks at src -> regions of dst (base of the matrix)
+static void repack_row(const uint8_t* src, uint8_t* dst, int t, int64_t out, int64_t in, int64_t o)
+{
+  const Regions rg = regions(t, out, in);
+  const int64_t G = in / 32, NB = in / 256;
+  switch (t) {
+  case DT_Q8_0:
+    for (int64_t b = 0; b < G; b++) {
+      const uint8_t* s = src + b * 34;
+      memcpy(dst + rg.s + (o * G + b) * 2, s, 2);
+      memcpy(dst + o * in + b * 32, s + 2, 32);
+    }
+    break;
+  case DT_Q4_0:
+    for (int64_t b = 0; b < G; b++) {
+      const uint8_t* s = src + b * 18;
+      memcpy(dst + rg.s + (o * G + b) * 2, s, 2);
+      memcpy(dst + (o * G + b) * 16, s + 2, 16);
+    }
+    break;
+  case DT_MXFP4:
+    for (int64_t b = 0; b < G; b++) {
+      const uint8_t* s = src + b * 17;
+      dst[rg.s + o * G + b] = s[0];
+      memcpy(dst + (o * G + b) * 16, s + 1, 16);
+    }
+    break;
+  case DT_Q5_0:
+    for (int64_t b = 0; b < G; b++) {
+      const uint8_t* s = src + b * 22;
+      memcpy(dst + rg.s + (o * G + b) * 2, s, 2);
+      memcpy(dst + rg.h + (o * G + b) * 4, s + 2, 4);
+      memcpy(dst + (o * G + b) * 16, s + 6, 16);
+    }
+    break;
+  case DT_Q5_1:
+    for (int64_t b = 0; b < G; b++) {
+      const uint8_t* s = src + b * 24;
+      memcpy(dst + rg.s + (o * G + b) * 4, s, 4);
+      memcpy(dst + rg.h + (o * G + b) * 4, s + 4, 4);
+      memcpy(dst + (o * G + b) * 16, s + 8, 16);
+    }
+    break;
+  case DT_Q4_K:
+    for (int64_t b = 0; b < NB; b++) {
+      const uint8_t* s = src + b * 144;
+      memcpy(dst + rg.s + (o * NB + b) * 16, s, 16);
+      const uint8_t* qs = s + 16;
+      for (int jj = 0; jj < 8; jj++) {
+        uint8_t* gq = dst + (o * G + b * 8 + jj) * 16;
+        int k = jj >> 1, sh = (jj & 1) * 4;
+        for (int j = 0; j < 16; j++) {
+          int lo = (qs[32 * k + j] >> sh) & 15, hi = (qs[32 * k + j + 16] >> sh) & 15;
+          gq[j] = (uint8_t)(lo | (hi << 4));
+        }
+      }
+    }
+    break;
+  case DT_Q6_K:
+    for (int64_t b = 0; b < NB; b++) {
+      const uint8_t* s = src + b * 210;
+      memcpy(dst + rg.s + (o * NB + b) * 16, s + 192, 16);
+      memcpy(dst + rg.s2 + (o * NB + b) * 2, s + 208, 2);
+      for (int u = 0; u < 8; u++) {
+        uint8_t* gq = dst + (o * G + b * 8 + u) * 16;
+        uint8_t* gh = dst + rg.h + (o * G + b * 8 + u) * 8;
+        memset(gh, 0, 8);
+        for (int j = 0; j < 16; j++) {
+          int lo = q6_value(s, 32 * u + j), hi = q6_value(s, 32 * u + j + 16);
+          gq[j] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+          int d = j >> 2, i = j & 3;
+          gh[i] |= (uint8_t)((lo >> 4) << (2 * d));
+          gh[4 + i] |= (uint8_t)((hi >> 4) << (2 * d));
+        }
+      }
+    }
+    break;
+  default:  // float types: unchanged
+    memcpy(dst + o * (int64_t)row_bytes(t, in), src, row_bytes(t, in));
+    break;
+  }
+}
+
+static void unpack_row(const uint8_t* src, uint8_t* dst, int t, int64_t out, int64_t in, int64_t o)
+{
+  const Regions rg = regions(t, out, in);
+  const int64_t G = in / 32, NB = in / 256;
+  switch (t) {
+  case DT_Q8_0:
+    for (int64_t b = 0; b < G; b++) {
+      memcpy(dst + b * 34, src + rg.s + (o * G + b) * 2, 2);
+      memcpy(dst + b * 34 + 2, src + o * in + b * 32, 32);
+    }
+    break;
+  case DT_Q4_0:
+    for (int64_t b = 0; b < G; b++) {
+      memcpy(dst + b * 18, src + rg.s + (o * G + b) * 2, 2);
+      memcpy(dst + b * 18 + 2, src + (o * G + b) * 16, 16);
+    }
+    break;
+  case DT_MXFP4:
+    for (int64_t b = 0; b < G; b++) {
+      dst[b * 17] = src[rg.s + o * G + b];
+      memcpy(dst + b * 17 + 1, src + (o * G + b) * 16, 16);
+    }
+    break;
+  case DT_Q5_0:
+    for (int64_t b = 0; b < G; b++) {
+      memcpy(dst + b * 22, src + rg.s + (o * G + b) * 2, 2);
+      memcpy(dst + b * 22 + 2, src + rg.h + (o * G + b) * 4, 4);
+      memcpy(dst + b * 22 + 6, src + (o * G + b) * 16, 16);
+    }
+    break;
+  case DT_Q5_1:
+    for (int64_t b = 0; b < G; b++) {
+      memcpy(dst + b * 24, src + rg.s + (o * G + b) * 4, 4);
+      memcpy(dst + b * 24 + 4, src + rg.h + (o * G + b) * 4, 4);
+      memcpy(dst + b * 24 + 8, src + (o * G + b) * 16, 16);
+    }
+    break;
+  case DT_Q4_K:
+    for (int64_t b = 0; b < NB; b++) {
+      uint8_t* d = dst + b * 144;
+      memcpy(d, src + rg.s + (o * NB + b) * 16, 16);
+      memset(d + 16, 0, 128);
+      for (int jj = 0; jj < 8; jj++) {
+        const uint8_t* gq = src + (o * G + b * 8 + jj) * 16;
+        int k = jj >> 1, sh = (jj & 1) * 4;
+        for (int j = 0; j < 16; j++) {
+          d[16 + 32 * k + j] |= (uint8_t)((gq[j] & 15) << sh);
+          d[16 + 32 * k + j + 16] |= (uint8_t)((gq[j] >> 4) << sh);
+        }
+      }
+    }
+    break;
+  case DT_Q6_K:
+    for (int64_t b = 0; b < NB; b++) {
+      uint8_t* d = dst + b * 210;
+      memset(d, 0, 192);
+      memcpy(d + 192, src + rg.s + (o * NB + b) * 16, 16);
+      memcpy(d + 208, src + rg.s2 + (o * NB + b) * 2, 2);
+      for (int u = 0; u < 8; u++) {
+        const uint8_t* gq = src + (o * G + b * 8 + u) * 16;
+        const uint8_t* gh = src + rg.h + (o * G + b * 8 + u) * 8;
+        for (int v = 0; v < 32; v++) {
+          int j = v & 15, hiv = v >> 4, dd = j >> 2, ii = j & 3;
+          int q = (hiv ? (gq[j] >> 4) : (gq[j] & 15)) | (((gh[4 * hiv + ii] >> (2 * dd)) & 3) << 4);
+          int i = 32 * u + v, n = i >> 7, l = i & 31, qq = (i & 127) >> 5;
+          d[128 + 32 * n + l] |= (uint8_t)((q >> 4) << (2 * qq));
+          int qi = 64 * n + l + ((qq & 1) ? 32 : 0);
+          d[qi] |= (uint8_t)((q & 15) << (qq >= 2 ? 4 : 0));
+        }
+      }
+    }
+    break;
+  default:
+    memcpy(dst, src + o * (int64_t)row_bytes(t, in), row_bytes(t, in));
+    break;
+  }
+}
+
+static void for_rows(int64_t total, const std::function<void(int64_t, int64_t)>& fn)
+{
+  unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (total < 4096 || nt == 1) {
+    fn(0, total);
+    return;
+  }
+  std::vector<std::thread> th;
+  int64_t per = (total + nt - 1) / nt;
+  for (unsigned i = 0; i < nt; i++) {
+    int64_t a = i * per, b = std::min(total, a + per);
+    if (a < b) th.emplace_back(fn, a, b);
+  }
+  for (auto& x : th) x.join();
+}
+
+void repack(const void* src, void* dst, int t, int64_t out, int64_t in, int64_t count)
+{
+  const uint64_t rb = row_bytes(t, in), mb = rb * out;
+  for_rows(count * out, [&](int64_t a, int64_t b) {
+    for (int64_t i = a; i < b; i++) {
+      int64_t m = i / out, o = i % out;
+      repack_row((const uint8_t*)src + m * mb + o * rb, (uint8_t*)dst + m * mb, t, out, in, o);
+    }
+  });
+}
+
+void unpack(const void* src, void* dst, int t, int64_t out, int64_t in, int64_t count)
+{
+  const uint64_t rb = row_bytes(t, in), mb = rb * out;
+  for_rows(count * out, [&](int64_t a, int64_t b) {
+    for (int64_t i = a; i < b; i++) {
+      int64_t m = i / out, o = i % out;
+      unpack_row((const uint8_t*)src + m * mb, (uint8_t*)dst + m * mb + o * rb, t, out, in, o);
+    }
+  });
+}
+
+// --------------------------------------------------------------- dispatch
+static const char* fmt_name(int t)
+{
+  switch (t) {
+  case DT_Q8_0: return "q8_0";
+  case DT_Q4_0: return "q4_0";
+  case DT_MXFP4: return "mxfp4";
+  case DT_Q5_0: return "q5_0";
+  case DT_Q5_1: return "q5_1";
+  case DT_Q4_K: return "q4_k";
+  case DT_Q6_K: return "q6_k";
+  case DT_F32: return "f32";
+  case DT_BF16: return "bf16";
+  case DT_F16: return "f16";
+  default: return nullptr;
+  }
+}
+
+int q8_kind(int t)
+{
+  if (t == DT_Q4_K || t == DT_Q6_K) return 1;
+  if (t == DT_F32 || t == DT_BF16 || t == DT_F16) return -1;
+  return 0;
+}
+
+static bool linear_ok(int t, int64_t in)
+{
+  if (!fmt_name(t) || in <= 0 || in % 32) return false;
+  if ((t == DT_Q4_K || t == DT_Q6_K) && in % 256) return false;
+  return in / 32 <= 256;  // the activation of a lane's groups stays in registers
+}
+
+// lanes per row and groups per lane: the least idle lanes, then wider rows
+static void pick_lpr(int64_t G, int& lpr, int& U)
+{
+  int best = -1;
+  for (int l : {64, 32, 16, 8}) {
+    int u = (int)((G + l - 1) / l);
+    if (u > 4) continue;
+    int waste = l * u - (int)G;
+    if (best < 0 || waste < best) {
+      best = waste;
+      lpr = l;
+      U = u;
+    }
+  }
+}
+
+uint64_t q8_row_bytes(int64_t in) { return (uint64_t)in + 4 * (uint64_t)(in / 32); }
+
+int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind, uint64_t xq)
+{
+  struct {
+    const float* x;
+    uint8_t* xq;
+    int* bad;
+    int32_t rows, in;
+  } a = {(const float*)x, (uint8_t*)xq, (int*)c->scratch_bad, (int32_t)rows, (int32_t)in};
+  if (kind == 0) {
+    int64_t G = in / 32;
+    return launch(c, "quantize_q8_0", dim3((unsigned)((G + 255) / 256), (unsigned)rows), dim3(256), &a);
+  }
+  int64_t NB = in / 256;
+  return launch(c, "quantize_q8_k", dim3((unsigned)((NB + 3) / 4), (unsigned)rows), dim3(256), &a);
+}
+
+int enqueue_linear(ihip_ctx* c, const LinearCall& k)
+{
+  if (!linear_ok(k.dtype, k.in) || k.out < 1 || k.out > INT32_MAX || k.rows < 1 || k.rows > 65535 ||
+      !k.w || !k.x || !k.y)
+    return fail(IHIP_E_ARG, "EnqueueLinear: " + std::to_string(k.rows) + " rows of " +
+                                std::to_string(k.in) + " dtype " + std::to_string(k.dtype) +
+                                " into " + std::to_string(k.out));
+  const int64_t G = k.in / 32;
+  int lpr = 64, U = 1;
+  pick_lpr(G, lpr, U);
+  uint64_t xq = k.xq;
+  const bool q8 = k.mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
+  if (q8 && !xq) {
+    int64_t xrows = k.ids ? (k.x_per_slot ? (k.rows + k.x_per_slot - 1) / k.x_per_slot : 1) : k.rows;
+    int rc = scratch(c, c->scratch_q, c->scratch_q_bytes, xrows * q8_row_bytes(k.in));
+    if (rc) return rc;
+    xq = c->scratch_q;
+    rc = enqueue_quantize(c, k.x, xrows, k.in, q8_kind(k.dtype), xq);
+    if (rc) return rc;
+  }
+  struct {
+    const uint8_t* w;
+    const float* x;
+    const uint8_t* xq;
+    const float* bias;
+    float* y;
+    const int* ids;
+    int64_t stride;
+    int32_t out, in, rows, lpr;
+    int32_t x_per_slot;
+    int32_t nexp;
+  } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
+         (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
+         (int32_t)k.rows, lpr, k.x_per_slot, k.nexp};
+  const bool batch = !k.ids && k.rows > 1;
+  char name[64];
+  snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
+           k.mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : "", U);
+  const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
+  int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
+  unsigned gy = (unsigned)(k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1));
+  return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
+}
+
+static WeightEntry* find_weight(ihip_ctx* c, const void* host, int t, uint64_t bytes)
+{
+  for (auto& w : c->weights)
+    if (w.host == host && w.dtype == t && w.bytes == bytes) return &w;
+  return nullptr;
+}
+
+}  // namespace ihip
+
+using namespace ihip;
+
+extern "C" {
+
+uint64_t ihip_type_bytes(int t, uint64_t count)
+{
+  int bv = block_values(t);
+  if (!bv || count % bv) return 0;
+  return count / bv * block_bytes(t);
+}
+
+int ihip_gpu_linear(int t, int64_t in) { return linear_ok(t, in) ? 1 : 0; }
+
+int ihip_repack(const void* src, void* dst, int t, int64_t out, int64_t in, int64_t count,
+                int inverse)
+{
+  if (!src || !dst || out < 1 || in < 1 || count < 1 || !block_values(t) || in % block_values(t) ||
+      (t != DT_F32 && t != DT_F16 && t != DT_BF16 && in % 32))
+    return fail(IHIP_E_ARG, "ihip_repack: bad shape or type");
+  if (inverse) unpack(src, dst, t, out, in, count);
+  else repack(src, dst, t, out, in, count);
+  return 0;
+}
+
+int ihip_weight(ihip_ctx* c, const void* host, int t, int64_t out, int64_t in, int64_t count,
+                uint64_t* dev)
+{
+  if (!c || !host || !dev || out < 1 || in < 1 || count < 1 || !block_values(t) ||
+      in % block_values(t))
+    return fail(IHIP_E_ARG, "ihip_weight: bad shape or type");
+  const uint64_t bytes = row_bytes(t, in) * (uint64_t)out * (uint64_t)count;
+  if (WeightEntry* w = find_weight(c, host, t, bytes)) {
+    *dev = w->dev;
+    return 0;
+  }
+  if (c->capturing) return fail(IHIP_E_CAPTURE, "ihip_weight: upload while capturing");
+  void* p = nullptr;
+  IHIP_CHECK(hipSetDevice(c->device));
+  // rounded up to 256 bytes: a 16-byte load never reaches past the buffer
+  IHIP_CHECK(hipMalloc(&p, (bytes + 255) & ~(uint64_t)255));
+  std::vector<uint8_t> staged(bytes);
+  repack(host, staged.data(), t, out, in, count);
+  hipError_t e = hipMemcpyHtoD((hipDeviceptr_t)p, staged.data(), bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "ihip_weight upload");
+  }
+  c->weights.push_back({host, t, bytes, (uint64_t)p});
+  *dev = (uint64_t)p;
+  return 0;
+}
+
+int ihip_weight_f32(ihip_ctx* c, const float* host, int64_t count, uint64_t* dev)
+{
+  return ihip_weight(c, host, DT_F32, 1, count, 1, dev);
+}
+
+int ihip_forget_weights(ihip_ctx* c, const void* from, const void* to)
+{
+  if (!c) return fail(IHIP_E_ARG, "ihip_forget_weights");
+  if ((uintptr_t)to <= (uintptr_t)from) return c->weight_epoch;
+  size_t n = 0, before = c->weights.size();
+  for (size_t i = 0; i < c->weights.size(); i++) {
+    WeightEntry& w = c->weights[i];
+    if ((uintptr_t)w.host < (uintptr_t)to && (uintptr_t)w.host + w.bytes > (uintptr_t)from) {
+      (void)hipStreamSynchronize(c->stream);
+      (void)hipFree((void*)w.dev);
+    } else {
+      c->weights[n++] = w;
+    }
+  }
+  c->weights.resize(n);
+  if (n != before) c->weight_epoch++;
+  return c->weight_epoch;
+}
+
+int ihip_clear_weights(ihip_ctx* c)
+{
+  if (!c) return fail(IHIP_E_ARG, "ihip_clear_weights");
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& w : c->weights) (void)hipFree((void*)w.dev);
+  c->weights.clear();
+  return ++c->weight_epoch;
+}
+
+int ihip_enqueue_linear_at(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int t, uint64_t w,
+                           int64_t out, uint64_t y, uint64_t bias, int mode)
+{
+  if (!c) return fail(IHIP_E_ARG, "no context");
+  LinearCall k;
+  k.x = x; k.rows = rows; k.in = in; k.dtype = t; k.w = w; k.out = out; k.y = y;
+  k.bias = bias; k.mode = mode;
+  return enqueue_linear(c, k);
+}
+
+int ihip_enqueue_linear_ids(ihip_ctx* c, uint64_t x, int64_t in, int t, uint64_t w,
+                            int64_t stride, int64_t out, uint64_t ids, int64_t slots,
+                            int x_per_slot, uint64_t y, uint64_t bias, int mode)
+{
+  if (!c || !ids || stride <= 0) return fail(IHIP_E_ARG, "EnqueueLinearIds: no ids or stride");
+  LinearCall k;
+  k.x = x; k.rows = slots; k.in = in; k.dtype = t; k.w = w; k.out = out; k.y = y;
+  k.bias = bias; k.mode = mode; k.ids = ids; k.stride = stride; k.x_per_slot = x_per_slot;
+  return enqueue_linear(c, k);
+}
+
+int ihip_linear(ihip_ctx* c, const float* x, int64_t rows, int64_t in, const void* w, int t,
+                int64_t out, const float* bias, float* y, int mode)
+{
+  if (!c || !x || !w || !y) return fail(IHIP_E_ARG, "ihip_linear: null buffer");
+  if (!linear_ok(t, in)) return fail(IHIP_E_UNSUPPORTED, "ihip_linear: not supported");
+  std::lock_guard<std::mutex> g(c->lock);
+  uint64_t dw = 0, db = 0;
+  int rc = ihip_weight(c, w, t, out, in, 1, &dw);
+  if (!rc && bias) rc = ihip_weight_f32(c, bias, out, &db);
+  if (!rc) rc = scratch(c, c->scratch_x, c->scratch_x_bytes, (uint64_t)rows * in * 4);
+  if (!rc) rc = scratch(c, c->scratch_y, c->scratch_y_bytes, (uint64_t)rows * out * 4);
+  if (rc) return rc;
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)c->scratch_x, (void*)x, (size_t)rows * in * 4, c->stream));
+  rc = ihip_enqueue_linear_at(c, c->scratch_x, rows, in, t, dw, out, c->scratch_y, db, mode);
+  if (rc) return rc;
+  IHIP_CHECK(hipMemcpyDtoHAsync(y, (hipDeviceptr_t)c->scratch_y, (size_t)rows * out * 4, c->stream));
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+int ihip_enqueue_dequant(ihip_ctx* c, uint64_t w, int t, int64_t out, int64_t in, int64_t row0,
+                         int64_t rows, uint64_t y)
+{
+  if (!c || !fmt_name(t) || in % 32 || ((t == DT_Q4_K || t == DT_Q6_K) && in % 256) || rows < 1 ||
+      row0 < 0 || row0 + rows > out)
+    return fail(IHIP_E_ARG, "ihip_enqueue_dequant: bad shape");
+  struct {
+    const uint8_t* w;
+    const int* ids;
+    float* y;
+    int64_t row0;
+    int32_t out, in, rows, pad;
+  } a = {(const uint8_t*)w, nullptr, (float*)y, row0, (int32_t)out, (int32_t)in, (int32_t)rows, 0};
+  char name[48];
+  snprintf(name, sizeof name, "dequant_%s", fmt_name(t));
+  return launch(c, name, dim3((unsigned)((rows + 3) / 4)), dim3(256), &a);
+}
+
+int ihip_enqueue_embed(ihip_ctx* c, uint64_t embed, int t, int64_t vocab, int64_t hidden,
+                       uint64_t ids, int64_t rows, uint64_t x)
+{
+  if (!c || !fmt_name(t) || hidden % 32 || rows < 1 || !ids)
+    return fail(IHIP_E_ARG, "ihip_enqueue_embed: bad shape");
+  struct {
+    const uint8_t* w;
+    const int* ids;
+    float* y;
+    int64_t row0;
+    int32_t out, in, rows, pad;
+  } a = {(const uint8_t*)embed, (const int*)ids, (float*)x, 0, (int32_t)vocab, (int32_t)hidden,
+         (int32_t)rows, 0};
+  char name[48];
+  snprintf(name, sizeof name, "dequant_%s", fmt_name(t));
+  return launch(c, name, dim3((unsigned)((rows + 3) / 4)), dim3(256), &a);
+}
+
+uint64_t ihip_q8_bytes(int64_t in, int k_quant)
+{
+  (void)k_quant;
+  return q8_row_bytes(in);
+}
+
+int ihip_enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int k_quant,
+                          uint64_t xq, uint64_t bad)
+{
+  if (!c || in % (k_quant ? 256 : 32) || rows < 1) return fail(IHIP_E_ARG, "ihip_enqueue_quantize");
+  uint64_t keep = c->scratch_bad;
+  if (bad) c->scratch_bad = bad;
+  int rc = enqueue_quantize(c, x, rows, in, k_quant ? 1 : 0, xq);
+  c->scratch_bad = keep;
+  return rc;
+}
+
+struct NormArgs {
+  float* x;
+  const float* t;
+  const float* w;
+  float* y;
+  double eps;
+  int32_t rows, cols;
+};
+
+int ihip_enqueue_rmsnorm(ihip_ctx* c, uint64_t x, uint64_t w, uint64_t y, int64_t rows,
+                         int64_t cols, double eps)
+{
+  if (!c || rows < 1 || cols < 1) return fail(IHIP_E_ARG, "ihip_enqueue_rmsnorm");
+  NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols};
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+}
+
+int ihip_enqueue_addnorm(ihip_ctx* c, uint64_t x, uint64_t t, uint64_t w, uint64_t y, int64_t rows,
+                         int64_t cols, double eps)
+{
+  if (!c || rows < 1 || cols < 1 || !t) return fail(IHIP_E_ARG, "ihip_enqueue_addnorm");
+  NormArgs a = {(float*)x, (const float*)t, (const float*)w, (float*)y, eps, (int32_t)rows,
+                (int32_t)cols};
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+}
+
+struct EltArgs {
+  float* x;
+  const float* t;
+  int64_t n;
+  float alpha, limit;
+};
+
+int ihip_enqueue_add(ihip_ctx* c, uint64_t x, uint64_t t, int64_t n)
+{
+  if (!c || n < 1) return fail(IHIP_E_ARG, "ihip_enqueue_add");
+  EltArgs a = {(float*)x, (const float*)t, n, 0.f, 0.f};
+  return launch(c, "add", dim3((unsigned)((n + 255) / 256)), dim3(256), &a);
+}
+
+int ihip_enqueue_swiglu(ihip_ctx* c, uint64_t gate, uint64_t up, int64_t n, float alpha, float limit)
+{
+  if (!c || n < 1) return fail(IHIP_E_ARG, "ihip_enqueue_swiglu");
+  EltArgs a = {(float*)gate, (const float*)up, n, alpha, limit};
+  return launch(c, "swiglu", dim3((unsigned)((n + 255) / 256)), dim3(256), &a);
+}
+
+int ihip_enqueue_qkrope(ihip_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_t qn, uint64_t kn,
+                        uint64_t cs, uint64_t kc, uint64_t vc, int64_t rows, int64_t heads,
+                        int64_t kvh, int64_t hd, int64_t past, double eps, int kv_f16)
+{
+  if (!c || rows < 1 || heads < 1 || kvh < 1 || hd < 2 || hd > 512 || (hd & 1) || past < 0)
+    return fail(IHIP_E_ARG, "ihip_enqueue_qkrope");
+  struct {
+    float* q;
+    const float* k;
+    const float* v;
+    const float* qn;
+    const float* kn;
+    const float* cs;
+    void* kc;
+    void* vc;
+    const int* pastp;
+    double eps;
+    int32_t rows, heads, kvh, hd, past, f16;
+  } a = {(float*)q, (const float*)k, (const float*)v, (const float*)qn, (const float*)kn,
+         (const float*)cs, (void*)kc, (void*)vc, nullptr, eps, (int32_t)rows, (int32_t)heads,
+         (int32_t)kvh, (int32_t)hd, (int32_t)past, kv_f16};
+  return launch(c, "qkrope", dim3((unsigned)(heads + kvh), (unsigned)rows), dim3(64), &a);
+}
+
+int ihip_enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y,
+                           int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
+                           int64_t window, uint64_t sinks, double scale, int kv_f16)
+{
+  if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 1 || hd > 256 || 256 % hd ||
+      past < 0 || window < 0)
+    return fail(IHIP_E_ARG, "ihip_enqueue_attention");
+  int64_t maxkeys = past + rows;
+  if (window > 0 && maxkeys > window) maxkeys = window;
+  if (maxkeys > 8000) return fail(IHIP_E_UNSUPPORTED, "attention: more than 8000 keys per row");
+  if (!(scale > 0)) scale = 1.0 / sqrt((double)hd);
+  struct {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* y;
+    const float* sinks;
+    const int* pastp;
+    double scale;
+    int32_t rows, heads, kvh, hd, past, window, f16, maxkeys;
+  } a = {(const float*)q, (const void*)kc, (const void*)vc, (float*)y, (const float*)sinks,
+         nullptr, scale,
+         (int32_t)rows, (int32_t)heads, (int32_t)kvh, (int32_t)hd, (int32_t)past, (int32_t)window,
+         kv_f16, (int32_t)maxkeys};
+  return launch(c, "attention", dim3((unsigned)heads, (unsigned)rows), dim3(256), &a,
+                (size_t)maxkeys * 8);
+}
+
+int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k, int norm_topk,
+                       uint64_t ids, uint64_t w)
+{
+  if (!c || experts < 1 || experts > 4096 || k < 1 || k > 64 || k > experts)
+    return fail(IHIP_E_ARG, "ihip_enqueue_route");
+  struct {
+    const float* logits;
+    int* ids;
+    float* w;
+    int32_t experts, k, norm, rows;
+  } a = {(const float*)logits, (int*)ids, (float*)w, (int32_t)experts, (int32_t)k, norm_topk, 1};
+  return launch(c, "route", dim3(1), dim3(64), &a);
+}
+
+int ihip_enqueue_moecombine(ihip_ctx* c, uint64_t d, uint64_t w, uint64_t y, int64_t k, int64_t n)
+{
+  if (!c || k < 1 || n < 1) return fail(IHIP_E_ARG, "ihip_enqueue_moecombine");
+  struct {
+    const float* d;
+    const float* w;
+    float* y;
+    int32_t k, n, rows, pad;
+  } a = {(const float*)d, (const float*)w, (float*)y, (int32_t)k, (int32_t)n, 1, 0};
+  return launch(c, "moecombine", dim3((unsigned)((n + 255) / 256), 1), dim3(256), &a);
+}
+
+int ihip_enqueue_argmax(ihip_ctx* c, uint64_t v, int64_t n, uint64_t out)
+{
+  if (!c || n < 1) return fail(IHIP_E_ARG, "ihip_enqueue_argmax");
+  struct {
+    const float* v;
+    int* out;
+    int64_t n;
+  } a = {(const float*)v, (int*)out, n};
+  return launch(c, "argmax", dim3(1), dim3(1024), &a);
+}
+
+}  // extern "C"

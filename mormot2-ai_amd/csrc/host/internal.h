@@ -1,0 +1,101 @@
+// internal.h - host-side internals of libmormot_ai_hip (C++17, HIP runtime).
+#pragma once
+
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../../include/mormot_ai_hip.h"
+#include "../layout.h"
+
+namespace ihip {
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define IHIP_CHECK(call)                                   \
+  do {                                                     \
+    hipError_t e_ = (call);                                \
+    if (e_ != hipSuccess) return ::ihip::hip_fail(e_, #call); \
+  } while (0)
+
+struct WeightEntry {
+  const void* host;
+  int dtype;
+  uint64_t bytes;
+  uint64_t dev;
+};
+
+struct Kernel {
+  hipFunction_t f = nullptr;
+};
+
+// the module of one embedded code object
+struct Module {
+  hipModule_t mod = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fn;
+};
+
+}  // namespace ihip
+
+// one device + one non-blocking stream + the embedded modules + the weight
+// cache (TInferCuda + TInferCudaBackend of the reference)
+struct ihip_ctx {
+  int device = 0;
+  int cus = 256;
+  hipStream_t stream = nullptr;
+  std::vector<ihip::Module> modules;
+  std::unordered_map<std::string, hipFunction_t> kernels;
+  std::vector<ihip::WeightEntry> weights;
+  int weight_epoch = 0;
+  std::vector<uint64_t> allocations;
+  // scratch of the synchronous Linear and of the quantized activations
+  uint64_t scratch_x = 0, scratch_x_bytes = 0;
+  uint64_t scratch_y = 0, scratch_y_bytes = 0;
+  uint64_t scratch_q = 0, scratch_q_bytes = 0;
+  uint64_t scratch_bad = 0;
+  bool capturing = false;
+  hipGraph_t graphs[16] = {};
+  hipGraphExec_t execs[16] = {};
+  hipEvent_t events[64] = {};
+  std::mutex lock;
+};
+
+namespace ihip {
+
+hipFunction_t kernel(ihip_ctx* c, const char* name);
+int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, size_t shmem = 0);
+// grows a scratch buffer to at least bytes (never while capturing)
+int scratch(ihip_ctx* c, uint64_t& buf, uint64_t& cap, uint64_t bytes);
+
+// repack [count, out, in] GGUF blocks into the HIP layout (multi-threaded)
+void repack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int64_t count);
+// and back (tests of the layout)
+void unpack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int64_t count);
+
+// the Linear dispatch shared by the public entry points and the model
+struct LinearCall {
+  uint64_t x = 0;      // float activations [rows, in]
+  uint64_t xq = 0;     // quantized activations (Q8 mode), 0: quantized here
+  int64_t rows = 1, in = 0, out = 0;
+  int dtype = 0;
+  uint64_t w = 0, bias = 0, y = 0;
+  int mode = IHIP_MODE_F32;
+  uint64_t ids = 0;    // expert ids: slots = rows
+  int64_t stride = 0;
+  int x_per_slot = 0;
+  int nexp = 0;        // experts behind ids (a bad id gives a zero row), 0: unchecked
+};
+int enqueue_linear(ihip_ctx* c, const LinearCall& call);
+// which activation quantizer a weight type needs in Q8 mode: -1 none (float
+// weights), 0 Q8_0, 1 Q8_K
+int q8_kind(int dtype);
+int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind, uint64_t xq);
+
+}  // namespace ihip

@@ -1,0 +1,598 @@
+// model.cpp - TQwen3Cuda of the reference
+// (src/infer/mormot.ai.infer.model.qwen3.cuda.pas:150-1761) for HIP: the
+// whole decoder on the device behind TDecoderDevice (decoder.pas:907-928).
+// Qwen3 dense, Qwen3-MoE and gpt-oss shapes: per-head q/k norms, biases,
+// sinks, sliding windows, clamped SwiGLU, experts chosen on the device.
+//
+// A prompt runs in chunks of up to CHUNK rows (the 256 of CHUNK_MAX,
+// model.qwen3.cuda.pas:308); a decode step (one row) is one HIP graph,
+// captured once and replayed: the position lives in device memory, the
+// token id and the cos/sin of the position are copied in before each launch,
+// and the argmax runs on the device, so one int32 comes back per token.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+
+#include "internal.h"
+
+namespace ihip {
+
+static const int64_t CHUNK = 256;
+
+struct DevLayer {
+  uint64_t input_norm = 0, post_norm = 0, q = 0, k = 0, v = 0, o = 0;
+  uint64_t qb = 0, kb = 0, vb = 0, ob = 0, qn = 0, kn = 0, sinks = 0;
+  uint64_t gate = 0, up = 0, down = 0, router = 0, router_b = 0;
+  uint64_t eg = 0, eu = 0, ed = 0, egb = 0, eub = 0, edb = 0;
+  int qd = 0, kd = 0, vd = 0, od = 0, gd = 0, ud = 0, dd = 0, rd = 0, egd = 0, eud = 0, edd = 0;
+  int64_t eg_stride = 0, ed_stride = 0;
+  uint64_t kc = 0, vc = 0;
+  int window = 0, moe = 0;
+};
+
+}  // namespace ihip
+
+struct ihip_model {
+  ihip_ctx* c = nullptr;
+  ihip_model_desc d{};
+  std::vector<ihip_layer_desc> layer_desc;
+  std::vector<ihip::DevLayer> L;
+  int mode = IHIP_MODE_Q8, kv_f16 = 0;
+  int64_t max_tokens = 0, length = 0;
+  uint64_t embed = 0, final_norm = 0, head = 0;
+  int embed_dt = 0, head_dt = 0;
+  // activations for CHUNK rows
+  uint64_t x = 0, h = 0, tmp = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0;
+  uint64_t route = 0, ids = 0, rw = 0, eout = 0, cs = 0, tok = 0, logits = 0, next = 0, pos = 0;
+  uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
+  uint64_t logits_all = 0;
+  int64_t logits_all_rows = 0;
+  std::vector<uint64_t> owned;
+  bool graph_ready = false;
+  double prefill_ms = 0, decode_ms = 0;
+};
+
+namespace ihip {
+
+// decoder.pas:1735-1741 and 1759-1829: inverse frequencies, every step
+// rounded to single as the reference's float32 tensors; YaRN when factor > 0
+static void inv_freq(const ihip_model_desc& d, std::vector<float>& f, float& scale)
+{
+  const int64_t dim = d.head_dim, half = dim / 2;
+  const double lt = std::log(d.rope_theta);
+  f.assign(half, 0.f);
+  for (int64_t i = 0; i < half; i++) {
+    float e = (float)((double)(2 * i) / (double)dim);
+    float p = (float)std::exp(lt * (double)e);
+    f[i] = 1.0f / p;
+  }
+  scale = 1.0f;
+  if (d.rope_factor == 0) return;
+  const double pi2 = 2 * M_PI;
+  auto corr = [&](double rot) {
+    return ((double)dim * std::log((double)d.rope_original / (rot * pi2))) / (2 * lt);
+  };
+  double lo = corr(d.rope_beta_fast), hi = corr(d.rope_beta_slow);
+  if (d.rope_truncate) {
+    lo = std::floor(lo);
+    hi = std::ceil(hi);
+  }
+  if (lo < 0) lo = 0;
+  if (hi > dim - 1) hi = (double)(dim - 1);
+  if (lo == hi) hi = hi + 0.001;
+  const float loS = (float)lo, spanS = (float)(hi - lo), fct = (float)d.rope_factor;
+  for (int64_t i = 0; i < half; i++) {
+    float e = (float)((double)(2 * i) / (double)dim);
+    float pos = (float)std::exp(lt * (double)e);
+    pos = fct * pos;
+    float inter = 1.0f / pos, extra = f[i];
+    float ramp = ((float)i - loS) / spanS;
+    ramp = ramp < 0 ? 0.f : (ramp > 1 ? 1.f : ramp);
+    float keep = 1.0f - ramp;
+    ramp = 1.0f - keep;
+    inter = inter * ramp;
+    extra = extra * keep;
+    f[i] = inter + extra;
+  }
+  if (d.rope_attention > 0) scale = (float)d.rope_attention;
+  else if (fct <= 1) scale = 1.0f;
+  else scale = (float)(0.1 * std::log((double)fct) + 1.0);
+}
+
+// TDecoderModel.Rotary (decoder.pas:2539-2561): the angle in single, cos and
+// sin rounded to single, then times the YaRN scale in single
+static void rotary(const ihip_model_desc& d, int64_t first, int64_t rows, float* cs)
+{
+  std::vector<float> f;
+  float rs;
+  inv_freq(d, f, rs);
+  const int64_t half = d.head_dim / 2;
+  float* sn = cs + rows * half;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t i = 0; i < half; i++) {
+      float angle = f[i] * (float)(first + r);
+      float c = (float)std::cos((double)angle), s = (float)std::sin((double)angle);
+      if (rs != 1.0f) {
+        c = c * rs;
+        s = s * rs;
+      }
+      cs[r * half + i] = c;
+      sn[r * half + i] = s;
+    }
+}
+
+static int dalloc(ihip_model* m, uint64_t bytes, uint64_t& p)
+{
+  void* q = nullptr;
+  IHIP_CHECK(hipMalloc(&q, bytes ? (bytes + 255) & ~(uint64_t)255 : 256));
+  m->owned.push_back((uint64_t)q);
+  p = (uint64_t)q;
+  return 0;
+}
+
+static int upw(ihip_model* m, const ihip_tensor& t, int64_t out, int64_t in, int64_t count,
+               uint64_t& dev, int& dt)
+{
+  dev = 0;
+  dt = t.dtype;
+  if (!t.data) return 0;
+  return ihip_weight(m->c, t.data, t.dtype, out, in, count, &dev);
+}
+
+static int upf(ihip_model* m, const ihip_tensor& t, int64_t n, uint64_t& dev)
+{
+  dev = 0;
+  if (!t.data) return 0;
+  if (t.dtype != DT_F32) return fail(IHIP_E_ARG, "model: norms, biases and sinks are F32");
+  return ihip_weight_f32(m->c, (const float*)t.data, n, &dev);
+}
+
+// the quantized copy of an activation buffer for a weight type, made once
+struct QCache {
+  uint64_t buf0 = 0, bufk = 0;
+  bool have0 = false, havek = false;
+};
+
+static int lin(ihip_model* m, uint64_t x, QCache* qc, int64_t rows, int64_t in, int dt,
+               uint64_t w, int64_t out, uint64_t bias, uint64_t y)
+{
+  LinearCall k;
+  k.x = x; k.rows = rows; k.in = in; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
+  k.y = y; k.mode = m->mode;
+  if (m->mode == IHIP_MODE_Q8 && qc && q8_kind(dt) >= 0) {
+    int kind = q8_kind(dt);
+    bool& have = kind ? qc->havek : qc->have0;
+    uint64_t buf = kind ? qc->bufk : qc->buf0;
+    if (!have) {
+      int rc = enqueue_quantize(m->c, x, rows, in, kind, buf);
+      if (rc) return rc;
+      have = true;
+    }
+    k.xq = buf;
+  }
+  return enqueue_linear(m->c, k);
+}
+
+static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int64_t in, int dt,
+                   uint64_t w, int64_t stride, int64_t out, uint64_t ids, int64_t slots,
+                   int x_div, uint64_t bias, uint64_t y, bool quantized)
+{
+  LinearCall k;
+  k.x = x; k.rows = slots; k.in = in; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
+  k.y = y; k.mode = m->mode; k.ids = ids; k.stride = stride; k.x_per_slot = x_div;
+  k.nexp = m->d.experts;
+  if (m->mode == IHIP_MODE_Q8 && q8_kind(dt) >= 0) {
+    if (!quantized) {
+      int rc = enqueue_quantize(m->c, x, xrows, in, q8_kind(dt), xqbuf);
+      if (rc) return rc;
+    }
+    k.xq = xqbuf;
+  }
+  return enqueue_linear(m->c, k);
+}
+
+static int rope_attn(ihip_model* m, const DevLayer& L, int64_t n, int64_t past, bool graph)
+{
+  const ihip_model_desc& d = m->d;
+  struct {
+    float* q;
+    const float* k;
+    const float* v;
+    const float* qn;
+    const float* kn;
+    const float* cs;
+    void* kc;
+    void* vc;
+    const int* pastp;
+    double eps;
+    int32_t rows, heads, kvh, hd, past, f16;
+  } ra = {(float*)m->q, (const float*)m->k, (const float*)m->v, (const float*)L.qn,
+          (const float*)L.kn, (const float*)m->cs, (void*)L.kc, (void*)L.vc,
+          graph ? (const int*)m->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads,
+          d.kv_heads, d.head_dim, (int32_t)past, m->kv_f16};
+  int rc = launch(m->c, "qkrope", dim3((unsigned)(d.heads + d.kv_heads), (unsigned)n), dim3(64), &ra);
+  if (rc) return rc;
+  int64_t maxkeys = graph ? m->max_tokens : past + n;
+  if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
+  if (maxkeys > 8000) return fail(IHIP_E_UNSUPPORTED, "attention: more than 8000 keys");
+  struct {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* y;
+    const float* sinks;
+    const int* pastp;
+    double scale;
+    int32_t rows, heads, kvh, hd, past, window, f16, maxkeys;
+  } aa = {(const float*)m->q, (const void*)L.kc, (const void*)L.vc, (float*)m->attn,
+          (const float*)L.sinks, graph ? (const int*)m->pos : nullptr,
+          1.0 / std::sqrt((double)d.head_dim), (int32_t)n, d.heads, d.kv_heads, d.head_dim,
+          (int32_t)past, L.window, m->kv_f16, (int32_t)maxkeys};
+  return launch(m->c, "attention", dim3((unsigned)d.heads, (unsigned)n), dim3(256), &aa,
+                (size_t)maxkeys * 8);
+}
+
+// the layers of one chunk of n rows at positions past.., x holding the
+// embeddings; leaves h = the final norm of x. graph: the position is read
+// from m->pos (decode step under capture)
+static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
+{
+  const ihip_model_desc& d = m->d;
+  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
+                kvw = (int64_t)d.kv_heads * hd;
+  int rc = ihip_enqueue_rmsnorm(m->c, m->x, m->L[0].input_norm, m->h, n, H, d.rms_eps);
+  if (rc) return rc;
+  for (int l = 0; l < d.layers; l++) {
+    const DevLayer& L = m->L[l];
+    QCache qh{m->xq0, m->xqk};
+    // attention block (decoder.pas:2625-2702)
+    if ((rc = lin(m, m->h, &qh, n, H, L.qd, L.q, qw, L.qb, m->q))) return rc;
+    if ((rc = lin(m, m->h, &qh, n, H, L.kd, L.k, kvw, L.kb, m->k))) return rc;
+    if ((rc = lin(m, m->h, &qh, n, H, L.vd, L.v, kvw, L.vb, m->v))) return rc;
+    if ((rc = rope_attn(m, L, n, past, graph))) return rc;
+    QCache qa{m->xq0, m->xqk};
+    if ((rc = lin(m, m->attn, &qa, n, qw, L.od, L.o, H, L.ob, m->tmp))) return rc;
+    // residual, then the pre-FFN norm
+    if ((rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, L.post_norm, m->h, n, H, d.rms_eps)))
+      return rc;
+    QCache qf{m->xq0, m->xqk};
+    if (!L.moe) {
+      // DenseFfn (decoder.pas:2866-2878)
+      const int64_t F = d.ffn;
+      if ((rc = lin(m, m->h, &qf, n, H, L.gd, L.gate, F, 0, m->gate))) return rc;
+      if ((rc = lin(m, m->h, &qf, n, H, L.ud, L.up, F, 0, m->up))) return rc;
+      if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * F, d.swiglu_alpha, d.swiglu_limit)))
+        return rc;
+      QCache qg{m->xqf, m->xqf};
+      if ((rc = lin(m, m->gate, &qg, n, F, L.dd, L.down, H, 0, m->tmp))) return rc;
+    } else {
+      // MoeBlock (decoder.pas:3037-3053) with the experts chosen on the
+      // device (model.qwen3.cuda.pas:1152-1205)
+      const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
+      if ((rc = lin(m, m->h, &qf, n, H, L.rd, L.router, E, L.router_b, m->route))) return rc;
+      struct {
+        const float* logits;
+        int* ids;
+        float* w;
+        int32_t experts, k, norm, rows;
+      } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
+              d.norm_topk, (int32_t)n};
+      if ((rc = launch(m->c, "route", dim3((unsigned)((n + 63) / 64)), dim3(64), &ra))) return rc;
+      // gate and up: slot s = row s / K, expert ids[s]
+      bool q0 = false;
+      if (m->mode == IHIP_MODE_Q8 && q8_kind(L.egd) >= 0) {
+        bool& hv = q8_kind(L.egd) ? qf.havek : qf.have0;
+        uint64_t buf = q8_kind(L.egd) ? qf.bufk : qf.buf0;
+        if (!hv) {
+          if ((rc = enqueue_quantize(m->c, m->h, n, H, q8_kind(L.egd), buf))) return rc;
+          hv = true;
+        }
+        q0 = true;
+      }
+      uint64_t xqg = q8_kind(L.egd) == 1 ? qf.bufk : qf.buf0;
+      if ((rc = lin_ids(m, m->h, xqg, n, H, L.egd, L.eg, L.eg_stride, FI, m->ids, n * K, (int)K,
+                        L.egb, m->gate, q0)))
+        return rc;
+      bool qu = q0 && q8_kind(L.eud) == q8_kind(L.egd);
+      uint64_t xqu = q8_kind(L.eud) == 1 ? qf.bufk : qf.buf0;
+      if ((rc = lin_ids(m, m->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, m->ids, n * K, (int)K,
+                        L.eub, m->up, qu)))
+        return rc;
+      if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * K * FI, d.swiglu_alpha,
+                                    d.swiglu_limit)))
+        return rc;
+      if ((rc = lin_ids(m, m->gate, m->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, m->ids, n * K,
+                        1, L.edb, m->eout, false)))
+        return rc;
+      struct {
+        const float* d;
+        const float* w;
+        float* y;
+        int32_t k, n, rows, pad;
+      } ca = {(const float*)m->eout, (const float*)m->rw, (float*)m->tmp, (int32_t)K, (int32_t)H,
+              (int32_t)n, 0};
+      if ((rc = launch(m->c, "moecombine", dim3((unsigned)((H + 255) / 256), (unsigned)n),
+                       dim3(256), &ca)))
+        return rc;
+    }
+    // residual, then the next layer's input norm (or the final norm)
+    uint64_t nw = l + 1 < d.layers ? m->L[l + 1].input_norm : m->final_norm;
+    if ((rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, nw, m->h, n, H, d.rms_eps))) return rc;
+  }
+  return 0;
+}
+
+static int head(ihip_model* m, int64_t n, bool all, uint64_t y)
+{
+  const ihip_model_desc& d = m->d;
+  QCache qh{m->xq0, m->xqk};
+  if (all) return lin(m, m->h, &qh, n, d.hidden, m->head_dt, m->head, d.vocab, 0, y);
+  return lin(m, m->h + (uint64_t)(n - 1) * d.hidden * 4, &qh, 1, d.hidden, m->head_dt, m->head,
+             d.vocab, 0, y);
+}
+
+// one chunk: ids and cos/sin uploaded, embeddings, layers, head
+static int chunk(ihip_model* m, const int32_t* ids, int64_t n, bool want_logits, bool all,
+                 uint64_t logits_dev)
+{
+  const ihip_model_desc& d = m->d;
+  std::vector<float> cs((size_t)n * d.head_dim);
+  rotary(d, m->length, n, cs.data());
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, (void*)ids, n * 4, m->c->stream));
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, m->c->stream));
+  int rc = ihip_enqueue_embed(m->c, m->embed, m->embed_dt, d.vocab, d.hidden, m->tok, n, m->x);
+  if (!rc) rc = layers(m, n, m->length, false);
+  if (!rc && want_logits) rc = head(m, n, all, logits_dev);
+  // the host vectors must outlive the copies
+  IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+  if (!rc) m->length += n;
+  return rc;
+}
+
+// the decode step as a graph: embed(tok) -> layers(pos) -> head -> argmax
+static int decode_graph(ihip_model* m)
+{
+  ihip_ctx* c = m->c;
+  int rc = ihip_capture_begin(c);
+  if (rc) return rc;
+  rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, m->tok, 1, m->x);
+  if (!rc) rc = layers(m, 1, 0, true);
+  if (!rc) rc = head(m, 1, false, m->logits);
+  if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+  int rc2 = ihip_capture_end(c, 0);
+  if (rc) return rc;
+  if (rc2) return rc2;
+  m->graph_ready = true;
+  return 0;
+}
+
+}  // namespace ihip
+
+using namespace ihip;
+
+extern "C" {
+
+int ihip_model_rotary(const ihip_model_desc* d, int64_t first, int64_t rows, float* cs)
+{
+  if (!d || !cs || rows < 1 || d->head_dim < 2) return fail(IHIP_E_ARG, "ihip_model_rotary");
+  rotary(*d, first, rows, cs);
+  return 0;
+}
+
+int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv_f16,
+                      int64_t max_tokens, ihip_model** out)
+{
+  if (!c || !desc || !out || !desc->layer || desc->layers < 1 || max_tokens < 1)
+    return fail(IHIP_E_ARG, "ihip_model_create");
+  *out = nullptr;
+  ihip_model* m = new ihip_model();
+  m->c = c;
+  m->d = *desc;
+  m->layer_desc.assign(desc->layer, desc->layer + desc->layers);
+  m->d.layer = m->layer_desc.data();
+  m->mode = mode;
+  m->kv_f16 = kv_f16;
+  m->max_tokens = max_tokens;
+  const ihip_model_desc& d = m->d;
+  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
+                kvw = (int64_t)d.kv_heads * hd;
+  int rc = 0;
+  auto bad = [&](int r) {
+    ihip_model_destroy(m);
+    return r;
+  };
+  // UploadWeights (model.qwen3.cuda.pas:602-828)
+  if ((rc = upw(m, d.embed, d.vocab, H, 1, m->embed, m->embed_dt))) return bad(rc);
+  if (d.head.data) {
+    if ((rc = upw(m, d.head, d.vocab, H, 1, m->head, m->head_dt))) return bad(rc);
+  } else {
+    m->head = m->embed;
+    m->head_dt = m->embed_dt;
+  }
+  if ((rc = upf(m, d.final_norm, H, m->final_norm))) return bad(rc);
+  m->L.resize(d.layers);
+  bool any_moe = false;
+  for (int l = 0; l < d.layers; l++) {
+    const ihip_layer_desc& s = m->layer_desc[l];
+    DevLayer& L = m->L[l];
+    L.window = s.window;
+    L.moe = s.moe;
+    any_moe |= s.moe != 0;
+    if ((rc = upf(m, s.input_norm, H, L.input_norm)) || (rc = upf(m, s.post_norm, H, L.post_norm)) ||
+        (rc = upw(m, s.q, qw, H, 1, L.q, L.qd)) || (rc = upw(m, s.k, kvw, H, 1, L.k, L.kd)) ||
+        (rc = upw(m, s.v, kvw, H, 1, L.v, L.vd)) || (rc = upw(m, s.o, H, qw, 1, L.o, L.od)) ||
+        (rc = upf(m, s.q_bias, qw, L.qb)) || (rc = upf(m, s.k_bias, kvw, L.kb)) ||
+        (rc = upf(m, s.v_bias, kvw, L.vb)) || (rc = upf(m, s.o_bias, H, L.ob)) ||
+        (rc = upf(m, s.q_norm, hd, L.qn)) || (rc = upf(m, s.k_norm, hd, L.kn)) ||
+        (rc = upf(m, s.sinks, d.heads, L.sinks)))
+      return bad(rc);
+    if (!s.moe) {
+      if ((rc = upw(m, s.gate, d.ffn, H, 1, L.gate, L.gd)) || (rc = upw(m, s.up, d.ffn, H, 1, L.up, L.ud)) ||
+          (rc = upw(m, s.down, H, d.ffn, 1, L.down, L.dd)))
+        return bad(rc);
+    } else {
+      const int64_t E = d.experts, FI = d.expert_ffn;
+      if ((rc = upw(m, s.router, E, H, 1, L.router, L.rd)) || (rc = upf(m, s.router_bias, E, L.router_b)) ||
+          (rc = upw(m, s.exp_gate, FI, H, E, L.eg, L.egd)) ||
+          (rc = upw(m, s.exp_up, FI, H, E, L.eu, L.eud)) ||
+          (rc = upw(m, s.exp_down, H, FI, E, L.ed, L.edd)) ||
+          (rc = upf(m, s.exp_gate_bias, E * FI, L.egb)) ||
+          (rc = upf(m, s.exp_up_bias, E * FI, L.eub)) ||
+          (rc = upf(m, s.exp_down_bias, E * H, L.edb)))
+        return bad(rc);
+      if (L.egd != L.eud) return bad(fail(IHIP_E_ARG, "experts: gate and up of one type"));
+      L.eg_stride = (int64_t)row_bytes(L.egd, H) * FI;
+      L.ed_stride = (int64_t)row_bytes(L.edd, FI) * H;
+    }
+    const uint64_t kvbytes = (uint64_t)max_tokens * kvw * (kv_f16 ? 2 : 4);
+    if ((rc = dalloc(m, kvbytes, L.kc)) || (rc = dalloc(m, kvbytes, L.vc))) return bad(rc);
+  }
+  // activations of one chunk
+  const int64_t N = CHUNK;
+  int64_t F = std::max<int64_t>(d.ffn, 1);
+  int64_t EK = any_moe ? (int64_t)d.experts_used * d.expert_ffn : 0;
+  int64_t wide = std::max<int64_t>({F, EK, qw, H, (int64_t)d.experts});
+  if ((rc = dalloc(m, N * H * 4, m->x)) || (rc = dalloc(m, N * H * 4, m->h)) ||
+      (rc = dalloc(m, N * H * 4, m->tmp)) || (rc = dalloc(m, N * qw * 4, m->q)) ||
+      (rc = dalloc(m, N * kvw * 4, m->k)) || (rc = dalloc(m, N * kvw * 4, m->v)) ||
+      (rc = dalloc(m, N * qw * 4, m->attn)) || (rc = dalloc(m, N * wide * 4, m->gate)) ||
+      (rc = dalloc(m, N * wide * 4, m->up)) ||
+      (rc = dalloc(m, N * std::max<int64_t>(d.experts, 1) * 4, m->route)) ||
+      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->ids)) ||
+      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->rw)) ||
+      (rc = dalloc(m, N * std::max(d.experts_used, 1) * H * 4, m->eout)) ||
+      (rc = dalloc(m, N * hd * 4, m->cs)) || (rc = dalloc(m, N * 4, m->tok)) ||
+      (rc = dalloc(m, (uint64_t)d.vocab * 4, m->logits)) || (rc = dalloc(m, 256, m->next)) ||
+      (rc = dalloc(m, 256, m->pos)))
+    return bad(rc);
+  const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
+  const uint64_t qrow = qin + 4 * (qin / 32);
+  if ((rc = dalloc(m, N * qrow, m->xq0)) || (rc = dalloc(m, N * qrow, m->xqk)) ||
+      (rc = dalloc(m, N * std::max(d.experts_used, 1) * qrow, m->xqf)))
+    return bad(rc);
+  *out = m;
+  return 0;
+}
+
+void ihip_model_destroy(ihip_model* m)
+{
+  if (!m) return;
+  (void)hipStreamSynchronize(m->c->stream);
+  for (auto p : m->owned) (void)hipFree((void*)p);
+  if (m->logits_all) (void)hipFree((void*)m->logits_all);
+  delete m;
+}
+
+int ihip_model_reset(ihip_model* m)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_reset");
+  m->length = 0;
+  return 0;
+}
+
+int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count, float* logits,
+                       int all_logits)
+{
+  if (!m || !ids || count < 1) return fail(IHIP_E_ARG, "ihip_model_forward: no tokens");
+  if (m->length + count > m->max_tokens)
+    return fail(IHIP_E_ARG, "ihip_model_forward: beyond the KV cache");
+  for (int64_t i = 0; i < count; i++)
+    if (ids[i] < 0 || ids[i] >= m->d.vocab) return fail(IHIP_E_ARG, "token id outside the vocabulary");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  for (int64_t s = 0; s < count; s += CHUNK) {
+    int64_t n = std::min(CHUNK, count - s);
+    bool last = s + n == count;
+    bool want = logits && (all_logits || last);
+    uint64_t ldev = m->logits;
+    if (want && all_logits) {
+      if (m->logits_all_rows < n) {
+        if (m->logits_all) (void)hipFree((void*)m->logits_all);
+        void* p = nullptr;
+        IHIP_CHECK(hipMalloc(&p, (uint64_t)CHUNK * m->d.vocab * 4));
+        m->logits_all = (uint64_t)p;
+        m->logits_all_rows = CHUNK;
+      }
+      ldev = m->logits_all;
+    }
+    int rc = chunk(m, ids + s, n, want, all_logits != 0, ldev);
+    if (rc) return rc;
+    if (want) {
+      float* dst = all_logits ? logits + s * m->d.vocab : logits;
+      uint64_t rows = all_logits ? n : 1;
+      IHIP_CHECK(hipMemcpyDtoHAsync(dst, (hipDeviceptr_t)ldev, rows * m->d.vocab * 4, m->c->stream));
+      IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+    }
+  }
+  return 0;
+}
+
+int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n, int64_t max_new,
+                      int32_t* out_ids)
+{
+  if (!m || !prompt || n < 1 || max_new < 1 || !out_ids) return fail(IHIP_E_ARG, "ihip_model_greedy");
+  if (m->length + n + max_new > m->max_tokens)
+    return fail(IHIP_E_ARG, "ihip_model_greedy: beyond the KV cache");
+  ihip_ctx* c = m->c;
+  auto t0 = std::chrono::steady_clock::now();
+  int rc = 0;
+  {
+    // the prompt: every chunk, logits of the last row only, argmax on device
+    std::lock_guard<std::mutex> g(c->lock);
+    for (int64_t s = 0; s < n && !rc; s += CHUNK) {
+      int64_t k = std::min(CHUNK, n - s);
+      rc = chunk(m, prompt + s, k, s + k == n, false, m->logits);
+    }
+    if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+    if (!rc) {
+      IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[0], (hipDeviceptr_t)m->next, 4, c->stream));
+      IHIP_CHECK(hipStreamSynchronize(c->stream));
+    }
+  }
+  if (rc) return rc;
+  auto t1 = std::chrono::steady_clock::now();
+  std::lock_guard<std::mutex> g(c->lock);
+  if (!m->graph_ready && (rc = decode_graph(m))) return rc;
+  const int64_t half = m->d.head_dim / 2;
+  std::vector<float> cs(m->d.head_dim);
+  for (int64_t i = 1; i < max_new; i++) {
+    int32_t tok = out_ids[i - 1];
+    int32_t pos = (int32_t)m->length;
+    rotary(m->d, pos, 1, cs.data());
+    (void)half;
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
+    if ((rc = ihip_graph_launch(c, 0))) return rc;
+    IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)m->next, 4, c->stream));
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    m->length++;
+  }
+  // the last token enters the cache too (TDecoderModel.Greedy: Forward
+  // without logits after the last step), through the same graph
+  {
+    int32_t tok = out_ids[max_new - 1];
+    int32_t pos = (int32_t)m->length;
+    rotary(m->d, pos, 1, cs.data());
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
+    if ((rc = ihip_graph_launch(c, 0))) return rc;
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    m->length++;
+  }
+  auto t2 = std::chrono::steady_clock::now();
+  m->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  m->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+  return 0;
+}
+
+int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_timing");
+  if (prefill_ms) *prefill_ms = m->prefill_ms;
+  if (decode_ms) *decode_ms = m->decode_ms;
+  return 0;
+}
+
+}  // extern "C"

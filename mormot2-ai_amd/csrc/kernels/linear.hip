@@ -1,0 +1,649 @@
+// linear.hip - dequant-fused GEMV for gfx950 (decode: 1 row; small batch: up
+// to 8 rows per launch row-chunk), plain and expert-indexed (MoE).
+//
+// What it computes: y[r, o] = bias[o] + sum_i W[o, i] x[r, i] for W in the
+// HIP layout of layout.h - the contract of TInferBackend.Linear
+// (src/infer/mormot.ai.infer.backend.pas:59-75) and of the reference's
+// EnqueueLinearAt / EnqueueLinearIds (backend.cuda.pas:338-412).
+//
+// Two arithmetics (template MODE):
+//  - F32 (0): x in float, W dequantized in float, the block scale applied to
+//    the group's sum - the contract of tools/cuda/linear.cu:1-6 (a tolerance
+//    against the double Linear over InferRowToF32 weights);
+//  - Q8 (1): x quantized per row (Q8_0 or Q8_K, by quantize.hip), exact
+//    integer group sums by v_dot4_i32_i8, scales applied and summed in double -
+//    TInferCpuBackend.Linear (backend.cpu.pas:1409-1566, 823-967); float
+//    weights summed in double.
+//
+// Mapping to CDNA4: one wave64 covers 64 / LPR output rows; the LPR lanes of
+// a row take its 32-value groups g = lane + k * LPR (k < U), so the lanes of
+// a wave read one contiguous run of the codes region with 16-byte loads. The
+// activation of a lane's groups stays in registers for every row the wave
+// visits (R = 1), the waves walk the rows grid-stride. Lane sums meet in a
+// butterfly of __shfl_xor within the LPR lanes. Q8 mode with K-quants: the 8
+// groups of a super-block sit in 8 neighbouring lanes, whose integer sums
+// are added exactly before the one double product of the super-block.
+#include "common.h"
+
+namespace ihip {
+
+struct LinArgs {
+  const uint8_t* w;    // matrix base (plain) or expert 0 (ids)
+  const float* x;      // [rows, in] float activations
+  const uint8_t* xq;   // [rows] quantized rows: int8[in] then float[G]
+  const float* bias;   // [out], [experts, out] with ids, or null
+  float* y;            // [rows or slots, out]
+  const int* ids;      // [slots] expert ids, or null
+  int64_t stride;      // bytes between experts
+  int32_t out, in, rows, lpr;
+  int32_t x_per_slot;  // ids: x row = slot / x_per_slot, or 0 when 0
+  int32_t nexp;        // ids: the number of experts (an id outside 0..nexp-1 gives a zero row), 0: unchecked
+};
+
+// ---------------------------------------------------------------- formats
+// A group of 32 values as raw registers, and its sums.
+
+struct Raw {
+  uint4 q0, q1;  // codes: 16 or 32 bytes
+  uint32_t a, b, c, d;  // scales, high bits, header words
+};
+
+template <int F>
+__device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, int64_t o,
+                                           int G, int g, int64_t in, Raw& r)
+{
+  int64_t og = o * G + g;
+  if constexpr (F == DT_Q8_0) {
+    const uint4* p = (const uint4*)(w + o * in + (int64_t)g * 32);
+    r.q0 = p[0];
+    r.q1 = p[1];
+    r.a = ((const uint16_t*)(w + rg.s))[og];
+  } else if constexpr (F == DT_Q4_0) {
+    r.q0 = ((const uint4*)w)[og];
+    r.a = ((const uint16_t*)(w + rg.s))[og];
+  } else if constexpr (F == DT_MXFP4) {
+    r.q0 = ((const uint4*)w)[og];
+    r.a = (w + rg.s)[og];
+  } else if constexpr (F == DT_Q5_0) {
+    r.q0 = ((const uint4*)w)[og];
+    r.b = ((const uint32_t*)(w + rg.h))[og];
+    r.a = ((const uint16_t*)(w + rg.s))[og];
+  } else if constexpr (F == DT_Q5_1) {
+    r.q0 = ((const uint4*)w)[og];
+    r.b = ((const uint32_t*)(w + rg.h))[og];
+    r.a = ((const uint32_t*)(w + rg.s))[og];
+  } else if constexpr (F == DT_Q4_K) {
+    r.q0 = ((const uint4*)w)[og];
+    r.q1 = ((const uint4*)(w + rg.s))[o * (G >> 3) + (g >> 3)];
+  } else if constexpr (F == DT_Q6_K) {
+    int64_t ob = o * (G >> 3) + (g >> 3);
+    r.q0 = ((const uint4*)w)[og];
+    uint2 h = ((const uint2*)(w + rg.h))[og];
+    r.b = h.x;
+    r.c = h.y;
+    r.a = ((const uint16_t*)(w + rg.s))[ob * 8 + (g & 7)];
+    r.d = ((const uint16_t*)(w + rg.s2))[ob];
+  }
+}
+
+// float weights: 32 values of row o, group g (F32 128 bytes, BF16/F16 64)
+template <int F>
+__device__ __forceinline__ void load_fgroup(const uint8_t* w, int64_t o, int g, int64_t in,
+                                            float (&v)[32])
+{
+  if constexpr (F == DT_F32) {
+    const float4* p = (const float4*)(w + (o * in + (int64_t)g * 32) * 4);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      float4 t = p[k];
+      v[4 * k] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+  } else {
+    const uint4* p = (const uint4*)(w + (o * in + (int64_t)g * 32) * 2);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint4 t = p[k];
+      uint32_t u[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        if constexpr (F == DT_BF16) {
+          v[8 * k + 2 * j] = bits_float(u[j] << 16);
+          v[8 * k + 2 * j + 1] = bits_float(u[j] & 0xffff0000u);
+        } else {
+          v[8 * k + 2 * j] = half_to_float(u[j] & 0xffffu);
+          v[8 * k + 2 * j + 1] = half_to_float(u[j] >> 16);
+        }
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t comp(const uint4& v, int d)
+{
+  return d == 0 ? v.x : (d == 1 ? v.y : (d == 2 ? v.z : v.w));
+}
+
+// the fifth bits of 4 values (bits 0..3 of b) moved to bit 4 of each byte
+__device__ __forceinline__ uint32_t spread5(uint32_t b)
+{
+  return ((b & 1u) << 4) | ((b & 2u) << 11) | ((b & 4u) << 18) | ((b & 8u) << 25);
+}
+
+// the 4 code bytes of dword d of the low (hi = 0: values 4d..4d+3) or high
+// (hi = 1: values 16 + 4d..) half of a group, as unsigned/signed int8
+template <int F>
+__device__ __forceinline__ uint32_t code_bytes(const Raw& r, int d, int hi)
+{
+  if constexpr (F == DT_Q8_0) {
+    return comp(hi ? r.q1 : r.q0, d);
+  } else {
+    uint32_t q = comp(r.q0, d);
+    uint32_t nib = hi ? ((q >> 4) & 0x0F0F0F0Fu) : (q & 0x0F0F0F0Fu);
+    if constexpr (F == DT_MXFP4)
+      return mxfp4_bytes(nib);
+    else if constexpr (F == DT_Q5_0 || F == DT_Q5_1)
+      return nib | spread5((r.b >> (hi * 16 + 4 * d)) & 15u);
+    else if constexpr (F == DT_Q6_K)
+      return nib | ((((hi ? r.c : r.b) >> (2 * d)) & 0x03030303u) << 4);
+    else
+      return nib;
+  }
+}
+
+// F32 mode: the group's contribution to the row sum. x: the 32 activations,
+// sx their sum.
+template <int F>
+__device__ __forceinline__ float group_f32(const Raw& r, const float (&x)[32], float sx, int g)
+{
+  // sum over the 32 values of the code (as float) times x: signed codes are
+  // read biased by 128 (byte ^ 0x80) and the bias removed through sx
+  constexpr bool sgn = (F == DT_Q8_0 || F == DT_MXFP4);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float accl = 0.f, acch = 0.f;  // Q6_K: the two scale halves
+#pragma unroll
+  for (int hi = 0; hi < 2; hi++) {
+    float part[2] = {0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      uint32_t c = code_bytes<F>(r, d, hi);
+      if (sgn) c ^= 0x80808080u;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float cf = (float)((c >> (8 * i)) & 255u);
+        part[i & 1] = __builtin_fmaf(cf, x[16 * hi + 4 * d + i], part[i & 1]);
+      }
+    }
+    if (F == DT_Q6_K) {
+      if (hi) acch = part[0] + part[1];
+      else accl = part[0] + part[1];
+    } else {
+      acc[2 * hi] = part[0];
+      acc[2 * hi + 1] = part[1];
+    }
+  }
+  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  if constexpr (F == DT_Q8_0) {
+    return half_to_float(r.a) * (s - 128.0f * sx);
+  } else if constexpr (F == DT_MXFP4) {
+    return e8m0_half(r.a) * (s - 128.0f * sx);
+  } else if constexpr (F == DT_Q4_0) {
+    return half_to_float(r.a) * (s - 8.0f * sx);
+  } else if constexpr (F == DT_Q5_0) {
+    return half_to_float(r.a) * (s - 16.0f * sx);
+  } else if constexpr (F == DT_Q5_1) {
+    return half_to_float(r.a & 0xffffu) * s + half_to_float(r.a >> 16) * sx;
+  } else if constexpr (F == DT_Q4_K) {
+    int sc, m;
+    scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, m);
+    float d1 = half_to_float(r.q1.x & 0xffffu) * (float)sc;
+    float m1 = half_to_float(r.q1.x >> 16) * (float)m;
+    return d1 * s - m1 * sx;
+  } else {  // Q6_K: (d * sc) * (q - 32) per half of 16 values
+    float d = half_to_float(r.d);
+    float ta = d * (float)(int)(int8_t)(r.a & 255u);
+    float tb = d * (float)(int)(int8_t)(r.a >> 8);
+    float sxl = 0.f, sxh = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      sxl += x[i];
+      sxh += x[16 + i];
+    }
+    return ta * (accl - 32.0f * sxl) + tb * (acch - 32.0f * sxh);
+  }
+}
+
+// Q8 mode, 32-value block types: the group's exact term in double.
+// xw: the 8 dwords of Q8_0 codes, dx the fp16 scale of the activation block
+// (as float), sxq the sum of the 32 activation codes
+template <int F>
+__device__ __forceinline__ double group_q8(const Raw& r, const int (&xw)[8], float dx, int sxq)
+{
+  int s = 0;
+#pragma unroll
+  for (int hi = 0; hi < 2; hi++)
+#pragma unroll
+    for (int d = 0; d < 4; d++) s = sdot4((int)code_bytes<F>(r, d, hi), xw[4 * hi + d], s);
+  double dxd = dx;
+  if constexpr (F == DT_Q8_0) {
+    return (double)s * ((double)half_to_float(r.a) * dxd);
+  } else if constexpr (F == DT_MXFP4) {
+    return (double)s * (mxfp4_q8_scale(r.a) * dxd);
+  } else if constexpr (F == DT_Q4_0) {
+    return (double)(s - 8 * sxq) * ((double)half_to_float(r.a) * dxd);
+  } else if constexpr (F == DT_Q5_0) {
+    return (double)(s - 16 * sxq) * ((double)half_to_float(r.a) * dxd);
+  } else {  // Q5_1: d * q part, then m * dx * sum(qx) (LinearQ8_0 with aMins)
+    double t = (double)s * ((double)half_to_float(r.a & 0xffffu) * dxd);
+    return t + (double)half_to_float(r.a >> 16) * (dxd * (double)sxq);
+  }
+}
+
+// Q8 mode, K-quants: the group's integer parts of the super-block sums
+// (InferQ4KSumsPascal / InferQ6KSumsPascal, kernels.pas:229-333)
+template <int F>
+__device__ __forceinline__ void group_q8k(const Raw& r, const int (&xw)[8], int sxl, int sxh,
+                                          int g, int& isum, int& msum)
+{
+  int sl = 0, sh = 0;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    sl = sdot4((int)code_bytes<F>(r, d, 0), xw[d], sl);
+    sh = sdot4((int)code_bytes<F>(r, d, 1), xw[4 + d], sh);
+  }
+  if constexpr (F == DT_Q4_K) {
+    int sc, m;
+    scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, m);
+    isum = sc * (sl + sh);
+    msum = m * (sxl + sxh);
+  } else {
+    int sa = (int)(int8_t)(r.a & 255u), sb = (int)(int8_t)(r.a >> 8);
+    isum = sa * (sl - 32 * sxl) + sb * (sh - 32 * sxh);
+    msum = 0;
+  }
+}
+
+template <int F>
+__device__ __forceinline__ double superblock_q8k(const Raw& r, int isum, int msum, float dx)
+{
+  double dxd = dx;
+  if constexpr (F == DT_Q4_K) {
+    double hd = half_to_float(r.q1.x & 0xffffu), hm = half_to_float(r.q1.x >> 16);
+    return (hd * dxd) * (double)isum - (hm * dxd) * (double)msum;
+  } else {
+    return ((double)half_to_float(r.d) * dxd) * (double)isum;
+  }
+}
+
+constexpr bool is_float_type(int F) { return F == DT_F32 || F == DT_BF16 || F == DT_F16; }
+constexpr bool is_k_quant(int F) { return F == DT_Q4_K || F == DT_Q6_K; }
+
+// activations of one group: float (F32 mode and float weights) or Q8 codes
+struct XGroup {
+  float f[32];
+  float sx;
+  int w[8];
+  float dx;
+  int sl, sh;
+};
+
+template <int F, int MODE>
+__device__ __forceinline__ void load_x(const LinArgs& a, int64_t xrow, int g, int G, XGroup& x)
+{
+  if (MODE == 0 || is_float_type(F)) {
+    const float4* p = (const float4*)(a.x + xrow * a.in + (int64_t)g * 32);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      float4 t = p[k];
+      x.f[4 * k] = t.x;
+      x.f[4 * k + 1] = t.y;
+      x.f[4 * k + 2] = t.z;
+      x.f[4 * k + 3] = t.w;
+    }
+#pragma unroll
+    for (int k = 0; k < 32; k++) s += x.f[k];
+    x.sx = s;
+  } else {
+    const uint8_t* row = a.xq + xrow * ((int64_t)a.in + 4 * (int64_t)G);
+    const uint4* p = (const uint4*)(row + (int64_t)g * 32);
+    uint4 u0 = p[0], u1 = p[1];
+    x.w[0] = (int)u0.x; x.w[1] = (int)u0.y; x.w[2] = (int)u0.z; x.w[3] = (int)u0.w;
+    x.w[4] = (int)u1.x; x.w[5] = (int)u1.y; x.w[6] = (int)u1.z; x.w[7] = (int)u1.w;
+    x.dx = ((const float*)(row + a.in))[g];
+    int sl = 0, sh = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      sl = sdot4(x.w[k], 0x01010101, sl);
+      sh = sdot4(x.w[4 + k], 0x01010101, sh);
+    }
+    x.sl = sl;
+    x.sh = sh;
+  }
+}
+
+// the contribution of group g of row o (raw already loaded) against x
+template <int F, int MODE>
+__device__ __forceinline__ void group_term(const uint8_t* w, const Raw& raw, int64_t o, int g,
+                                           int64_t in, const XGroup& x, float& accf,
+                                           double& accd, int& isum, int& msum)
+{
+  if constexpr (is_float_type(F)) {
+    float v[32];
+    load_fgroup<F>(w, o, g, in, v);
+    if constexpr (MODE == 0) {
+      float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 32; k += 2) {
+        p0 = __builtin_fmaf(v[k], x.f[k], p0);
+        p1 = __builtin_fmaf(v[k + 1], x.f[k + 1], p1);
+      }
+      accf += p0 + p1;
+    } else {
+      double p = 0;
+#pragma unroll
+      for (int k = 0; k < 32; k++) p = __builtin_fma((double)v[k], (double)x.f[k], p);
+      accd += p;
+    }
+  } else if constexpr (MODE == 0) {
+    accf += group_f32<F>(raw, x.f, x.sx, g);
+  } else if constexpr (is_k_quant(F)) {
+    group_q8k<F>(raw, x.w, x.sl, x.sh, g, isum, msum);
+  } else {
+    accd += group_q8<F>(raw, x.w, x.dx, x.sl + x.sh);
+  }
+}
+
+// one row's total from its lanes; K-quant Q8: the exact super-block sums of 8
+// lanes first. Returns the value in lane 0 of the row segment.
+template <int F, int MODE>
+__device__ __forceinline__ double row_total(int lpr, const Raw& hdr, float dxsb, bool has_sb,
+                                            float accf, double accd, int isum, int msum, int g0)
+{
+  if constexpr (MODE == 0 && !is_float_type(F)) {
+    return (double)wave_sum(accf, lpr);
+  } else if constexpr (MODE == 0) {
+    return (double)wave_sum(accf, lpr);
+  } else if constexpr (is_k_quant(F)) {
+    (void)g0;
+    isum = wave_sum(isum, 8);
+    msum = wave_sum(msum, 8);
+    double t = has_sb ? superblock_q8k<F>(hdr, isum, msum, dxsb) : 0.0;
+    return wave_sum(t, lpr);
+  } else {
+    return wave_sum(accd, lpr);
+  }
+}
+
+// ------------------------------------------------------------------ kernel
+// R = 1: one activation row, kept in registers. R = 8: up to 8 rows per
+// blockIdx.y chunk, activations read per group (from L1/L2).
+template <int F, int MODE, int U, int R>
+__device__ __forceinline__ void gemv(const LinArgs& a)
+{
+  const int lane = threadIdx.x & 63;
+  const int lpr = a.lpr;
+  const int lr = lane & (lpr - 1);
+  const int rsub = lane / lpr;
+  const int rpw = 64 / lpr;
+  const int G = a.in >> 5;
+  const uint8_t* w = a.w;
+  const float* bias = a.bias;
+  int64_t xrow0, yrow0;
+  int nrows;
+  if (a.ids) {
+    int slot = blockIdx.y;
+    int e = a.ids[slot];
+    if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
+      for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
+           o += (int64_t)gridDim.x * blockDim.x)
+        a.y[(int64_t)slot * a.out + o] = 0.f;
+      return;
+    }
+    w += (int64_t)e * a.stride;
+    if (bias) bias += (int64_t)e * a.out;
+    xrow0 = a.x_per_slot ? slot / a.x_per_slot : 0;
+    yrow0 = slot;
+    nrows = 1;
+  } else {
+    xrow0 = (int64_t)blockIdx.y * R;
+    yrow0 = xrow0;
+    nrows = min(R, a.rows - (int)xrow0);
+  }
+  const Regions rg = regions(F, a.out, a.in);
+  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+
+  if constexpr (R == 1) {
+    XGroup xg[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      int g = lr + k * lpr;
+      if (g < G) load_x<F, MODE>(a, xrow0, g, G, xg[k]);
+    }
+    for (int64_t t = wid; t < tiles; t += nw) {
+      int64_t o = t * rpw + rsub;
+      bool valid = o < a.out;
+      Raw raw[U];
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        int g = lr + k * lpr;
+        if (valid && g < G && !is_float_type(F)) load_group<F>(w, rg, o, G, g, a.in, raw[k]);
+      }
+      float accf = 0.f;
+      double accd = 0.0, tot = 0.0;
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        int g = lr + k * lpr;
+        int isum = 0, msum = 0;
+        if (valid && g < G)
+          group_term<F, MODE>(w, raw[k], o, g, a.in, xg[k], accf, accd, isum, msum);
+        if constexpr (MODE == 1 && is_k_quant(F)) {
+          // every k-th group set of the lanes forms whole super-blocks
+          bool lead = (g & 7) == 0 && valid && g < G;
+          tot += row_total<F, MODE>(lpr, raw[k], xg[k].dx, lead, 0.f, 0.0, isum, msum, g);
+        }
+      }
+      double v;
+      if constexpr (MODE == 1 && is_k_quant(F))
+        v = tot;
+      else
+        v = row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
+      if (lr == 0 && valid) {
+        if (bias) v = (double)bias[o] + v;
+        a.y[yrow0 * a.out + o] = (float)v;
+      }
+    }
+  } else {
+    for (int64_t t = wid; t < tiles; t += nw) {
+      int64_t o = t * rpw + rsub;
+      bool valid = o < a.out;
+      float accf[R];
+      double accd[R], tot[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        accf[r] = 0.f;
+        accd[r] = 0.0;
+        tot[r] = 0.0;
+      }
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        int g = lr + k * lpr;
+        bool has = valid && g < G;
+        Raw raw;
+        if (has && !is_float_type(F)) load_group<F>(w, rg, o, G, g, a.in, raw);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          if (r < nrows) {
+            int isum = 0, msum = 0;
+            XGroup xg;
+            if (has) {
+              load_x<F, MODE>(a, xrow0 + r, g, G, xg);
+              group_term<F, MODE>(w, raw, o, g, a.in, xg, accf[r], accd[r], isum, msum);
+            }
+            if constexpr (MODE == 1 && is_k_quant(F)) {
+              bool lead = (g & 7) == 0 && has;
+              tot[r] += row_total<F, MODE>(lpr, raw, has ? xg.dx : 0.f, lead, 0.f, 0.0, isum,
+                                           msum, g);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if (r < nrows) {
+          double v;
+          if constexpr (MODE == 1 && is_k_quant(F))
+            v = tot[r];
+          else
+            v = row_total<F, MODE>(lpr, Raw{}, 0.f, false, accf[r], accd[r], 0, 0, 0);
+          if (lr == 0 && valid) {
+            if (bias) v = (double)bias[o] + v;
+            a.y[(yrow0 + r) * a.out + o] = (float)v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ dequant/embed
+// y[r] = InferRowToF32 of row (ids ? ids[r] : row0 + r), bit-exact: every
+// value formed as tensor.pas:467-602 forms it. One wave per row, one group
+// per lane step.
+struct DeqArgs {
+  const uint8_t* w;
+  const int* ids;
+  float* y;
+  int64_t row0;
+  int32_t out, in, rows, pad;
+};
+
+template <int F>
+__device__ __forceinline__ void dequant(const DeqArgs& a)
+{
+  int wrow = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  int lane = threadIdx.x & 63;
+  if (wrow >= a.rows) return;
+  int64_t o = a.ids ? (int64_t)a.ids[wrow] : a.row0 + wrow;
+  int G = a.in >> 5;
+  if (o < 0 || o >= a.out) {  // an id outside the table: a zero row
+    for (int c = lane; c < a.in; c += 64) a.y[(int64_t)wrow * a.in + c] = 0.f;
+    return;
+  }
+  const Regions rg = regions(F, a.out, a.in);
+  float* yr = a.y + (int64_t)wrow * a.in;
+  for (int g = lane; g < G; g += 64) {
+    float v[32];
+    if constexpr (is_float_type(F)) {
+      load_fgroup<F>(a.w, o, g, a.in, v);
+    } else {
+      Raw r;
+      load_group<F>(a.w, rg, o, G, g, a.in, r);
+#pragma unroll
+      for (int hi = 0; hi < 2; hi++)
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          uint32_t c = code_bytes<F>(r, d, hi);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            int j = 16 * hi + 4 * d + i;
+            uint32_t u = (c >> (8 * i)) & 255u;
+            float val;
+            if constexpr (F == DT_Q8_0) {
+              val = half_to_float(r.a) * (float)(int)(int8_t)u;
+            } else if constexpr (F == DT_MXFP4) {
+              val = e8m0_half(r.a) * (float)(int)(int8_t)u;
+            } else if constexpr (F == DT_Q4_0) {
+              val = half_to_float(r.a) * (float)((int)u - 8);
+            } else if constexpr (F == DT_Q5_0) {
+              val = half_to_float(r.a) * (float)((int)u - 16);
+            } else if constexpr (F == DT_Q5_1) {
+              float t = half_to_float(r.a & 0xffffu) * (float)u;
+              val = t + half_to_float(r.a >> 16);
+            } else if constexpr (F == DT_Q4_K) {
+              int sc, m;
+              scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, m);
+              float d1 = half_to_float(r.q1.x & 0xffffu) * (float)sc;
+              float m1 = half_to_float(r.q1.x >> 16) * (float)m;
+              float t = d1 * (float)u;
+              val = t - m1;
+            } else {  // Q6_K
+              float t = half_to_float(r.d) * (float)(int)(int8_t)(hi ? (r.a >> 8) : (r.a & 255u));
+              val = t * (float)((int)u - 32);
+            }
+            v[j] = val;
+          }
+        }
+    }
+    float4* p = (float4*)(yr + (int64_t)g * 32);
+#pragma unroll
+    for (int k = 0; k < 8; k++) p[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  }
+}
+
+}  // namespace ihip
+
+// ------------------------------------------------------- exported symbols
+#define IHIP_GEMV(NAME, F, M, U, R) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R>(a); }
+
+#define IHIP_GEMV_U(PFX, F, M)          \
+  IHIP_GEMV(PFX##_u1, F, M, 1, 1)       \
+  IHIP_GEMV(PFX##_u2, F, M, 2, 1)       \
+  IHIP_GEMV(PFX##_u3, F, M, 3, 1)       \
+  IHIP_GEMV(PFX##_u4, F, M, 4, 1)       \
+  IHIP_GEMV(PFX##_b8u1, F, M, 1, 8)     \
+  IHIP_GEMV(PFX##_b8u2, F, M, 2, 8)     \
+  IHIP_GEMV(PFX##_b8u3, F, M, 3, 8)     \
+  IHIP_GEMV(PFX##_b8u4, F, M, 4, 8)
+
+#define IHIP_GEMV_FMT(NAME, F) \
+  IHIP_GEMV_U(gemv_##NAME##_f32, F, 0) \
+  IHIP_GEMV_U(gemv_##NAME##_q8, F, 1)
+
+#define IHIP_DEQ(NAME, F) \
+  extern "C" __global__ __launch_bounds__(256) void dequant_##NAME(ihip::DeqArgs a) { ihip::dequant<F>(a); }
+#ifdef IHIP_ONLY_FMT_Q8_0
+IHIP_GEMV_FMT(q8_0, ihip::DT_Q8_0)
+IHIP_DEQ(q8_0, ihip::DT_Q8_0)
+#endif
+#ifdef IHIP_ONLY_FMT_Q4_0
+IHIP_GEMV_FMT(q4_0, ihip::DT_Q4_0)
+IHIP_DEQ(q4_0, ihip::DT_Q4_0)
+#endif
+#ifdef IHIP_ONLY_FMT_MXFP4
+IHIP_GEMV_FMT(mxfp4, ihip::DT_MXFP4)
+IHIP_DEQ(mxfp4, ihip::DT_MXFP4)
+#endif
+#ifdef IHIP_ONLY_FMT_Q5_0
+IHIP_GEMV_FMT(q5_0, ihip::DT_Q5_0)
+IHIP_DEQ(q5_0, ihip::DT_Q5_0)
+#endif
+#ifdef IHIP_ONLY_FMT_Q5_1
+IHIP_GEMV_FMT(q5_1, ihip::DT_Q5_1)
+IHIP_DEQ(q5_1, ihip::DT_Q5_1)
+#endif
+#ifdef IHIP_ONLY_FMT_Q4_K
+IHIP_GEMV_FMT(q4_k, ihip::DT_Q4_K)
+IHIP_DEQ(q4_k, ihip::DT_Q4_K)
+#endif
+#ifdef IHIP_ONLY_FMT_Q6_K
+IHIP_GEMV_FMT(q6_k, ihip::DT_Q6_K)
+IHIP_DEQ(q6_k, ihip::DT_Q6_K)
+#endif
+#ifdef IHIP_ONLY_FMT_F32
+IHIP_GEMV_FMT(f32, ihip::DT_F32)
+IHIP_DEQ(f32, ihip::DT_F32)
+#endif
+#ifdef IHIP_ONLY_FMT_BF16
+IHIP_GEMV_FMT(bf16, ihip::DT_BF16)
+IHIP_DEQ(bf16, ihip::DT_BF16)
+#endif
+#ifdef IHIP_ONLY_FMT_F16
+IHIP_GEMV_FMT(f16, ihip::DT_F16)
+IHIP_DEQ(f16, ihip::DT_F16)
+#endif

@@ -1,0 +1,215 @@
+"""GPU parity of the dequant and the Linear kernels through the C-ABI
+(LinearMatchesReference and LinearIdsMatchesReference of the reference,
+tests/test.infer.cuda.pas:714-967, 2333-2447):
+
+- tier 1: the device dequant of every type equals the oracle's InferRowToF32
+  bit for bit;
+- tier 2 (IHIP_MODE_F32): RelError (max|a-b|/max|b|) <= 1e-5 and relative L2
+  <= 1e-5 against the double Linear over InferRowToF32 weights;
+- Q8 mode: the CPU reference Linear's bits (x quantized to Q8_0 / Q8_K, exact
+  integer sums, double scaling), allowing a 1-ulp difference only where the
+  order of a double sum differs - counted and bounded.
+"""
+import numpy as np
+import pytest
+
+import infer_hip as H
+import oracle_lib as O
+from golden_io import GoldenSet, compare, rel_error, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+BLOCK_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K]
+ALL_FMTS = BLOCK_FMTS + [H.F32, H.BF16, H.F16]
+# (rows, in, out): the LinearMatchesReference shapes that fit the block sizes
+SHAPES = [(1, 256, 70001), (70, 512, 130), (1, 896, 65), (1, 2560, 37), (3, 1024, 515),
+          (8, 768, 300), (1, 3072, 1024), (9, 2048, 257), (1, 2880, 129)]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = H.Context(0)
+    print("device:", c.info(), flush=True)
+    yield c
+    c.close()
+
+
+def weights(dtype, out, cols, seed):
+    if dtype in (H.F32, H.BF16, H.F16):
+        return H.synth_normal(dtype, out, cols, seed, 0.5)
+    return H.synth_blocks(dtype, out, cols, seed, -8, -4)
+
+
+def fits(dtype, cols):
+    return cols % H.BLOCK[dtype][0] == 0 and cols % 32 == 0
+
+
+@pytest.mark.parametrize("dtype", ALL_FMTS)
+def test_dequant_bit_exact(ctx, dtype):
+    for out, cols in ((37, 512), (5, 2816), (129, 3072)):
+        if not fits(dtype, cols):
+            continue
+        w = weights(dtype, out, cols, out + cols)
+        dw = ctx.weight(w, dtype, out, cols)
+        y = ctx.alloc(out * cols * 4)
+        H.check(H.lib().ihip_enqueue_dequant(ctx.h, dw, dtype, out, cols, 0, out, y.ptr))
+        got = y.download(np.float32, out * cols).reshape(out, cols)
+        ref = O.dequant(w, dtype, out, cols)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (H.NAMES[dtype], out, cols)
+        y.free()
+
+
+@pytest.mark.parametrize("dtype", [H.MXFP4])
+def test_mxfp4_edge_exponents(ctx, dtype):
+    # test.infer.cuda.pas:840-864: exponents {0, 1, 2, 127, 128, 200}, x = 1
+    out, cols = 6, 64
+    w = H.synth_blocks(H.MXFP4, out, cols, 3).reshape(out, 2, 17)
+    for i, e in enumerate((0, 1, 2, 127, 128, 200)):
+        w[i, :, 0] = e
+    w = w.ravel().copy()
+    x = np.ones((1, cols), np.float32)
+    y = ctx.linear(x, w, H.MXFP4, out)
+    ref = O.linear(x, w, H.MXFP4, out, f32=True)
+    assert np.array_equal(y, ref)
+
+
+@pytest.mark.parametrize("dtype", ALL_FMTS)
+def test_linear_f32_mode(ctx, dtype):
+    rng = np.random.default_rng(7)
+    for rows, cols, out in SHAPES:
+        if not fits(dtype, cols):
+            continue
+        w = weights(dtype, out, cols, rows * 31 + cols + out)
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        b = rng.standard_normal(out).astype(np.float32)
+        y = ctx.linear(x, w, dtype, out, b, mode=H.MODE_F32)
+        ref = O.linear(x, w, dtype, out, b, f32=True)
+        e1, e2 = rel_error(y, ref), rel_l2(y, ref)
+        assert e1 <= 1e-5 and e2 <= 1e-5, (H.NAMES[dtype], rows, cols, out, e1, e2)
+        # the second, cached call gives the same bits (test.infer.cuda.pas:833-837)
+        y2 = ctx.linear(x, w, dtype, out, b, mode=H.MODE_F32)
+        assert np.array_equal(y, y2)
+
+
+def ulp_diff(a, b):
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("dtype", ALL_FMTS)
+def test_linear_q8_mode_cpu_bits(ctx, dtype):
+    rng = np.random.default_rng(9)
+    total, differ = 0, 0
+    for rows, cols, out in SHAPES:
+        if not fits(dtype, cols):
+            continue
+        w = weights(dtype, out, cols, rows * 17 + cols + out)
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        b = rng.standard_normal(out).astype(np.float32)
+        y = ctx.linear(x, w, dtype, out, b, mode=H.MODE_Q8)
+        ref = O.linear(x, w, dtype, out, b)
+        u = ulp_diff(y, ref)
+        assert u.max() <= 1, (H.NAMES[dtype], rows, cols, out, int(u.max()))
+        total += u.size
+        differ += int(np.count_nonzero(u))
+    assert differ <= max(2, total // 1000), (differ, total)
+
+
+@pytest.mark.parametrize("name,wkey,ykey,dtype,atol,rtol", [
+    ("q8", "linear/weight", "linear/y", H.Q8_0, 1e-5, 1e-5),
+    ("q4", "linear/weight", "linear/y", H.Q4_0, 1e-5, 1e-5),
+    ("q5", "linear/weight", "linear/y", H.Q5_0, 1e-5, 1e-5),
+    ("q51", "linear/weight", "linear/y", H.Q5_1, 2e-3, 2e-4),
+    ("mxfp4", "linear/weight", "linear/y", H.MXFP4, 1e-5, 1e-5),
+    ("qk", "q4_K/weight", "q4_K/y", H.Q4_K, 1e-4, 1e-5),
+    ("qk", "q6_K/weight", "q6_K/y", H.Q6_K, 1e-4, 1e-5)])
+def test_linear_q8_mode_golden(ctx, name, wkey, ykey, dtype, atol, rtol):
+    # the reference's ggml fixtures, at the reference's tolerances
+    g = GoldenSet(name)
+    x, b, w, y = g["linear/x"], g["linear/bias"], np.ascontiguousarray(g[wkey]), g[ykey]
+    mine = ctx.linear(x, w, dtype, b.size, b, mode=H.MODE_Q8)
+    ok, err = compare(mine, y, atol, rtol)
+    assert ok, err
+
+
+@pytest.mark.parametrize("mode", [H.MODE_F32, H.MODE_Q8])
+@pytest.mark.parametrize("dtype", [H.Q8_0, H.Q4_K, H.Q6_K, H.MXFP4, H.BF16])
+def test_linear_ids(ctx, dtype, mode):
+    # LinearIdsMatchesReference: 5 experts, 4 slots with ids (3, 0, 4, 3), x
+    # per slot or shared, with and without a bias
+    E, cols, out = 5, 512, 96
+    w = weights(dtype, E * out, cols, 77)
+    dw = ctx.weight(w, dtype, out, cols, E)
+    rng = np.random.default_rng(5)
+    ids = np.array([3, 0, 4, 3], np.int32)
+    bias = rng.standard_normal((E, out)).astype(np.float32)
+    xs = rng.standard_normal((4, cols)).astype(np.float32)
+    stride = out * H.row_bytes(dtype, cols)
+    dids = ctx.array(ids)
+    dx = ctx.array(xs)
+    db = ctx.array(bias)
+    dy = ctx.alloc(4 * out * 4)
+    for per_slot in (1, 0):
+        for with_bias in (True, False):
+            H.check(H.lib().ihip_enqueue_linear_ids(ctx.h, dx.ptr, cols, dtype, dw, stride, out,
+                                                    dids.ptr, 4, per_slot, dy.ptr,
+                                                    db.ptr if with_bias else 0, mode))
+            got = dy.download(np.float32, 4 * out).reshape(4, out)
+            for s in range(4):
+                e = ids[s]
+                we = w[e * stride:(e + 1) * stride]
+                xr = xs[s:s + 1] if per_slot else xs[0:1]
+                bb = bias[e] if with_bias else None
+                if mode == H.MODE_F32:
+                    ref = O.linear(xr, we, dtype, out, bb, f32=True)[0]
+                    assert rel_error(got[s], ref) <= 1e-5
+                else:
+                    ref = O.linear(xr, we, dtype, out, bb)[0]
+                    assert ulp_diff(got[s], ref).max() <= 1
+    for b in (dids, dx, db, dy):
+        b.free()
+
+
+def test_linear_big_head_shape(ctx):
+    # the 151936 x 1024 head at batch 1, both modes
+    out, cols = 151936, 1024
+    w = H.synth_blocks(H.Q8_0, out, cols, 12)
+    x = np.random.default_rng(2).standard_normal((1, cols)).astype(np.float32)
+    y = ctx.linear(x, w, H.Q8_0, out, mode=H.MODE_F32)
+    ref = O.linear(x, w, H.Q8_0, out, f32=True)
+    assert rel_error(y, ref) <= 1e-5
+    y = ctx.linear(x, w, H.Q8_0, out, mode=H.MODE_Q8)
+    ref = O.linear(x, w, H.Q8_0, out)
+    assert ulp_diff(y, ref).max() <= 1
+
+
+def test_quantize_like_cpu(ctx):
+    # the device quantizers give the CPU's codes and scales (Q8_0 ties to
+    # even, Q8_K): checked on the ggml fixtures of the reference
+    for name, key, kq in (("q8", "quant", 0), ("qk", "q8k", 1)):
+        g = GoldenSet(name)
+        x = g[f"{key}/x"]
+        blocks = g[f"{key}/blocks"]
+        rows, cols = x.shape
+        dx = ctx.array(x)
+        qb = int(H.lib().ihip_q8_bytes(cols, kq))
+        dq = ctx.alloc(rows * qb)
+        H.check(H.lib().ihip_enqueue_quantize(ctx.h, dx.ptr, rows, cols, kq, dq.ptr, 0))
+        got = dq.download(np.uint8, rows * qb).reshape(rows, qb)
+        for r in range(rows):
+            codes = got[r, :cols].view(np.int8)
+            scales = got[r, cols:].view(np.float32)
+            if kq == 0:
+                ref = blocks[r].reshape(-1, 34)
+                assert np.array_equal(codes.reshape(-1, 32), ref[:, 2:].view(np.int8))
+                assert np.array_equal(scales, ref[:, :2].copy().view(np.float16).astype(np.float32).ravel())
+            else:
+                ref = blocks[r].reshape(-1, 292)
+                assert np.array_equal(codes.reshape(-1, 256), ref[:, 4:260].view(np.int8))
+                d = ref[:, :4].copy().view(np.float32).ravel()
+                assert np.array_equal(scales.reshape(-1, 8), np.repeat(d[:, None], 8, axis=1))
+        dx.free()
+        dq.free()

@@ -1,0 +1,162 @@
+"""GPU parity of the layer operations against the CPU oracle (OpsMatchCpu,
+RouteMatchesHost of tests/test.infer.cuda.pas:970-1535, 2663-): the device
+kernels follow the CPU's arithmetic, so the results must agree to the last
+bit up to the order of double sums (max 1 ulp)."""
+import numpy as np
+import pytest
+
+import infer_hip as H
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = H.Context(0)
+    yield c
+    c.close()
+
+
+def ulp(a, b):
+    ia = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    return int(np.abs(ia - ib).max()) if ia.size else 0
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 160, 2880])
+def test_rmsnorm_addnorm(ctx, cols):
+    rng = np.random.default_rng(cols)
+    rows = 3
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    t = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = rng.standard_normal(cols).astype(np.float32)
+    dx, dt, dw, dy = ctx.array(x), ctx.array(t), ctx.array(w), ctx.alloc(x.nbytes)
+    H.check(H.lib().ihip_enqueue_rmsnorm(ctx.h, dx.ptr, dw.ptr, dy.ptr, rows, cols, 1e-6))
+    got = dy.download(np.float32, x.size).reshape(x.shape)
+    assert ulp(got, O.rmsnorm(x, w, 1e-6)) <= 1
+    H.check(H.lib().ihip_enqueue_addnorm(ctx.h, dx.ptr, dt.ptr, dw.ptr, dy.ptr, rows, cols, 1e-5))
+    xs = x + t
+    assert np.array_equal(dx.download(np.float32, x.size).reshape(x.shape), xs)
+    assert ulp(dy.download(np.float32, x.size).reshape(x.shape), O.rmsnorm(xs, w, 1e-5)) <= 1
+
+
+@pytest.mark.parametrize("limit", [0.0, 7.0])
+def test_swiglu(ctx, limit):
+    rng = np.random.default_rng(3)
+    n = 10000
+    g = (rng.standard_normal(n) * 6).astype(np.float32)
+    u = (rng.standard_normal(n) * 6).astype(np.float32)
+    dg, du = ctx.array(g), ctx.array(u)
+    H.check(H.lib().ihip_enqueue_swiglu(ctx.h, dg.ptr, du.ptr, n, 1.702, limit))
+    got = dg.download(np.float32, n)
+    ref = O.swiglu(g, u, 1.702 if limit else 1.0, limit)
+    assert ulp(got, ref) <= 1
+
+
+@pytest.mark.parametrize("hd,heads,kvh,norm,f16", [(128, 16, 8, True, False), (64, 64, 8, False, True)])
+def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
+    rng = np.random.default_rng(hd)
+    rows, past = 3, 5
+    q = rng.standard_normal((rows, heads * hd)).astype(np.float32)
+    k = rng.standard_normal((rows, kvh * hd)).astype(np.float32)
+    v = rng.standard_normal((rows, kvh * hd)).astype(np.float32)
+    qn = (rng.standard_normal(hd) * 0.1 + 1).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.1 + 1).astype(np.float32)
+    ang = rng.uniform(0, 6.28, (rows, hd // 2)).astype(np.float32)
+    cs = np.concatenate([np.cos(ang).ravel(), np.sin(ang).ravel()]).astype(np.float32)
+    cache = (past + rows) * kvh * hd * (2 if f16 else 4)
+    dq, dk, dv, dqn, dkn, dcs = (ctx.array(a) for a in (q, k, v, qn, kn, cs))
+    dkc, dvc = ctx.alloc(cache), ctx.alloc(cache)
+    H.check(H.lib().ihip_enqueue_qkrope(ctx.h, dq.ptr, dk.ptr, dv.ptr, dqn.ptr if norm else 0,
+                                        dkn.ptr if norm else 0, dcs.ptr, dkc.ptr, dvc.ptr, rows,
+                                        heads, kvh, hd, past, 1e-6, int(f16)))
+    qr = O.rmsnorm(q.reshape(-1, hd), qn, 1e-6).reshape(q.shape) if norm else q
+    kr = O.rmsnorm(k.reshape(-1, hd), kn, 1e-6).reshape(k.shape) if norm else k
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    qr = O.rope(qr, heads, hd, c, s)
+    kr = O.rope(kr, kvh, hd, c, s)
+    assert ulp(dq.download(np.float32, q.size).reshape(q.shape), qr) <= 1
+    n = rows * kvh * hd
+    off = past * kvh * hd
+    if f16:
+        kc = dkc.download(np.float16, off + n)[off:].astype(np.float32)
+        vc = dvc.download(np.float16, off + n)[off:].astype(np.float32)
+        assert np.array_equal(kc, kr.ravel().astype(np.float16).astype(np.float32)) or \
+            ulp(kc, kr.ravel().astype(np.float16).astype(np.float32)) <= 1 << 13
+        assert np.array_equal(vc, v.ravel().astype(np.float16).astype(np.float32))
+    else:
+        assert ulp(dkc.download(np.float32, off + n)[off:], kr.ravel()) <= 1
+        assert np.array_equal(dvc.download(np.float32, off + n)[off:], v.ravel())
+
+
+@pytest.mark.parametrize("hd,heads,kvh,past,rows,window,sinks,f16", [
+    (128, 16, 8, 40, 1, 0, False, False),
+    (128, 32, 4, 300, 3, 0, False, False),
+    (64, 64, 8, 200, 2, 128, True, False),
+    (64, 64, 8, 20, 5, 0, True, False),
+    (128, 16, 8, 100, 1, 0, False, True)])
+def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
+    rng = np.random.default_rng(past + rows)
+    T = past + rows
+    q = rng.standard_normal((rows, heads * hd)).astype(np.float32)
+    keys = rng.standard_normal((T, kvh * hd)).astype(np.float32)
+    vals = rng.standard_normal((T, kvh * hd)).astype(np.float32)
+    sk = rng.standard_normal(heads).astype(np.float32) * 2 if sinks else None
+    if f16:
+        keys = keys.astype(np.float16).astype(np.float32)
+        vals = vals.astype(np.float16).astype(np.float32)
+        dkc, dvc = ctx.array(keys.astype(np.float16)), ctx.array(vals.astype(np.float16))
+    else:
+        dkc, dvc = ctx.array(keys), ctx.array(vals)
+    dq = ctx.array(q)
+    dy = ctx.alloc(q.nbytes)
+    ds = ctx.array(sk) if sinks else None
+    H.check(H.lib().ihip_enqueue_attention(ctx.h, dq.ptr, dkc.ptr, dvc.ptr, dy.ptr, rows, heads,
+                                           kvh, hd, past, window, ds.ptr if sinks else 0, 0.0,
+                                           int(f16)))
+    got = dy.download(np.float32, q.size).reshape(q.shape)
+    ref = O.causal_attention(q, heads, hd, keys, vals, past, kvh, window, sk)
+    assert ulp(got, ref) <= 2
+
+
+@pytest.mark.parametrize("E,k,norm", [(128, 8, True), (32, 4, True), (16, 3, False)])
+def test_route(ctx, E, k, norm):
+    rng = np.random.default_rng(E)
+    for trial in range(5):
+        lg = rng.standard_normal(E).astype(np.float32)
+        if trial == 1:
+            lg[3] = lg[7] = lg.max() + 1  # a tie: the lower id first
+        dl = ctx.array(lg)
+        di, dw = ctx.alloc(4 * k), ctx.alloc(4 * k)
+        H.check(H.lib().ihip_enqueue_route(ctx.h, dl.ptr, E, k, int(norm), di.ptr, dw.ptr))
+        ids, w = O.route(lg, k, norm)
+        order = np.argsort(ids, kind="stable")
+        assert np.array_equal(di.download(np.int32, k), ids[order])
+        assert np.array_equal(dw.download(np.float32, k), w[order])
+
+
+def test_moecombine_and_argmax(ctx):
+    rng = np.random.default_rng(1)
+    k, n = 8, 2048
+    d = rng.standard_normal((k, n)).astype(np.float32)
+    w = rng.random(k).astype(np.float32)
+    dd, dw, dy = ctx.array(d), ctx.array(w), ctx.alloc(n * 4)
+    H.check(H.lib().ihip_enqueue_moecombine(ctx.h, dd.ptr, dw.ptr, dy.ptr, k, n))
+    ref = np.zeros(n, np.float32)
+    for s in range(k):
+        ref = (ref + (w[s] * d[s]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(dy.download(np.float32, n), ref)
+    for case in range(4):
+        v = rng.standard_normal(151936).astype(np.float32)
+        if case == 1:
+            v[[5, 70000]] = v.max() + 1  # tie: the first index
+        if case == 2:
+            v[::3] = np.nan
+        if case == 3:
+            v[:] = np.nan
+        dv, do = ctx.array(v), ctx.alloc(4)
+        H.check(H.lib().ihip_enqueue_argmax(ctx.h, dv.ptr, v.size, do.ptr))
+        assert int(do.download(np.int32, 1)[0]) == O.argmax(v)
