@@ -49,6 +49,10 @@ struct ihip_model {
   uint64_t logits_all = 0;
   int64_t logits_all_rows = 0;
   std::vector<uint64_t> owned;
+  // the host ranges of the uploaded weights: forgotten when the model goes,
+  // as a model does in its destructor (backend.pas:151-158) - new host
+  // tensors at a reused address must not meet the stale device copy
+  std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
   bool graph_ready = false;
   double prefill_ms = 0, decode_ms = 0;
 };
@@ -137,6 +141,7 @@ static int upw(ihip_model* m, const ihip_tensor& t, int64_t out, int64_t in, int
   dev = 0;
   dt = t.dtype;
   if (!t.data) return 0;
+  m->uploaded.emplace_back((const uint8_t*)t.data, row_bytes(t.dtype, in) * out * count);
   return ihip_weight(m->c, t.data, t.dtype, out, in, count, &dev);
 }
 
@@ -145,6 +150,7 @@ static int upf(ihip_model* m, const ihip_tensor& t, int64_t n, uint64_t& dev)
   dev = 0;
   if (!t.data) return 0;
   if (t.dtype != DT_F32) return fail(IHIP_E_ARG, "model: norms, biases and sinks are F32");
+  m->uploaded.emplace_back((const uint8_t*)t.data, (uint64_t)n * 4);
   return ihip_weight_f32(m->c, (const float*)t.data, n, &dev);
 }
 
@@ -481,6 +487,7 @@ void ihip_model_destroy(ihip_model* m)
   (void)hipStreamSynchronize(m->c->stream);
   for (auto p : m->owned) (void)hipFree((void*)p);
   if (m->logits_all) (void)hipFree((void*)m->logits_all);
+  for (auto& u : m->uploaded) ihip_forget_weights(m->c, u.first, u.first + u.second);
   delete m;
 }
 

@@ -288,6 +288,10 @@ class Model:
             lib().ihip_model_destroy(self.h)
             self.h = None
 
+    def __del__(self):
+        if getattr(self, "h", None) and getattr(self.ctx, "h", None):
+            self.close()
+
     def reset(self):
         check(lib().ihip_model_reset(self.h), "reset")
 

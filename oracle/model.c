@@ -12,7 +12,7 @@ struct orc_model {
   ihip_model_desc d;
   ihip_layer_desc* layer;
   int64_t max_tokens, length;
-  int kv_f16, threads;
+  int kv_f16, threads, f32;
   float** keys;
   float** values;
 };
@@ -43,6 +43,8 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
   return 0;
 }
 
+void orc_model_set_f32(orc_model* m, int f32) { m->f32 = f32; }
+
 void orc_model_destroy(orc_model* m)
 {
   if (!m) return;
@@ -59,6 +61,9 @@ void orc_model_destroy(orc_model* m)
 static int lin(orc_model* m, const float* x, int64_t rows, int64_t in, ihip_tensor w,
                uint64_t offset, int64_t out, const float* bias, float* y)
 {
+  if (m->f32)
+    return orc_linear_f32(x, rows, in, (const uint8_t*)w.data + offset, w.dtype, out, bias, y,
+                          m->threads);
   return orc_linear(x, rows, in, (const uint8_t*)w.data + offset, w.dtype, out, bias, y,
                     m->threads);
 }

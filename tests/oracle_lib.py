@@ -54,6 +54,8 @@ def lib():
         L.orc_model_create.argtypes = [vp, i64, C.c_int, C.c_int, C.POINTER(vp)]
         L.orc_model_destroy.argtypes = [vp]
         L.orc_model_destroy.restype = None
+        L.orc_model_set_f32.argtypes = [vp, C.c_int]
+        L.orc_model_set_f32.restype = None
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
         L.orc_model_greedy.argtypes = [vp, vp, i64, i64, vp, vp]
         _lib = L
@@ -158,7 +160,7 @@ def argmax(v):
 class Model:
     """The CPU decoder over a model description (mormot_ai_hip.ihip_model_desc)."""
 
-    def __init__(self, desc, max_tokens, kv_f16=False, threads=8):
+    def __init__(self, desc, max_tokens, kv_f16=False, threads=8, f32=False):
         self.desc = desc  # keeps the host tensors alive
         h = C.c_void_p()
         rc = lib().orc_model_create(C.addressof(desc.struct), max_tokens, int(kv_f16), threads,
@@ -166,6 +168,8 @@ class Model:
         if rc:
             raise RuntimeError(rc)
         self.h = h
+        if f32:
+            lib().orc_model_set_f32(self.h, 1)
 
     def close(self):
         if self.h:

@@ -213,3 +213,38 @@ def test_quantize_like_cpu(ctx):
                 assert np.array_equal(scales.reshape(-1, 8), np.repeat(d[:, None], 8, axis=1))
         dx.free()
         dq.free()
+
+
+def test_forget_weights_serves_new(ctx):
+    # ForgetWeightsServesNew (test.infer.cuda.pas:3339): host memory rewritten
+    # at the same address is served anew once forgotten, stale before
+    out, cols = 64, 256
+    w = H.synth_blocks(H.Q8_0, out, cols, 1)
+    x = np.random.default_rng(3).standard_normal((1, cols)).astype(np.float32)
+    y1 = ctx.linear(x, w, H.Q8_0, out)
+    w[:] = H.synth_blocks(H.Q8_0, out, cols, 2)
+    assert np.array_equal(ctx.linear(x, w, H.Q8_0, out), y1)  # the cached copy
+    import ctypes as C
+    ep = H.lib().ihip_forget_weights(ctx.h, C.c_void_p(w.ctypes.data),
+                                     C.c_void_p(w.ctypes.data + w.nbytes))
+    assert ep > 0
+    y2 = ctx.linear(x, w, H.Q8_0, out)
+    assert rel_error(y2, O.linear(x, w, H.Q8_0, out, f32=True)) <= 1e-5
+    assert not np.array_equal(y1, y2)
+
+
+def test_two_models_at_reused_addresses(ctx):
+    # a model forgets its weights when it goes: the next model's host tensors
+    # may sit at the same addresses and must not meet the stale copies
+    from infer_hip import models
+    outs = []
+    for seed in (1, 2, 1):
+        spec = models.Spec(models.tiny("qwen3-0.6b-q8_0", layers=1, vocab=512, hidden=256,
+                                       heads=4, kv_heads=2, head_dim=64, ffn=512), seed=seed)
+        m = H.Model(ctx, spec, max_tokens=16)
+        outs.append(m.forward([1, 2, 3]))
+        ref = O.Model(spec, 16).forward([1, 2, 3])
+        m.close()
+        del spec
+        assert np.abs(outs[-1] - ref).max() <= 1e-5 * np.abs(ref).max()
+    assert np.array_equal(outs[0], outs[2]) and not np.array_equal(outs[0], outs[1])
