@@ -1,0 +1,295 @@
+"""Benchmark of mormot.ai.infer.hip on one MI355X.
+
+Workload (BASELINE.json metric "decode tok/s + quant GEMV HBM GB/s (% peak),
+Qwen3-30B-A3B-shape Q4_K_M"): configs[3], a Qwen3-30B-A3B-shaped MoE with
+Q4_K_M weights (seeded synthetic bytes), a 1024-token prompt, then greedy
+decode. A step is one decode token (batch 1); `value` is decode tokens/s.
+
+Beside it, on the same process and device:
+- roofline: the dominant decode kernel (the Q4_K expert GEMV of the MoE
+  layers, 8 experts of 768x2048 per launch, expert matrices of all 48 layers
+  cycled so they come from HBM) timed with HIP events on the library's stream;
+- gemv: the configs[1] sweep (Q8_0, Q4_0, Q4_K, Q6_K, MXFP4 over the five
+  shapes, batch 1 and 8) in GB/s of algorithmic bytes, each timed group
+  cycling > 512 MB of distinct weight copies (beyond the 256 MB MALL);
+- stream: a read-only streaming kernel, the achievable HBM read rate;
+- cpu_baseline: the CPU oracle (a C restatement of the reference's CPU
+  decoder arithmetic) decoding the same model on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "mormot2-ai_amd"), os.path.join(ROOT, "tests")]
+
+METRIC = "decode tok/s + quant GEMV HBM GB/s (% peak), Qwen3-30B-A3B-shape Q4_K_M"
+HBM_PEAK = 8000.0  # GB/s, MI355X published
+SWEEP_SHAPES = [(3072, 1024), (1024, 3072), (6144, 2048), (2880, 2880), (151936, 1024)]
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(dtype, out, cols, rows, mode_q8):
+    import infer_hip as H
+    w = out * H.row_bytes(dtype, cols)
+    x = rows * (cols + cols // 8) if mode_q8 else rows * cols * 4
+    return w + x + rows * out * 4
+
+
+def time_graph(ctx, enqueue, reps):
+    """Capture the launches enqueue() makes into a graph, replay it reps
+    times between two events; returns ms per replay."""
+    import infer_hip as H
+    L = H.lib()
+    H.check(L.ihip_capture_begin(ctx.h), "capture")
+    try:
+        enqueue()
+    finally:
+        H.check(L.ihip_capture_end(ctx.h, 1), "capture end")
+    H.check(L.ihip_graph_launch(ctx.h, 1), "graph")
+    ctx.sync()
+    ctx.record(0)
+    for _ in range(reps):
+        H.check(L.ihip_graph_launch(ctx.h, 1), "graph")
+    ctx.record(1)
+    return ctx.elapsed(0, 1) / reps
+
+
+def stream_peak(ctx):
+    import infer_hip as H
+    nbytes = 4 << 30
+    buf = ctx.alloc(nbytes)
+    out = ctx.alloc(256)
+    L = H.lib()
+    for _ in range(2):
+        H.check(L.ihip_enqueue_stream_read(ctx.h, buf.ptr, nbytes, out.ptr))
+    ctx.sync()
+    ctx.record(0)
+    reps = 10
+    for _ in range(reps):
+        H.check(L.ihip_enqueue_stream_read(ctx.h, buf.ptr, nbytes, out.ptr))
+    ctx.record(1)
+    ms = ctx.elapsed(0, 1) / reps
+    buf.free()
+    out.free()
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20):
+    """GB/s of one (type, shape, batch, mode): distinct copies of the matrix
+    cycled inside a graph, so the weights stream from HBM."""
+    import infer_hip as H
+    L = H.lib()
+    wbytes = out * H.row_bytes(dtype, cols)
+    ncopies = max(4, -(-min_bytes // wbytes))
+    host = H.synth_blocks(dtype, out, cols, out * 7 + cols, -8, -4)
+    dev0 = ctx.weight(host, dtype, out, cols)
+    stride = (wbytes + 255) // 256 * 256
+    big = ctx.alloc(stride * ncopies)
+    for i in range(ncopies):
+        H.check(L.ihip_copy_async(ctx.h, big.ptr + i * stride, dev0, wbytes))
+    x = np.random.default_rng(1).standard_normal((rows, cols)).astype(np.float32)
+    dx = ctx.array(x)
+    dy = ctx.alloc(rows * out * 4)
+    xin, m = dx.ptr, mode
+    if mode == H.MODE_Q8:
+        kq = 1 if dtype in (H.Q4_K, H.Q6_K) else 0
+        dq = ctx.alloc(rows * int(L.ihip_q8_bytes(cols, kq)))
+        H.check(L.ihip_enqueue_quantize(ctx.h, dx.ptr, rows, cols, kq, dq.ptr, 0))
+        xin, m = dq.ptr, mode | 2
+    ctx.sync()
+
+    def enq():
+        for i in range(ncopies):
+            H.check(L.ihip_enqueue_linear_at(ctx.h, xin, rows, cols, dtype, big.ptr + i * stride,
+                                             out, dy.ptr, 0, m), "gemv")
+
+    reps = 3
+    ms = time_graph(ctx, enq, reps) / ncopies
+    nb = algo_bytes(dtype, out, cols, rows, mode == H.MODE_Q8)
+    big.free()
+    dx.free()
+    dy.free()
+    if mode == H.MODE_Q8:
+        dq.free()
+    H.lib().ihip_forget_weights(ctx.h, host.ctypes.data, host.ctypes.data + host.nbytes)
+    return nb / (ms * 1e-3) / 1e9, ms * 1e3
+
+
+def expert_gemv(ctx, spec, reps=4):
+    """The dominant decode kernel: 8 experts of the gate projection of every
+    MoE layer (Q4_K 768x2048 each), one launch per layer, timed with events."""
+    import infer_hip as H
+    L = H.lib()
+    c = spec.cfg
+    Hd, FI, E, K = c["hidden"], c["expert_ffn"], c["experts"], c["experts_used"]
+    devs = []
+    for li in range(c["layers"]):
+        t = spec.layers[li].exp_gate
+        d = __import__("ctypes").c_uint64()
+        H.check(L.ihip_weight(ctx.h, t.data, t.dtype, FI, Hd, E, __import__("ctypes").byref(d)))
+        devs.append((d.value, t.dtype))
+    dtype = devs[0][1]
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((1, Hd)).astype(np.float32)
+    dx = ctx.array(x)
+    kq = 1 if dtype in (H.Q4_K, H.Q6_K) else 0
+    dq = ctx.alloc(int(L.ihip_q8_bytes(Hd, kq)))
+    H.check(L.ihip_enqueue_quantize(ctx.h, dx.ptr, 1, Hd, kq, dq.ptr, 0))
+    ids = ctx.array(np.sort(rng.choice(E, K, replace=False)).astype(np.int32))
+    dy = ctx.alloc(K * FI * 4)
+    stride = FI * H.row_bytes(dtype, Hd)
+    for w, _ in devs:
+        H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K, 0,
+                                          dy.ptr, 0, H.MODE_Q8 | 2))
+    ctx.sync()
+    ctx.record(2)
+    n = 0
+    for _ in range(reps):
+        for w, _ in devs:
+            H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K,
+                                              0, dy.ptr, 0, H.MODE_Q8 | 2))
+            n += 1
+    ctx.record(3)
+    ms = ctx.elapsed(2, 3) / n
+    nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + K * 4 + K * FI * 4
+    for b in (dx, dq, ids, dy):
+        b.free()
+    return {"kernel": f"gemv_{H.NAMES[dtype].lower()}_q8 (ids, {K} experts {FI}x{Hd})",
+            "bytes_per_launch": nb, "avg_us": ms * 1e3, "GBps": nb / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline(spec, prompt, steps, threads):
+    import oracle_lib as O
+    m = O.Model(spec, len(prompt) + steps + 2, kv_f16=True, threads=threads)
+    lg = m.forward(prompt)
+    tok = int(np.argmax(lg))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lg = m.forward([tok])
+        tok = O.argmax(lg)
+    dt = time.perf_counter() - t0
+    m.close()
+    return steps / dt
+
+
+def cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=1024)
+    ap.add_argument("--config", default="qwen3-30b-a3b-q4_k_m")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kv-f32", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"{args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import infer_hip as H
+    from infer_hip import models
+
+    ctx = H.Context(0)
+    dev_name, dev_mem, cus = ctx.info()
+    log("device", dev_name, dev_mem >> 30, "GiB", cus, "CUs")
+    stream = stream_peak(ctx)
+    log(f"stream read {stream:.0f} GB/s")
+
+    t = time.time()
+    spec = models.Spec(models.CONFIGS[args.config], seed=1)
+    log(f"synthetic {args.config} built in {time.time() - t:.1f}s")
+    max_tokens = args.prompt + args.warmup + args.steps + 8
+    t = time.time()
+    model = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=not args.kv_f32, max_tokens=max_tokens)
+    log(f"uploaded in {time.time() - t:.1f}s")
+    prompt = np.random.default_rng(2024).integers(0, spec.vocab, args.prompt).astype(np.int32)
+    ctx.sync()
+    t = time.perf_counter()
+    lg = model.forward(prompt)
+    prefill_s = time.perf_counter() - t
+    first = int(np.argmax(lg))
+    log(f"prefill {args.prompt} tokens {prefill_s * 1e3:.1f} ms")
+    ids = model.decode(first, args.warmup)
+    ctx.sync()
+    t0 = time.perf_counter()
+    ids2 = model.decode(int(ids[-1]), args.steps)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    log(f"decode {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    wbytes = spec.weight_bytes_per_token()
+    dom = expert_gemv(ctx, spec)  # the model's own device copies (same host tensors)
+    log("dominant kernel", dom)
+    model.close()
+
+    sweep = {}
+    if not args.no_sweep:
+        for dtype in (H.Q8_0, H.Q4_0, H.Q4_K, H.Q6_K, H.MXFP4):
+            for out, cols in SWEEP_SHAPES:
+                if cols % H.BLOCK[dtype][0]:
+                    continue  # 2880 is no whole number of 256-value super-blocks
+                for rows, mode in ((1, H.MODE_Q8), (1, H.MODE_F32), (8, H.MODE_Q8)):
+                    gbps, us = gemv_case(ctx, dtype, out, cols, rows, mode)
+                    key = f"{H.NAMES[dtype]} {out}x{cols} b{rows} {'q8' if mode else 'f32'}"
+                    sweep[key] = {"GBps": round(gbps, 1), "us": round(us, 2),
+                                  "frac": round(gbps / HBM_PEAK, 3)}
+                    log(key, sweep[key])
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        t = time.time()
+        cpu_tok_s = cpu_baseline(spec, prompt[:8], 4, threads)
+        cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{args.config} decode, 4 tokens after an 8-token prompt, the C oracle "
+                         f"(exact int8 sums, double scaling), {threads} threads on {cpu_name()}"}
+        log(f"cpu baseline {cpu_tok_s:.3f} tok/s in {time.time() - t:.1f}s")
+
+    big = [v["GBps"] for k, v in sweep.items() if "151936" in k and "b1 q8" in k]
+    result = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 (Q8_K activations x Q4_K/Q6_K codes, int32 sums, f64 scaling)",
+        "data": "synthetic (seeded random Q4_K_M bytes of the architecture)",
+        "config": {"workload": f"{args.config} greedy decode after a {args.prompt}-token prompt",
+                   "prompt": args.prompt, "kv_cache": "f32" if args.kv_f32 else "f16",
+                   "weight_bytes_per_token": wbytes, "parallelism": "single GPU"},
+        "prefill_tok_s": round(args.prompt / prefill_s, 1),
+        "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
+                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": None,
+                     "kernel": dom["kernel"], "bytes_per_launch": dom["bytes_per_launch"],
+                     "avg_us": round(dom["avg_us"], 3)},
+        "stream_read_GBps": round(stream, 1),
+        "gemv_head_151936x1024_b1_GBps": big,
+        "gemv": sweep,
+        "cpu_baseline": cpu,
+        "device": dev_name,
+    }
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

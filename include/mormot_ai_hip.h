@@ -52,6 +52,10 @@ enum {
  *   sums, the scales applied and summed in double; F32/BF16 weights summed in
  *   double. Same bits as the CPU up to the order of a double sum. */
 enum { IHIP_MODE_F32 = 0, IHIP_MODE_Q8 = 1 };
+/* or'ed into IHIP_MODE_Q8: x is a buffer already quantized by
+ * ihip_enqueue_quantize (the quantization of a row shared by several
+ * Linears is then done once) */
+enum { IHIP_MODE_XQ = 2 };
 
 /* ---- status codes ---- */
 enum {
@@ -221,6 +225,10 @@ int ihip_enqueue_embed(ihip_ctx* ctx, uint64_t embed, int dtype, int64_t vocab,
 /* the first index of the maximum of n floats, NaN skipped, lowest id on a tie
  * (InferArgMax, sampler.pas:123-160), written as int32 to `out` */
 int ihip_enqueue_argmax(ihip_ctx* ctx, uint64_t v, int64_t n, uint64_t out);
+/* a read-only streaming kernel over `bytes` at p (16-byte loads, every CU):
+ * the achievable HBM read bandwidth, measured beside the GEMV (diagnostic,
+ * no counterpart in the reference) */
+int ihip_enqueue_stream_read(ihip_ctx* ctx, uint64_t p, uint64_t bytes, uint64_t out);
 
 /* ======================================================================
  * TQwen3Cuda (src/infer/mormot.ai.infer.model.qwen3.cuda.pas:150-301):
@@ -284,6 +292,11 @@ int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count,
  * then max_new ids by argmax; with the argmax on the device */
 int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n,
                       int64_t max_new, int32_t* out_ids);
+/* steps greedy decode steps continuing the cache: token `first` (the last
+ * id, not yet in the cache) enters it, out_ids[i] is the argmax after step i;
+ * each step is one replay of the decode graph (the Forward(id, 1) of
+ * TDecoderModel.Greedy, decoder.pas:3410-3422) */
+int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_ids);
 /* the cos/sin table the model uploads for positions [first, first + rows):
  * [rows, rope/2] cos then sin (TDecoderModel.Rotary, decoder.pas:2539-2561) */
 int ihip_model_rotary(const ihip_model_desc* desc, int64_t first, int64_t rows,

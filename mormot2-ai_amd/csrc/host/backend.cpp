@@ -310,9 +310,13 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   int lpr = 64, U = 1;
   pick_lpr(G, lpr, U);
   uint64_t xq = k.xq;
-  const bool q8 = k.mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
+  const int mode = k.mode & 1;
+  const bool q8 = mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
+  if (q8 && (k.mode & IHIP_MODE_XQ)) xq = k.x;  // x is already quantized
   if (q8 && !xq) {
-    int64_t xrows = k.ids ? (k.x_per_slot ? (k.rows + k.x_per_slot - 1) / k.x_per_slot : 1) : k.rows;
+    int64_t xrows = (k.ids || k.items)
+                        ? (k.x_per_slot ? (k.rows + k.x_per_slot - 1) / k.x_per_slot : 1)
+                        : k.rows;
     int rc = scratch(c, c->scratch_q, c->scratch_q_bytes, xrows * q8_row_bytes(k.in));
     if (rc) return rc;
     xq = c->scratch_q;
@@ -330,16 +334,18 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     int32_t out, in, rows, lpr;
     int32_t x_per_slot;
     int32_t nexp;
+    const void* items;
+    const int* perm;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
-         (int32_t)k.rows, lpr, k.x_per_slot, k.nexp};
-  const bool batch = !k.ids && k.rows > 1;
+         (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm};
+  const bool batch = k.items || (!k.ids && k.rows > 1);
   char name[64];
   snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
-           k.mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : "", U);
+           mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : "", U);
   const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
   int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
-  unsigned gy = (unsigned)(k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1));
+  unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
 }
 
@@ -668,3 +674,14 @@ int ihip_enqueue_argmax(ihip_ctx* c, uint64_t v, int64_t n, uint64_t out)
 }
 
 }  // extern "C"
+
+extern "C" int ihip_enqueue_stream_read(ihip_ctx* c, uint64_t p, uint64_t bytes, uint64_t out)
+{
+  if (!c || !p || bytes < 16 || bytes % 16 || !out) return fail(IHIP_E_ARG, "ihip_enqueue_stream_read");
+  struct {
+    const void* p;
+    uint64_t n16;
+    uint32_t* out;
+  } a = {(const void*)p, bytes / 16, (uint32_t*)out};
+  return launch(c, "stream_read", dim3((unsigned)c->cus * 8), dim3(256), &a);
+}

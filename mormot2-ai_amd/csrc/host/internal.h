@@ -91,6 +91,9 @@ struct LinearCall {
   int64_t stride = 0;
   int x_per_slot = 0;
   int nexp = 0;        // experts behind ids (a bad id gives a zero row), 0: unchecked
+  uint64_t items = 0;  // grouped experts: int4 work items (expert, start, count)
+  uint64_t perm = 0;   // and the slots sorted by expert; rows = slots
+  int64_t nitems = 0;
 };
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // which activation quantizer a weight type needs in Q8 mode: -1 none (float

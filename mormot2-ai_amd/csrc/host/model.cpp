@@ -46,6 +46,7 @@ struct ihip_model {
   uint64_t x = 0, h = 0, tmp = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0;
   uint64_t route = 0, ids = 0, rw = 0, eout = 0, cs = 0, tok = 0, logits = 0, next = 0, pos = 0;
   uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
+  uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
   uint64_t logits_all = 0;
   int64_t logits_all_rows = 0;
   std::vector<uint64_t> owned;
@@ -188,6 +189,14 @@ static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int
   k.x = x; k.rows = slots; k.in = in; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
   k.y = y; k.mode = m->mode; k.ids = ids; k.stride = stride; k.x_per_slot = x_div;
   k.nexp = m->d.experts;
+  if (slots > m->d.experts_used) {
+    // a prompt chunk: the slots grouped by expert (moe_plan), 8 rows per
+    // work item, so an expert's matrix is read once per 8 of its tokens
+    k.ids = 0;
+    k.items = m->items;
+    k.perm = m->perm;
+    k.nitems = (slots + 7) / 8 + m->d.experts;
+  }
   if (m->mode == IHIP_MODE_Q8 && q8_kind(dt) >= 0) {
     if (!quantized) {
       int rc = enqueue_quantize(m->c, x, xrows, in, q8_kind(dt), xqbuf);
@@ -285,6 +294,16 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
       } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n};
       if ((rc = launch(m->c, "route", dim3((unsigned)((n + 63) / 64)), dim3(64), &ra))) return rc;
+      if (n > 1) {
+        struct {
+          const int* ids;
+          int* perm;
+          void* items;
+          int32_t slots, experts, max_items, pad;
+        } pa = {(const int*)m->ids, (int*)m->perm, (void*)m->items, (int32_t)(n * K), (int32_t)E,
+                (int32_t)((n * K + 7) / 8 + E), 0};
+        if ((rc = launch(m->c, "moe_plan", dim3(1), dim3(256), &pa))) return rc;
+      }
       // gate and up: slot s = row s / K, expert ids[s]
       bool q0 = false;
       if (m->mode == IHIP_MODE_Q8 && q8_kind(L.egd) >= 0) {
@@ -370,6 +389,30 @@ static int decode_graph(ihip_model* m)
   if (rc) return rc;
   if (rc2) return rc2;
   m->graph_ready = true;
+  return 0;
+}
+
+// steps decode steps from token `first` (not yet in the cache): each one
+// graph launch that writes the next id; out_ids[i] the id after step i
+static int decode_steps(ihip_model* m, int32_t first, int64_t steps, int32_t* out_ids)
+{
+  ihip_ctx* c = m->c;
+  int rc = 0;
+  if (!m->graph_ready && (rc = decode_graph(m))) return rc;
+  std::vector<float> cs(m->d.head_dim);
+  int32_t tok = first;
+  for (int64_t i = 0; i < steps; i++) {
+    int32_t pos = (int32_t)m->length;
+    rotary(m->d, pos, 1, cs.data());
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
+    if ((rc = ihip_graph_launch(c, 0))) return rc;
+    IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)m->next, 4, c->stream));
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    m->length++;
+    tok = out_ids[i];
+  }
   return 0;
 }
 
@@ -470,8 +513,13 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       (rc = dalloc(m, N * std::max(d.experts_used, 1) * H * 4, m->eout)) ||
       (rc = dalloc(m, N * hd * 4, m->cs)) || (rc = dalloc(m, N * 4, m->tok)) ||
       (rc = dalloc(m, (uint64_t)d.vocab * 4, m->logits)) || (rc = dalloc(m, 256, m->next)) ||
-      (rc = dalloc(m, 256, m->pos)))
+      (rc = dalloc(m, 256, m->pos)) ||
+      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->perm)) ||
+      (rc = dalloc(m, (N * std::max(d.experts_used, 1) / 8 + 1 + std::max(d.experts, 1)) * 16,
+                   m->items)))
     return bad(rc);
+  if (any_moe && (d.experts > 4096 || N * d.experts_used > 4096))
+    return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or slots per chunk"));
   const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
   const uint64_t qrow = qin + 4 * (qin / 32);
   if ((rc = dalloc(m, N * qrow, m->xq0)) || (rc = dalloc(m, N * qrow, m->xqk)) ||
@@ -559,39 +607,27 @@ int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n, int64_t m
   if (rc) return rc;
   auto t1 = std::chrono::steady_clock::now();
   std::lock_guard<std::mutex> g(c->lock);
-  if (!m->graph_ready && (rc = decode_graph(m))) return rc;
-  const int64_t half = m->d.head_dim / 2;
-  std::vector<float> cs(m->d.head_dim);
-  for (int64_t i = 1; i < max_new; i++) {
-    int32_t tok = out_ids[i - 1];
-    int32_t pos = (int32_t)m->length;
-    rotary(m->d, pos, 1, cs.data());
-    (void)half;
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
-    if ((rc = ihip_graph_launch(c, 0))) return rc;
-    IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)m->next, 4, c->stream));
-    IHIP_CHECK(hipStreamSynchronize(c->stream));
-    m->length++;
-  }
-  // the last token enters the cache too (TDecoderModel.Greedy: Forward
-  // without logits after the last step), through the same graph
-  {
-    int32_t tok = out_ids[max_new - 1];
-    int32_t pos = (int32_t)m->length;
-    rotary(m->d, pos, 1, cs.data());
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
-    if ((rc = ihip_graph_launch(c, 0))) return rc;
-    IHIP_CHECK(hipStreamSynchronize(c->stream));
-    m->length++;
-  }
+  // the new ids, then the last one into the cache too (TDecoderModel.Greedy:
+  // a Forward without logits after the last step), through the same graph
+  if (max_new > 1 && (rc = decode_steps(m, out_ids[0], max_new - 1, out_ids + 1))) return rc;
+  int32_t spare;
+  if ((rc = decode_steps(m, out_ids[max_new - 1], 1, &spare))) return rc;
   auto t2 = std::chrono::steady_clock::now();
   m->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
   m->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
   return 0;
+}
+
+int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_ids)
+{
+  if (!m || steps < 1 || !out_ids || first < 0 || first >= m->d.vocab)
+    return fail(IHIP_E_ARG, "ihip_model_decode");
+  if (m->length + steps > m->max_tokens) return fail(IHIP_E_ARG, "ihip_model_decode: beyond the KV cache");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  auto t0 = std::chrono::steady_clock::now();
+  int rc = decode_steps(m, first, steps, out_ids);
+  m->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  return rc;
 }
 
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms)

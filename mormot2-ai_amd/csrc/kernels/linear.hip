@@ -38,6 +38,11 @@ struct LinArgs {
   int32_t out, in, rows, lpr;
   int32_t x_per_slot;  // ids: x row = slot / x_per_slot, or 0 when 0
   int32_t nexp;        // ids: the number of experts (an id outside 0..nexp-1 gives a zero row), 0: unchecked
+  // grouped experts (a prompt chunk): work item blockIdx.y = (expert, start,
+  // count <= 8) over perm, the slots sorted by expert; slot s reads x row
+  // s / x_per_slot and writes y row s
+  const int4* items;
+  const int* perm;
 };
 
 // ---------------------------------------------------------------- formats
@@ -393,7 +398,16 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const float* bias = a.bias;
   int64_t xrow0, yrow0;
   int nrows;
-  if (a.ids) {
+  int pstart = -1;  // grouped: the first entry of perm
+  if (a.items) {
+    const int4 it = a.items[blockIdx.y];
+    if (it.z <= 0) return;
+    w += (int64_t)it.x * a.stride;
+    if (bias) bias += (int64_t)it.x * a.out;
+    pstart = it.y;
+    nrows = min(R, it.z);
+    xrow0 = yrow0 = 0;
+  } else if (a.ids) {
     int slot = blockIdx.y;
     int e = a.ids[slot];
     if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
@@ -458,6 +472,19 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       }
     }
   } else {
+    // the activation and output rows of the batch
+    int64_t xr[R], yr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (pstart >= 0) {
+        int s = r < nrows ? a.perm[pstart + r] : 0;
+        xr[r] = a.x_per_slot ? s / a.x_per_slot : 0;
+        yr[r] = s;
+      } else {
+        xr[r] = xrow0 + r;
+        yr[r] = yrow0 + r;
+      }
+    }
     for (int64_t t = wid; t < tiles; t += nw) {
       int64_t o = t * rpw + rsub;
       bool valid = o < a.out;
@@ -481,7 +508,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
             int isum = 0, msum = 0;
             XGroup xg;
             if (has) {
-              load_x<F, MODE>(a, xrow0 + r, g, G, xg);
+              load_x<F, MODE>(a, xr[r], g, G, xg);
               group_term<F, MODE>(w, raw, o, g, a.in, xg, accf[r], accd[r], isum, msum);
             }
             if constexpr (MODE == 1 && is_k_quant(F)) {
@@ -502,7 +529,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
             v = row_total<F, MODE>(lpr, Raw{}, 0.f, false, accf[r], accd[r], 0, 0, 0);
           if (lr == 0 && valid) {
             if (bias) v = (double)bias[o] + v;
-            a.y[(yrow0 + r) * a.out + o] = (float)v;
+            a.y[yr[r] * a.out + o] = (float)v;
           }
         }
       }

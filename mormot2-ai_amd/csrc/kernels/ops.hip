@@ -495,3 +495,73 @@ extern "C" __global__ __launch_bounds__(1024) void argmax(ArgmaxArgs a)
 }
 
 }  // namespace ihip
+
+// ---------------------------------------------------------- HBM streaming
+struct StreamArgs {
+  const uint4* p;
+  uint64_t n16;
+  uint32_t* out;
+};
+
+// reads n16 16-byte words once (grid-stride, 4 in flight per lane) and folds
+// them so the loads are not dropped: the achievable read bandwidth
+extern "C" __global__ __launch_bounds__(256) void stream_read(StreamArgs a)
+{
+  uint32_t acc = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < a.n16; i += 4 * stride) {
+    uint4 v0 = a.p[i], v1 = a.p[i + stride], v2 = a.p[i + 2 * stride], v3 = a.p[i + 3 * stride];
+    acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+    acc ^= v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^ v3.w;
+  }
+  for (; i < a.n16; i += stride) {
+    uint4 v = a.p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u) a.out[0] = acc;
+}
+
+// ------------------------------------------------------- MoE prompt plan
+struct PlanArgs {
+  const int* ids;  // [slots] expert of each slot (route, sorted per token)
+  int* perm;       // [slots] the slots sorted by expert, in slot order within one
+  int4* items;     // [max_items] (expert, start in perm, count <= 8), count 0 after the last
+  int32_t slots, experts, max_items, pad;
+};
+
+// the experts of a prompt chunk grouped for the batched GEMV (the host-side
+// expert loop of model.qwen3.cuda.pas:1077-1150, on the device): a count per
+// expert, their offsets, then per expert its slots in order - thread e
+// collects expert e, so the order is deterministic
+extern "C" __global__ __launch_bounds__(256) void moe_plan(PlanArgs a)
+{
+  __shared__ int cnt[4096];
+  __shared__ int off[4096];
+  __shared__ int sid[4096];
+  const int t = threadIdx.x, E = a.experts, S = a.slots;
+  for (int e = t; e < E; e += blockDim.x) cnt[e] = 0;
+  for (int s = t; s < S; s += blockDim.x) sid[s] = a.ids[s];
+  __syncthreads();
+  for (int s = t; s < S; s += blockDim.x) {
+    int e = sid[s];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (t == 0) {
+    int run = 0, it = 0;
+    for (int e = 0; e < E; e++) {
+      off[e] = run;
+      for (int st = 0; st < cnt[e] && it < a.max_items; st += 8)
+        a.items[it++] = make_int4(e, run + st, min(8, cnt[e] - st), 0);
+      run += cnt[e];
+    }
+    for (; it < a.max_items; it++) a.items[it] = make_int4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  for (int e = t; e < E; e += blockDim.x) {
+    int k = off[e];
+    for (int s = 0; s < S; s++)
+      if (sid[s] == e) a.perm[k++] = s;
+  }
+}

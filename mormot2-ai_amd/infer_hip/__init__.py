@@ -92,6 +92,8 @@ def lib():
             "ihip_model_reset": (i32, [vp]),
             "ihip_model_forward": (i32, [vp, vp, i64, vp, i32]),
             "ihip_model_greedy": (i32, [vp, vp, i64, i64, vp]),
+            "ihip_model_decode": (i32, [vp, C.c_int32, i64, vp]),
+            "ihip_enqueue_stream_read": (i32, [vp, u64, u64, u64]),
             "ihip_model_rotary": (i32, [vp, i64, i64, vp]),
             "ihip_model_timing": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
             "ihip_synth_blocks": (i32, [vp, i32, i64, i64, u64, i32, i32, i32]),
@@ -306,6 +308,11 @@ class Model:
         p = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(max_new, np.int32)
         check(lib().ihip_model_greedy(self.h, _p(p), len(p), max_new, _p(out)), "greedy")
+        return out
+
+    def decode(self, first, steps):
+        out = np.empty(steps, np.int32)
+        check(lib().ihip_model_decode(self.h, int(first), steps, _p(out)), "decode")
         return out
 
     def timing(self):
