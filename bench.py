@@ -200,6 +200,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kv-f32", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="direct launches per decode step (the profiler cannot trace graphs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -222,6 +224,8 @@ def main():
     t = time.time()
     model = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=not args.kv_f32, max_tokens=max_tokens)
     log(f"uploaded in {time.time() - t:.1f}s")
+    if args.no_graphs:
+        model.use_graphs(False)
     prompt = np.random.default_rng(2024).integers(0, spec.vocab, args.prompt).astype(np.int32)
     ctx.sync()
     t = time.perf_counter()
@@ -274,7 +278,8 @@ def main():
         "data": "synthetic (seeded random Q4_K_M bytes of the architecture)",
         "config": {"workload": f"{args.config} greedy decode after a {args.prompt}-token prompt",
                    "prompt": args.prompt, "kv_cache": "f32" if args.kv_f32 else "f16",
-                   "weight_bytes_per_token": wbytes, "parallelism": "single GPU"},
+                   "weight_bytes_per_token": wbytes, "parallelism": "single GPU",
+                   "graphs": not args.no_graphs},
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,

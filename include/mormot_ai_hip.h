@@ -301,6 +301,9 @@ int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_
  * [rows, rope/2] cos then sin (TDecoderModel.Rotary, decoder.pas:2539-2561) */
 int ihip_model_rotary(const ihip_model_desc* desc, int64_t first, int64_t rows,
                       float* cs);
+/* decode steps as one replayed HIP graph (on, the default) or as direct
+ * launches (TQwen3Cuda.UseGraphs, model.qwen3.cuda.pas:253-262) */
+int ihip_model_use_graphs(ihip_model* m, int on);
 /* timings of the last greedy call: prefill and decode milliseconds */
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
 

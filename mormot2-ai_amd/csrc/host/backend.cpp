@@ -615,25 +615,15 @@ int ihip_enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, ui
   if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 1 || hd > 256 || 256 % hd ||
       past < 0 || window < 0)
     return fail(IHIP_E_ARG, "ihip_enqueue_attention");
+  if (hd % 8) return fail(IHIP_E_ARG, "attention: head size not a multiple of 8");
   int64_t maxkeys = past + rows;
   if (window > 0 && maxkeys > window) maxkeys = window;
-  if (maxkeys > 8000) return fail(IHIP_E_UNSUPPORTED, "attention: more than 8000 keys per row");
-  if (!(scale > 0)) scale = 1.0 / sqrt((double)hd);
-  struct {
-    const float* q;
-    const void* kc;
-    const void* vc;
-    float* y;
-    const float* sinks;
-    const int* pastp;
-    double scale;
-    int32_t rows, heads, kvh, hd, past, window, f16, maxkeys;
-  } a = {(const float*)q, (const void*)kc, (const void*)vc, (float*)y, (const float*)sinks,
-         nullptr, scale,
-         (int32_t)rows, (int32_t)heads, (int32_t)kvh, (int32_t)hd, (int32_t)past, (int32_t)window,
-         kv_f16, (int32_t)maxkeys};
-  return launch(c, "attention", dim3((unsigned)heads, (unsigned)rows), dim3(256), &a,
-                (size_t)maxkeys * 8);
+  const int splits = attention_splits(maxkeys);
+  int rc = scratch(c, c->scratch_attn, c->scratch_attn_bytes,
+                   (uint64_t)heads * rows * splits * (hd + 2) * 8);
+  if (rc) return rc;
+  return enqueue_attention(c, q, kc, vc, y, c->scratch_attn, rows, heads, kvh, hd, past, 0, window,
+                           sinks, scale, kv_f16, splits);
 }
 
 int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k, int norm_topk,
@@ -685,3 +675,34 @@ extern "C" int ihip_enqueue_stream_read(ihip_ctx* c, uint64_t p, uint64_t bytes,
   } a = {(const void*)p, bytes / 16, (uint32_t*)out};
   return launch(c, "stream_read", dim3((unsigned)c->cus * 8), dim3(256), &a);
 }
+
+namespace ihip {
+
+int attention_splits(int64_t maxkeys) { return (int)std::max<int64_t>(1, (maxkeys + 255) / 256); }
+
+int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
+                      int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
+                      uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,
+                      int splits)
+{
+  if (!(scale > 0)) scale = 1.0 / std::sqrt((double)hd);
+  struct {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* y;
+    const float* sinks;
+    const int* pastp;
+    double* part;
+    double scale;
+    int32_t rows, heads, kvh, hd, past, window, f16, splits;
+  } a = {(const float*)q, (const void*)kc, (const void*)vc, (float*)y, (const float*)sinks,
+         (const int*)pastp, (double*)part, scale, (int32_t)rows, (int32_t)heads, (int32_t)kvh,
+         (int32_t)hd, (int32_t)past, (int32_t)window, f16, splits};
+  int rc = launch(c, "attention_part", dim3((unsigned)heads, (unsigned)rows, (unsigned)splits),
+                  dim3(256), &a);
+  if (rc) return rc;
+  return launch(c, "attention_merge", dim3((unsigned)heads, (unsigned)rows), dim3(128), &a);
+}
+
+}  // namespace ihip

@@ -60,6 +60,7 @@ struct ihip_ctx {
   uint64_t scratch_y = 0, scratch_y_bytes = 0;
   uint64_t scratch_q = 0, scratch_q_bytes = 0;
   uint64_t scratch_bad = 0;
+  uint64_t scratch_attn = 0, scratch_attn_bytes = 0;
   bool capturing = false;
   hipGraph_t graphs[16] = {};
   hipGraphExec_t execs[16] = {};
@@ -100,5 +101,13 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // weights), 0 Q8_0, 1 Q8_K
 int q8_kind(int dtype);
 int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind, uint64_t xq);
+// flash-decoding attention: ranges of at most 256 keys per block, then a merge;
+// part holds heads * rows * splits * (hd + 2) doubles; pastp: the position
+// of row 0 in device memory (graph replay), or 0: past
+int attention_splits(int64_t maxkeys);
+int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
+                      int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
+                      uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,
+                      int splits);
 
 }  // namespace ihip

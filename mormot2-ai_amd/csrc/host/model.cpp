@@ -47,6 +47,7 @@ struct ihip_model {
   uint64_t route = 0, ids = 0, rw = 0, eout = 0, cs = 0, tok = 0, logits = 0, next = 0, pos = 0;
   uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
   uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
+  uint64_t attn_part = 0;               // flash-decoding partials
   uint64_t logits_all = 0;
   int64_t logits_all_rows = 0;
   std::vector<uint64_t> owned;
@@ -55,6 +56,7 @@ struct ihip_model {
   // tensors at a reused address must not meet the stale device copy
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
   bool graph_ready = false;
+  bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
   double prefill_ms = 0, decode_ms = 0;
 };
 
@@ -230,22 +232,11 @@ static int rope_attn(ihip_model* m, const DevLayer& L, int64_t n, int64_t past, 
   if (rc) return rc;
   int64_t maxkeys = graph ? m->max_tokens : past + n;
   if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
-  if (maxkeys > 8000) return fail(IHIP_E_UNSUPPORTED, "attention: more than 8000 keys");
-  struct {
-    const float* q;
-    const void* kc;
-    const void* vc;
-    float* y;
-    const float* sinks;
-    const int* pastp;
-    double scale;
-    int32_t rows, heads, kvh, hd, past, window, f16, maxkeys;
-  } aa = {(const float*)m->q, (const void*)L.kc, (const void*)L.vc, (float*)m->attn,
-          (const float*)L.sinks, graph ? (const int*)m->pos : nullptr,
-          1.0 / std::sqrt((double)d.head_dim), (int32_t)n, d.heads, d.kv_heads, d.head_dim,
-          (int32_t)past, L.window, m->kv_f16, (int32_t)maxkeys};
-  return launch(m->c, "attention", dim3((unsigned)d.heads, (unsigned)n), dim3(256), &aa,
-                (size_t)maxkeys * 8);
+  // a graph replays one grid for every position: splits for the longest
+  return enqueue_attention(m->c, m->q, L.kc, L.vc, m->attn, m->attn_part, n, d.heads, d.kv_heads,
+                           d.head_dim, past, graph ? m->pos : 0, L.window, L.sinks,
+                           1.0 / std::sqrt((double)d.head_dim), m->kv_f16,
+                           attention_splits(maxkeys));
 }
 
 // the layers of one chunk of n rows at positions past.., x holding the
@@ -293,7 +284,7 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
         int32_t experts, k, norm, rows;
       } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n};
-      if ((rc = launch(m->c, "route", dim3((unsigned)((n + 63) / 64)), dim3(64), &ra))) return rc;
+      if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(64), &ra))) return rc;
       if (n > 1) {
         struct {
           const int* ids;
@@ -376,15 +367,22 @@ static int chunk(ihip_model* m, const int32_t* ids, int64_t n, bool want_logits,
 }
 
 // the decode step as a graph: embed(tok) -> layers(pos) -> head -> argmax
+static int decode_body(ihip_model* m)
+{
+  ihip_ctx* c = m->c;
+  int rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, m->tok, 1, m->x);
+  if (!rc) rc = layers(m, 1, 0, true);
+  if (!rc) rc = head(m, 1, false, m->logits);
+  if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+  return rc;
+}
+
 static int decode_graph(ihip_model* m)
 {
   ihip_ctx* c = m->c;
   int rc = ihip_capture_begin(c);
   if (rc) return rc;
-  rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, m->tok, 1, m->x);
-  if (!rc) rc = layers(m, 1, 0, true);
-  if (!rc) rc = head(m, 1, false, m->logits);
-  if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+  rc = decode_body(m);
   int rc2 = ihip_capture_end(c, 0);
   if (rc) return rc;
   if (rc2) return rc2;
@@ -398,7 +396,7 @@ static int decode_steps(ihip_model* m, int32_t first, int64_t steps, int32_t* ou
 {
   ihip_ctx* c = m->c;
   int rc = 0;
-  if (!m->graph_ready && (rc = decode_graph(m))) return rc;
+  if (m->use_graphs && !m->graph_ready && (rc = decode_graph(m))) return rc;
   std::vector<float> cs(m->d.head_dim);
   int32_t tok = first;
   for (int64_t i = 0; i < steps; i++) {
@@ -407,7 +405,7 @@ static int decode_steps(ihip_model* m, int32_t first, int64_t steps, int32_t* ou
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
-    if ((rc = ihip_graph_launch(c, 0))) return rc;
+    if ((rc = m->use_graphs ? ihip_graph_launch(c, 0) : decode_body(m))) return rc;
     IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)m->next, 4, c->stream));
     IHIP_CHECK(hipStreamSynchronize(c->stream));
     m->length++;
@@ -517,6 +515,10 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->perm)) ||
       (rc = dalloc(m, (N * std::max(d.experts_used, 1) / 8 + 1 + std::max(d.experts, 1)) * 16,
                    m->items)))
+    return bad(rc);
+  if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
+  if ((rc = dalloc(m, (uint64_t)d.heads * N * attention_splits(max_tokens) * (hd + 2) * 8,
+                   m->attn_part)))
     return bad(rc);
   if (any_moe && (d.experts > 4096 || N * d.experts_used > 4096))
     return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or slots per chunk"));
@@ -628,6 +630,13 @@ int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_
   int rc = decode_steps(m, first, steps, out_ids);
   m->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   return rc;
+}
+
+int ihip_model_use_graphs(ihip_model* m, int on)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_use_graphs");
+  m->use_graphs = on != 0;
+  return 0;
 }
 
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms)

@@ -159,7 +159,7 @@ void ihip_destroy(ihip_ctx* c)
   }
   for (auto& w : c->weights) (void)hipFree((void*)w.dev);
   for (auto a : c->allocations) (void)hipFree((void*)a);
-  for (uint64_t b : {c->scratch_x, c->scratch_y, c->scratch_q, c->scratch_bad})
+  for (uint64_t b : {c->scratch_x, c->scratch_y, c->scratch_q, c->scratch_bad, c->scratch_attn})
     if (b) (void)hipFree((void*)b);
   for (auto ev : c->events)
     if (ev) (void)hipEventDestroy(ev);

@@ -285,8 +285,9 @@ struct AttnArgs {
   float* y;
   const float* sinks;
   const int* pastp;  // device position of row 0 (graph replay), or null: past
+  double* part;      // [heads, rows, splits, hd + 2] partial sums, maxima, sums
   double scale;
-  int32_t rows, heads, kvh, hd, past, window, f16, maxkeys;
+  int32_t rows, heads, kvh, hd, past, window, f16, splits;
 };
 
 __device__ __forceinline__ double cache_at(const void* c, int64_t i, int f16)
@@ -294,74 +295,148 @@ __device__ __forceinline__ double cache_at(const void* c, int64_t i, int f16)
   return f16 ? (double)half_to_float(((const uint16_t*)c)[i]) : (double)((const float*)c)[i];
 }
 
-// the reference rows of CausalRows (backend.cpu.pas:1305-1354): each score a
-// sequential double dot product (the CPU's bits), the maximum and the sink
-// taken out, exp in double, the weighted values summed in double, divided at
-// the end. One block of 256 per (head, row); the scores of the keys live in
-// LDS (maxkeys doubles, checked by the host).
-extern "C" __global__ __launch_bounds__(256) void attention(AttnArgs a)
+// the keys of one (head, row) cut into `splits` ranges (flash-decoding): each
+// block of 256 scores its range - every score the CPU's sequential double dot
+// product (CausalRows, backend.cpu.pas:1305-1354) - then sums
+// exp(score - range max) and the weighted values in double, and writes them
+// with the range's maximum and sum to part; attention_merge adds the ranges
+// (and the sink) as the CPU adds one softmax. A range of at most 256 keys
+// (splits >= keys / 256, set by the host).
+extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
 {
-  extern __shared__ double sc[];
+  __shared__ double qd[256];
+  __shared__ double sc[256];
   __shared__ double red[8];
-  __shared__ double part[256];
-  int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-  int d = a.hd;
-  int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
-  int g = h / (a.heads / a.kvh);
+  __shared__ double acc4[4][256];
+  const int h = blockIdx.x, r = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
+  const int d = a.hd;
+  const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
+  const int g = h / (a.heads / a.kvh);
   const int past = a.pastp ? *a.pastp : a.past;
-  int total = past + r + 1, first = 0;
-  if (a.window > 0 && total > a.window) first = total - a.window;
-  int cnt = total - first;
+  const int total = past + r + 1;
+  const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
+  const int cnt = total - first;
+  const int chunk = (cnt + a.splits - 1) / a.splits;
+  const int j0 = min(cnt, s * chunk), j1 = min(cnt, j0 + chunk);
+  const int n = j1 - j0;
+  double* out = a.part + (((int64_t)h * a.rows + r) * a.splits + s) * (d + 2);
+  if (n <= 0) {  // an empty range: weight 0 in the merge
+    if (t == 0) {
+      out[d] = -1.0e308;
+      out[d + 1] = 0.0;
+    }
+    return;
+  }
   const float* q = a.q + (int64_t)r * qw + (int64_t)h * d;
-  double mloc = -1.0e308;
-  for (int j = t; j < cnt; j += blockDim.x) {
-    int64_t kb = (int64_t)(first + j) * kvw + (int64_t)g * d;
+  for (int i = t; i < d; i += 256) qd[i] = (double)q[i];
+  __syncthreads();
+  double m = -1.0e308;
+  if (t < n) {
+    // the CPU's sequential double dot product, the key read 8 x 16 bytes at
+    // a time so the loads of a row are in flight together
+    const int64_t kb = (int64_t)(first + j0 + t) * kvw + (int64_t)g * d;
     double acc = 0;
-    for (int i = 0; i < d; i++) acc = acc + (double)q[i] * cache_at(a.kc, kb + i, a.f16);
+    if (a.f16) {
+      const uint4* p = (const uint4*)((const uint16_t*)a.kc + kb);
+      for (int k0 = 0; k0 < d / 8; k0 += 8) {
+        uint4 u[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          if (k0 + k < d / 8) u[k] = p[k0 + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          if (k0 + k < d / 8) {
+            uint32_t wv[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              int i = 8 * (k0 + k) + 2 * j;
+              acc = acc + qd[i] * (double)half_to_float(wv[j] & 0xffffu);
+              acc = acc + qd[i + 1] * (double)half_to_float(wv[j] >> 16);
+            }
+          }
+      }
+    } else {
+      const float4* p = (const float4*)((const float*)a.kc + kb);
+      for (int k0 = 0; k0 < d / 4; k0 += 8) {
+        float4 u[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          if (k0 + k < d / 4) u[k] = p[k0 + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          if (k0 + k < d / 4) {
+            int i = 4 * (k0 + k);
+            acc = acc + qd[i] * (double)u[k].x;
+            acc = acc + qd[i + 1] * (double)u[k].y;
+            acc = acc + qd[i + 2] * (double)u[k].z;
+            acc = acc + qd[i + 3] * (double)u[k].w;
+          }
+      }
+    }
     acc = acc * a.scale;
-    sc[j] = acc;
-    if (acc > mloc) mloc = acc;
+    sc[t] = acc;
+    m = acc;
   }
-  // the maximum of the block
   for (int o = 1; o < 64; o <<= 1) {
-    double ov = __shfl_xor(mloc, o);
-    if (ov > mloc) mloc = ov;
+    double ov = __shfl_xor(m, o);
+    if (ov > m) m = ov;
   }
-  if ((t & 63) == 0) red[t >> 6] = mloc;
+  if ((t & 63) == 0) red[t >> 6] = m;
   __syncthreads();
-  double m = red[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); i++)
-    if (red[i] > m) m = red[i];
-  if (a.sinks && (double)a.sinks[h] > m) m = a.sinks[h];
-  double s = 0;
-  for (int j = t; j < cnt; j += blockDim.x) {
-    double e = exp(sc[j] - m);
-    sc[j] = e;
-    s = s + e;
+  m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+  double e = 0;
+  if (t < n) {
+    e = exp(sc[t] - m);
+    sc[t] = e;
   }
+  e = wave_sum(e, 64);
   __syncthreads();
-  s = wave_sum(s, 64);
-  if ((t & 63) == 0) red[4 + (t >> 6)] = s;
-  __syncthreads();
-  double sum = 0;
-  for (int i = 0; i < (int)(blockDim.x >> 6); i++) sum = sum + red[4 + i];
-  if (a.sinks) sum = sum + exp((double)a.sinks[h] - m);
-  // the weighted values: thread t sums dimension t % d over its key share
-  int nsplit = blockDim.x / d;  // hd 64: 4, hd 128: 2, hd 256: 1
-  int dim = t % d, sp = t / d;
-  double acc = 0;
-  if (sp < nsplit) {
-    int per = (cnt + nsplit - 1) / nsplit;
-    int j0 = sp * per, j1 = min(cnt, j0 + per);
-    for (int j = j0; j < j1; j++)
-      acc = acc + sc[j] * cache_at(a.vc, (int64_t)(first + j) * kvw + (int64_t)g * d + dim, a.f16);
+  if ((t & 63) == 0) red[4 + (t >> 6)] = e;
+  // the weighted values: wave w takes keys w, w + 4, ...; lane l dims l, l + 64..
+  const int w = t >> 6, l = t & 63;
+  double acc[4] = {0, 0, 0, 0};
+  const int64_t vb = (int64_t)(first + j0) * kvw + (int64_t)g * d;
+#pragma unroll 8
+  for (int j = w; j < n; j += 4) {
+    double p = sc[j];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (l + 64 * c < d) acc[c] = acc[c] + p * cache_at(a.vc, vb + (int64_t)j * kvw + l + 64 * c, a.f16);
   }
-  part[t] = acc;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+    if (l + 64 * c < d) acc4[w][l + 64 * c] = acc[c];
   __syncthreads();
-  if (t < d) {
-    double tot = part[t];
-    for (int i = 1; i < nsplit; i++) tot = tot + part[i * d + t];
-    a.y[(int64_t)r * qw + (int64_t)h * d + t] = (float)(tot * (1.0 / sum));
+  for (int i = t; i < d; i += 256) out[i] = (acc4[0][i] + acc4[1][i]) + (acc4[2][i] + acc4[3][i]);
+  if (t == 0) {
+    out[d] = m;
+    out[d + 1] = (red[4] + red[5]) + (red[6] + red[7]);
+  }
+}
+
+// y = sum_s exp(m_s - M) acc_s / (sum_s exp(m_s - M) l_s + exp(sink - M)),
+// M the largest range maximum (and the sink); one block per (head, row)
+extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
+{
+  const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+  const int d = a.hd;
+  const double* b = a.part + ((int64_t)h * a.rows + r) * a.splits * (d + 2);
+  double M = -1.0e308;
+  for (int s = 0; s < a.splits; s++) M = fmax(M, b[s * (d + 2) + d]);
+  if (a.sinks && (double)a.sinks[h] > M) M = a.sinks[h];
+  double den = 0;
+  for (int s = 0; s < a.splits; s++) {
+    double ms = b[s * (d + 2) + d];
+    if (ms > -1.0e308) den = den + exp(ms - M) * b[s * (d + 2) + d + 1];
+  }
+  if (a.sinks) den = den + exp((double)a.sinks[h] - M);
+  for (int i = t; i < d; i += blockDim.x) {
+    double acc = 0;
+    for (int s = 0; s < a.splits; s++) {
+      double ms = b[s * (d + 2) + d];
+      if (ms > -1.0e308) acc = acc + exp(ms - M) * b[s * (d + 2) + i];
+    }
+    a.y[(int64_t)r * a.heads * d + (int64_t)h * d + i] = (float)(acc * (1.0 / den));
   }
 }
 
@@ -374,49 +449,67 @@ struct RouteArgs {
 };
 
 // TDecoderModel.Route (decoder.pas:2901-2949) = route of ops.cu:664-720:
-// softmax in double, the k highest logits (lower id on a tie), weights
-// rounded to single, renormed, then sorted by id; one thread per row
+// softmax in double, the k highest logits (the lower id on a tie), weights
+// rounded to single, renormed, then sorted by id. One wave per row: the lanes
+// hold the logits, each pick a wave-wide argmax
 extern "C" __global__ __launch_bounds__(64) void route(RouteArgs a)
 {
-  int row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= a.rows) return;
-  const float* lg = a.logits + (int64_t)row * a.experts;
-  uint32_t taken[128];
-  int chosen[64];
-  float wt[64];
-  for (int i = 0; i < 128; i++) taken[i] = 0;
-  double m = lg[0];
-  for (int i = 1; i < a.experts; i++)
-    if (lg[i] > m) m = lg[i];
+  __shared__ int chosen[64];
+  __shared__ float wt[64];
+  const int row = blockIdx.x, l = threadIdx.x, E = a.experts;
+  const float* lg = a.logits + (int64_t)row * E;
+  float mx = -INFINITY;
+  for (int i = l; i < E; i += 64) mx = fmaxf(mx, lg[i]);
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const double m = mx;
   double sum = 0;
-  for (int i = 0; i < a.experts; i++) sum = sum + exp((double)lg[i] - m);
-  double picked = 0;
+  for (int i = l; i < E; i += 64) sum = sum + exp((double)lg[i] - m);
+  sum = wave_sum(sum, 64);
+  uint64_t taken = 0;  // bit (i / 64) of this lane's experts i = l + 64 * bit
   for (int j = 0; j < a.k; j++) {
-    int best = -1;
-    for (int i = 0; i < a.experts; i++)
-      if (((taken[i >> 5] >> (i & 31)) & 1u) == 0u && (best < 0 || lg[i] > lg[best])) best = i;
-    taken[best >> 5] |= 1u << (best & 31);
-    chosen[j] = best;
-    wt[j] = (float)(exp((double)lg[best] - m) / sum);
-    picked = picked + (double)wt[j];
-  }
-  if (a.norm)
-    for (int j = 0; j < a.k; j++) wt[j] = (float)((double)wt[j] / picked);
-  for (int j = 1; j < a.k; j++) {
-    int id = chosen[j];
-    float v = wt[j];
-    int p = j;
-    while (p > 0 && chosen[p - 1] > id) {
-      chosen[p] = chosen[p - 1];
-      wt[p] = wt[p - 1];
-      p--;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = l, b = 0; i < E; i += 64, b++)
+      if (!((taken >> b) & 1) && (bi == 0x7fffffff || lg[i] > bv)) {
+        bv = lg[i];
+        bi = i;
+      }
+    for (int o = 1; o < 64; o <<= 1) {
+      float ov = __shfl_xor(bv, o);
+      int oi = __shfl_xor(bi, o);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+      }
     }
-    chosen[p] = id;
-    wt[p] = v;
+    if ((bi & 63) == l) taken |= 1ull << (bi >> 6);
+    if (l == 0) {
+      chosen[j] = bi;
+      wt[j] = (float)(exp((double)bv - m) / sum);
+    }
   }
-  for (int j = 0; j < a.k; j++) {
-    a.ids[(int64_t)row * a.k + j] = chosen[j];
-    a.w[(int64_t)row * a.k + j] = wt[j];
+  __syncthreads();
+  if (l == 0) {
+    double picked = 0;
+    for (int j = 0; j < a.k; j++) picked = picked + (double)wt[j];
+    if (a.norm)
+      for (int j = 0; j < a.k; j++) wt[j] = (float)((double)wt[j] / picked);
+    for (int j = 1; j < a.k; j++) {
+      int id = chosen[j];
+      float v = wt[j];
+      int p = j;
+      while (p > 0 && chosen[p - 1] > id) {
+        chosen[p] = chosen[p - 1];
+        wt[p] = wt[p - 1];
+        p--;
+      }
+      chosen[p] = id;
+      wt[p] = v;
+    }
+    for (int j = 0; j < a.k; j++) {
+      a.ids[(int64_t)row * a.k + j] = chosen[j];
+      a.w[(int64_t)row * a.k + j] = wt[j];
+    }
   }
 }
 
