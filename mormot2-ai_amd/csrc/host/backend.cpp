@@ -313,7 +313,10 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   const int mode = k.mode & 1;
   const bool q8 = mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
   if (q8 && (k.mode & IHIP_MODE_XQ)) xq = k.x;  // x is already quantized
-  if (q8 && !xq) {
+  const bool batch = k.items || (!k.ids && k.rows > 1);
+  // one activation row per block (decode, experts of a token): the GEMV
+  // quantizes its own groups in registers, no separate launch
+  if (q8 && !xq && batch) {
     int64_t xrows = (k.ids || k.items)
                         ? (k.x_per_slot ? (k.rows + k.x_per_slot - 1) / k.x_per_slot : 1)
                         : k.rows;
@@ -336,10 +339,15 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     int32_t nexp;
     const void* items;
     const int* perm;
+    const uint8_t* w2;
+    const float* bias2;
+    float alpha, limit;
+    int* bad;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
-         (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm};
-  const bool batch = k.items || (!k.ids && k.rows > 1);
+         (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
+         (const uint8_t*)k.w2, (const float*)k.bias2, k.alpha, k.limit, (int*)c->scratch_bad};
+  if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   char name[64];
   snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
            mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : "", U);
@@ -544,13 +552,17 @@ struct NormArgs {
   float* y;
   double eps;
   int32_t rows, cols;
+  const float* cd;
+  const float* cw;
+  int32_t k, pad;
 };
 
 int ihip_enqueue_rmsnorm(ihip_ctx* c, uint64_t x, uint64_t w, uint64_t y, int64_t rows,
                          int64_t cols, double eps)
 {
   if (!c || rows < 1 || cols < 1) return fail(IHIP_E_ARG, "ihip_enqueue_rmsnorm");
-  NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols};
+  NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols,
+                nullptr, nullptr, 0, 0};
   return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
 }
 
@@ -559,7 +571,7 @@ int ihip_enqueue_addnorm(ihip_ctx* c, uint64_t x, uint64_t t, uint64_t w, uint64
 {
   if (!c || rows < 1 || cols < 1 || !t) return fail(IHIP_E_ARG, "ihip_enqueue_addnorm");
   NormArgs a = {(float*)x, (const float*)t, (const float*)w, (float*)y, eps, (int32_t)rows,
-                (int32_t)cols};
+                (int32_t)cols, nullptr, nullptr, 0, 0};
   return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
 }
 
@@ -569,6 +581,22 @@ struct EltArgs {
   int64_t n;
   float alpha, limit;
 };
+
+}  // extern "C"
+
+namespace ihip {
+
+int enqueue_addnorm_moe(ihip_ctx* c, uint64_t x, uint64_t cd, uint64_t cw, int64_t k, uint64_t w,
+                        uint64_t y, int64_t rows, int64_t cols, double eps)
+{
+  NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols,
+                (const float*)cd, (const float*)cw, (int32_t)k, 0};
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+}
+
+}  // namespace ihip
+
+extern "C" {
 
 int ihip_enqueue_add(ihip_ctx* c, uint64_t x, uint64_t t, int64_t n)
 {
@@ -678,7 +706,7 @@ extern "C" int ihip_enqueue_stream_read(ihip_ctx* c, uint64_t p, uint64_t bytes,
 
 namespace ihip {
 
-int attention_splits(int64_t maxkeys) { return (int)std::max<int64_t>(1, (maxkeys + 255) / 256); }
+int attention_splits(int64_t maxkeys) { return (int)std::max<int64_t>(1, (maxkeys + 127) / 128); }
 
 int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
                       int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
@@ -699,7 +727,8 @@ int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_
   } a = {(const float*)q, (const void*)kc, (const void*)vc, (float*)y, (const float*)sinks,
          (const int*)pastp, (double*)part, scale, (int32_t)rows, (int32_t)heads, (int32_t)kvh,
          (int32_t)hd, (int32_t)past, (int32_t)window, f16, splits};
-  int rc = launch(c, "attention_part", dim3((unsigned)heads, (unsigned)rows, (unsigned)splits),
+  int rc = launch(c, f16 ? "attention_part_f16" : "attention_part_f32",
+                  dim3((unsigned)heads, (unsigned)rows, (unsigned)splits),
                   dim3(256), &a);
   if (rc) return rc;
   return launch(c, "attention_merge", dim3((unsigned)heads, (unsigned)rows), dim3(128), &a);

@@ -95,16 +95,22 @@ struct LinearCall {
   uint64_t items = 0;  // grouped experts: int4 work items (expert, start, count)
   uint64_t perm = 0;   // and the slots sorted by expert; rows = slots
   int64_t nitems = 0;
+  // fused SwiGLU: y = swiglu(x W^T + bias, x W2^T + bias2) (one row per block)
+  uint64_t w2 = 0, bias2 = 0;
+  float alpha = 1.0f, limit = 0.0f;
 };
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // which activation quantizer a weight type needs in Q8 mode: -1 none (float
 // weights), 0 Q8_0, 1 Q8_K
 int q8_kind(int dtype);
 int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind, uint64_t xq);
-// flash-decoding attention: ranges of at most 256 keys per block, then a merge;
+// flash-decoding attention: ranges of at most 128 keys per block, then a merge;
 // part holds heads * rows * splits * (hd + 2) doubles; pastp: the position
 // of row 0 in device memory (graph replay), or 0: past
 int attention_splits(int64_t maxkeys);
+// x += the k expert rows cd weighted by cw in slot order, then y = rmsnorm(x)
+int enqueue_addnorm_moe(ihip_ctx* c, uint64_t x, uint64_t cd, uint64_t cw, int64_t k, uint64_t w,
+                        uint64_t y, int64_t rows, int64_t cols, double eps);
 int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
                       int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                       uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,

@@ -247,36 +247,53 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
   const ihip_model_desc& d = m->d;
   const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
                 kvw = (int64_t)d.kv_heads * hd;
+  // one row (decode): every GEMV quantizes its activation row in registers;
+  // a chunk: the rows are quantized once per activation buffer
+  const bool one = n == 1;
   int rc = ihip_enqueue_rmsnorm(m->c, m->x, m->L[0].input_norm, m->h, n, H, d.rms_eps);
   if (rc) return rc;
   for (int l = 0; l < d.layers; l++) {
     const DevLayer& L = m->L[l];
     QCache qh{m->xq0, m->xqk};
+    QCache* qhp = one ? nullptr : &qh;
     // attention block (decoder.pas:2625-2702)
-    if ((rc = lin(m, m->h, &qh, n, H, L.qd, L.q, qw, L.qb, m->q))) return rc;
-    if ((rc = lin(m, m->h, &qh, n, H, L.kd, L.k, kvw, L.kb, m->k))) return rc;
-    if ((rc = lin(m, m->h, &qh, n, H, L.vd, L.v, kvw, L.vb, m->v))) return rc;
+    if ((rc = lin(m, m->h, qhp, n, H, L.qd, L.q, qw, L.qb, m->q))) return rc;
+    if ((rc = lin(m, m->h, qhp, n, H, L.kd, L.k, kvw, L.kb, m->k))) return rc;
+    if ((rc = lin(m, m->h, qhp, n, H, L.vd, L.v, kvw, L.vb, m->v))) return rc;
     if ((rc = rope_attn(m, L, n, past, graph))) return rc;
     QCache qa{m->xq0, m->xqk};
-    if ((rc = lin(m, m->attn, &qa, n, qw, L.od, L.o, H, L.ob, m->tmp))) return rc;
+    if ((rc = lin(m, m->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, m->tmp))) return rc;
     // residual, then the pre-FFN norm
     if ((rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, L.post_norm, m->h, n, H, d.rms_eps)))
       return rc;
     QCache qf{m->xq0, m->xqk};
+    QCache* qfp = one ? nullptr : &qf;
+    bool moe_out = false;  // the FFN output is the expert rows (added by the next norm)
     if (!L.moe) {
       // DenseFfn (decoder.pas:2866-2878)
       const int64_t F = d.ffn;
-      if ((rc = lin(m, m->h, &qf, n, H, L.gd, L.gate, F, 0, m->gate))) return rc;
-      if ((rc = lin(m, m->h, &qf, n, H, L.ud, L.up, F, 0, m->up))) return rc;
-      if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * F, d.swiglu_alpha, d.swiglu_limit)))
-        return rc;
+      if (one) {
+        // gate, up and SwiGLU in one pass
+        LinearCall k;
+        k.x = m->h; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
+        k.y = m->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
+        k.limit = d.swiglu_limit;
+        if (L.gd != L.ud) return fail(IHIP_E_ARG, "model: gate and up of one type");
+        if ((rc = enqueue_linear(m->c, k))) return rc;
+      } else {
+        if ((rc = lin(m, m->h, qfp, n, H, L.gd, L.gate, F, 0, m->gate))) return rc;
+        if ((rc = lin(m, m->h, qfp, n, H, L.ud, L.up, F, 0, m->up))) return rc;
+        if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * F, d.swiglu_alpha,
+                                      d.swiglu_limit)))
+          return rc;
+      }
       QCache qg{m->xqf, m->xqf};
-      if ((rc = lin(m, m->gate, &qg, n, F, L.dd, L.down, H, 0, m->tmp))) return rc;
+      if ((rc = lin(m, m->gate, one ? nullptr : &qg, n, F, L.dd, L.down, H, 0, m->tmp))) return rc;
     } else {
       // MoeBlock (decoder.pas:3037-3053) with the experts chosen on the
       // device (model.qwen3.cuda.pas:1152-1205)
       const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
-      if ((rc = lin(m, m->h, &qf, n, H, L.rd, L.router, E, L.router_b, m->route))) return rc;
+      if ((rc = lin(m, m->h, qfp, n, H, L.rd, L.router, E, L.router_b, m->route))) return rc;
       struct {
         const float* logits;
         int* ids;
@@ -285,7 +302,21 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
       } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n};
       if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(64), &ra))) return rc;
-      if (n > 1) {
+      if (one) {
+        // the token's K experts: gate, up and SwiGLU in one pass per slot,
+        // then down per slot; the weighted sum goes into the next norm
+        LinearCall k;
+        k.x = m->h; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
+        k.y = m->gate; k.mode = m->mode; k.ids = m->ids; k.stride = L.eg_stride; k.x_per_slot = 0;
+        k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
+        k.limit = d.swiglu_limit;
+        if ((rc = enqueue_linear(m->c, k))) return rc;
+        LinearCall dn;
+        dn.x = m->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
+        dn.y = m->eout; dn.mode = m->mode; dn.ids = m->ids; dn.stride = L.ed_stride;
+        dn.x_per_slot = 1; dn.nexp = (int)E; dn.bias = L.edb;
+        if ((rc = enqueue_linear(m->c, dn))) return rc;
+      } else {
         struct {
           const int* ids;
           int* perm;
@@ -294,47 +325,42 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
         } pa = {(const int*)m->ids, (int*)m->perm, (void*)m->items, (int32_t)(n * K), (int32_t)E,
                 (int32_t)((n * K + 7) / 8 + E), 0};
         if ((rc = launch(m->c, "moe_plan", dim3(1), dim3(256), &pa))) return rc;
-      }
-      // gate and up: slot s = row s / K, expert ids[s]
-      bool q0 = false;
-      if (m->mode == IHIP_MODE_Q8 && q8_kind(L.egd) >= 0) {
-        bool& hv = q8_kind(L.egd) ? qf.havek : qf.have0;
-        uint64_t buf = q8_kind(L.egd) ? qf.bufk : qf.buf0;
-        if (!hv) {
-          if ((rc = enqueue_quantize(m->c, m->h, n, H, q8_kind(L.egd), buf))) return rc;
-          hv = true;
+        // gate and up: slot s = row s / K, expert ids[s], grouped by expert
+        bool q0 = false;
+        if (m->mode == IHIP_MODE_Q8 && q8_kind(L.egd) >= 0) {
+          bool& hv = q8_kind(L.egd) ? qf.havek : qf.have0;
+          uint64_t buf = q8_kind(L.egd) ? qf.bufk : qf.buf0;
+          if (!hv) {
+            if ((rc = enqueue_quantize(m->c, m->h, n, H, q8_kind(L.egd), buf))) return rc;
+            hv = true;
+          }
+          q0 = true;
         }
-        q0 = true;
+        uint64_t xqg = q8_kind(L.egd) == 1 ? qf.bufk : qf.buf0;
+        if ((rc = lin_ids(m, m->h, xqg, n, H, L.egd, L.eg, L.eg_stride, FI, m->ids, n * K, (int)K,
+                          L.egb, m->gate, q0)))
+          return rc;
+        bool qu = q0 && q8_kind(L.eud) == q8_kind(L.egd);
+        uint64_t xqu = q8_kind(L.eud) == 1 ? qf.bufk : qf.buf0;
+        if ((rc = lin_ids(m, m->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, m->ids, n * K, (int)K,
+                          L.eub, m->up, qu)))
+          return rc;
+        if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * K * FI, d.swiglu_alpha,
+                                      d.swiglu_limit)))
+          return rc;
+        if ((rc = lin_ids(m, m->gate, m->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, m->ids,
+                          n * K, 1, L.edb, m->eout, false)))
+          return rc;
       }
-      uint64_t xqg = q8_kind(L.egd) == 1 ? qf.bufk : qf.buf0;
-      if ((rc = lin_ids(m, m->h, xqg, n, H, L.egd, L.eg, L.eg_stride, FI, m->ids, n * K, (int)K,
-                        L.egb, m->gate, q0)))
-        return rc;
-      bool qu = q0 && q8_kind(L.eud) == q8_kind(L.egd);
-      uint64_t xqu = q8_kind(L.eud) == 1 ? qf.bufk : qf.buf0;
-      if ((rc = lin_ids(m, m->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, m->ids, n * K, (int)K,
-                        L.eub, m->up, qu)))
-        return rc;
-      if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * K * FI, d.swiglu_alpha,
-                                    d.swiglu_limit)))
-        return rc;
-      if ((rc = lin_ids(m, m->gate, m->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, m->ids, n * K,
-                        1, L.edb, m->eout, false)))
-        return rc;
-      struct {
-        const float* d;
-        const float* w;
-        float* y;
-        int32_t k, n, rows, pad;
-      } ca = {(const float*)m->eout, (const float*)m->rw, (float*)m->tmp, (int32_t)K, (int32_t)H,
-              (int32_t)n, 0};
-      if ((rc = launch(m->c, "moecombine", dim3((unsigned)((H + 255) / 256), (unsigned)n),
-                       dim3(256), &ca)))
-        return rc;
+      moe_out = true;
     }
     // residual, then the next layer's input norm (or the final norm)
     uint64_t nw = l + 1 < d.layers ? m->L[l + 1].input_norm : m->final_norm;
-    if ((rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, nw, m->h, n, H, d.rms_eps))) return rc;
+    if (moe_out)
+      rc = enqueue_addnorm_moe(m->c, m->x, m->eout, m->rw, d.experts_used, nw, m->h, n, H, d.rms_eps);
+    else
+      rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, nw, m->h, n, H, d.rms_eps);
+    if (rc) return rc;
   }
   return 0;
 }
@@ -344,8 +370,8 @@ static int head(ihip_model* m, int64_t n, bool all, uint64_t y)
   const ihip_model_desc& d = m->d;
   QCache qh{m->xq0, m->xqk};
   if (all) return lin(m, m->h, &qh, n, d.hidden, m->head_dt, m->head, d.vocab, 0, y);
-  return lin(m, m->h + (uint64_t)(n - 1) * d.hidden * 4, &qh, 1, d.hidden, m->head_dt, m->head,
-             d.vocab, 0, y);
+  return lin(m, m->h + (uint64_t)(n - 1) * d.hidden * 4, nullptr, 1, d.hidden, m->head_dt,
+             m->head, d.vocab, 0, y);
 }
 
 // one chunk: ids and cos/sin uploaded, embeddings, layers, head

@@ -75,6 +75,27 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
   }
 }
 
+// TInferCpuBackend.SwiGlu (backend.cpu.pas:1797-1834) of one value pair:
+// silu(g) * u, or with limit > 0 the clamped gpt-oss form; every step
+// rounded to single, the exponential in double
+__device__ __forceinline__ float swiglu_value(float g, float u, float alpha, float limit)
+{
+  if (limit > 0) {
+    if (g > limit) g = limit;
+    if (u > limit) u = limit;
+    else if (u < -limit) u = -limit;
+    float b = g * alpha;
+    double d = b;
+    b = (float)(1.0 / (1.0 + exp(-d)));
+    b = g * b;
+    u = u + 1.0f;
+    return u * b;
+  }
+  double d = g;
+  float b = (float)(d / (1.0 + exp(-d)));
+  return b * u;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v, int width)
 {

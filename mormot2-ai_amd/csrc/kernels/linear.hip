@@ -43,6 +43,12 @@ struct LinArgs {
   // s / x_per_slot and writes y row s
   const int4* items;
   const int* perm;
+  // fused SwiGLU: w2 the up projection (same layout, stride and experts as
+  // w), bias2 its bias; y = swiglu(x W^T + bias, x W2^T + bias2)
+  const uint8_t* w2;
+  const float* bias2;
+  float alpha, limit;
+  int* bad;  // set to 1 + row when an activation quantized here is not finite
 };
 
 // ---------------------------------------------------------------- formats
@@ -382,6 +388,112 @@ __device__ __forceinline__ double row_total(int lpr, const Raw& hdr, float dxsb,
   }
 }
 
+// the value of row o against the lane's activation groups: the lanes of the
+// row meet in row_total (lane 0 of the row segment holds it)
+template <int F, int MODE, int U>
+__device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&raw)[U], int64_t o,
+                                            bool valid, const XGroup (&xg)[U], int lr, int lpr,
+                                            int G, int64_t in)
+{
+  float accf = 0.f;
+  double accd = 0.0, tot = 0.0;
+#pragma unroll
+  for (int k = 0; k < U; k++) {
+    int g = lr + k * lpr;
+    int isum = 0, msum = 0;
+    if (valid && g < G) group_term<F, MODE>(w, raw[k], o, g, in, xg[k], accf, accd, isum, msum);
+    if constexpr (MODE == 1 && is_k_quant(F)) {
+      // every k-th group set of the lanes forms whole super-blocks
+      bool lead = (g & 7) == 0 && valid && g < G;
+      tot += row_total<F, MODE>(lpr, raw[k], xg[k].dx, lead, 0.f, 0.0, isum, msum, g);
+    }
+  }
+  if constexpr (MODE == 1 && is_k_quant(F)) return tot;
+  return row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
+}
+
+// Q8 activations of group g formed in registers: Q8_0 per group (one lane,
+// InferQuantizeRowQ8_0), Q8_K per super-block (the 8 lanes of the block
+// meet to find the first value of the largest magnitude, InferQuantizeRowQ8_K);
+// every lane takes part, those past the row with zeros
+template <int F>
+__device__ __forceinline__ void quantize_x(const LinArgs& a, int64_t xrow, int g, int G, XGroup& x)
+{
+  float v[32];
+  const bool has = g < G;
+  if (has) {
+    const float4* p = (const float4*)(a.x + xrow * a.in + (int64_t)g * 32);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      float4 t = p[k];
+      v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 32; k++) v[k] = 0.f;
+  }
+  bool nonfinite = false;
+  float amax = 0.f, m = 0.f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
+    float f = fabsf(v[j]);
+    if (f > amax) {
+      amax = f;
+      m = v[j];
+      idx = j;
+    }
+  }
+  if (nonfinite && a.bad) a.bad[0] = 1 + (int)xrow;
+  uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float dx = 0.f;
+  if constexpr (!is_k_quant(F)) {
+    float d = amax / 127.0f;
+    if (!(d < 2.9387359e-39f)) {
+      float id = 1.0f / d;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        int c = (int)__builtin_rintf(v[j] * id);
+        q[j >> 2] |= ((uint32_t)c & 255u) << (8 * (j & 3));
+      }
+    }
+    dx = half_to_float(float_to_half(d));
+  } else {
+    idx += 32 * g;
+    for (int o = 1; o < 8; o <<= 1) {
+      float oa = __shfl_xor(amax, o), om = __shfl_xor(m, o);
+      int oi = __shfl_xor(idx, o);
+      if (oa > amax || (oa == amax && oi < idx)) {
+        amax = oa;
+        m = om;
+        idx = oi;
+      }
+    }
+    if (!(amax < 3.7320437e-37f)) {
+      float iscale = -127.0f / m;
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        int c = (int)__builtin_rintf(iscale * v[j]);
+        if (c > 127) c = 127;
+        q[j >> 2] |= ((uint32_t)c & 255u) << (8 * (j & 3));
+      }
+      dx = 1.0f / iscale;
+    }
+  }
+  int sl = 0, sh = 0;
+#pragma unroll
+  for (int k = 0; k < 8; k++) x.w[k] = (int)q[k];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    sl = sdot4(x.w[k], 0x01010101, sl);
+    sh = sdot4(x.w[4 + k], 0x01010101, sh);
+  }
+  x.sl = sl;
+  x.sh = sh;
+  x.dx = dx;
+}
+
 // ------------------------------------------------------------------ kernel
 // R = 1: one activation row, kept in registers. R = 8: up to 8 rows per
 // blockIdx.y chunk, activations read per group (from L1/L2).
@@ -399,9 +511,11 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   int64_t xrow0, yrow0;
   int nrows;
   int pstart = -1;  // grouped: the first entry of perm
+  int64_t expert = 0;
   if (a.items) {
     const int4 it = a.items[blockIdx.y];
     if (it.z <= 0) return;
+    expert = it.x;
     w += (int64_t)it.x * a.stride;
     if (bias) bias += (int64_t)it.x * a.out;
     pstart = it.y;
@@ -416,6 +530,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         a.y[(int64_t)slot * a.out + o] = 0.f;
       return;
     }
+    expert = e;
     w += (int64_t)e * a.stride;
     if (bias) bias += (int64_t)e * a.out;
     xrow0 = a.x_per_slot ? slot / a.x_per_slot : 0;
@@ -432,43 +547,45 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
+    // the activations of this lane's groups, quantized here when no
+    // quantized row was given (Q8 mode): the quantize kernels' arithmetic
     XGroup xg[U];
+    const bool inq = MODE == 1 && !is_float_type(F) && a.xq == nullptr;
 #pragma unroll
     for (int k = 0; k < U; k++) {
       int g = lr + k * lpr;
-      if (g < G) load_x<F, MODE>(a, xrow0, g, G, xg[k]);
+      if (inq) {
+        if constexpr (MODE == 1 && !is_float_type(F)) quantize_x<F>(a, xrow0, g, G, xg[k]);
+      } else if (g < G) {
+        load_x<F, MODE>(a, xrow0, g, G, xg[k]);
+      }
     }
+    // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
+    const bool glu = a.w2 != nullptr;
+    const uint8_t* w2 = glu ? a.w2 + (w - a.w) : nullptr;
+    const float* bias2 = a.bias2 ? a.bias2 + expert * a.out : nullptr;
     for (int64_t t = wid; t < tiles; t += nw) {
       int64_t o = t * rpw + rsub;
       bool valid = o < a.out;
-      Raw raw[U];
+      Raw raw[U], raw2[U];
 #pragma unroll
       for (int k = 0; k < U; k++) {
         int g = lr + k * lpr;
-        if (valid && g < G && !is_float_type(F)) load_group<F>(w, rg, o, G, g, a.in, raw[k]);
-      }
-      float accf = 0.f;
-      double accd = 0.0, tot = 0.0;
-#pragma unroll
-      for (int k = 0; k < U; k++) {
-        int g = lr + k * lpr;
-        int isum = 0, msum = 0;
-        if (valid && g < G)
-          group_term<F, MODE>(w, raw[k], o, g, a.in, xg[k], accf, accd, isum, msum);
-        if constexpr (MODE == 1 && is_k_quant(F)) {
-          // every k-th group set of the lanes forms whole super-blocks
-          bool lead = (g & 7) == 0 && valid && g < G;
-          tot += row_total<F, MODE>(lpr, raw[k], xg[k].dx, lead, 0.f, 0.0, isum, msum, g);
+        if (valid && g < G && !is_float_type(F)) {
+          load_group<F>(w, rg, o, G, g, a.in, raw[k]);
+          if (glu) load_group<F>(w2, rg, o, G, g, a.in, raw2[k]);
         }
       }
-      double v;
-      if constexpr (MODE == 1 && is_k_quant(F))
-        v = tot;
-      else
-        v = row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
+      double v = row_value<F, MODE, U>(w, raw, o, valid, xg, lr, lpr, G, a.in);
+      double v2 = glu ? row_value<F, MODE, U>(w2, raw2, o, valid, xg, lr, lpr, G, a.in) : 0.0;
       if (lr == 0 && valid) {
         if (bias) v = (double)bias[o] + v;
-        a.y[yrow0 * a.out + o] = (float)v;
+        float r = (float)v;
+        if (glu) {
+          if (bias2) v2 = (double)bias2[o] + v2;
+          r = swiglu_value(r, (float)v2, a.alpha, a.limit);
+        }
+        a.y[yrow0 * a.out + o] = r;
       }
     }
   } else {

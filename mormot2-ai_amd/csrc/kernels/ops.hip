@@ -140,11 +140,19 @@ struct NormArgs {
   float* y;
   double eps;
   int32_t rows, cols;
+  // the MoE output of the row as its k expert rows cd [rows * k, cols] and
+  // weights cw [rows * k], summed here in slot (= id) order (moecombine) and
+  // added like t; null: t as given
+  const float* cd;
+  const float* cw;
+  int32_t k, pad;
 };
 
 // TInferCpuBackend.RmsNorm (backend.cpu.pas:1769-1795): the sum of squares in
 // double, inv = 1 / sqrt(mean + eps) in double, x * inv rounded to single
-// before the weight; with t: x += t first (addnorm, ops.cu:135-150)
+// before the weight; with t: x += t first (addnorm, ops.cu:135-150); with
+// cd: x += the expert rows weighted in slot order, each step single-rounded
+// as TDecoderModel.Experts adds them (decoder.pas:3140-3148)
 extern "C" __global__ __launch_bounds__(256) void rmsnorm(NormArgs a)
 {
   __shared__ double sh[4];
@@ -152,7 +160,16 @@ extern "C" __global__ __launch_bounds__(256) void rmsnorm(NormArgs a)
   double s = 0;
   for (int c = threadIdx.x; c < a.cols; c += blockDim.x) {
     float v = a.x[base + c];
-    if (a.t) {
+    if (a.cd) {
+      float acc = 0.f;
+      for (int j = 0; j < a.k; j++) {
+        int64_t sl = (int64_t)blockIdx.x * a.k + j;
+        float p = a.cw[sl] * a.cd[sl * a.cols + c];
+        acc = acc + p;
+      }
+      v = v + acc;
+      a.x[base + c] = v;
+    } else if (a.t) {
       v = v + a.t[base + c];
       a.x[base + c] = v;
     }
@@ -295,19 +312,23 @@ __device__ __forceinline__ double cache_at(const void* c, int64_t i, int f16)
   return f16 ? (double)half_to_float(((const uint16_t*)c)[i]) : (double)((const float*)c)[i];
 }
 
-// the keys of one (head, row) cut into `splits` ranges (flash-decoding): each
-// block of 256 scores its range - every score the CPU's sequential double dot
-// product (CausalRows, backend.cpu.pas:1305-1354) - then sums
-// exp(score - range max) and the weighted values in double, and writes them
-// with the range's maximum and sum to part; attention_merge adds the ranges
-// (and the sink) as the CPU adds one softmax. A range of at most 256 keys
-// (splits >= keys / 256, set by the host).
-extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
+// the keys of one (head, row) cut into `splits` ranges of at most ATT_CHUNK
+// keys (flash-decoding): each block scores its range - every score the CPU's
+// sequential double dot product (CausalRows, backend.cpu.pas:1305-1354) -
+// then sums exp(score - range max) and the weighted values in double, and
+// writes them with the range's maximum and sum to part; attention_merge adds
+// the ranges (and the sink) as the CPU adds one softmax. Every load of a
+// range is issued before its first use: one thread per key reads the whole
+// key row at once, and each lane of the value pass holds a dimension pair of
+// all its keys, so a block waits for memory once per pass.
+#define ATT_CHUNK 128
+template <bool F16>
+__device__ __forceinline__ void attention_part_t(const AttnArgs& a)
 {
   __shared__ double qd[256];
-  __shared__ double sc[256];
+  __shared__ double sc[ATT_CHUNK];
   __shared__ double red[8];
-  __shared__ double acc4[4][256];
+  __shared__ double accs[4][256];
   const int h = blockIdx.x, r = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
   const int d = a.hd;
   const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
@@ -316,8 +337,7 @@ extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
   const int total = past + r + 1;
   const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
   const int cnt = total - first;
-  const int chunk = (cnt + a.splits - 1) / a.splits;
-  const int j0 = min(cnt, s * chunk), j1 = min(cnt, j0 + chunk);
+  const int j0 = min(cnt, s * ATT_CHUNK), j1 = min(cnt, j0 + ATT_CHUNK);
   const int n = j1 - j0;
   double* out = a.part + (((int64_t)h * a.rows + r) * a.splits + s) * (d + 2);
   if (n <= 0) {  // an empty range: weight 0 in the merge
@@ -331,20 +351,19 @@ extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
   for (int i = t; i < d; i += 256) qd[i] = (double)q[i];
   __syncthreads();
   double m = -1.0e308;
+  const int64_t base = (int64_t)(first + j0) * kvw + (int64_t)g * d;
   if (t < n) {
-    // the CPU's sequential double dot product, the key read 8 x 16 bytes at
-    // a time so the loads of a row are in flight together
-    const int64_t kb = (int64_t)(first + j0 + t) * kvw + (int64_t)g * d;
+    const int64_t kb = base + (int64_t)t * kvw;
     double acc = 0;
-    if (a.f16) {
+    if constexpr (F16) {
       const uint4* p = (const uint4*)((const uint16_t*)a.kc + kb);
-      for (int k0 = 0; k0 < d / 8; k0 += 8) {
-        uint4 u[8];
+      for (int k0 = 0; k0 < d / 8; k0 += 16) {
+        uint4 u[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < 16; k++)
           if (k0 + k < d / 8) u[k] = p[k0 + k];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < 16; k++)
           if (k0 + k < d / 8) {
             uint32_t wv[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
 #pragma unroll
@@ -357,13 +376,13 @@ extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
       }
     } else {
       const float4* p = (const float4*)((const float*)a.kc + kb);
-      for (int k0 = 0; k0 < d / 4; k0 += 8) {
-        float4 u[8];
+      for (int k0 = 0; k0 < d / 4; k0 += 16) {
+        float4 u[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < 16; k++)
           if (k0 + k < d / 4) u[k] = p[k0 + k];
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < 16; k++)
           if (k0 + k < d / 4) {
             int i = 4 * (k0 + k);
             acc = acc + qd[i] * (double)u[k].x;
@@ -392,26 +411,97 @@ extern "C" __global__ __launch_bounds__(256) void attention_part(AttnArgs a)
   e = wave_sum(e, 64);
   __syncthreads();
   if ((t & 63) == 0) red[4 + (t >> 6)] = e;
-  // the weighted values: wave w takes keys w, w + 4, ...; lane l dims l, l + 64..
+  // the weighted values: a key takes hd / 2 lanes, each a dimension pair;
+  // the 4 waves and the key slots of a wave split the range
+  const int lpk = d >> 1;                      // lanes per key (32 or 64 for hd 64/128)
+  const int kpw = lpk >= 64 ? 1 : 64 / lpk;    // keys side by side in a wave
   const int w = t >> 6, l = t & 63;
-  double acc[4] = {0, 0, 0, 0};
-  const int64_t vb = (int64_t)(first + j0) * kvw + (int64_t)g * d;
-#pragma unroll 8
-  for (int j = w; j < n; j += 4) {
-    double p = sc[j];
+  const int lane_key = lpk >= 64 ? 0 : l / lpk, pair = lpk >= 64 ? l : l % lpk;
+  const int step = 4 * kpw;
+  double a0[2] = {0, 0}, a1[2] = {0, 0};  // two dimension pairs (hd 256)
+  const int npair = d > 128 ? 2 : 1;
+  constexpr int VB = F16 ? 32 : 16;  // value loads in flight per lane
+  for (int jb = w * kpw + lane_key; jb < n; jb += VB * step) {
+    if constexpr (F16) {
+      uint32_t v[VB][2];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (l + 64 * c < d) acc[c] = acc[c] + p * cache_at(a.vc, vb + (int64_t)j * kvw + l + 64 * c, a.f16);
+      for (int u = 0; u < VB; u++) {
+        int j = jb + u * step;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+          v[u][c] = (j < n && c < npair)
+                        ? ((const uint32_t*)((const uint16_t*)a.vc + base + (int64_t)j * kvw))[pair + 64 * c]
+                        : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < VB; u++) {
+        int j = jb + u * step;
+        if (j < n) {
+          double p = sc[j];
+#pragma unroll
+          for (int c = 0; c < 2; c++)
+            if (c < npair) {
+              a0[c] = a0[c] + p * (double)half_to_float(v[u][c] & 0xffffu);
+              a1[c] = a1[c] + p * (double)half_to_float(v[u][c] >> 16);
+            }
+        }
+      }
+    } else {
+      float2 v[VB][2];
+#pragma unroll
+      for (int u = 0; u < VB; u++) {
+        int j = jb + u * step;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+          v[u][c] = (j < n && c < npair)
+                        ? ((const float2*)((const float*)a.vc + base + (int64_t)j * kvw))[pair + 64 * c]
+                        : make_float2(0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < VB; u++) {
+        int j = jb + u * step;
+        if (j < n) {
+          double p = sc[j];
+#pragma unroll
+          for (int c = 0; c < 2; c++)
+            if (c < npair) {
+              a0[c] = a0[c] + p * (double)v[u][c].x;
+              a1[c] = a1[c] + p * (double)v[u][c].y;
+            }
+        }
+      }
+    }
   }
+  // the key slots of a wave, then the waves
+  for (int o = lpk; o < 64; o <<= 1)
 #pragma unroll
-  for (int c = 0; c < 4; c++)
-    if (l + 64 * c < d) acc4[w][l + 64 * c] = acc[c];
+    for (int c = 0; c < 2; c++) {
+      a0[c] += __shfl_xor(a0[c], o);
+      a1[c] += __shfl_xor(a1[c], o);
+    }
+  if (lane_key == 0)
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+      if (c < npair) {
+        accs[w][2 * (pair + 64 * c)] = a0[c];
+        accs[w][2 * (pair + 64 * c) + 1] = a1[c];
+      }
   __syncthreads();
-  for (int i = t; i < d; i += 256) out[i] = (acc4[0][i] + acc4[1][i]) + (acc4[2][i] + acc4[3][i]);
+  for (int i = t; i < d; i += 256) out[i] = (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]);
   if (t == 0) {
     out[d] = m;
     out[d + 1] = (red[4] + red[5]) + (red[6] + red[7]);
   }
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_part_f16(AttnArgs a)
+{
+  attention_part_t<true>(a);
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_part_f32(AttnArgs a)
+{
+  attention_part_t<false>(a);
 }
 
 // y = sum_s exp(m_s - M) acc_s / (sum_s exp(m_s - M) l_s + exp(sink - M)),
