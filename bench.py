@@ -125,7 +125,8 @@ def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20):
 
 def expert_gemv(ctx, spec, reps=4):
     """The dominant decode kernel: 8 experts of the gate projection of every
-    MoE layer (Q4_K 768x2048 each), one launch per layer, timed with events."""
+    MoE layer (Q4_K 768x2048 each), one launch per layer, the 48 launches in
+    one graph timed with events (as the decode step replays them)."""
     import infer_hip as H
     L = H.lib()
     c = spec.cfg
@@ -146,19 +147,14 @@ def expert_gemv(ctx, spec, reps=4):
     ids = ctx.array(np.sort(rng.choice(E, K, replace=False)).astype(np.int32))
     dy = ctx.alloc(K * FI * 4)
     stride = FI * H.row_bytes(dtype, Hd)
-    for w, _ in devs:
-        H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K, 0,
-                                          dy.ptr, 0, H.MODE_Q8 | 2))
     ctx.sync()
-    ctx.record(2)
-    n = 0
-    for _ in range(reps):
+
+    def enq():
         for w, _ in devs:
             H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K,
                                               0, dy.ptr, 0, H.MODE_Q8 | 2))
-            n += 1
-    ctx.record(3)
-    ms = ctx.elapsed(2, 3) / n
+
+    ms = time_graph(ctx, enq, reps) / len(devs)
     nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + K * 4 + K * FI * 4
     for b in (dx, dq, ids, dy):
         b.free()

@@ -350,7 +350,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   char name[64];
   snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
-           mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : "", U);
+           mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
   int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
@@ -563,7 +563,7 @@ int ihip_enqueue_rmsnorm(ihip_ctx* c, uint64_t x, uint64_t w, uint64_t y, int64_
   if (!c || rows < 1 || cols < 1) return fail(IHIP_E_ARG, "ihip_enqueue_rmsnorm");
   NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols,
                 nullptr, nullptr, 0, 0};
-  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(1024), &a);
 }
 
 int ihip_enqueue_addnorm(ihip_ctx* c, uint64_t x, uint64_t t, uint64_t w, uint64_t y, int64_t rows,
@@ -572,7 +572,7 @@ int ihip_enqueue_addnorm(ihip_ctx* c, uint64_t x, uint64_t t, uint64_t w, uint64
   if (!c || rows < 1 || cols < 1 || !t) return fail(IHIP_E_ARG, "ihip_enqueue_addnorm");
   NormArgs a = {(float*)x, (const float*)t, (const float*)w, (float*)y, eps, (int32_t)rows,
                 (int32_t)cols, nullptr, nullptr, 0, 0};
-  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(1024), &a);
 }
 
 struct EltArgs {
@@ -591,7 +591,7 @@ int enqueue_addnorm_moe(ihip_ctx* c, uint64_t x, uint64_t cd, uint64_t cw, int64
 {
   NormArgs a = {(float*)x, nullptr, (const float*)w, (float*)y, eps, (int32_t)rows, (int32_t)cols,
                 (const float*)cd, (const float*)cw, (int32_t)k, 0};
-  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(256), &a);
+  return launch(c, "rmsnorm", dim3((unsigned)rows), dim3(1024), &a);
 }
 
 }  // namespace ihip
@@ -708,12 +708,16 @@ namespace ihip {
 
 int attention_splits(int64_t maxkeys) { return (int)std::max<int64_t>(1, (maxkeys + 127) / 128); }
 
+// the ranges attention_merge weighs in one block
+static const int MAX_SPLITS = 256;
+
 int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
                       int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                       uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,
                       int splits)
 {
   if (!(scale > 0)) scale = 1.0 / std::sqrt((double)hd);
+  if (splits > MAX_SPLITS) return fail(IHIP_E_UNSUPPORTED, "attention: more than 32768 keys per row");
   struct {
     const float* q;
     const void* kc;

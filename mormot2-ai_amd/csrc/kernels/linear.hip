@@ -497,7 +497,7 @@ __device__ __forceinline__ void quantize_x(const LinArgs& a, int64_t xrow, int g
 // ------------------------------------------------------------------ kernel
 // R = 1: one activation row, kept in registers. R = 8: up to 8 rows per
 // blockIdx.y chunk, activations read per group (from L1/L2).
-template <int F, int MODE, int U, int R>
+template <int F, int MODE, int U, int R, bool GLU>
 __device__ __forceinline__ void gemv(const LinArgs& a)
 {
   const int lane = threadIdx.x & 63;
@@ -547,45 +547,63 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
-    // the activations of this lane's groups, quantized here when no
-    // quantized row was given (Q8 mode): the quantize kernels' arithmetic
-    XGroup xg[U];
+    // T tiles per wave step, their weight loads issued together (and the
+    // first ones before the activation row is read), so a wave keeps several
+    // 16-byte loads per lane in flight
+    constexpr int T = GLU ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
     const bool inq = MODE == 1 && !is_float_type(F) && a.xq == nullptr;
-#pragma unroll
-    for (int k = 0; k < U; k++) {
-      int g = lr + k * lpr;
-      if (inq) {
-        if constexpr (MODE == 1 && !is_float_type(F)) quantize_x<F>(a, xrow0, g, G, xg[k]);
-      } else if (g < G) {
-        load_x<F, MODE>(a, xrow0, g, G, xg[k]);
-      }
-    }
     // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
-    const bool glu = a.w2 != nullptr;
-    const uint8_t* w2 = glu ? a.w2 + (w - a.w) : nullptr;
+    const uint8_t* w2 = GLU ? a.w2 + (w - a.w) : nullptr;
     const float* bias2 = a.bias2 ? a.bias2 + expert * a.out : nullptr;
-    for (int64_t t = wid; t < tiles; t += nw) {
-      int64_t o = t * rpw + rsub;
-      bool valid = o < a.out;
-      Raw raw[U], raw2[U];
+    XGroup xg[U];
+    bool have_x = false;
+    for (int64_t tb = wid; tb < tiles; tb += (int64_t)T * nw) {
+      Raw raw[T][U], raw2[T][U];
 #pragma unroll
-      for (int k = 0; k < U; k++) {
-        int g = lr + k * lpr;
-        if (valid && g < G && !is_float_type(F)) {
-          load_group<F>(w, rg, o, G, g, a.in, raw[k]);
-          if (glu) load_group<F>(w2, rg, o, G, g, a.in, raw2[k]);
+      for (int i = 0; i < T; i++) {
+        const int64_t t = tb + (int64_t)i * nw;
+        const int64_t o = t * rpw + rsub;
+        const bool valid = t < tiles && o < a.out;
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+          int g = lr + k * lpr;
+          if (valid && g < G && !is_float_type(F)) {
+            load_group<F>(w, rg, o, G, g, a.in, raw[i][k]);
+            if constexpr (GLU) load_group<F>(w2, rg, o, G, g, a.in, raw2[i][k]);
+          }
         }
       }
-      double v = row_value<F, MODE, U>(w, raw, o, valid, xg, lr, lpr, G, a.in);
-      double v2 = glu ? row_value<F, MODE, U>(w2, raw2, o, valid, xg, lr, lpr, G, a.in) : 0.0;
-      if (lr == 0 && valid) {
-        if (bias) v = (double)bias[o] + v;
-        float r = (float)v;
-        if (glu) {
-          if (bias2) v2 = (double)bias2[o] + v2;
-          r = swiglu_value(r, (float)v2, a.alpha, a.limit);
+      if (!have_x) {
+        // the activations of this lane's groups, quantized here when no
+        // quantized row was given (Q8 mode): the quantize kernels' arithmetic
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+          int g = lr + k * lpr;
+          if (inq) {
+            if constexpr (MODE == 1 && !is_float_type(F)) quantize_x<F>(a, xrow0, g, G, xg[k]);
+          } else if (g < G) {
+            load_x<F, MODE>(a, xrow0, g, G, xg[k]);
+          }
         }
-        a.y[yrow0 * a.out + o] = r;
+        have_x = true;
+      }
+#pragma unroll
+      for (int i = 0; i < T; i++) {
+        const int64_t t = tb + (int64_t)i * nw;
+        const int64_t o = t * rpw + rsub;
+        const bool valid = t < tiles && o < a.out;
+        double v = row_value<F, MODE, U>(w, raw[i], o, valid, xg, lr, lpr, G, a.in);
+        double v2 = 0.0;
+        if constexpr (GLU) v2 = row_value<F, MODE, U>(w2, raw2[i], o, valid, xg, lr, lpr, G, a.in);
+        if (lr == 0 && valid) {
+          if (bias) v = (double)bias[o] + v;
+          float r = (float)v;
+          if constexpr (GLU) {
+            if (bias2) v2 = (double)bias2[o] + v2;
+            r = swiglu_value(r, (float)v2, a.alpha, a.limit);
+          }
+          a.y[yrow0 * a.out + o] = r;
+        }
       }
     }
   } else {
@@ -732,18 +750,22 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
 }  // namespace ihip
 
 // ------------------------------------------------------- exported symbols
-#define IHIP_GEMV(NAME, F, M, U, R) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R>(a); }
+#define IHIP_GEMV(NAME, F, M, U, R, GLU) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R, GLU>(a); }
 
-#define IHIP_GEMV_U(PFX, F, M)          \
-  IHIP_GEMV(PFX##_u1, F, M, 1, 1)       \
-  IHIP_GEMV(PFX##_u2, F, M, 2, 1)       \
-  IHIP_GEMV(PFX##_u3, F, M, 3, 1)       \
-  IHIP_GEMV(PFX##_u4, F, M, 4, 1)       \
-  IHIP_GEMV(PFX##_b8u1, F, M, 1, 8)     \
-  IHIP_GEMV(PFX##_b8u2, F, M, 2, 8)     \
-  IHIP_GEMV(PFX##_b8u3, F, M, 3, 8)     \
-  IHIP_GEMV(PFX##_b8u4, F, M, 4, 8)
+#define IHIP_GEMV_U(PFX, F, M)                 \
+  IHIP_GEMV(PFX##_u1, F, M, 1, 1, false)       \
+  IHIP_GEMV(PFX##_u2, F, M, 2, 1, false)       \
+  IHIP_GEMV(PFX##_u3, F, M, 3, 1, false)       \
+  IHIP_GEMV(PFX##_u4, F, M, 4, 1, false)       \
+  IHIP_GEMV(PFX##_glu_u1, F, M, 1, 1, true)    \
+  IHIP_GEMV(PFX##_glu_u2, F, M, 2, 1, true)    \
+  IHIP_GEMV(PFX##_glu_u3, F, M, 3, 1, true)    \
+  IHIP_GEMV(PFX##_glu_u4, F, M, 4, 1, true)    \
+  IHIP_GEMV(PFX##_b8u1, F, M, 1, 8, false)     \
+  IHIP_GEMV(PFX##_b8u2, F, M, 2, 8, false)     \
+  IHIP_GEMV(PFX##_b8u3, F, M, 3, 8, false)     \
+  IHIP_GEMV(PFX##_b8u4, F, M, 4, 8, false)
 
 #define IHIP_GEMV_FMT(NAME, F) \
   IHIP_GEMV_U(gemv_##NAME##_f32, F, 0) \

@@ -153,32 +153,73 @@ struct NormArgs {
 // before the weight; with t: x += t first (addnorm, ops.cu:135-150); with
 // cd: x += the expert rows weighted in slot order, each step single-rounded
 // as TDecoderModel.Experts adds them (decoder.pas:3140-3148)
-extern "C" __global__ __launch_bounds__(256) void rmsnorm(NormArgs a)
+// One block of 1024 per row; a thread keeps its NV columns c = t + 1024 i in
+// registers and issues all their loads (and those of the k expert rows)
+// before the first sum, so a row costs one memory round trip.
+#define NORM_NV 4
+extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
 {
-  __shared__ double sh[4];
-  int64_t base = (int64_t)blockIdx.x * a.cols;
+  __shared__ double sh[16];
+  const int64_t base = (int64_t)blockIdx.x * a.cols;
+  const int t = threadIdx.x;
   double s = 0;
-  for (int c = threadIdx.x; c < a.cols; c += blockDim.x) {
-    float v = a.x[base + c];
-    if (a.cd) {
-      float acc = 0.f;
-      for (int j = 0; j < a.k; j++) {
-        int64_t sl = (int64_t)blockIdx.x * a.k + j;
-        float p = a.cw[sl] * a.cd[sl * a.cols + c];
-        acc = acc + p;
-      }
-      v = v + acc;
-      a.x[base + c] = v;
-    } else if (a.t) {
-      v = v + a.t[base + c];
-      a.x[base + c] = v;
+  for (int c0 = 0; c0 < a.cols; c0 += NORM_NV * 1024) {
+    float v[NORM_NV], add[NORM_NV];
+#pragma unroll
+    for (int i = 0; i < NORM_NV; i++) {
+      int c = c0 + t + 1024 * i;
+      v[i] = c < a.cols ? a.x[base + c] : 0.f;
+      add[i] = 0.f;
     }
-    double d = v;
-    s = s + d * d;
+    if (a.cd) {
+      float cwv[16];
+      float cdv[16][NORM_NV];
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        int64_t sl = (int64_t)blockIdx.x * a.k + j;
+        cwv[j] = j < a.k ? a.cw[sl] : 0.f;
+#pragma unroll
+        for (int i = 0; i < NORM_NV; i++) {
+          int c = c0 + t + 1024 * i;
+          cdv[j][i] = (j < a.k && c < a.cols) ? a.cd[sl * a.cols + c] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        if (j < a.k)
+#pragma unroll
+          for (int i = 0; i < NORM_NV; i++) {
+            float p = cwv[j] * cdv[j][i];
+            add[i] = add[i] + p;
+          }
+    } else if (a.t) {
+#pragma unroll
+      for (int i = 0; i < NORM_NV; i++) {
+        int c = c0 + t + 1024 * i;
+        add[i] = c < a.cols ? a.t[base + c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NORM_NV; i++) {
+      int c = c0 + t + 1024 * i;
+      if (c < a.cols) {
+        float x = v[i];
+        if (a.cd || a.t) {
+          x = x + add[i];
+          a.x[base + c] = x;
+        }
+        double d = x;
+        s = s + d * d;
+      }
+    }
   }
-  s = block_sum_d(s, sh);
-  double inv = 1.0 / sqrt(s / (double)a.cols + a.eps);
-  for (int c = threadIdx.x; c < a.cols; c += blockDim.x) {
+  s = wave_sum(s, 64);
+  if ((t & 63) == 0) sh[t >> 6] = s;
+  __syncthreads();
+  s = 0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
+  const double inv = 1.0 / sqrt(s / (double)a.cols + a.eps);
+  for (int c = t; c < a.cols; c += 1024) {
     float n = (float)((double)a.x[base + c] * inv);
     a.y[base + c] = a.w[c] * n;
   }
@@ -508,25 +549,36 @@ extern "C" __global__ __launch_bounds__(256) void attention_part_f32(AttnArgs a)
 // M the largest range maximum (and the sink); one block per (head, row)
 extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
 {
+  // the range weights exp(m_s - M) once, in LDS; the sums in range order
+  __shared__ double wts[256];
+  __shared__ double dsh[2];
   const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
   const int d = a.hd;
   const double* b = a.part + ((int64_t)h * a.rows + r) * a.splits * (d + 2);
-  double M = -1.0e308;
-  for (int s = 0; s < a.splits; s++) M = fmax(M, b[s * (d + 2) + d]);
-  if (a.sinks && (double)a.sinks[h] > M) M = a.sinks[h];
-  double den = 0;
-  for (int s = 0; s < a.splits; s++) {
-    double ms = b[s * (d + 2) + d];
-    if (ms > -1.0e308) den = den + exp(ms - M) * b[s * (d + 2) + d + 1];
+  if (t < 64) {
+    double M = -1.0e308;
+    for (int s = t; s < a.splits; s += 64) M = fmax(M, b[s * (d + 2) + d]);
+    for (int o = 1; o < 64; o <<= 1) M = fmax(M, __shfl_xor(M, o));
+    if (a.sinks && (double)a.sinks[h] > M) M = a.sinks[h];
+    for (int s = t; s < a.splits; s += 64) {
+      double ms = b[s * (d + 2) + d];
+      wts[s] = ms > -1.0e308 ? exp(ms - M) : 0.0;
+    }
+    if (t == 0) dsh[0] = M;
   }
-  if (a.sinks) den = den + exp((double)a.sinks[h] - M);
+  __syncthreads();
+  if (t == 0) {
+    double den = 0;
+    for (int s = 0; s < a.splits; s++) den = den + wts[s] * b[s * (d + 2) + d + 1];
+    if (a.sinks) den = den + exp((double)a.sinks[h] - dsh[0]);
+    dsh[1] = 1.0 / den;
+  }
+  __syncthreads();
+  const double inv = dsh[1];
   for (int i = t; i < d; i += blockDim.x) {
     double acc = 0;
-    for (int s = 0; s < a.splits; s++) {
-      double ms = b[s * (d + 2) + d];
-      if (ms > -1.0e308) acc = acc + exp(ms - M) * b[s * (d + 2) + i];
-    }
-    a.y[(int64_t)r * a.heads * d + (int64_t)h * d + i] = (float)(acc * (1.0 / den));
+    for (int s = 0; s < a.splits; s++) acc = acc + wts[s] * b[s * (d + 2) + i];
+    a.y[(int64_t)r * a.heads * d + (int64_t)h * d + i] = (float)(acc * inv);
   }
 }
 
@@ -546,8 +598,13 @@ extern "C" __global__ __launch_bounds__(64) void route(RouteArgs a)
 {
   __shared__ int chosen[64];
   __shared__ float wt[64];
+  __shared__ float lg[4096];  // the row's logits, read once
   const int row = blockIdx.x, l = threadIdx.x, E = a.experts;
-  const float* lg = a.logits + (int64_t)row * E;
+  {
+    const float* src = a.logits + (int64_t)row * E;
+    for (int i = l; i < E; i += 64) lg[i] = src[i];
+    __syncthreads();
+  }
   float mx = -INFINITY;
   for (int i = l; i < E; i += 64) mx = fmaxf(mx, lg[i]);
   for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
