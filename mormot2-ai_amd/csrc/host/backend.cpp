@@ -352,8 +352,20 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
            mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
-  int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
+  int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
+  if (!batch) {
+    // one-row blocks stage the activation row once per block: give each wave
+    // the T tiles of a step (the kernel's T), as long as the launch keeps
+    // about two blocks per CU
+    const int T = k.w2 ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
+    const int64_t want = ((int64_t)c->cus * c->gemv_blocks_per_cu + gy - 1) / gy;
+    wgs = std::min(wgs, std::max<int64_t>((tiles + 4 * T - 1) / (4 * T), want));
+    // and no more blocks than the chip holds at once: the waves walk the
+    // rest of the rows, each block stages its row once
+    const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) + gy - 1) / gy;
+    wgs = std::max<int64_t>(1, std::min(wgs, hold));
+  }
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
 }
 

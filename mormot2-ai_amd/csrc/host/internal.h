@@ -49,9 +49,11 @@ struct Module {
 struct ihip_ctx {
   int device = 0;
   int cus = 256;
+  int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   hipStream_t stream = nullptr;
   std::vector<ihip::Module> modules;
   std::unordered_map<std::string, hipFunction_t> kernels;
+  std::unordered_map<std::string, int> resident;  // blocks of a kernel one CU holds at once
   std::vector<ihip::WeightEntry> weights;
   int weight_epoch = 0;
   std::vector<uint64_t> allocations;
@@ -71,6 +73,8 @@ struct ihip_ctx {
 namespace ihip {
 
 hipFunction_t kernel(ihip_ctx* c, const char* name);
+// the blocks of `block` threads of kernel `name` that one CU runs at once
+int resident_blocks(ihip_ctx* c, const char* name, int block);
 int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, size_t shmem = 0);
 // grows a scratch buffer to at least bytes (never while capturing)
 int scratch(ihip_ctx* c, uint64_t& buf, uint64_t& cap, uint64_t bytes);

@@ -45,6 +45,20 @@ hipFunction_t kernel(ihip_ctx* c, const char* name)
   return nullptr;
 }
 
+int resident_blocks(ihip_ctx* c, const char* name, int block)
+{
+  auto it = c->resident.find(name);
+  if (it != c->resident.end()) return it->second;
+  int n = 1;
+  hipFunction_t f = kernel(c, name);
+  if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, block, 0) != hipSuccess || n < 1) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  c->resident.emplace(name, n);
+  return n;
+}
+
 int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, size_t shmem)
 {
   hipFunction_t f = kernel(c, name);
@@ -118,6 +132,7 @@ int ihip_create(int device, ihip_ctx** out)
   ihip_ctx* c = new ihip_ctx();
   c->device = device;
   c->cus = p.multiProcessorCount;
+  if (const char* v = getenv("IHIP_GEMV_BLOCKS_PER_CU")) c->gemv_blocks_per_cu = std::max(1, atoi(v));
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;

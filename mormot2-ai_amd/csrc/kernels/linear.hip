@@ -412,86 +412,204 @@ __device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&raw)[U
   return row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
 }
 
-// Q8 activations of group g formed in registers: Q8_0 per group (one lane,
-// InferQuantizeRowQ8_0), Q8_K per super-block (the 8 lanes of the block
-// meet to find the first value of the largest magnitude, InferQuantizeRowQ8_K);
-// every lane takes part, those past the row with zeros
-template <int F>
-__device__ __forceinline__ void quantize_x(const LinArgs& a, int64_t xrow, int g, int G, XGroup& x)
+// ------------------------------------------------- activation row in LDS
+// An R = 1 block (256 threads, as the host launches it) stages its one
+// activation row in LDS once; every wave then reads its lanes' groups from
+// there. Q8 mode with quantized weights: the codes [in] then float dx[G] (the
+// quantized-row layout of quantize_q8_0 / quantize_q8_k), else the floats.
+constexpr int XB = 256;
+
+template <int F, int MODE>
+constexpr bool stage_q8() { return MODE == 1 && !is_float_type(F); }
+
+template <int F, int MODE>
+constexpr int xs_bytes() { return stage_q8<F, MODE>() ? 8192 + 4 * 256 : 4 * 8192; }
+
+// a thread's share of the row in registers between the two staging phases
+struct XStage {
+  float4 f[8];    // floats: 4 per slot; quantized here: 2 slots per 8-value quarter
+  uint32_t d[9];  // a given quantized row, one dword per slot
+};
+
+template <int F, int MODE>
+__device__ __forceinline__ void stage_load(const LinArgs& a, int64_t xrow, XStage& s)
 {
-  float v[32];
-  const bool has = g < G;
-  if (has) {
-    const float4* p = (const float4*)(a.x + xrow * a.in + (int64_t)g * 32);
+  const int G = a.in >> 5;
+  const int tid = threadIdx.x;
+  if constexpr (!stage_q8<F, MODE>()) {
+    const float4* p = (const float4*)(a.x + xrow * a.in);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if (k * XB < (a.in >> 2)) s.f[k] = p[min(tid + k * XB, (a.in >> 2) - 1)];
+    }
+  } else if (a.xq) {
+    const int n = (a.in + 4 * G) >> 2;
+    const uint32_t* p = (const uint32_t*)(a.xq + xrow * (int64_t)(a.in + 4 * G));
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+      if (k * XB < n) s.d[k] = p[min(tid + k * XB, n - 1)];
+    }
+  } else {
+    const float4* p = (const float4*)(a.x + xrow * a.in);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int q = min(tid + k * XB, 4 * G - 1);  // the quarter of 8 values (group q / 4)
+      if (k * XB < 4 * G) {
+        s.f[2 * k] = p[2 * q];
+        s.f[2 * k + 1] = p[2 * q + 1];
+      }
+    }
+  }
+}
+
+// the second phase: into LDS, quantized on the way when no quantized row was
+// given - the arithmetic of quantize_q8_0 / quantize_q8_k (InferQuantizeRowQ8_0,
+// InferQuantizeRowQ8_K) with 4 threads per group of 32 values
+template <int F, int MODE>
+__device__ __forceinline__ void stage_store(const LinArgs& a, int64_t xrow, const XStage& s,
+                                            uint8_t* xs)
+{
+  const int G = a.in >> 5;
+  const int tid = threadIdx.x;
+  if constexpr (!stage_q8<F, MODE>()) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      int i = tid + k * XB;
+      if (i < (a.in >> 2)) ((float4*)xs)[i] = s.f[k];
+    }
+  } else if (a.xq) {
+    const int n = (a.in + 4 * G) >> 2;
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+      int i = tid + k * XB;
+      if (i < n) ((uint32_t*)xs)[i] = s.d[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if (k * XB >= 4 * G) break;  // the same for the whole block
+      const int q = tid + k * XB;
+      const bool has = q < 4 * G;  // whole groups (and super-blocks) on each side
+      const float4 t0 = s.f[2 * k], t1 = s.f[2 * k + 1];
+      float v[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+      bool nonfinite = false;
+      float amax = 0.f, m = 0.f;
+      int idx = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        if (!has) v[j] = 0.f;
+        nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
+        float f = fabsf(v[j]);
+        if (f > amax) {
+          amax = f;
+          m = v[j];
+          idx = 8 * q + j;
+        }
+      }
+      if (nonfinite && a.bad) a.bad[0] = 1 + (int)xrow;
+      uint32_t c0 = 0, c1 = 0;
+      float dx = 0.f;
+      if constexpr (!is_k_quant(F)) {
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        float d = amax / 127.0f;
+        if (!(d < 2.9387359e-39f)) {
+          float id = 1.0f / d;
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            uint32_t c = (uint32_t)(int)__builtin_rintf(v[j] * id) & 255u;
+            if (j < 4) c0 |= c << (8 * j);
+            else c1 |= c << (8 * (j - 4));
+          }
+        }
+        dx = half_to_float(float_to_half(d));
+      } else {
+        // the super-block's first value of the largest magnitude: 32 lanes
+        for (int o = 1; o < 32; o <<= 1) {
+          float oa = __shfl_xor(amax, o), om = __shfl_xor(m, o);
+          int oi = __shfl_xor(idx, o);
+          if (oa > amax || (oa == amax && oi < idx)) {
+            amax = oa;
+            m = om;
+            idx = oi;
+          }
+        }
+        if (!(amax < 3.7320437e-37f)) {
+          float iscale = -127.0f / m;
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            int ci = (int)__builtin_rintf(iscale * v[j]);
+            if (ci > 127) ci = 127;
+            uint32_t c = (uint32_t)ci & 255u;
+            if (j < 4) c0 |= c << (8 * j);
+            else c1 |= c << (8 * (j - 4));
+          }
+          dx = 1.0f / iscale;
+        }
+      }
+      if (has) {
+        ((uint2*)xs)[q] = make_uint2(c0, c1);
+        if ((q & 3) == 0) ((float*)(xs + a.in))[q >> 2] = dx;
+      }
+    }
+  }
+}
+
+// the lane's group g from the staged row
+template <int F, int MODE>
+__device__ __forceinline__ void lds_x(const uint8_t* xs, int in, int g, XGroup& x)
+{
+  if constexpr (!stage_q8<F, MODE>()) {
+    const float4* p = (const float4*)(xs + g * 128);
+    float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       float4 t = p[k];
-      v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+      x.f[4 * k] = t.x;
+      x.f[4 * k + 1] = t.y;
+      x.f[4 * k + 2] = t.z;
+      x.f[4 * k + 3] = t.w;
     }
+#pragma unroll
+    for (int k = 0; k < 32; k++) s += x.f[k];
+    x.sx = s;
   } else {
+    const uint4* p = (const uint4*)(xs + g * 32);
+    uint4 u0 = p[0], u1 = p[1];
+    x.w[0] = (int)u0.x; x.w[1] = (int)u0.y; x.w[2] = (int)u0.z; x.w[3] = (int)u0.w;
+    x.w[4] = (int)u1.x; x.w[5] = (int)u1.y; x.w[6] = (int)u1.z; x.w[7] = (int)u1.w;
+    x.dx = ((const float*)(xs + in))[g];
+    int sl = 0, sh = 0;
 #pragma unroll
-    for (int k = 0; k < 32; k++) v[k] = 0.f;
+    for (int k = 0; k < 4; k++) {
+      sl = sdot4(x.w[k], 0x01010101, sl);
+      sh = sdot4(x.w[4 + k], 0x01010101, sh);
+    }
+    x.sl = sl;
+    x.sh = sh;
   }
-  bool nonfinite = false;
-  float amax = 0.f, m = 0.f;
-  int idx = 0x7fffffff;
+}
+
+// the weight registers of the T tiles tb, tb + nw, ... of a wave step
+template <int F, int U, int T, bool GLU>
+__device__ __forceinline__ void load_tiles(const uint8_t* w, const uint8_t* w2, const Regions& rg,
+                                           int64_t tb, int64_t nw, int rpw,
+                                           int rsub, int lr, int lpr, int G, int64_t in,
+                                           int64_t out, Raw (&raw)[T][U], Raw (&raw2)[T][U])
+{
+  if constexpr (is_float_type(F)) return;
+  // every load is issued (a row or group past the end reads the last one, its
+  // value unused), so the wait for the activation row ahead of them is exact
 #pragma unroll
-  for (int j = 0; j < 32; j++) {
-    nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
-    float f = fabsf(v[j]);
-    if (f > amax) {
-      amax = f;
-      m = v[j];
-      idx = j;
+  for (int i = 0; i < T; i++) {
+    const int64_t o = min((tb + (int64_t)i * nw) * rpw + rsub, out - 1);
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      const int g = min(lr + k * lpr, G - 1);
+      load_group<F>(w, rg, o, G, g, in, raw[i][k]);
+      if constexpr (GLU) load_group<F>(w2, rg, o, G, g, in, raw2[i][k]);
     }
   }
-  if (nonfinite && a.bad) a.bad[0] = 1 + (int)xrow;
-  uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  float dx = 0.f;
-  if constexpr (!is_k_quant(F)) {
-    float d = amax / 127.0f;
-    if (!(d < 2.9387359e-39f)) {
-      float id = 1.0f / d;
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        int c = (int)__builtin_rintf(v[j] * id);
-        q[j >> 2] |= ((uint32_t)c & 255u) << (8 * (j & 3));
-      }
-    }
-    dx = half_to_float(float_to_half(d));
-  } else {
-    idx += 32 * g;
-    for (int o = 1; o < 8; o <<= 1) {
-      float oa = __shfl_xor(amax, o), om = __shfl_xor(m, o);
-      int oi = __shfl_xor(idx, o);
-      if (oa > amax || (oa == amax && oi < idx)) {
-        amax = oa;
-        m = om;
-        idx = oi;
-      }
-    }
-    if (!(amax < 3.7320437e-37f)) {
-      float iscale = -127.0f / m;
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        int c = (int)__builtin_rintf(iscale * v[j]);
-        if (c > 127) c = 127;
-        q[j >> 2] |= ((uint32_t)c & 255u) << (8 * (j & 3));
-      }
-      dx = 1.0f / iscale;
-    }
-  }
-  int sl = 0, sh = 0;
-#pragma unroll
-  for (int k = 0; k < 8; k++) x.w[k] = (int)q[k];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    sl = sdot4(x.w[k], 0x01010101, sl);
-    sh = sdot4(x.w[4 + k], 0x01010101, sh);
-  }
-  x.sl = sl;
-  x.sh = sh;
-  x.dx = dx;
 }
 
 // ------------------------------------------------------------------ kernel
@@ -551,42 +669,27 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     // first ones before the activation row is read), so a wave keeps several
     // 16-byte loads per lane in flight
     constexpr int T = GLU ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
-    const bool inq = MODE == 1 && !is_float_type(F) && a.xq == nullptr;
     // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
     const uint8_t* w2 = GLU ? a.w2 + (w - a.w) : nullptr;
     const float* bias2 = a.bias2 ? a.bias2 + expert * a.out : nullptr;
     XGroup xg[U];
-    bool have_x = false;
-    for (int64_t tb = wid; tb < tiles; tb += (int64_t)T * nw) {
-      Raw raw[T][U], raw2[T][U];
+    Raw raw[T][U], raw2[T][U];
+    __shared__ __align__(16) uint8_t xs[xs_bytes<F, MODE>()];
+    // the activation row's global loads first, then the first step's weight
+    // loads, so the row is staged while the weights are on their way
+    XStage st;
+    stage_load<F, MODE>(a, xrow0, st);
+    int64_t tb = wid;
+    load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, a.out, raw,
+                             raw2);
+    stage_store<F, MODE>(a, xrow0, st, xs);
+    __syncthreads();
 #pragma unroll
-      for (int i = 0; i < T; i++) {
-        const int64_t t = tb + (int64_t)i * nw;
-        const int64_t o = t * rpw + rsub;
-        const bool valid = t < tiles && o < a.out;
-#pragma unroll
-        for (int k = 0; k < U; k++) {
-          int g = lr + k * lpr;
-          if (valid && g < G && !is_float_type(F)) {
-            load_group<F>(w, rg, o, G, g, a.in, raw[i][k]);
-            if constexpr (GLU) load_group<F>(w2, rg, o, G, g, a.in, raw2[i][k]);
-          }
-        }
-      }
-      if (!have_x) {
-        // the activations of this lane's groups, quantized here when no
-        // quantized row was given (Q8 mode): the quantize kernels' arithmetic
-#pragma unroll
-        for (int k = 0; k < U; k++) {
-          int g = lr + k * lpr;
-          if (inq) {
-            if constexpr (MODE == 1 && !is_float_type(F)) quantize_x<F>(a, xrow0, g, G, xg[k]);
-          } else if (g < G) {
-            load_x<F, MODE>(a, xrow0, g, G, xg[k]);
-          }
-        }
-        have_x = true;
-      }
+    for (int k = 0; k < U; k++) {
+      int g = lr + k * lpr;
+      if (g < G) lds_x<F, MODE>(xs, a.in, g, xg[k]);
+    }
+    while (tb < tiles) {
 #pragma unroll
       for (int i = 0; i < T; i++) {
         const int64_t t = tb + (int64_t)i * nw;
@@ -605,6 +708,10 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
           a.y[yrow0 * a.out + o] = r;
         }
       }
+      tb += (int64_t)T * nw;
+      if (tb < tiles)
+        load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, a.out,
+                                 raw, raw2);
     }
   } else {
     // the activation and output rows of the batch
