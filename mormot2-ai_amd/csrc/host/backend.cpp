@@ -343,15 +343,38 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     const float* bias2;
     float alpha, limit;
     int* bad;
+    const float* nw;
+    double eps;
+    const float* res;
+    const float* cw;
+    int32_t kslots, pad2;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
-         (const uint8_t*)k.w2, (const float*)k.bias2, k.alpha, k.limit, (int*)c->scratch_bad};
+         (const uint8_t*)k.w2, (const float*)k.bias2, k.alpha, k.limit, (int*)c->scratch_bad,
+         (const float*)k.nw, k.eps, (const float*)k.res, (const float*)k.cw,
+         k.cw ? (int32_t)k.rows : 0, 0};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
+  if (k.nw && (batch || k.in > 4096 || xq))
+    return fail(IHIP_E_ARG, "EnqueueLinear: the fused rmsnorm takes one float row of at most 4096");
+  if ((k.res || k.cw) && (batch || k.w2 || (k.ids && !k.cw)))
+    return fail(IHIP_E_ARG, "EnqueueLinear: a residual add takes one plain or combined row");
   char name[64];
-  snprintf(name, sizeof name, "gemv_%s_%s_%su%d", fmt_name(k.dtype),
-           mode == IHIP_MODE_Q8 ? "q8" : "f32", batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
+  if (k.cw) {
+    // the experts of one token added into the residual: one block per tile
+    const int64_t xbytes = q8 ? k.rows * k.in + k.rows * k.in / 8 : k.rows * k.in * 4;
+    if (!k.ids || k.rows < 1 || k.rows > 8 || xq || k.w2 || k.x_per_slot != 1 || xbytes > 65536)
+      return fail(IHIP_E_ARG, "EnqueueLinear: combine takes 1..8 slots of float rows (64 KB)");
+    snprintf(name, sizeof name, "gemv_%s_%s_cmb_u%d", fmt_name(k.dtype),
+             mode == IHIP_MODE_Q8 ? "q8" : "f32", U);
+    const int64_t hold = (int64_t)c->cus * resident_blocks(c, name, 256, (size_t)xbytes);
+    return launch(c, name, dim3((unsigned)std::max<int64_t>(1, std::min(tiles, hold))), dim3(256), &a,
+                  (size_t)xbytes);
+  }
+  snprintf(name, sizeof name, "gemv_%s_%s_%s%su%d", fmt_name(k.dtype),
+           mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
+           batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
   int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
   if (!batch) {
@@ -677,7 +700,7 @@ int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k,
     float* w;
     int32_t experts, k, norm, rows;
   } a = {(const float*)logits, (int*)ids, (float*)w, (int32_t)experts, (int32_t)k, norm_topk, 1};
-  return launch(c, "route", dim3(1), dim3(64), &a);
+  return launch(c, "route", dim3(1), dim3(256), &a);
 }
 
 int ihip_enqueue_moecombine(ihip_ctx* c, uint64_t d, uint64_t w, uint64_t y, int64_t k, int64_t n)

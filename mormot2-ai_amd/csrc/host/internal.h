@@ -74,7 +74,7 @@ namespace ihip {
 
 hipFunction_t kernel(ihip_ctx* c, const char* name);
 // the blocks of `block` threads of kernel `name` that one CU runs at once
-int resident_blocks(ihip_ctx* c, const char* name, int block);
+int resident_blocks(ihip_ctx* c, const char* name, int block, size_t shmem = 0);
 int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, size_t shmem = 0);
 // grows a scratch buffer to at least bytes (never while capturing)
 int scratch(ihip_ctx* c, uint64_t& buf, uint64_t& cap, uint64_t bytes);
@@ -102,6 +102,15 @@ struct LinearCall {
   // fused SwiGLU: y = swiglu(x W^T + bias, x W2^T + bias2) (one row per block)
   uint64_t w2 = 0, bias2 = 0;
   float alpha = 1.0f, limit = 0.0f;
+  // one row: the activation row is rmsnorm(x) * nw (eps) before the GEMV
+  // (TInferCpuBackend.RmsNorm fused into the staging), in <= 4096
+  uint64_t nw = 0;
+  double eps = 0;
+  // y[o] = res[o] + value (y may be res): the caller's residual add
+  uint64_t res = 0;
+  // combine: rows = slots, ids [slots] (<= 8), x [slots, in]; y [out] =
+  // res + the slot-order sum of cw[s] * the expert rows (TDecoderModel.Experts)
+  uint64_t cw = 0;
 };
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // which activation quantizer a weight type needs in Q8 mode: -1 none (float

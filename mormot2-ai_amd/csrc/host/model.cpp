@@ -239,6 +239,92 @@ static int rope_attn(ihip_model* m, const DevLayer& L, int64_t n, int64_t past, 
                            attention_splits(maxkeys));
 }
 
+// whether one row runs through layers_one: the norms fused into the GEMVs
+// (hidden <= 4096), a token's experts combined in one launch (<= 8 slots)
+static bool one_row_fused(const ihip_model* m)
+{
+  const ihip_model_desc& d = m->d;
+  if (d.hidden > 4096) return false;
+  if (d.experts > 0) {
+    const int64_t K = d.experts_used;
+    if (K < 1 || K > 8 || K * d.expert_ffn * 4 > 65536) return false;
+  }
+  return true;
+}
+
+// one row through the layers, x holding its embedding: every RMSNorm is
+// computed by the GEMVs that read it (their staging), the residual adds by
+// the GEMVs that produce them (o projection, FFN down, the experts'
+// combine), so the row costs no norm or add launches. The arithmetic is that
+// of layers() step for step. Leaves x = the residual (the final norm is the
+// head's).
+static int layers_one(ihip_model* m, int64_t past, bool graph)
+{
+  const ihip_model_desc& d = m->d;
+  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
+                kvw = (int64_t)d.kv_heads * hd;
+  int rc = 0;
+  auto normed = [&](uint64_t nw, int dt, uint64_t w, int64_t out, uint64_t bias, uint64_t y) {
+    LinearCall k;
+    k.x = m->x; k.rows = 1; k.in = H; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
+    k.y = y; k.mode = m->mode; k.nw = nw; k.eps = d.rms_eps;
+    return enqueue_linear(m->c, k);
+  };
+  for (int l = 0; l < d.layers; l++) {
+    const DevLayer& L = m->L[l];
+    // attention block (decoder.pas:2625-2702)
+    if ((rc = normed(L.input_norm, L.qd, L.q, qw, L.qb, m->q)) ||
+        (rc = normed(L.input_norm, L.kd, L.k, kvw, L.kb, m->k)) ||
+        (rc = normed(L.input_norm, L.vd, L.v, kvw, L.vb, m->v)) ||
+        (rc = rope_attn(m, L, 1, past, graph)))
+      return rc;
+    {
+      LinearCall k;
+      k.x = m->attn; k.rows = 1; k.in = qw; k.dtype = L.od; k.w = L.o; k.out = H; k.bias = L.ob;
+      k.y = m->x; k.res = m->x; k.mode = m->mode;
+      if ((rc = enqueue_linear(m->c, k))) return rc;
+    }
+    if (!L.moe) {
+      // DenseFfn (decoder.pas:2866-2878): gate, up and SwiGLU in one pass
+      const int64_t F = d.ffn;
+      if (L.gd != L.ud) return fail(IHIP_E_ARG, "model: gate and up of one type");
+      LinearCall k;
+      k.x = m->x; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
+      k.y = m->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
+      k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
+      if ((rc = enqueue_linear(m->c, k))) return rc;
+      LinearCall dn;
+      dn.x = m->gate; dn.rows = 1; dn.in = F; dn.dtype = L.dd; dn.w = L.down; dn.out = H;
+      dn.y = m->x; dn.res = m->x; dn.mode = m->mode;
+      if ((rc = enqueue_linear(m->c, dn))) return rc;
+      continue;
+    }
+    // MoeBlock (decoder.pas:3037-3053), the experts chosen on the device
+    const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
+    if ((rc = normed(L.post_norm, L.rd, L.router, E, L.router_b, m->route))) return rc;
+    struct {
+      const float* logits;
+      int* ids;
+      float* w;
+      int32_t experts, k, norm, rows;
+    } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
+            d.norm_topk, 1};
+    if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
+    LinearCall k;
+    k.x = m->x; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
+    k.y = m->gate; k.mode = m->mode; k.ids = m->ids; k.stride = L.eg_stride; k.x_per_slot = 0;
+    k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
+    k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
+    if ((rc = enqueue_linear(m->c, k))) return rc;
+    LinearCall dn;
+    dn.x = m->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
+    dn.y = m->x; dn.res = m->x; dn.cw = m->rw; dn.mode = m->mode; dn.ids = m->ids;
+    dn.stride = L.ed_stride; dn.x_per_slot = 1; dn.nexp = (int)E; dn.bias = L.edb;
+    if ((rc = enqueue_linear(m->c, dn))) return rc;
+  }
+  return 0;
+}
+
 // the layers of one chunk of n rows at positions past.., x holding the
 // embeddings; leaves h = the final norm of x. graph: the position is read
 // from m->pos (decode step under capture)
@@ -250,6 +336,7 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
   // one row (decode): every GEMV quantizes its activation row in registers;
   // a chunk: the rows are quantized once per activation buffer
   const bool one = n == 1;
+  if (one && one_row_fused(m)) return layers_one(m, past, graph);
   int rc = ihip_enqueue_rmsnorm(m->c, m->x, m->L[0].input_norm, m->h, n, H, d.rms_eps);
   if (rc) return rc;
   for (int l = 0; l < d.layers; l++) {
@@ -301,7 +388,7 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
         int32_t experts, k, norm, rows;
       } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n};
-      if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(64), &ra))) return rc;
+      if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
       if (one) {
         // the token's K experts: gate, up and SwiGLU in one pass per slot,
         // then down per slot; the weighted sum goes into the next norm
@@ -369,6 +456,13 @@ static int head(ihip_model* m, int64_t n, bool all, uint64_t y)
 {
   const ihip_model_desc& d = m->d;
   QCache qh{m->xq0, m->xqk};
+  if (n == 1 && one_row_fused(m)) {
+    // layers_one left the residual: the final norm is staged by the head
+    LinearCall k;
+    k.x = m->x; k.rows = 1; k.in = d.hidden; k.dtype = m->head_dt; k.w = m->head;
+    k.out = d.vocab; k.y = y; k.mode = m->mode; k.nw = m->final_norm; k.eps = d.rms_eps;
+    return enqueue_linear(m->c, k);
+  }
   if (all) return lin(m, m->h, &qh, n, d.hidden, m->head_dt, m->head, d.vocab, 0, y);
   return lin(m, m->h + (uint64_t)(n - 1) * d.hidden * 4, nullptr, 1, d.hidden, m->head_dt,
              m->head, d.vocab, 0, y);

@@ -45,17 +45,19 @@ hipFunction_t kernel(ihip_ctx* c, const char* name)
   return nullptr;
 }
 
-int resident_blocks(ihip_ctx* c, const char* name, int block)
+int resident_blocks(ihip_ctx* c, const char* name, int block, size_t shmem)
 {
-  auto it = c->resident.find(name);
+  const std::string key = std::string(name) + ":" + std::to_string(block) + ":" + std::to_string(shmem);
+  auto it = c->resident.find(key);
   if (it != c->resident.end()) return it->second;
   int n = 1;
   hipFunction_t f = kernel(c, name);
-  if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, block, 0) != hipSuccess || n < 1) {
+  if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, block, shmem) != hipSuccess ||
+      n < 1) {
     (void)hipGetLastError();
     n = 1;
   }
-  c->resident.emplace(name, n);
+  c->resident.emplace(key, n);
   return n;
 }
 

@@ -49,6 +49,15 @@ struct LinArgs {
   const float* bias2;
   float alpha, limit;
   int* bad;  // set to 1 + row when an activation quantized here is not finite
+  // one-row blocks: the staged row is rmsnorm(x row) * nw when nw is set
+  const float* nw;
+  double eps;
+  // y[o] = res[o] + value, the caller's residual add (y may be res)
+  const float* res;
+  // combine: slot s < kslots reads x row s and expert ids[s]; y[o] = res[o] +
+  // the sum over the slots, in order, of cw[s] * value_s
+  const float* cw;
+  int32_t kslots, pad2;
 };
 
 // ---------------------------------------------------------------- formats
@@ -413,91 +422,164 @@ __device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&raw)[U
 }
 
 // ------------------------------------------------- activation row in LDS
-// An R = 1 block (256 threads, as the host launches it) stages its one
-// activation row in LDS once; every wave then reads its lanes' groups from
-// there. Q8 mode with quantized weights: the codes [in] then float dx[G] (the
-// quantized-row layout of quantize_q8_0 / quantize_q8_k), else the floats.
+// An R = 1 block (256 threads, as the host launches it) stages its
+// activations in LDS once; every wave then reads its lanes' groups from
+// there. Q8 mode with quantized weights: the codes [n] then float dx[n / 32]
+// (the quantized-row layout of quantize_q8_0 / quantize_q8_k), else the
+// floats. A staging call takes n <= 8192 contiguous values: one row, or the
+// rows of several slots back to back (no group crosses a row); with the
+// fused rmsnorm (NORM) one row of n <= XN / 2.
 constexpr int XB = 256;
+constexpr int XN = 8192;  // values per staging call
 
 template <int F, int MODE>
 constexpr bool stage_q8() { return MODE == 1 && !is_float_type(F); }
 
 template <int F, int MODE>
-constexpr int xs_bytes() { return stage_q8<F, MODE>() ? 8192 + 4 * 256 : 4 * 8192; }
+constexpr int xs_bytes() { return stage_q8<F, MODE>() ? XN + XN / 8 : 4 * XN; }
 
-// a thread's share of the row in registers between the two staging phases
+// a thread's share between the two staging phases: values (and norm weights)
 struct XStage {
   float4 f[8];    // floats: 4 per slot; quantized here: 2 slots per 8-value quarter
+  float4 g[8];    // the norm weights of the same values
   uint32_t d[9];  // a given quantized row, one dword per slot
 };
 
-template <int F, int MODE>
-__device__ __forceinline__ void stage_load(const LinArgs& a, int64_t xrow, XStage& s)
+// phase 1: the global loads. src: n floats (nw: their norm weights, or null);
+// qsrc: a quantized row of n values instead (Q8 mode, no norm)
+template <int F, int MODE, bool NORM>
+__device__ __forceinline__ void stage_load(const float* src, const uint8_t* qsrc, int n,
+                                           const float* nw, XStage& s)
 {
-  const int G = a.in >> 5;
   const int tid = threadIdx.x;
+  const float4* p = (const float4*)src;
+  const float4* pw = (const float4*)nw;
   if constexpr (!stage_q8<F, MODE>()) {
-    const float4* p = (const float4*)(a.x + xrow * a.in);
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      if (k * XB < (a.in >> 2)) s.f[k] = p[min(tid + k * XB, (a.in >> 2) - 1)];
+    for (int k = 0; k < (NORM ? 4 : 8); k++) {
+      if (k * XB < (n >> 2)) {
+        const int i = min(tid + k * XB, (n >> 2) - 1);
+        s.f[k] = p[i];
+        if constexpr (NORM) s.g[k] = pw[i];
+      }
     }
-  } else if (a.xq) {
-    const int n = (a.in + 4 * G) >> 2;
-    const uint32_t* p = (const uint32_t*)(a.xq + xrow * (int64_t)(a.in + 4 * G));
+  } else if (qsrc) {
+    const int nd = (n + 4 * (n >> 5)) >> 2;
 #pragma unroll
     for (int k = 0; k < 9; k++) {
-      if (k * XB < n) s.d[k] = p[min(tid + k * XB, n - 1)];
+      if (k * XB < nd) s.d[k] = ((const uint32_t*)qsrc)[min(tid + k * XB, nd - 1)];
     }
   } else {
-    const float4* p = (const float4*)(a.x + xrow * a.in);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const int q = min(tid + k * XB, 4 * G - 1);  // the quarter of 8 values (group q / 4)
-      if (k * XB < 4 * G) {
+    for (int k = 0; k < (NORM ? 2 : 4); k++) {
+      const int q = min(tid + k * XB, (n >> 3) - 1);  // the quarter of 8 values (group q / 4)
+      if (k * XB < (n >> 3)) {
         s.f[2 * k] = p[2 * q];
         s.f[2 * k + 1] = p[2 * q + 1];
+        if constexpr (NORM) {
+          s.g[2 * k] = pw[2 * q];
+          s.g[2 * k + 1] = pw[2 * q + 1];
+        }
       }
     }
   }
 }
 
-// the second phase: into LDS, quantized on the way when no quantized row was
-// given - the arithmetic of quantize_q8_0 / quantize_q8_k (InferQuantizeRowQ8_0,
-// InferQuantizeRowQ8_K) with 4 threads per group of 32 values
-template <int F, int MODE>
-__device__ __forceinline__ void stage_store(const LinArgs& a, int64_t xrow, const XStage& s,
-                                            uint8_t* xs)
+// the rmsnorm of the staged values in place, TInferCpuBackend.RmsNorm
+// (backend.cpu.pas:1769-1795): the sum of squares in double over the block,
+// inv = 1 / sqrt(mean + eps), w * (float)(x * inv). Every thread calls it.
+template <int NV>
+__device__ __forceinline__ void stage_norm(float (&v)[NV], const float (&w)[NV], const bool (&has)[NV],
+                                           int n, double eps)
 {
-  const int G = a.in >> 5;
+  __shared__ double red[XB / 64];
+  double ss = 0;
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+    if (has[j]) {
+      double d = v[j];
+      ss = ss + d * d;
+    }
+  ss = wave_sum(ss, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = 0;
+#pragma unroll
+  for (int i = 0; i < XB / 64; i++) ss += red[i];
+  const double inv = 1.0 / sqrt(ss / (double)n + eps);
+#pragma unroll
+  for (int j = 0; j < NV; j++) v[j] = w[j] * (float)((double)v[j] * inv);
+}
+
+__device__ __forceinline__ void unpack8(const float4& a, const float4& b, float* v)
+{
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// phase 2: into LDS (codes / dx, or floats at xs), normed first with NORM
+// (one row of n values), quantized on the way when no quantized row was given
+// - the arithmetic of quantize_q8_0 / quantize_q8_k (InferQuantizeRowQ8_0,
+// InferQuantizeRowQ8_K) with 4 threads per group of 32 values. bad: set to
+// badrow when a value is not finite.
+template <int F, int MODE, bool NORM>
+__device__ __forceinline__ void stage_store(const XStage& s, bool quantized, int n, double eps,
+                                            uint8_t* xs, float* dxs, int* bad, int badrow)
+{
   const int tid = threadIdx.x;
   if constexpr (!stage_q8<F, MODE>()) {
+    constexpr int KF = NORM ? 4 : 8;  // float4 slots per thread
+    float v[4 * KF], w[4 * KF];
+    bool has[4 * KF];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      int i = tid + k * XB;
-      if (i < (a.in >> 2)) ((float4*)xs)[i] = s.f[k];
+    for (int k = 0; k < KF; k++) {
+      has[4 * k] = has[4 * k + 1] = has[4 * k + 2] = has[4 * k + 3] = tid + k * XB < (n >> 2);
+      v[4 * k] = s.f[k].x; v[4 * k + 1] = s.f[k].y; v[4 * k + 2] = s.f[k].z; v[4 * k + 3] = s.f[k].w;
+      if constexpr (NORM) {
+        w[4 * k] = s.g[k].x; w[4 * k + 1] = s.g[k].y; w[4 * k + 2] = s.g[k].z; w[4 * k + 3] = s.g[k].w;
+      }
     }
-  } else if (a.xq) {
-    const int n = (a.in + 4 * G) >> 2;
+    if constexpr (NORM) stage_norm<4 * KF>(v, w, has, n, eps);
+#pragma unroll
+    for (int k = 0; k < KF; k++)
+      if (has[4 * k]) ((float4*)xs)[tid + k * XB] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+  } else if (quantized) {
+    const int nd = (n + 4 * (n >> 5)) >> 2;
 #pragma unroll
     for (int k = 0; k < 9; k++) {
       int i = tid + k * XB;
-      if (i < n) ((uint32_t*)xs)[i] = s.d[k];
+      if (i < nd) ((uint32_t*)xs)[i] = s.d[k];
     }
   } else {
+    const int G = n >> 5;
+    constexpr int KQ = NORM ? 2 : 4;  // 8-value quarters per thread
+    float vv[8 * KQ], ww[8 * KQ];
+    bool hh[8 * KQ];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < KQ; k++) {
+      const bool has = tid + k * XB < 4 * G;
+      unpack8(s.f[2 * k], s.f[2 * k + 1], &vv[8 * k]);
+      if constexpr (NORM) unpack8(s.g[2 * k], s.g[2 * k + 1], &ww[8 * k]);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        hh[8 * k + j] = has;
+        if (!has) vv[8 * k + j] = 0.f;
+      }
+    }
+    if constexpr (NORM) stage_norm<8 * KQ>(vv, ww, hh, n, eps);
+#pragma unroll
+    for (int k = 0; k < KQ; k++) {
       if (k * XB >= 4 * G) break;  // the same for the whole block
       const int q = tid + k * XB;
       const bool has = q < 4 * G;  // whole groups (and super-blocks) on each side
-      const float4 t0 = s.f[2 * k], t1 = s.f[2 * k + 1];
-      float v[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = has ? vv[8 * k + j] : 0.f;
       bool nonfinite = false;
       float amax = 0.f, m = 0.f;
       int idx = 0x7fffffff;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        if (!has) v[j] = 0.f;
         nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
         float f = fabsf(v[j]);
         if (f > amax) {
@@ -506,7 +588,7 @@ __device__ __forceinline__ void stage_store(const LinArgs& a, int64_t xrow, cons
           idx = 8 * q + j;
         }
       }
-      if (nonfinite && a.bad) a.bad[0] = 1 + (int)xrow;
+      if (nonfinite && bad) bad[0] = badrow;
       uint32_t c0 = 0, c1 = 0;
       float dx = 0.f;
       if constexpr (!is_k_quant(F)) {
@@ -549,18 +631,19 @@ __device__ __forceinline__ void stage_store(const LinArgs& a, int64_t xrow, cons
       }
       if (has) {
         ((uint2*)xs)[q] = make_uint2(c0, c1);
-        if ((q & 3) == 0) ((float*)(xs + a.in))[q >> 2] = dx;
+        if ((q & 3) == 0) dxs[q >> 2] = dx;
       }
     }
   }
 }
 
-// the lane's group g from the staged row
+// the lane's group gi (counted over the staged values) from LDS: codes at
+// xs + 32 gi and dxs[gi], or floats at xs + 128 gi
 template <int F, int MODE>
-__device__ __forceinline__ void lds_x(const uint8_t* xs, int in, int g, XGroup& x)
+__device__ __forceinline__ void lds_x(const uint8_t* xs, const float* dxs, int gi, XGroup& x)
 {
   if constexpr (!stage_q8<F, MODE>()) {
-    const float4* p = (const float4*)(xs + g * 128);
+    const float4* p = (const float4*)(xs + gi * 128);
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -574,11 +657,11 @@ __device__ __forceinline__ void lds_x(const uint8_t* xs, int in, int g, XGroup& 
     for (int k = 0; k < 32; k++) s += x.f[k];
     x.sx = s;
   } else {
-    const uint4* p = (const uint4*)(xs + g * 32);
+    const uint4* p = (const uint4*)(xs + gi * 32);
     uint4 u0 = p[0], u1 = p[1];
     x.w[0] = (int)u0.x; x.w[1] = (int)u0.y; x.w[2] = (int)u0.z; x.w[3] = (int)u0.w;
     x.w[4] = (int)u1.x; x.w[5] = (int)u1.y; x.w[6] = (int)u1.z; x.w[7] = (int)u1.w;
-    x.dx = ((const float*)(xs + in))[g];
+    x.dx = dxs[gi];
     int sl = 0, sh = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -615,7 +698,7 @@ __device__ __forceinline__ void load_tiles(const uint8_t* w, const uint8_t* w2, 
 // ------------------------------------------------------------------ kernel
 // R = 1: one activation row, kept in registers. R = 8: up to 8 rows per
 // blockIdx.y chunk, activations read per group (from L1/L2).
-template <int F, int MODE, int U, int R, bool GLU>
+template <int F, int MODE, int U, int R, bool GLU, bool NORM>
 __device__ __forceinline__ void gemv(const LinArgs& a)
 {
   const int lane = threadIdx.x & 63;
@@ -678,16 +761,19 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     // the activation row's global loads first, then the first step's weight
     // loads, so the row is staged while the weights are on their way
     XStage st;
-    stage_load<F, MODE>(a, xrow0, st);
+    const bool quantized = !NORM && stage_q8<F, MODE>() && a.xq != nullptr;
+    stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
+                        quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in, a.nw, st);
     int64_t tb = wid;
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, a.out, raw,
                              raw2);
-    stage_store<F, MODE>(a, xrow0, st, xs);
+    stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
+                         1 + (int)xrow0);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < U; k++) {
       int g = lr + k * lpr;
-      if (g < G) lds_x<F, MODE>(xs, a.in, g, xg[k]);
+      if (g < G) lds_x<F, MODE>(xs, (const float*)(xs + a.in), g, xg[k]);
     }
     while (tb < tiles) {
 #pragma unroll
@@ -705,6 +791,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
             if (bias2) v2 = (double)bias2[o] + v2;
             r = swiglu_value(r, (float)v2, a.alpha, a.limit);
           }
+          if (a.res) r = a.res[o] + r;
           a.y[yrow0 * a.out + o] = r;
         }
       }
@@ -776,6 +863,100 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         }
       }
     }
+  }
+}
+
+// ------------------------------------------------------------------ combine
+// The down projection of one token's experts, added into the residual:
+// TDecoderModel.Experts (decoder.pas:3140-3148) - every expert row as a float
+// (its bias added in double first), then the rows weighted by cw and summed
+// in slot order, each step single-rounded, then added to the residual.
+// A block of 4 waves takes one tile of rows per step; wave w computes slots
+// w and w + 4 (kslots <= 8), the values meet in LDS and wave 0 adds them in
+// slot order. The kslots activation rows x[s] (contiguous) are staged once
+// per block into the dynamic LDS.
+template <int F, int MODE, int U>
+__device__ __forceinline__ void gemv_cmb(const LinArgs& a)
+{
+  extern __shared__ __align__(16) uint8_t cmb_xs[];
+  __shared__ float dv[8][8];  // [slot][row of the tile]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = a.lpr, lr = lane & (lpr - 1), rsub = lane / lpr, rpw = 64 / lpr;
+  const int G = a.in >> 5, K = a.kslots;
+  const Regions rg = regions(F, a.out, a.in);
+  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
+  const int n = K * a.in;
+  float* dxs = (float*)(cmb_xs + n);
+  // this wave's slots and their experts (a bad id adds nothing)
+  const uint8_t* wi[2];
+  bool ok[2];
+  int64_t e[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int sl = wave + 4 * i;
+    const int id = sl < K ? a.ids[sl] : -1;
+    ok[i] = sl < K && id >= 0 && (a.nexp <= 0 || id < a.nexp);
+    e[i] = ok[i] ? id : 0;
+    wi[i] = a.w + e[i] * a.stride;
+  }
+  Raw raw[2][U];
+  int64_t t = blockIdx.x;
+  auto load = [&](int64_t tt) {
+    if constexpr (!is_float_type(F)) {
+      const int64_t o = min(tt * rpw + rsub, (int64_t)a.out - 1);
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < U; k++)
+          load_group<F>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
+    }
+  };
+  load(t);
+  for (int c0 = 0; c0 < n; c0 += XN) {
+    XStage st;
+    const int nc = min(XN, n - c0);
+    stage_load<F, MODE, false>(a.x + c0, nullptr, nc, nullptr, st);
+    stage_store<F, MODE, false>(st, false, nc, 0.0,
+                         cmb_xs + (stage_q8<F, MODE>() ? c0 : 4 * c0), dxs + c0 / 32, a.bad, 1);
+  }
+  __syncthreads();
+  while (t < tiles) {
+    const int64_t o = t * rpw + rsub;
+    const bool valid = o < a.out;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int sl = wave + 4 * i;
+      if (sl < K) {  // the same for the whole wave
+        XGroup xg[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+          const int g = lr + k * lpr;
+          if (g < G) lds_x<F, MODE>(cmb_xs, dxs, sl * G + g, xg[k]);
+        }
+        double v = row_value<F, MODE, U>(wi[i], raw[i], o, valid && ok[i], xg, lr, lpr, G, a.in);
+        if (lr == 0) {
+          float d = 0.f;
+          if (valid && ok[i]) {
+            if (a.bias) v = (double)a.bias[e[i] * a.out + o] + v;
+            d = (float)v;
+          }
+          dv[sl][rsub] = d;
+        }
+      }
+    }
+    __syncthreads();
+    const int64_t tn = t + gridDim.x;
+    if (tn < tiles) load(tn);
+    if (wave == 0 && lr == 0 && valid) {
+      float add = 0.f;
+      for (int sl = 0; sl < K; sl++) {
+        float p = a.cw[sl] * dv[sl][rsub];
+        add = add + p;
+      }
+      a.y[o] = a.res ? a.res[o] + add : add;
+    }
+    __syncthreads();
+    t = tn;
   }
 }
 
@@ -857,26 +1038,45 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
 }  // namespace ihip
 
 // ------------------------------------------------------- exported symbols
-#define IHIP_GEMV(NAME, F, M, U, R, GLU) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R, GLU>(a); }
+#define IHIP_GEMV(NAME, F, M, U, R, GLU, ...) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R, GLU, __VA_ARGS__>(a); }
 
-#define IHIP_GEMV_U(PFX, F, M)                 \
-  IHIP_GEMV(PFX##_u1, F, M, 1, 1, false)       \
-  IHIP_GEMV(PFX##_u2, F, M, 2, 1, false)       \
-  IHIP_GEMV(PFX##_u3, F, M, 3, 1, false)       \
-  IHIP_GEMV(PFX##_u4, F, M, 4, 1, false)       \
-  IHIP_GEMV(PFX##_glu_u1, F, M, 1, 1, true)    \
-  IHIP_GEMV(PFX##_glu_u2, F, M, 2, 1, true)    \
-  IHIP_GEMV(PFX##_glu_u3, F, M, 3, 1, true)    \
-  IHIP_GEMV(PFX##_glu_u4, F, M, 4, 1, true)    \
-  IHIP_GEMV(PFX##_b8u1, F, M, 1, 8, false)     \
-  IHIP_GEMV(PFX##_b8u2, F, M, 2, 8, false)     \
-  IHIP_GEMV(PFX##_b8u3, F, M, 3, 8, false)     \
-  IHIP_GEMV(PFX##_b8u4, F, M, 4, 8, false)
+#define IHIP_GEMV_U(PFX, F, M)                       \
+  IHIP_GEMV(PFX##_u1, F, M, 1, 1, false, false)      \
+  IHIP_GEMV(PFX##_u2, F, M, 2, 1, false, false)      \
+  IHIP_GEMV(PFX##_u3, F, M, 3, 1, false, false)      \
+  IHIP_GEMV(PFX##_u4, F, M, 4, 1, false, false)      \
+  IHIP_GEMV(PFX##_glu_u1, F, M, 1, 1, true, false)   \
+  IHIP_GEMV(PFX##_glu_u2, F, M, 2, 1, true, false)   \
+  IHIP_GEMV(PFX##_glu_u3, F, M, 3, 1, true, false)   \
+  IHIP_GEMV(PFX##_glu_u4, F, M, 4, 1, true, false)   \
+  IHIP_GEMV(PFX##_norm_u1, F, M, 1, 1, false, true)  \
+  IHIP_GEMV(PFX##_norm_u2, F, M, 2, 1, false, true)  \
+  IHIP_GEMV(PFX##_norm_u3, F, M, 3, 1, false, true)  \
+  IHIP_GEMV(PFX##_norm_u4, F, M, 4, 1, false, true)  \
+  IHIP_GEMV(PFX##_norm_glu_u1, F, M, 1, 1, true, true) \
+  IHIP_GEMV(PFX##_norm_glu_u2, F, M, 2, 1, true, true) \
+  IHIP_GEMV(PFX##_norm_glu_u3, F, M, 3, 1, true, true) \
+  IHIP_GEMV(PFX##_norm_glu_u4, F, M, 4, 1, true, true) \
+  IHIP_GEMV(PFX##_b8u1, F, M, 1, 8, false, false)    \
+  IHIP_GEMV(PFX##_b8u2, F, M, 2, 8, false, false)    \
+  IHIP_GEMV(PFX##_b8u3, F, M, 3, 8, false, false)    \
+  IHIP_GEMV(PFX##_b8u4, F, M, 4, 8, false, false)
+
+#define IHIP_CMB(NAME, F, M, U) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv_cmb<F, M, U>(a); }
+
+#define IHIP_CMB_U(PFX, F, M)      \
+  IHIP_CMB(PFX##_cmb_u1, F, M, 1) \
+  IHIP_CMB(PFX##_cmb_u2, F, M, 2) \
+  IHIP_CMB(PFX##_cmb_u3, F, M, 3) \
+  IHIP_CMB(PFX##_cmb_u4, F, M, 4)
 
 #define IHIP_GEMV_FMT(NAME, F) \
   IHIP_GEMV_U(gemv_##NAME##_f32, F, 0) \
-  IHIP_GEMV_U(gemv_##NAME##_q8, F, 1)
+  IHIP_GEMV_U(gemv_##NAME##_q8, F, 1) \
+  IHIP_CMB_U(gemv_##NAME##_f32, F, 0) \
+  IHIP_CMB_U(gemv_##NAME##_q8, F, 1)
 
 #define IHIP_DEQ(NAME, F) \
   extern "C" __global__ __launch_bounds__(256) void dequant_##NAME(ihip::DeqArgs a) { ihip::dequant<F>(a); }

@@ -162,6 +162,10 @@ extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
   __shared__ double sh[16];
   const int64_t base = (int64_t)blockIdx.x * a.cols;
   const int t = threadIdx.x;
+  // a row of up to NORM_NV * 1024 columns stays in registers with its norm
+  // weights, loaded with it: the output needs no second read
+  const bool one = a.cols <= NORM_NV * 1024;
+  float keep[NORM_NV], wv[NORM_NV];
   double s = 0;
   for (int c0 = 0; c0 < a.cols; c0 += NORM_NV * 1024) {
     float v[NORM_NV], add[NORM_NV];
@@ -169,6 +173,7 @@ extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
     for (int i = 0; i < NORM_NV; i++) {
       int c = c0 + t + 1024 * i;
       v[i] = c < a.cols ? a.x[base + c] : 0.f;
+      wv[i] = (one && c < a.cols) ? a.w[c] : 0.f;
       add[i] = 0.f;
     }
     if (a.cd) {
@@ -202,12 +207,14 @@ extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
 #pragma unroll
     for (int i = 0; i < NORM_NV; i++) {
       int c = c0 + t + 1024 * i;
+      keep[i] = 0.f;
       if (c < a.cols) {
         float x = v[i];
         if (a.cd || a.t) {
           x = x + add[i];
           a.x[base + c] = x;
         }
+        keep[i] = x;
         double d = x;
         s = s + d * d;
       }
@@ -219,9 +226,17 @@ extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
   s = 0;
   for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
   const double inv = 1.0 / sqrt(s / (double)a.cols + a.eps);
-  for (int c = t; c < a.cols; c += 1024) {
-    float n = (float)((double)a.x[base + c] * inv);
-    a.y[base + c] = a.w[c] * n;
+  if (one) {
+#pragma unroll
+    for (int i = 0; i < NORM_NV; i++) {
+      int c = t + 1024 * i;
+      if (c < a.cols) a.y[base + c] = wv[i] * (float)((double)keep[i] * inv);
+    }
+  } else {
+    for (int c = t; c < a.cols; c += 1024) {
+      float n = (float)((double)a.x[base + c] * inv);
+      a.y[base + c] = a.w[c] * n;
+    }
   }
 }
 
@@ -592,19 +607,25 @@ struct RouteArgs {
 
 // TDecoderModel.Route (decoder.pas:2901-2949) = route of ops.cu:664-720:
 // softmax in double, the k highest logits (the lower id on a tie), weights
-// rounded to single, renormed, then sorted by id. One wave per row: the lanes
-// hold the logits, each pick a wave-wide argmax
-extern "C" __global__ __launch_bounds__(64) void route(RouteArgs a)
+// rounded to single, renormed in pick order, then sorted by id. One block of
+// 256 per row. The pick order is a rank: logit i is the j-th pick when j
+// logits are higher, or equal with a lower id; each thread counts it for its
+// own logits against the row in LDS, eight 16-byte reads in flight.
+extern "C" __global__ __launch_bounds__(256) void route(RouteArgs a)
 {
-  __shared__ int chosen[64];
-  __shared__ float wt[64];
-  __shared__ float lg[4096];  // the row's logits, read once
-  const int row = blockIdx.x, l = threadIdx.x, E = a.experts;
+  __shared__ __align__(16) float lg[4096 + 32];  // the row's logits, padded to 32
+  __shared__ float pw[64];                       // the picks' weights and ids in pick order
+  __shared__ int pid[64];
+  const int row = blockIdx.x, t = threadIdx.x, l = t & 63, E = a.experts, K = a.k;
+  const int E32 = (E + 31) & ~31;
   {
     const float* src = a.logits + (int64_t)row * E;
-    for (int i = l; i < E; i += 64) lg[i] = src[i];
+    for (int i = t; i < E; i += 256) lg[i] = src[i];
+    // below every logit and never the lower id: the padding is no pick
+    if (E + t < E32) lg[E + t] = -INFINITY;
     __syncthreads();
   }
+  // every wave forms the same maximum and sum
   float mx = -INFINITY;
   for (int i = l; i < E; i += 64) mx = fmaxf(mx, lg[i]);
   for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -612,51 +633,43 @@ extern "C" __global__ __launch_bounds__(64) void route(RouteArgs a)
   double sum = 0;
   for (int i = l; i < E; i += 64) sum = sum + exp((double)lg[i] - m);
   sum = wave_sum(sum, 64);
-  uint64_t taken = 0;  // bit (i / 64) of this lane's experts i = l + 64 * bit
-  for (int j = 0; j < a.k; j++) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = l, b = 0; i < E; i += 64, b++)
-      if (!((taken >> b) & 1) && (bi == 0x7fffffff || lg[i] > bv)) {
-        bv = lg[i];
-        bi = i;
-      }
-    for (int o = 1; o < 64; o <<= 1) {
-      float ov = __shfl_xor(bv, o);
-      int oi = __shfl_xor(bi, o);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
-        bv = ov;
-        bi = oi;
+  for (int i = t; i < E; i += 256) {
+    const float v = lg[i];
+    int rank = 0;
+    for (int j = 0; j < E32; j += 32) {
+      float4 u[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) u[q] = *(const float4*)&lg[j + 4 * q];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const int jj = j + 4 * q;
+        rank += (u[q].x > v || (u[q].x == v && jj < i)) ? 1 : 0;
+        rank += (u[q].y > v || (u[q].y == v && jj + 1 < i)) ? 1 : 0;
+        rank += (u[q].z > v || (u[q].z == v && jj + 2 < i)) ? 1 : 0;
+        rank += (u[q].w > v || (u[q].w == v && jj + 3 < i)) ? 1 : 0;
       }
     }
-    if ((bi & 63) == l) taken |= 1ull << (bi >> 6);
-    if (l == 0) {
-      chosen[j] = bi;
-      wt[j] = (float)(exp((double)bv - m) / sum);
+    if (rank < K) {
+      pw[rank] = (float)(exp((double)v - m) / sum);
+      pid[rank] = i;
     }
   }
   __syncthreads();
-  if (l == 0) {
+  if (t >= 64) return;
+  float wt = l < K ? pw[l] : 0.f;
+  const int my_id = l < K ? pid[l] : 0x7fffffff;
+  if (a.norm) {
+    // the picked weights summed in pick order, as the reference's loop does
     double picked = 0;
-    for (int j = 0; j < a.k; j++) picked = picked + (double)wt[j];
-    if (a.norm)
-      for (int j = 0; j < a.k; j++) wt[j] = (float)((double)wt[j] / picked);
-    for (int j = 1; j < a.k; j++) {
-      int id = chosen[j];
-      float v = wt[j];
-      int p = j;
-      while (p > 0 && chosen[p - 1] > id) {
-        chosen[p] = chosen[p - 1];
-        wt[p] = wt[p - 1];
-        p--;
-      }
-      chosen[p] = id;
-      wt[p] = v;
-    }
-    for (int j = 0; j < a.k; j++) {
-      a.ids[(int64_t)row * a.k + j] = chosen[j];
-      a.w[(int64_t)row * a.k + j] = wt[j];
-    }
+    for (int j = 0; j < K; j++) picked = picked + (double)pw[j];
+    wt = (float)((double)wt / picked);
+  }
+  // sorted by id: a pick's place is the number of smaller ids picked
+  int place = 0;
+  for (int j = 0; j < K; j++) place += pid[j] < my_id ? 1 : 0;
+  if (l < K) {
+    a.ids[(int64_t)row * K + place] = my_id;
+    a.w[(int64_t)row * K + place] = wt;
   }
 }
 
