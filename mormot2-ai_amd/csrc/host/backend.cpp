@@ -746,6 +746,44 @@ int attention_splits(int64_t maxkeys) { return (int)std::max<int64_t>(1, (maxkey
 // the ranges attention_merge weighs in one block
 static const int MAX_SPLITS = 256;
 
+int enqueue_attention_one(ihip_ctx* c, const AttnOne& o)
+{
+  if (o.hd != 64 && o.hd != 128) return fail(IHIP_E_UNSUPPORTED, "attention_one: head_dim 64 or 128");
+  if (o.splits < 1 || o.splits > MAX_SPLITS || o.heads < 1 || o.kvh < 1 || o.heads % o.kvh)
+    return fail(IHIP_E_ARG, "attention_one: heads / splits");
+  struct {
+    const float *q, *k, *v, *qn, *kn, *cs;
+    void *kc, *vc;
+    float* y;
+    const float* sinks;
+    const int* pastp;
+    double* part;
+    double scale, eps;
+    int32_t heads, kvh, hd, past, window, splits;
+  } a = {(const float*)o.q, (const float*)o.k, (const float*)o.v, (const float*)o.qn,
+         (const float*)o.kn, (const float*)o.cs, (void*)o.kc, (void*)o.vc, (float*)o.y,
+         (const float*)o.sinks, (const int*)o.pastp, (double*)o.part,
+         o.scale > 0 ? o.scale : 1.0 / std::sqrt((double)o.hd), o.eps, (int32_t)o.heads,
+         (int32_t)o.kvh, (int32_t)o.hd, (int32_t)o.past, (int32_t)o.window, o.splits};
+  char name[32];
+  snprintf(name, sizeof name, "attention_one_%s_%d", o.f16 ? "f16" : "f32", (int)o.hd);
+  int rc = launch(c, name, dim3((unsigned)o.heads, 1, (unsigned)o.splits), dim3(256), &a);
+  if (rc) return rc;
+  struct {
+    const float* q;
+    const void* kc;
+    const void* vc;
+    float* y;
+    const float* sinks;
+    const int* pastp;
+    double* part;
+    double scale;
+    int32_t rows, heads, kvh, hd, past, window, f16, splits;
+  } mg = {nullptr, nullptr, nullptr, (float*)o.y, (const float*)o.sinks, nullptr, (double*)o.part,
+          0.0, 1, (int32_t)o.heads, (int32_t)o.kvh, (int32_t)o.hd, 0, 0, o.f16, o.splits};
+  return launch(c, "attention_merge", dim3((unsigned)o.heads, 1), dim3(128), &mg);
+}
+
 int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
                       int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                       uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,

@@ -124,6 +124,18 @@ int attention_splits(int64_t maxkeys);
 // x += the k expert rows cd weighted by cw in slot order, then y = rmsnorm(x)
 int enqueue_addnorm_moe(ihip_ctx* c, uint64_t x, uint64_t cd, uint64_t cw, int64_t k, uint64_t w,
                         uint64_t y, int64_t rows, int64_t cols, double eps);
+// the decode step's attention of one row: head norms and RoPE of q and the
+// new key (stored into the cache with its value) and the ranges in one
+// launch, then attention_merge; part [heads, splits, hd + 2] doubles; hd 64
+// or 128
+struct AttnOne {
+  uint64_t q = 0, k = 0, v = 0, qn = 0, kn = 0, cs = 0, kc = 0, vc = 0, y = 0, sinks = 0;
+  uint64_t pastp = 0, part = 0;
+  double scale = 0, eps = 0;
+  int64_t heads = 0, kvh = 0, hd = 0, past = 0, window = 0;
+  int splits = 1, f16 = 0;
+};
+int enqueue_attention_one(ihip_ctx* c, const AttnOne& o);
 int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t y, uint64_t part,
                       int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                       uint64_t pastp, int64_t window, uint64_t sinks, double scale, int f16,

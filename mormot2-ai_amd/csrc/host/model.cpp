@@ -275,9 +275,23 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
     // attention block (decoder.pas:2625-2702)
     if ((rc = normed(L.input_norm, L.qd, L.q, qw, L.qb, m->q)) ||
         (rc = normed(L.input_norm, L.kd, L.k, kvw, L.kb, m->k)) ||
-        (rc = normed(L.input_norm, L.vd, L.v, kvw, L.vb, m->v)) ||
-        (rc = rope_attn(m, L, 1, past, graph)))
+        (rc = normed(L.input_norm, L.vd, L.v, kvw, L.vb, m->v)))
       return rc;
+    if (hd == 64 || hd == 128) {
+      // head norms, RoPE, cache store and the ranges in one launch, then the merge
+      AttnOne o;
+      o.q = m->q; o.k = m->k; o.v = m->v; o.qn = L.qn; o.kn = L.kn; o.cs = m->cs;
+      o.kc = L.kc; o.vc = L.vc; o.y = m->attn; o.sinks = L.sinks; o.pastp = graph ? m->pos : 0;
+      o.part = m->attn_part; o.scale = 1.0 / std::sqrt((double)hd);
+      o.eps = d.rms_eps; o.heads = d.heads; o.kvh = d.kv_heads; o.hd = hd; o.past = past;
+      o.window = L.window; o.f16 = m->kv_f16;
+      int64_t maxkeys = graph ? m->max_tokens : past + 1;
+      if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
+      o.splits = attention_splits(maxkeys);
+      if ((rc = enqueue_attention_one(m->c, o))) return rc;
+    } else if ((rc = rope_attn(m, L, 1, past, graph))) {
+      return rc;
+    }
     {
       LinearCall k;
       k.x = m->attn; k.rows = 1; k.in = qw; k.dtype = L.od; k.w = L.o; k.out = H; k.bias = L.ob;

@@ -96,10 +96,82 @@ __device__ __forceinline__ float swiglu_value(float g, float u, float alpha, flo
   return b * u;
 }
 
+// ------------------------------------------------ wave reductions in VGPRs
+// xpart<K>(v): the value of a lane in the sibling block of K lanes (the block
+// that differs in lane bit K), moved inside the register file: DPP quad
+// permutes (K 1, 2), row half-mirror and mirror (K 4, 8), and gfx950's
+// permlane16/32 swaps (K 16, 32). For K 4 and 8 the partner is the mirrored
+// lane, not lane ^ K: use it in a butterfly that starts at K = 1, where every
+// lane of a block holds the same value by then. K 1, 2, 16 and 32 are lane ^ K.
+template <int K>
+__device__ __forceinline__ uint32_t xpart_u(uint32_t v)
+{
+  if constexpr (K == 1) return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (K == 2) return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (K == 4) return __builtin_amdgcn_update_dpp(0u, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (K == 8) return __builtin_amdgcn_update_dpp(0u, v, 0x140, 0xF, 0xF, false);
+  else if constexpr (K == 16) {
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? p[0] : p[1];
+  } else {
+    static_assert(K == 32, "xpart: K is 1, 2, 4, 8, 16 or 32");
+    auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? p[0] : p[1];
+  }
+}
+
+template <int K, typename T>
+__device__ __forceinline__ T xpart(T v)
+{
+  if constexpr (sizeof(T) == 8) {
+    uint64_t b = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = xpart_u<K>((uint32_t)b), hi = xpart_u<K>((uint32_t)(b >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, xpart_u<K>(__builtin_bit_cast(uint32_t, v)));
+  }
+}
+
+// the sum over aligned blocks of `width` lanes (1..64, a power of two), in
+// every lane of the block: own + partner at each level, so the result is the
+// one of the lane ^ K butterfly bit for bit
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v, int width)
 {
-  for (int o = 1; o < width; o <<= 1) v += __shfl_xor(v, o);
+  if (width > 1) v = v + xpart<1>(v);
+  if (width > 2) v = v + xpart<2>(v);
+  if (width > 4) v = v + xpart<4>(v);
+  if (width > 8) v = v + xpart<8>(v);
+  if (width > 16) v = v + xpart<16>(v);
+  if (width > 32) v = v + xpart<32>(v);
+  return v;
+}
+
+// one butterfly level of "the first value of the largest magnitude": the
+// larger magnitude, the lower index on a tie (InferQuantizeRowQ8_K's scan)
+template <int K>
+__device__ __forceinline__ void first_max(float& amax, float& m, int& idx)
+{
+  const float oa = xpart<K>(amax), om = xpart<K>(m);
+  const int oi = xpart<K>(idx);
+  if (oa > amax || (oa == amax && oi < idx)) {
+    amax = oa;
+    m = om;
+    idx = oi;
+  }
+}
+
+// the maximum over the wave, in every lane
+template <typename T>
+__device__ __forceinline__ T wave_max(T v)
+{
+  T o;
+  o = xpart<1>(v); if (o > v) v = o;
+  o = xpart<2>(v); if (o > v) v = o;
+  o = xpart<4>(v); if (o > v) v = o;
+  o = xpart<8>(v); if (o > v) v = o;
+  o = xpart<16>(v); if (o > v) v = o;
+  o = xpart<32>(v); if (o > v) v = o;
   return v;
 }
 

@@ -20,7 +20,7 @@
 // a wave read one contiguous run of the codes region with 16-byte loads. The
 // activation of a lane's groups stays in registers for every row the wave
 // visits (R = 1), the waves walk the rows grid-stride. Lane sums meet in a
-// butterfly of __shfl_xor within the LPR lanes. Q8 mode with K-quants: the 8
+// register butterfly (wave_sum) within the LPR lanes. Q8 mode with K-quants: the 8
 // groups of a super-block sit in 8 neighbouring lanes, whose integer sums
 // are added exactly before the one double product of the super-block.
 #include "common.h"
@@ -592,8 +592,8 @@ __device__ __forceinline__ void stage_store(const XStage& s, bool quantized, int
       uint32_t c0 = 0, c1 = 0;
       float dx = 0.f;
       if constexpr (!is_k_quant(F)) {
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, xpart<1>(amax));
+        amax = fmaxf(amax, xpart<2>(amax));
         float d = amax / 127.0f;
         if (!(d < 2.9387359e-39f)) {
           float id = 1.0f / d;
@@ -607,15 +607,11 @@ __device__ __forceinline__ void stage_store(const XStage& s, bool quantized, int
         dx = half_to_float(float_to_half(d));
       } else {
         // the super-block's first value of the largest magnitude: 32 lanes
-        for (int o = 1; o < 32; o <<= 1) {
-          float oa = __shfl_xor(amax, o), om = __shfl_xor(m, o);
-          int oi = __shfl_xor(idx, o);
-          if (oa > amax || (oa == amax && oi < idx)) {
-            amax = oa;
-            m = om;
-            idx = oi;
-          }
-        }
+        first_max<1>(amax, m, idx);
+        first_max<2>(amax, m, idx);
+        first_max<4>(amax, m, idx);
+        first_max<8>(amax, m, idx);
+        first_max<16>(amax, m, idx);
         if (!(amax < 3.7320437e-37f)) {
           float iscale = -127.0f / m;
 #pragma unroll

@@ -90,15 +90,12 @@ extern "C" __global__ __launch_bounds__(256) void quantize_q8_k(QuantArgs a)
       idx = 4 * lane + j;
     }
   }
-  for (int o = 1; o < 64; o <<= 1) {
-    float oa = __shfl_xor(amax, o), om = __shfl_xor(m, o);
-    int oi = __shfl_xor(idx, o);
-    if (oa > amax || (oa == amax && oi < idx)) {
-      amax = oa;
-      m = om;
-      idx = oi;
-    }
-  }
+  first_max<1>(amax, m, idx);
+  first_max<2>(amax, m, idx);
+  first_max<4>(amax, m, idx);
+  first_max<8>(amax, m, idx);
+  first_max<16>(amax, m, idx);
+  first_max<32>(amax, m, idx);
   if (__any(nonfinite) && lane == 0 && a.bad) a.bad[0] = 1 + row;
   uint8_t* row_q = a.xq + (int64_t)row * ((int64_t)a.in + 4 * (int64_t)G);
   float* scales = (float*)(row_q + a.in);
@@ -452,10 +449,7 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
     sc[t] = acc;
     m = acc;
   }
-  for (int o = 1; o < 64; o <<= 1) {
-    double ov = __shfl_xor(m, o);
-    if (ov > m) m = ov;
-  }
+  m = wave_max(m);
   if ((t & 63) == 0) red[t >> 6] = m;
   __syncthreads();
   m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
@@ -573,7 +567,7 @@ extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
   if (t < 64) {
     double M = -1.0e308;
     for (int s = t; s < a.splits; s += 64) M = fmax(M, b[s * (d + 2) + d]);
-    for (int o = 1; o < 64; o <<= 1) M = fmax(M, __shfl_xor(M, o));
+    M = wave_max(M);
     if (a.sinks && (double)a.sinks[h] > M) M = a.sinks[h];
     for (int s = t; s < a.splits; s += 64) {
       double ms = b[s * (d + 2) + d];
@@ -598,6 +592,261 @@ extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
 }
 
 // ------------------------------------------------------------------- MoE
+// ------------------------------------------------- attention of one row
+// The decode step's attention ranges in one launch per layer: per (head,
+// range of ATT_CHUNK keys) block, the Q/K head RMSNorm and RoPE of qkrope (the
+// new key and value also stored into the cache by the blocks that hold
+// them) and the range's partial softmax of attention_part; attention_merge
+// adds the ranges. Every global load of a block - q, the new k/v, its keys
+// and its values - is issued before the first arithmetic.
+struct AttnOneArgs {
+  const float* q;   // the row's q [heads * hd], k and v [kvh * hd] (GEMV outputs)
+  const float* k;
+  const float* v;
+  const float* qn;  // head norms [hd] or null
+  const float* kn;
+  const float* cs;  // cos [hd / 2] then sin [hd / 2]
+  void* kc;
+  void* vc;
+  float* y;         // [heads * hd]
+  const float* sinks;
+  const int* pastp;  // device position of the row (graph replay), or null: past
+  double* part;      // [heads, splits, hd + 2]
+  double scale, eps;
+  int32_t heads, kvh, hd, past, window, splits;
+};
+
+// the sums of two values over a block of 256 (wave sums, then 4 waves)
+__device__ __forceinline__ void block_sum2(double& a, double& b, double* red)
+{
+  a = wave_sum(a, 64);
+  b = wave_sum(b, 64);
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = a;
+    red[4 + (threadIdx.x >> 6)] = b;
+  }
+  __syncthreads();
+  a = (red[0] + red[1]) + (red[2] + red[3]);
+  b = (red[4] + red[5]) + (red[6] + red[7]);
+  __syncthreads();
+}
+
+template <bool F16, int HD>
+__device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
+{
+  __shared__ double qd[HD];
+  __shared__ float nq[HD], nk[HD];
+  __shared__ float knew[HD], vnew[HD];
+  __shared__ double sc[ATT_CHUNK];
+  __shared__ double red[8];
+  __shared__ double accs[4][HD];
+  const int h = blockIdx.x, s = blockIdx.z, t = threadIdx.x;
+  constexpr int d = HD, half = HD / 2;
+  const int64_t kvw = (int64_t)a.kvh * d;
+  const int g = h / (a.heads / a.kvh);
+  const int past = a.pastp ? *a.pastp : a.past;
+  const int total = past + 1;
+  const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
+  const int cnt = total - first;
+  const int j0 = min(cnt, s * ATT_CHUNK), j1 = min(cnt, j0 + ATT_CHUNK);
+  const int n = j1 - j0;
+  const int jn = cnt - 1 - j0;  // the new key within the range (valid when hasnew)
+  const bool hasnew = n > 0 && j1 == cnt;
+  double* out = a.part + ((int64_t)h * a.splits + s) * (d + 2);
+  const int64_t base = (int64_t)(first + j0) * kvw + (int64_t)g * d;
+  const int w = t >> 6, l = t & 63;
+  constexpr int lpk = HD / 2;      // value pass: lanes per key (a dimension pair each)
+  constexpr int kpw = 64 / lpk;     // keys side by side in a wave
+  const int lane_key = l / lpk, pair = l % lpk;
+  constexpr int step = 4 * kpw;
+  constexpr int VB = ATT_CHUNK / step;            // a lane's keys: the whole range at once
+  constexpr int KB = HD * (F16 ? 2 : 4) / 16;     // 16-byte loads of a key row
+
+  // ---- every load first, each from a valid address (a clamped index; the
+  // value of a key or lane past the end is not used), so that no load waits
+  // for another
+  const int tc = min(t, d - 1), th = min(t, half - 1);
+  float qv = a.q[(int64_t)h * d + tc];
+  const float qw = a.qn ? a.qn[tc] : 1.f;
+  float kv = a.k[(int64_t)g * d + tc];
+  const float vv = a.v[(int64_t)g * d + tc];
+  const float kw = a.kn ? a.kn[tc] : 1.f;
+  const float cv = a.cs[th], sv = a.cs[half + th];
+  if (t >= d) qv = kv = 0.f;
+  // the range's rows (an empty range reads row 0 of the cache)
+  const int64_t rbase = n > 0 ? base : (int64_t)g * d;
+  const int nmax = max(n - 1, 0);
+  uint4 kr[KB];
+  {
+    const uint4* p = (const uint4*)((const uint8_t*)a.kc + (rbase + (int64_t)min(t, nmax) * kvw) * (F16 ? 2 : 4));
+#pragma unroll
+    for (int k = 0; k < KB; k++) kr[k] = p[k];
+  }
+  uint32_t vr[VB][F16 ? 1 : 2];
+  const int jb0 = w * kpw + lane_key;
+#pragma unroll
+  for (int u = 0; u < VB; u++) {
+    const int64_t e = rbase + (int64_t)min(jb0 + u * step, nmax) * kvw + 2 * pair;
+    if constexpr (F16) {
+      vr[u][0] = *(const uint32_t*)((const uint16_t*)a.vc + e);
+    } else {
+      uint2 x = *(const uint2*)((const float*)a.vc + e);
+      vr[u][0] = x.x;
+      vr[u][1] = x.y;
+    }
+  }
+
+  // ---- the head norms (qkrope's arithmetic) and RoPE of q and the new key
+  {
+    double sq = (double)qv * (double)qv, sk = (double)kv * (double)kv;
+    if (t >= d) sq = sk = 0;
+    if (a.qn || (hasnew && a.kn)) block_sum2(sq, sk, red);
+    float xq = qv, xk = kv;
+    if (a.qn) xq = qw * (float)((double)qv * (1.0 / sqrt(sq / (double)d + a.eps)));
+    if (hasnew && a.kn) xk = kw * (float)((double)kv * (1.0 / sqrt(sk / (double)d + a.eps)));
+    if (t < d) {
+      nq[t] = xq;
+      nk[t] = xk;
+    }
+    __syncthreads();
+    if (t < half) {
+      double x0 = nq[t], x1 = nq[t + half], c = cv, sn = sv;
+      qd[t] = (double)(float)(x0 * c - x1 * sn);
+      qd[t + half] = (double)(float)(x1 * c + x0 * sn);
+      if (hasnew) {
+        double k0 = nk[t], k1 = nk[t + half];
+        float o0 = (float)(k0 * c - k1 * sn), o1 = (float)(k1 * c + k0 * sn);
+        const int64_t dst = (int64_t)past * kvw + (int64_t)g * d;
+        if constexpr (F16) {
+          uint16_t h0 = float_to_half(o0), h1 = float_to_half(o1);
+          ((uint16_t*)a.kc)[dst + t] = h0;
+          ((uint16_t*)a.kc)[dst + t + half] = h1;
+          o0 = half_to_float(h0);
+          o1 = half_to_float(h1);
+        } else {
+          ((float*)a.kc)[dst + t] = o0;
+          ((float*)a.kc)[dst + t + half] = o1;
+        }
+        knew[t] = o0;
+        knew[t + half] = o1;
+      }
+    }
+    if (hasnew && t < d) {
+      const int64_t dst = (int64_t)past * kvw + (int64_t)g * d;
+      float x = vv;
+      if constexpr (F16) {
+        uint16_t hv = float_to_half(x);
+        ((uint16_t*)a.vc)[dst + t] = hv;
+        x = half_to_float(hv);
+      } else {
+        ((float*)a.vc)[dst + t] = x;
+      }
+      vnew[t] = x;
+    }
+    __syncthreads();
+  }
+
+  // ---- scores: the CPU's sequential double dot per key, one thread per key
+  double m = -1.0e308;
+  if (t < n) {
+    double acc = 0;
+    if (hasnew && t == jn) {
+      for (int i = 0; i < d; i++) acc = acc + qd[i] * (double)knew[i];
+    } else {
+#pragma unroll
+      for (int k = 0; k < KB; k++) {
+          uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
+          if constexpr (F16) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              int i = 8 * k + 2 * j;
+              acc = acc + qd[i] * (double)half_to_float(wv[j] & 0xffffu);
+              acc = acc + qd[i + 1] * (double)half_to_float(wv[j] >> 16);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc = acc + qd[4 * k + j] * (double)bits_float(wv[j]);
+          }
+        }
+    }
+    acc = acc * a.scale;
+    sc[t] = acc;
+    m = acc;
+  }
+  m = wave_max(m);
+  if (l == 0) red[w] = m;
+  __syncthreads();
+  m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+  double e = 0;
+  if (t < n) {
+    e = exp(sc[t] - m);
+    sc[t] = e;
+  }
+  e = wave_sum(e, 64);
+  __syncthreads();
+  if (l == 0) red[4 + w] = e;
+
+  // ---- the weighted values: the loads above, the new value from LDS
+  double a0 = 0, a1 = 0;
+#pragma unroll
+  for (int u = 0; u < VB; u++) {
+    const int j = jb0 + u * step;
+    if (j < n) {
+      const double p = sc[j];
+      float x0, x1;
+      if (hasnew && j == jn) {
+        x0 = vnew[2 * pair];
+        x1 = vnew[2 * pair + 1];
+      } else if constexpr (F16) {
+        x0 = half_to_float(vr[u][0] & 0xffffu);
+        x1 = half_to_float(vr[u][0] >> 16);
+      } else {
+        x0 = bits_float(vr[u][0]);
+        x1 = bits_float(vr[u][F16 ? 0 : 1]);
+      }
+      a0 = a0 + p * (double)x0;
+      a1 = a1 + p * (double)x1;
+    }
+  }
+  if constexpr (lpk == 32) {  // the two keys of a wave: lanes l and l ^ 32
+    a0 = a0 + xpart<32>(a0);
+    a1 = a1 + xpart<32>(a1);
+  }
+  if (lane_key == 0) {
+    accs[w][2 * pair] = a0;
+    accs[w][2 * pair + 1] = a1;
+  }
+  __syncthreads();
+  if (n > 0) {
+    for (int i = t; i < d; i += 256) out[i] = (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]);
+    if (t == 0) {
+      out[d] = m;
+      out[d + 1] = (red[4] + red[5]) + (red[6] + red[7]);
+    }
+  } else if (t == 0) {  // an empty range: weight 0 in the merge
+    out[d] = -1.0e308;
+    out[d + 1] = 0.0;
+  }
+
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_one_f16_64(AttnOneArgs a)
+{
+  attention_one_t<true, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_one_f16_128(AttnOneArgs a)
+{
+  attention_one_t<true, 128>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_one_f32_64(AttnOneArgs a)
+{
+  attention_one_t<false, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_one_f32_128(AttnOneArgs a)
+{
+  attention_one_t<false, 128>(a);
+}
+
 struct RouteArgs {
   const float* logits;
   int* ids;
@@ -628,7 +877,7 @@ extern "C" __global__ __launch_bounds__(256) void route(RouteArgs a)
   // every wave forms the same maximum and sum
   float mx = -INFINITY;
   for (int i = l; i < E; i += 64) mx = fmaxf(mx, lg[i]);
-  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = wave_max(mx);
   const double m = mx;
   double sum = 0;
   for (int i = l; i < E; i += 64) sum = sum + exp((double)lg[i] - m);

@@ -79,3 +79,28 @@ def test_baseline_shape_greedy_64(ctx, name, prompt_len):
     assert np.array_equal(got, ref), (np.nonzero(got != ref)[0][:5], margins)
     dev.close()
     cpu.close()
+
+
+LONG = [
+    ("qwen3-30b-a3b-q4_k_m", dict(layers=2, vocab=2048, hidden=512, heads=8, kv_heads=2,
+                                  head_dim=128, experts=16, experts_used=4, expert_ffn=256)),
+    ("gpt-oss-20b-mxfp4", dict(layers=2, vocab=2048, hidden=512, heads=8, kv_heads=2,
+                               head_dim=64, experts=8, experts_used=2, expert_ffn=512,
+                               window=160)),
+]
+
+
+@pytest.mark.parametrize("name,over", LONG)
+def test_tiny_greedy_long_context(ctx, name, over):
+    # a context of several 128-key ranges (and a window across them): the
+    # decode attention's ranges and their merge, replayed by the graph
+    spec = models.Spec(models.tiny(name, **over), seed=57)
+    prompt = np.random.default_rng(9).integers(0, spec.vocab, 300).astype(np.int32)
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=True, max_tokens=512)
+    cpu = O.Model(spec, 512, kv_f16=True, threads=16)
+    got = dev.greedy(prompt, 24)
+    ref, margins = cpu.greedy(prompt, 24)
+    print(name, "min margin", float(margins.min()), flush=True)
+    assert np.array_equal(got, ref), (got, ref, margins)
+    dev.close()
+    cpu.close()
