@@ -123,10 +123,41 @@ def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20):
     return nb / (ms * 1e-3) / 1e9, ms * 1e3
 
 
-def expert_gemv(ctx, spec, reps=4):
+def time_direct(ctx, enqueue, reps):
+    """The launches of enqueue() made reps times back to back between two
+    events, without a graph (the --no-graphs mode a profiled run uses, where
+    the host's launch rate bounds the figure); ms per repetition."""
+    enqueue()
+    ctx.sync()
+    ctx.record(0)
+    for _ in range(reps):
+        enqueue()
+    ctx.record(1)
+    return ctx.elapsed(0, 1) / reps
+
+
+def copy_calibration(ctx, nbytes=256 << 20):
+    """A plain device copy of known size: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters of a profile to bytes."""
+    import infer_hip as H
+    L = H.lib()
+    a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    H.check(L.ihip_copy_async(ctx.h, b.ptr, a.ptr, nbytes), "copy")
+    ctx.sync()
+    ctx.record(0)
+    H.check(L.ihip_copy_async(ctx.h, b.ptr, a.ptr, nbytes), "copy")
+    ctx.record(1)
+    ms = ctx.elapsed(0, 1)
+    a.free()
+    b.free()
+    return nbytes, 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def expert_gemv(ctx, spec, reps=4, graphs=True):
     """The dominant decode kernel: 8 experts of the gate projection of every
     MoE layer (Q4_K 768x2048 each), one launch per layer, the 48 launches in
-    one graph timed with events (as the decode step replays them)."""
+    one graph timed with events (as the decode step replays them); without
+    graphs (a profiled run) launched directly."""
     import infer_hip as H
     L = H.lib()
     c = spec.cfg
@@ -154,12 +185,27 @@ def expert_gemv(ctx, spec, reps=4):
             H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K,
                                               0, dy.ptr, 0, H.MODE_Q8 | 2))
 
-    ms = time_graph(ctx, enq, reps) / len(devs)
+    ms = (time_graph(ctx, enq, reps) if graphs else time_direct(ctx, enq, reps)) / len(devs)
     nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + K * 4 + K * FI * 4
     for b in (dx, dq, ids, dy):
         b.free()
     return {"kernel": f"gemv_{H.NAMES[dtype].lower()}_q8 (ids, {K} experts {FI}x{Hd})",
             "bytes_per_launch": nb, "avg_us": ms * 1e3, "GBps": nb / (ms * 1e-3) / 1e9}
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed counter
+    profile (FETCH_SIZE + WRITE_SIZE, each scaled by a copy of known size),
+    or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4_k_ids_8x768x2048_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def cpu_baseline(spec, prompt, steps, threads):
@@ -212,6 +258,8 @@ def main():
     log("device", dev_name, dev_mem >> 30, "GiB", cus, "CUs")
     stream = stream_peak(ctx)
     log(f"stream read {stream:.0f} GB/s")
+    copy_bytes, copy_gbps = copy_calibration(ctx)
+    log(f"copy {copy_bytes} B (the counter calibration): {copy_gbps:.0f} GB/s read+write")
 
     t = time.time()
     spec = models.Spec(models.CONFIGS[args.config], seed=1)
@@ -238,7 +286,8 @@ def main():
     tok_s = args.steps / dt
     log(f"decode {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
     wbytes = spec.weight_bytes_per_token()
-    dom = expert_gemv(ctx, spec)  # the model's own device copies (same host tensors)
+    # the model's own device copies (same host tensors)
+    dom = expert_gemv(ctx, spec, graphs=not args.no_graphs)
     log("dominant kernel", dom)
     model.close()
 
@@ -279,10 +328,11 @@ def main():
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
-                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": profiled_traffic(),
                      "kernel": dom["kernel"], "bytes_per_launch": dom["bytes_per_launch"],
                      "avg_us": round(dom["avg_us"], 3)},
         "stream_read_GBps": round(stream, 1),
+        "copy_GBps": round(copy_gbps, 1),
         "gemv_head_151936x1024_b1_GBps": big,
         "gemv": sweep,
         "cpu_baseline": cpu,
