@@ -717,13 +717,21 @@ int ihip_enqueue_moecombine(ihip_ctx* c, uint64_t d, uint64_t w, uint64_t y, int
 
 int ihip_enqueue_argmax(ihip_ctx* c, uint64_t v, int64_t n, uint64_t out)
 {
-  if (!c || n < 1) return fail(IHIP_E_ARG, "ihip_enqueue_argmax");
+  if (!c || n < 1 || n >= 0xffffffffLL) return fail(IHIP_E_ARG, "ihip_enqueue_argmax");
+  // blocks of at least 1024 values, at most ARGMAX_PARTS of them
+  const int64_t chunk = std::max<int64_t>(1024, (n + ARGMAX_PARTS - 1) / ARGMAX_PARTS);
+  const int parts = (int)((n + chunk - 1) / chunk);
   struct {
     const float* v;
     int* out;
     int64_t n;
-  } a = {(const float*)v, (int*)out, n};
-  return launch(c, "argmax", dim3(1), dim3(1024), &a);
+    uint64_t* part;
+    int64_t chunk;
+    int32_t parts, pad;
+  } a = {(const float*)v, (int*)out, n, (uint64_t*)c->scratch_argmax, chunk, parts, 0};
+  int rc = launch(c, "argmax_part", dim3((unsigned)parts), dim3(256), &a);
+  if (rc) return rc;
+  return launch(c, "argmax_final", dim3(1), dim3(256), &a);
 }
 
 }  // extern "C"

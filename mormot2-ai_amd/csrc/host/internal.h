@@ -62,6 +62,7 @@ struct ihip_ctx {
   uint64_t scratch_y = 0, scratch_y_bytes = 0;
   uint64_t scratch_q = 0, scratch_q_bytes = 0;
   uint64_t scratch_bad = 0;
+  uint64_t scratch_argmax = 0;  // [ARGMAX_PARTS] block results of argmax_part
   uint64_t scratch_attn = 0, scratch_attn_bytes = 0;
   bool capturing = false;
   hipGraph_t graphs[16] = {};
@@ -85,6 +86,9 @@ void repack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int6
 void unpack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int64_t count);
 
 // the Linear dispatch shared by the public entry points and the model
+// block results of the two-stage argmax
+constexpr int ARGMAX_PARTS = 1024;
+
 struct LinearCall {
   uint64_t x = 0;      // float activations [rows, in]
   uint64_t xq = 0;     // quantized activations (Q8 mode), 0: quantized here

@@ -161,6 +161,12 @@ int ihip_create(int device, ihip_ctx** out)
     return fail(IHIP_E_NOMEM, "hipMalloc");
   }
   c->scratch_bad = (uint64_t)bad;
+  void* am = nullptr;
+  if (hipMalloc(&am, ARGMAX_PARTS * 8) != hipSuccess) {
+    ihip_destroy(c);
+    return fail(IHIP_E_NOMEM, "hipMalloc");
+  }
+  c->scratch_argmax = (uint64_t)am;
   *out = c;
   return 0;
 }
@@ -176,7 +182,8 @@ void ihip_destroy(ihip_ctx* c)
   }
   for (auto& w : c->weights) (void)hipFree((void*)w.dev);
   for (auto a : c->allocations) (void)hipFree((void*)a);
-  for (uint64_t b : {c->scratch_x, c->scratch_y, c->scratch_q, c->scratch_bad, c->scratch_attn})
+  for (uint64_t b : {c->scratch_x, c->scratch_y, c->scratch_q, c->scratch_bad, c->scratch_attn,
+                     c->scratch_argmax})
     if (b) (void)hipFree((void*)b);
   for (auto ev : c->events)
     if (ev) (void)hipEventDestroy(ev);

@@ -949,51 +949,64 @@ struct ArgmaxArgs {
   const float* v;
   int* out;
   int64_t n;
+  uint64_t* part;  // [parts] block results
+  int64_t chunk;   // values per block of argmax_part
+  int32_t parts, pad;
 };
 
 // InferArgMax (sampler.pas:123-160): the float bits ordered as integers (the
 // lower 31 flipped when negative, -0 as +0), NaN skipped, the first index of
-// the maximum; all NaN gives 0. One block of 1024.
-extern "C" __global__ __launch_bounds__(1024) void argmax(ArgmaxArgs a)
+// the maximum; all NaN gives 0. A candidate is packed into one uint64 - the
+// key (sign flipped) above the inverted index - so the largest packed value
+// is the largest key at its lowest index, and 0 is "no candidate".
+__device__ __forceinline__ uint64_t argmax_pack(float f, int64_t i)
 {
-  __shared__ int bk[16];
-  __shared__ int64_t bi[16];
-  int best = INT32_MIN;
-  int64_t bidx = INT64_MAX;
-  for (int64_t i = threadIdx.x; i < a.n; i += blockDim.x) {
-    uint32_t b = float_bits(a.v[i]);
-    if ((b & 0x7fffffffu) > 0x7f800000u) continue;
-    int k = (int)(b ^ ((b >> 31) * 0x7fffffffu));
-    if (k == -1) k = 0;
-    if (k > best) {
-      best = k;
-      bidx = i;
-    }
-  }
-  for (int o = 1; o < 64; o <<= 1) {
-    int ok = __shfl_xor(best, o);
-    int64_t oi = __shfl_xor(bidx, o);
-    if (ok > best || (ok == best && oi < bidx)) {
-      best = ok;
-      bidx = oi;
-    }
-  }
-  int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    bk[w] = best;
-    bi[w] = bidx;
-  }
+  uint32_t b = float_bits(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 0;  // NaN
+  int k = (int)(b ^ ((b >> 31) * 0x7fffffffu));
+  if (k == -1) k = 0;
+  return ((uint64_t)((uint32_t)k ^ 0x80000000u) << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* sh)
+{
+  uint64_t o;
+  o = xpart<1>(v); v = o > v ? o : v;
+  o = xpart<2>(v); v = o > v ? o : v;
+  o = xpart<4>(v); v = o > v ? o : v;
+  o = xpart<8>(v); v = o > v ? o : v;
+  o = xpart<16>(v); v = o > v ? o : v;
+  o = xpart<32>(v); v = o > v ? o : v;
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int b = bk[0];
-    int64_t ix = bi[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++)
-      if (bk[i] > b || (bk[i] == b && bi[i] < ix)) {
-        b = bk[i];
-        ix = bi[i];
-      }
-    a.out[0] = ix == INT64_MAX ? 0 : (int)ix;
+  v = 0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) v = sh[i] > v ? sh[i] : v;
+  return v;
+}
+
+// stage 1: block b reduces values [b chunk, (b + 1) chunk)
+extern "C" __global__ __launch_bounds__(256) void argmax_part(ArgmaxArgs a)
+{
+  __shared__ uint64_t sh[4];
+  const int64_t i0 = (int64_t)blockIdx.x * a.chunk;
+  const int64_t i1 = min(a.n, i0 + a.chunk);
+  uint64_t best = 0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    uint64_t c = argmax_pack(a.v[i], i);
+    best = c > best ? c : best;
   }
+  best = block_max_u64(best, sh);
+  if (threadIdx.x == 0) a.part[blockIdx.x] = best;
+}
+
+// stage 2: the block results
+extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxArgs a)
+{
+  __shared__ uint64_t sh[4];
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < a.parts; i += 256) best = a.part[i] > best ? a.part[i] : best;
+  best = block_max_u64(best, sh);
+  if (threadIdx.x == 0) a.out[0] = best ? (int)(0xffffffffu - (uint32_t)best) : 0;
 }
 
 }  // namespace ihip

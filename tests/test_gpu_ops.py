@@ -149,7 +149,7 @@ def test_moecombine_and_argmax(ctx):
     for s in range(k):
         ref = (ref + (w[s] * d[s]).astype(np.float32)).astype(np.float32)
     assert np.array_equal(dy.download(np.float32, n), ref)
-    for case in range(4):
+    for case in range(8):
         v = rng.standard_normal(151936).astype(np.float32)
         if case == 1:
             v[[5, 70000]] = v.max() + 1  # tie: the first index
@@ -157,6 +157,16 @@ def test_moecombine_and_argmax(ctx):
             v[::3] = np.nan
         if case == 3:
             v[:] = np.nan
+        if case == 4:  # -0 before +0 at the top: equal keys, the first index
+            v = -np.abs(v) - 1
+            v[[77, 150000]] = [-0.0, 0.0]
+        if case == 5:  # one value; a short row
+            v = v[:1]
+        if case == 6:
+            v = v[:1000]
+        if case == 7:  # -inf everywhere but a NaN and +inf at the end
+            v[:] = -np.inf
+            v[-2:] = [np.nan, np.inf]
         dv, do = ctx.array(v), ctx.alloc(4)
         H.check(H.lib().ihip_enqueue_argmax(ctx.h, dv.ptr, v.size, do.ptr))
         assert int(do.download(np.int32, 1)[0]) == O.argmax(v)
