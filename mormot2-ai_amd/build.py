@@ -14,8 +14,11 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 # linear.hip is built once per weight type (IHIP_ONLY_FMT), in parallel
 LINEAR_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf16", "f16"]
-KERNELS = [("ops", "ops", [])] + [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()])
-                                   for f in LINEAR_FMTS]
+# gemm.hip (the MFMA prefill GEMM) once per quantized weight type
+GEMM_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k"]
+KERNELS = ([("ops", "ops", [])] +
+           [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in LINEAR_FMTS] +
+           [("gemm_" + f, "gemm", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in GEMM_FMTS])
 HOST = ["runtime", "backend", "model", "synth"]
 HIP_FLAGS = ["--genco", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", CSRC]
@@ -47,7 +50,7 @@ def _host(name):
 
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=8) as ex:
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 8)) as ex:
         kfut = {k[0]: ex.submit(_kernel, k) for k in KERNELS}
         hfut = [ex.submit(_host, h) for h in HOST]
         cos = {k: f.result() for k, f in kfut.items()}

@@ -299,6 +299,13 @@ int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind
   return launch(c, "quantize_q8_k", dim3((unsigned)((NB + 3) / 4), (unsigned)rows), dim3(256), &a);
 }
 
+// weight types of gemm.hip
+static bool gemm_fmt(int t)
+{
+  return t == DT_Q8_0 || t == DT_Q4_0 || t == DT_MXFP4 || t == DT_Q5_0 || t == DT_Q5_1 ||
+         t == DT_Q4_K || t == DT_Q6_K;
+}
+
 int enqueue_linear(ihip_ctx* c, const LinearCall& k)
 {
   if (!linear_ok(k.dtype, k.in) || k.out < 1 || k.out > INT32_MAX || k.rows < 1 || k.rows > 65535 ||
@@ -355,6 +362,25 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          (const float*)k.nw, k.eps, (const float*)k.res, (const float*)k.cw,
          k.cw ? (int32_t)k.rows : 0, 0};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
+  // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
+  if (batch && q8 && !k.items && k.rows >= GEMM_MIN_ROWS && gemm_fmt(k.dtype) && c->use_gemm) {
+    struct {
+      const uint8_t* w;
+      const uint8_t* xq;
+      const float* bias;
+      float* y;
+      int64_t stride;
+      int32_t out, in, rows, pad;
+      const void* items;
+      const int* perm;
+      int32_t x_per_slot, pad2;
+    } g = {(const uint8_t*)k.w, (const uint8_t*)xq, (const float*)k.bias, (float*)k.y, k.stride,
+           (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, nullptr, nullptr, 0, 0};
+    char gname[32];
+    snprintf(gname, sizeof gname, "gemm_%s", fmt_name(k.dtype));
+    return launch(c, gname, dim3((unsigned)((k.out + 63) / 64), (unsigned)((k.rows + 63) / 64)),
+                  dim3(256), &g);
+  }
   if (k.nw && (batch || k.in > 4096 || xq))
     return fail(IHIP_E_ARG, "EnqueueLinear: the fused rmsnorm takes one float row of at most 4096");
   if ((k.res || k.cw) && (batch || k.w2 || (k.ids && !k.cw)))

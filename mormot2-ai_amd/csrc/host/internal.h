@@ -49,6 +49,7 @@ struct Module {
 struct ihip_ctx {
   int device = 0;
   int cus = 256;
+  bool use_gemm = true;        // Q8 chunks of >= GEMM_MIN_ROWS rows on the MFMA GEMM (IHIP_GEMM=0: off)
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   hipStream_t stream = nullptr;
   std::vector<ihip::Module> modules;
@@ -88,6 +89,8 @@ void unpack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int6
 // the Linear dispatch shared by the public entry points and the model
 // block results of the two-stage argmax
 constexpr int ARGMAX_PARTS = 1024;
+// rows from which a Q8 Linear runs on the MFMA GEMM instead of 8-row GEMVs
+constexpr int GEMM_MIN_ROWS = 16;
 
 struct LinearCall {
   uint64_t x = 0;      // float activations [rows, in]

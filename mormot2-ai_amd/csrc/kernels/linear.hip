@@ -23,7 +23,7 @@
 // register butterfly (wave_sum) within the LPR lanes. Q8 mode with K-quants: the 8
 // groups of a super-block sit in 8 neighbouring lanes, whose integer sums
 // are added exactly before the one double product of the super-block.
-#include "common.h"
+#include "formats.h"
 
 namespace ihip {
 
@@ -59,119 +59,6 @@ struct LinArgs {
   const float* cw;
   int32_t kslots, pad2;
 };
-
-// ---------------------------------------------------------------- formats
-// A group of 32 values as raw registers, and its sums.
-
-struct Raw {
-  uint4 q0, q1;  // codes: 16 or 32 bytes
-  uint32_t a, b, c, d;  // scales, high bits, header words
-};
-
-template <int F>
-__device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, int64_t o,
-                                           int G, int g, int64_t in, Raw& r)
-{
-  int64_t og = o * G + g;
-  if constexpr (F == DT_Q8_0) {
-    const uint4* p = (const uint4*)(w + o * in + (int64_t)g * 32);
-    r.q0 = p[0];
-    r.q1 = p[1];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
-  } else if constexpr (F == DT_Q4_0) {
-    r.q0 = ((const uint4*)w)[og];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
-  } else if constexpr (F == DT_MXFP4) {
-    r.q0 = ((const uint4*)w)[og];
-    r.a = (w + rg.s)[og];
-  } else if constexpr (F == DT_Q5_0) {
-    r.q0 = ((const uint4*)w)[og];
-    r.b = ((const uint32_t*)(w + rg.h))[og];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
-  } else if constexpr (F == DT_Q5_1) {
-    r.q0 = ((const uint4*)w)[og];
-    r.b = ((const uint32_t*)(w + rg.h))[og];
-    r.a = ((const uint32_t*)(w + rg.s))[og];
-  } else if constexpr (F == DT_Q4_K) {
-    r.q0 = ((const uint4*)w)[og];
-    r.q1 = ((const uint4*)(w + rg.s))[o * (G >> 3) + (g >> 3)];
-  } else if constexpr (F == DT_Q6_K) {
-    int64_t ob = o * (G >> 3) + (g >> 3);
-    r.q0 = ((const uint4*)w)[og];
-    uint2 h = ((const uint2*)(w + rg.h))[og];
-    r.b = h.x;
-    r.c = h.y;
-    r.a = ((const uint16_t*)(w + rg.s))[ob * 8 + (g & 7)];
-    r.d = ((const uint16_t*)(w + rg.s2))[ob];
-  }
-}
-
-// float weights: 32 values of row o, group g (F32 128 bytes, BF16/F16 64)
-template <int F>
-__device__ __forceinline__ void load_fgroup(const uint8_t* w, int64_t o, int g, int64_t in,
-                                            float (&v)[32])
-{
-  if constexpr (F == DT_F32) {
-    const float4* p = (const float4*)(w + (o * in + (int64_t)g * 32) * 4);
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      float4 t = p[k];
-      v[4 * k] = t.x;
-      v[4 * k + 1] = t.y;
-      v[4 * k + 2] = t.z;
-      v[4 * k + 3] = t.w;
-    }
-  } else {
-    const uint4* p = (const uint4*)(w + (o * in + (int64_t)g * 32) * 2);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      uint4 t = p[k];
-      uint32_t u[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        if constexpr (F == DT_BF16) {
-          v[8 * k + 2 * j] = bits_float(u[j] << 16);
-          v[8 * k + 2 * j + 1] = bits_float(u[j] & 0xffff0000u);
-        } else {
-          v[8 * k + 2 * j] = half_to_float(u[j] & 0xffffu);
-          v[8 * k + 2 * j + 1] = half_to_float(u[j] >> 16);
-        }
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ uint32_t comp(const uint4& v, int d)
-{
-  return d == 0 ? v.x : (d == 1 ? v.y : (d == 2 ? v.z : v.w));
-}
-
-// the fifth bits of 4 values (bits 0..3 of b) moved to bit 4 of each byte
-__device__ __forceinline__ uint32_t spread5(uint32_t b)
-{
-  return ((b & 1u) << 4) | ((b & 2u) << 11) | ((b & 4u) << 18) | ((b & 8u) << 25);
-}
-
-// the 4 code bytes of dword d of the low (hi = 0: values 4d..4d+3) or high
-// (hi = 1: values 16 + 4d..) half of a group, as unsigned/signed int8
-template <int F>
-__device__ __forceinline__ uint32_t code_bytes(const Raw& r, int d, int hi)
-{
-  if constexpr (F == DT_Q8_0) {
-    return comp(hi ? r.q1 : r.q0, d);
-  } else {
-    uint32_t q = comp(r.q0, d);
-    uint32_t nib = hi ? ((q >> 4) & 0x0F0F0F0Fu) : (q & 0x0F0F0F0Fu);
-    if constexpr (F == DT_MXFP4)
-      return mxfp4_bytes(nib);
-    else if constexpr (F == DT_Q5_0 || F == DT_Q5_1)
-      return nib | spread5((r.b >> (hi * 16 + 4 * d)) & 15u);
-    else if constexpr (F == DT_Q6_K)
-      return nib | ((((hi ? r.c : r.b) >> (2 * d)) & 0x03030303u) << 4);
-    else
-      return nib;
-  }
-}
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
 // sx their sum.

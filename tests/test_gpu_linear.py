@@ -118,6 +118,31 @@ def test_linear_q8_mode_cpu_bits(ctx, dtype):
     assert differ <= max(2, total // 1000), (differ, total)
 
 
+GEMM_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K]
+GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100)]
+
+
+@pytest.mark.parametrize("dtype", GEMM_FMTS)
+def test_gemm_q8_mode_cpu_bits(ctx, dtype):
+    # chunks of >= 16 rows run on the MFMA GEMM: exact int32 group sums from
+    # the int8 matrix cores, the scales in double, as the CPU
+    rng = np.random.default_rng(19)
+    total, differ = 0, 0
+    for rows, cols, out in GEMM_SHAPES:
+        if not fits(dtype, cols):
+            continue
+        w = weights(dtype, out, cols, rows * 5 + cols + out)
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        b = rng.standard_normal(out).astype(np.float32)
+        y = ctx.linear(x, w, dtype, out, b, mode=H.MODE_Q8)
+        ref = O.linear(x, w, dtype, out, b)
+        u = ulp_diff(y, ref)
+        assert u.max() <= 1, (H.NAMES[dtype], rows, cols, out, int(u.max()))
+        total += u.size
+        differ += int(np.count_nonzero(u))
+    assert differ <= max(2, total // 1000), (differ, total)
+
+
 @pytest.mark.parametrize("name,wkey,ykey,dtype,atol,rtol", [
     ("q8", "linear/weight", "linear/y", H.Q8_0, 1e-5, 1e-5),
     ("q4", "linear/weight", "linear/y", H.Q4_0, 1e-5, 1e-5),
