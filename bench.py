@@ -29,6 +29,7 @@ sys.path[:0] = [os.path.join(ROOT, "mormot2-ai_amd"), os.path.join(ROOT, "tests"
 
 METRIC = "decode tok/s + quant GEMV HBM GB/s (% peak), Qwen3-30B-A3B-shape Q4_K_M"
 HBM_PEAK = 8000.0  # GB/s, MI355X published
+INT8_PEAK = 5000.0  # TOP/s, MI355X dense int8 MFMA, published
 SWEEP_SHAPES = [(3072, 1024), (1024, 3072), (6144, 2048), (2880, 2880), (151936, 1024)]
 
 
@@ -297,11 +298,19 @@ def main():
             for out, cols in SWEEP_SHAPES:
                 if cols % H.BLOCK[dtype][0]:
                     continue  # 2880 is no whole number of 256-value super-blocks
-                for rows, mode in ((1, H.MODE_Q8), (1, H.MODE_F32), (8, H.MODE_Q8)):
+                for rows, mode in ((1, H.MODE_Q8), (1, H.MODE_F32), (8, H.MODE_Q8),
+                                   (512, H.MODE_Q8)):
                     gbps, us = gemv_case(ctx, dtype, out, cols, rows, mode)
                     key = f"{H.NAMES[dtype]} {out}x{cols} b{rows} {'q8' if mode else 'f32'}"
-                    sweep[key] = {"GBps": round(gbps, 1), "us": round(us, 2),
-                                  "frac": round(gbps / HBM_PEAK, 3)}
+                    if rows >= 16:
+                        # the MFMA GEMM: int8 operations per second against the
+                        # dense int8 MFMA peak (the instruction it runs on)
+                        tops = 2.0 * rows * cols * out / (us * 1e-6) / 1e12
+                        sweep[key] = {"TOPs": round(tops, 1), "us": round(us, 2),
+                                      "mfma_frac": round(tops / INT8_PEAK, 4)}
+                    else:
+                        sweep[key] = {"GBps": round(gbps, 1), "us": round(us, 2),
+                                      "frac": round(gbps / HBM_PEAK, 3)}
                     log(key, sweep[key])
 
     cpu = None

@@ -306,6 +306,11 @@ static bool gemm_fmt(int t)
          t == DT_Q4_K || t == DT_Q6_K;
 }
 
+bool gemm_runs(const ihip_ctx* c, int dtype, int mode)
+{
+  return c->use_gemm && (mode & 1) == IHIP_MODE_Q8 && gemm_fmt(dtype);
+}
+
 int enqueue_linear(ihip_ctx* c, const LinearCall& k)
 {
   if (!linear_ok(k.dtype, k.in) || k.out < 1 || k.out > INT32_MAX || k.rows < 1 || k.rows > 65535 ||
@@ -363,7 +368,10 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          k.cw ? (int32_t)k.rows : 0, 0};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
-  if (batch && q8 && !k.items && k.rows >= GEMM_MIN_ROWS && gemm_fmt(k.dtype) && c->use_gemm) {
+  if (k.items && k.item_rows > 8 && !(q8 && gemm_runs(c, k.dtype, mode)))
+    return fail(IHIP_E_ARG, "EnqueueLinear: items of more than 8 slots need the GEMM");
+  if (batch && q8 && gemm_runs(c, k.dtype, mode) &&
+      (k.items ? k.item_rows > 8 : k.rows >= GEMM_MIN_ROWS)) {
     struct {
       const uint8_t* w;
       const uint8_t* xq;
@@ -375,11 +383,13 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       const int* perm;
       int32_t x_per_slot, pad2;
     } g = {(const uint8_t*)k.w, (const uint8_t*)xq, (const float*)k.bias, (float*)k.y, k.stride,
-           (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, nullptr, nullptr, 0, 0};
+           (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, (const void*)k.items,
+           (const int*)k.perm, k.x_per_slot, 0};
+    if (k.items && k.item_rows > 64) return fail(IHIP_E_ARG, "EnqueueLinear: items of at most 64 slots");
     char gname[32];
     snprintf(gname, sizeof gname, "gemm_%s", fmt_name(k.dtype));
-    return launch(c, gname, dim3((unsigned)((k.out + 63) / 64), (unsigned)((k.rows + 63) / 64)),
-                  dim3(256), &g);
+    const unsigned gy = (unsigned)(k.items ? k.nitems : (k.rows + 63) / 64);
+    return launch(c, gname, dim3((unsigned)((k.out + 63) / 64), gy), dim3(256), &g);
   }
   if (k.nw && (batch || k.in > 4096 || xq))
     return fail(IHIP_E_ARG, "EnqueueLinear: the fused rmsnorm takes one float row of at most 4096");

@@ -106,6 +106,7 @@ struct LinearCall {
   uint64_t items = 0;  // grouped experts: int4 work items (expert, start, count)
   uint64_t perm = 0;   // and the slots sorted by expert; rows = slots
   int64_t nitems = 0;
+  int item_rows = 8;   // the most slots per item (moe_plan's chunk): 8, or 64 for the GEMM
   // fused SwiGLU: y = swiglu(x W^T + bias, x W2^T + bias2) (one row per block)
   uint64_t w2 = 0, bias2 = 0;
   float alpha = 1.0f, limit = 0.0f;
@@ -120,6 +121,9 @@ struct LinearCall {
   uint64_t cw = 0;
 };
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
+// whether enqueue_linear runs a Q8 chunk of this weight type on the MFMA GEMM
+// (and takes grouped items of up to 64 slots)
+bool gemm_runs(const ihip_ctx* c, int dtype, int mode);
 // which activation quantizer a weight type needs in Q8 mode: -1 none (float
 // weights), 0 Q8_0, 1 Q8_K
 int q8_kind(int dtype);

@@ -57,6 +57,7 @@ struct ihip_model {
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
   bool graph_ready = false;
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
+  int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
   double prefill_ms = 0, decode_ms = 0;
 };
 
@@ -192,12 +193,14 @@ static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int
   k.y = y; k.mode = m->mode; k.ids = ids; k.stride = stride; k.x_per_slot = x_div;
   k.nexp = m->d.experts;
   if (slots > m->d.experts_used) {
-    // a prompt chunk: the slots grouped by expert (moe_plan), 8 rows per
-    // work item, so an expert's matrix is read once per 8 of its tokens
+    // a prompt chunk: the slots grouped by expert (moe_plan), up to
+    // item_rows rows per work item (8 for the 8-row GEMV, 64 for the GEMM),
+    // so an expert's matrix is read once per that many of its tokens
     k.ids = 0;
     k.items = m->items;
     k.perm = m->perm;
-    k.nitems = (slots + 7) / 8 + m->d.experts;
+    k.item_rows = m->item_rows;
+    k.nitems = (slots + m->item_rows - 1) / m->item_rows + m->d.experts;
   }
   if (m->mode == IHIP_MODE_Q8 && q8_kind(dt) >= 0) {
     if (!quantized) {
@@ -422,9 +425,9 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
           const int* ids;
           int* perm;
           void* items;
-          int32_t slots, experts, max_items, pad;
+          int32_t slots, experts, max_items, chunk;
         } pa = {(const int*)m->ids, (int*)m->perm, (void*)m->items, (int32_t)(n * K), (int32_t)E,
-                (int32_t)((n * K + 7) / 8 + E), 0};
+                (int32_t)((n * K + m->item_rows - 1) / m->item_rows + E), m->item_rows};
         if ((rc = launch(m->c, "moe_plan", dim3(1), dim3(256), &pa))) return rc;
         // gate and up: slot s = row s / K, expert ids[s], grouped by expert
         bool q0 = false;
@@ -656,6 +659,14 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
     return bad(rc);
   if (any_moe && (d.experts > 4096 || N * d.experts_used > 4096))
     return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or slots per chunk"));
+  // a prompt chunk's experts on the MFMA GEMM when every expert matrix can
+  // run there: work items of 64 slots
+  bool all_gemm = any_moe;
+  for (const DevLayer& L : m->L)
+    if (L.moe)
+      all_gemm = all_gemm && gemm_runs(c, L.egd, mode) && gemm_runs(c, L.eud, mode) &&
+                 gemm_runs(c, L.edd, mode);
+  m->item_rows = all_gemm ? 64 : 8;
   const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
   const uint64_t qrow = qin + 4 * (qin / 32);
   if ((rc = dalloc(m, N * qrow, m->xq0)) || (rc = dalloc(m, N * qrow, m->xqk)) ||

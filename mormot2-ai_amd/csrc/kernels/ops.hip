@@ -1040,43 +1040,67 @@ extern "C" __global__ __launch_bounds__(256) void stream_read(StreamArgs a)
 // ------------------------------------------------------- MoE prompt plan
 struct PlanArgs {
   const int* ids;  // [slots] expert of each slot (route, sorted per token)
-  int* perm;       // [slots] the slots sorted by expert, in slot order within one
-  int4* items;     // [max_items] (expert, start in perm, count <= 8), count 0 after the last
-  int32_t slots, experts, max_items, pad;
+  int* perm;       // [slots] the slots grouped by expert (any order within one)
+  int4* items;     // [max_items] (expert, start in perm, count <= chunk), count 0 after the last
+  int32_t slots, experts, max_items, chunk;
 };
 
-// the experts of a prompt chunk grouped for the batched GEMV (the host-side
-// expert loop of model.qwen3.cuda.pas:1077-1150, on the device): a count per
-// expert, their offsets, then per expert its slots in order - thread e
-// collects expert e, so the order is deterministic
+// the work items of a grouped expert Linear (EnqueueMoe's grouping on the
+// device, model.qwen3.cuda.pas:1077-1150): a histogram of the slots per
+// expert, a scan for their offsets and for the items' offsets, then every
+// slot placed by a counter of its expert. A slot's place within its expert
+// changes no output row (each row is its own GEMV/GEMM row), so the counters
+// need no order. One block.
 extern "C" __global__ __launch_bounds__(256) void moe_plan(PlanArgs a)
 {
-  __shared__ int cnt[4096];
-  __shared__ int off[4096];
-  __shared__ int sid[4096];
-  const int t = threadIdx.x, E = a.experts, S = a.slots;
-  for (int e = t; e < E; e += blockDim.x) cnt[e] = 0;
-  for (int s = t; s < S; s += blockDim.x) sid[s] = a.ids[s];
+  __shared__ int cnt[4096], off[4096], fill[4096];
+  __shared__ int part[256], ipart[256];
+  __shared__ int ntot;
+  const int t = threadIdx.x, E = a.experts, S = a.slots, CH = a.chunk;
+  for (int e = t; e < E; e += 256) cnt[e] = fill[e] = 0;
   __syncthreads();
-  for (int s = t; s < S; s += blockDim.x) {
-    int e = sid[s];
+  for (int s = t; s < S; s += 256) {
+    const int e = a.ids[s];
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
+  // thread t owns experts [e0, e1): its sums, scanned over the threads
+  const int per = (E + 255) / 256, e0 = min(E, t * per), e1 = min(E, e0 + per);
+  int sc = 0, si = 0;
+  for (int e = e0; e < e1; e++) {
+    sc += cnt[e];
+    si += (cnt[e] + CH - 1) / CH;
+  }
+  part[t] = sc;
+  ipart[t] = si;
+  __syncthreads();
   if (t == 0) {
-    int run = 0, it = 0;
-    for (int e = 0; e < E; e++) {
-      off[e] = run;
-      for (int st = 0; st < cnt[e] && it < a.max_items; st += 8)
-        a.items[it++] = make_int4(e, run + st, min(8, cnt[e] - st), 0);
-      run += cnt[e];
+    int rs = 0, ri = 0;
+    for (int i = 0; i < 256; i++) {
+      const int c = part[i], ci = ipart[i];
+      part[i] = rs;
+      ipart[i] = ri;
+      rs += c;
+      ri += ci;
     }
-    for (; it < a.max_items; it++) a.items[it] = make_int4(0, 0, 0, 0);
+    ntot = ri;
   }
   __syncthreads();
-  for (int e = t; e < E; e += blockDim.x) {
-    int k = off[e];
-    for (int s = 0; s < S; s++)
-      if (sid[s] == e) a.perm[k++] = s;
+  {
+    int rs = part[t], ri = ipart[t];
+    for (int e = e0; e < e1; e++) {
+      off[e] = rs;
+      for (int st = 0; st < cnt[e]; st += CH)
+        if (ri + st / CH < a.max_items)
+          a.items[ri + st / CH] = make_int4(e, rs + st, min(CH, cnt[e] - st), 0);
+      rs += cnt[e];
+      ri += (cnt[e] + CH - 1) / CH;
+    }
   }
+  __syncthreads();
+  for (int s = t; s < S; s += 256) {
+    const int e = a.ids[s];
+    if (e >= 0 && e < E) a.perm[off[e] + atomicAdd(&fill[e], 1)] = s;
+  }
+  for (int it = ntot + t; it < a.max_items; it += 256) a.items[it] = make_int4(0, 0, 0, 0);
 }
