@@ -359,13 +359,22 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     double eps;
     const float* res;
     const float* cw;
-    int32_t kslots, pad2;
+    int32_t kslots;
+    int32_t nseg;
+    const uint8_t* wseg[3];
+    const float* bseg[3];
+    float* yseg[3];
+    int32_t oseg[3], pad3;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
          (const uint8_t*)k.w2, (const float*)k.bias2, k.alpha, k.limit, (int*)c->scratch_bad,
          (const float*)k.nw, k.eps, (const float*)k.res, (const float*)k.cw,
-         k.cw ? (int32_t)k.rows : 0, 0};
+         k.cw ? (int32_t)k.rows : 0, k.nseg > 1 ? k.nseg : 0,
+         {(const uint8_t*)k.wseg[0], (const uint8_t*)k.wseg[1], (const uint8_t*)k.wseg[2]},
+         {(const float*)k.bseg[0], (const float*)k.bseg[1], (const float*)k.bseg[2]},
+         {(float*)k.yseg[0], (float*)k.yseg[1], (float*)k.yseg[2]},
+         {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]}, 0};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
   if (k.items && k.item_rows > 8 && !(q8 && gemm_runs(c, k.dtype, mode)))
@@ -395,6 +404,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     return fail(IHIP_E_ARG, "EnqueueLinear: the fused rmsnorm takes one float row of at most 4096");
   if ((k.res || k.cw) && (batch || k.w2 || (k.ids && !k.cw)))
     return fail(IHIP_E_ARG, "EnqueueLinear: a residual add takes one plain or combined row");
+  if (k.nseg > 1 && (k.nseg > 3 || batch || k.ids || k.w2 || k.res || k.cw))
+    return fail(IHIP_E_ARG, "EnqueueLinear: 2..3 matrices take one plain row");
   char name[64];
   const int64_t rpw = 64 / lpr, tiles = (k.out + rpw - 1) / rpw;
   if (k.cw) {
@@ -412,17 +423,28 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
            mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
            batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
-  int64_t wgs = std::min<int64_t>((tiles + 3) / 4, (int64_t)c->cus * 8);
+  int64_t tiles_all = tiles;
+  if (k.nseg > 1) {
+    gy = (unsigned)k.nseg;
+    tiles_all = 0;
+    for (int i = 0; i < k.nseg; i++) {
+      if (k.oseg[i] < 1 || !k.wseg[i] || !k.yseg[i]) return fail(IHIP_E_ARG, "EnqueueLinear: matrix");
+      tiles_all = std::max<int64_t>(tiles_all, (k.oseg[i] + rpw - 1) / rpw);
+    }
+  }
+  int64_t wgs = std::min<int64_t>((tiles_all + 3) / 4, (int64_t)c->cus * 8);
   if (!batch) {
     // one-row blocks stage the activation row once per block: give each wave
     // the T tiles of a step (the kernel's T), as long as the launch keeps
-    // about two blocks per CU
+    // about two blocks per CU. Matrices of one launch (nseg) are sized by
+    // the largest; the blocks of a smaller one past its rows end at once.
     const int T = k.w2 ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
-    const int64_t want = ((int64_t)c->cus * c->gemv_blocks_per_cu + gy - 1) / gy;
-    wgs = std::min(wgs, std::max<int64_t>((tiles + 4 * T - 1) / (4 * T), want));
+    const unsigned share = k.nseg > 1 ? 1u : gy;
+    const int64_t want = ((int64_t)c->cus * c->gemv_blocks_per_cu + share - 1) / share;
+    wgs = std::min(wgs, std::max<int64_t>((tiles_all + 4 * T - 1) / (4 * T), want));
     // and no more blocks than the chip holds at once: the waves walk the
     // rest of the rows, each block stages its row once
-    const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) + gy - 1) / gy;
+    const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) + share - 1) / share;
     wgs = std::max<int64_t>(1, std::min(wgs, hold));
   }
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);

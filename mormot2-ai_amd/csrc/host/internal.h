@@ -119,6 +119,11 @@ struct LinearCall {
   // combine: rows = slots, ids [slots] (<= 8), x [slots, in]; y [out] =
   // res + the slot-order sum of cw[s] * the expert rows (TDecoderModel.Experts)
   uint64_t cw = 0;
+  // nseg > 1: one row through up to 3 matrices of this type in one launch,
+  // matrix s = (wseg[s], oseg[s] outputs, yseg[s], bseg[s]); w/out/y/bias unused
+  int nseg = 0;
+  uint64_t wseg[3] = {}, bseg[3] = {}, yseg[3] = {};
+  int64_t oseg[3] = {};
 };
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // whether enqueue_linear runs a Q8 chunk of this weight type on the MFMA GEMM

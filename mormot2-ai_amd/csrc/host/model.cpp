@@ -276,10 +276,33 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
   for (int l = 0; l < d.layers; l++) {
     const DevLayer& L = m->L[l];
     // attention block (decoder.pas:2625-2702)
-    if ((rc = normed(L.input_norm, L.qd, L.q, qw, L.qb, m->q)) ||
-        (rc = normed(L.input_norm, L.kd, L.k, kvw, L.kb, m->k)) ||
-        (rc = normed(L.input_norm, L.vd, L.v, kvw, L.vb, m->v)))
-      return rc;
+    {
+      // q, k and v: the matrices of one weight type in one launch
+      const int dts[3] = {L.qd, L.kd, L.vd};
+      const uint64_t ws[3] = {L.q, L.k, L.v}, bs[3] = {L.qb, L.kb, L.vb},
+                     ys[3] = {m->q, m->k, m->v};
+      const int64_t os[3] = {qw, kvw, kvw};
+      bool done[3] = {false, false, false};
+      for (int i = 0; i < 3 && !rc; i++) {
+        if (done[i]) continue;
+        LinearCall k;
+        k.x = m->x; k.rows = 1; k.in = H; k.dtype = dts[i]; k.mode = m->mode;
+        k.nw = L.input_norm; k.eps = d.rms_eps;
+        for (int j = i; j < 3; j++)
+          if (!done[j] && dts[j] == dts[i]) {
+            k.wseg[k.nseg] = ws[j]; k.bseg[k.nseg] = bs[j]; k.yseg[k.nseg] = ys[j];
+            k.oseg[k.nseg] = os[j]; k.nseg++;
+            done[j] = true;
+          }
+        if (k.nseg == 1) {
+          k.w = k.wseg[0]; k.bias = k.bseg[0]; k.y = k.yseg[0]; k.out = k.oseg[0]; k.nseg = 0;
+        } else {
+          k.w = k.wseg[0]; k.y = k.yseg[0]; k.out = k.oseg[0];
+        }
+        rc = enqueue_linear(m->c, k);
+      }
+      if (rc) return rc;
+    }
     if (hd == 64 || hd == 128) {
       // head norms, RoPE, cache store and the ranges in one launch, then the merge
       AttnOne o;

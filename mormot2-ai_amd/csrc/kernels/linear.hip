@@ -57,7 +57,14 @@ struct LinArgs {
   // combine: slot s < kslots reads x row s and expert ids[s]; y[o] = res[o] +
   // the sum over the slots, in order, of cw[s] * value_s
   const float* cw;
-  int32_t kslots, pad2;
+  int32_t kslots;
+  // matrices of one launch (R = 1, nseg > 1): blockIdx.y = matrix s with
+  // weights wseg[s], oseg[s] outputs into yseg[s], bias bseg[s]
+  int32_t nseg;
+  const uint8_t* wseg[3];
+  const float* bseg[3];
+  float* yseg[3];
+  int32_t oseg[3], pad3;
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
@@ -592,6 +599,8 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const int G = a.in >> 5;
   const uint8_t* w = a.w;
   const float* bias = a.bias;
+  int out = a.out;
+  float* yp = a.y;
   int64_t xrow0, yrow0;
   int nrows;
   int pstart = -1;  // grouped: the first entry of perm
@@ -620,24 +629,34 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     xrow0 = a.x_per_slot ? slot / a.x_per_slot : 0;
     yrow0 = slot;
     nrows = 1;
+  } else if (R == 1 && a.nseg > 1) {
+    // several matrices of this type over the same row: blockIdx.y = matrix
+    const int sg = blockIdx.y;
+    w = a.wseg[sg];
+    bias = a.bseg[sg];
+    out = a.oseg[sg];
+    yp = a.yseg[sg];
+    xrow0 = yrow0 = 0;
+    nrows = 1;
   } else {
     xrow0 = (int64_t)blockIdx.y * R;
     yrow0 = xrow0;
     nrows = min(R, a.rows - (int)xrow0);
   }
-  const Regions rg = regions(F, a.out, a.in);
-  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
+  const Regions rg = regions(F, out, a.in);
+  const int64_t tiles = ((int64_t)out + rpw - 1) / rpw;
   const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
   const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
+    if ((int64_t)blockIdx.x * (blockDim.x >> 6) >= tiles) return;  // the whole block: no tile
     // T tiles per wave step, their weight loads issued together (and the
     // first ones before the activation row is read), so a wave keeps several
     // 16-byte loads per lane in flight
     constexpr int T = GLU ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
     // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
     const uint8_t* w2 = GLU ? a.w2 + (w - a.w) : nullptr;
-    const float* bias2 = a.bias2 ? a.bias2 + expert * a.out : nullptr;
+    const float* bias2 = a.bias2 ? a.bias2 + expert * out : nullptr;
     XGroup xg[U];
     Raw raw[T][U], raw2[T][U];
     __shared__ __align__(16) uint8_t xs[xs_bytes<F, MODE>()];
@@ -648,7 +667,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
                         quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in, a.nw, st);
     int64_t tb = wid;
-    load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, a.out, raw,
+    load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
     stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
                          1 + (int)xrow0);
@@ -663,7 +682,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       for (int i = 0; i < T; i++) {
         const int64_t t = tb + (int64_t)i * nw;
         const int64_t o = t * rpw + rsub;
-        const bool valid = t < tiles && o < a.out;
+        const bool valid = t < tiles && o < out;
         double v = row_value<F, MODE, U>(w, raw[i], o, valid, xg, lr, lpr, G, a.in);
         double v2 = 0.0;
         if constexpr (GLU) v2 = row_value<F, MODE, U>(w2, raw2[i], o, valid, xg, lr, lpr, G, a.in);
@@ -675,12 +694,12 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
             r = swiglu_value(r, (float)v2, a.alpha, a.limit);
           }
           if (a.res) r = a.res[o] + r;
-          a.y[yrow0 * a.out + o] = r;
+          yp[yrow0 * out + o] = r;
         }
       }
       tb += (int64_t)T * nw;
       if (tb < tiles)
-        load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, a.out,
+        load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out,
                                  raw, raw2);
     }
   } else {
@@ -699,7 +718,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     }
     for (int64_t t = wid; t < tiles; t += nw) {
       int64_t o = t * rpw + rsub;
-      bool valid = o < a.out;
+      bool valid = o < out;
       float accf[R];
       double accd[R], tot[R];
 #pragma unroll
@@ -741,7 +760,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
             v = row_total<F, MODE>(lpr, Raw{}, 0.f, false, accf[r], accd[r], 0, 0, 0);
           if (lr == 0 && valid) {
             if (bias) v = (double)bias[o] + v;
-            a.y[yr[r] * a.out + o] = (float)v;
+            yp[yr[r] * out + o] = (float)v;
           }
         }
       }
