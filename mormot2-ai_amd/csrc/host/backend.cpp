@@ -306,6 +306,17 @@ static bool gemm_fmt(int t)
          t == DT_Q4_K || t == DT_Q6_K;
 }
 
+bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in)
+{
+  if (!linear_ok(a, in) || !linear_ok(b, in)) return false;
+  int lpr = 64, U = 1;
+  pick_lpr(in / 32, lpr, U);
+  char name[64];
+  snprintf(name, sizeof name, "gemv_%s_%s_%s_norm_u%d", fmt_name(a), fmt_name(b),
+           (mode & 1) == IHIP_MODE_Q8 ? "q8" : "f32", U);
+  return kernel(c, name) != nullptr;
+}
+
 bool gemm_runs(const ihip_ctx* c, int dtype, int mode)
 {
   return c->use_gemm && (mode & 1) == IHIP_MODE_Q8 && gemm_fmt(dtype);
@@ -364,7 +375,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     const uint8_t* wseg[3];
     const float* bseg[3];
     float* yseg[3];
-    int32_t oseg[3], pad3;
+    int32_t oseg[3];
+    int32_t nseg1;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
@@ -374,7 +386,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          {(const uint8_t*)k.wseg[0], (const uint8_t*)k.wseg[1], (const uint8_t*)k.wseg[2]},
          {(const float*)k.bseg[0], (const float*)k.bseg[1], (const float*)k.bseg[2]},
          {(float*)k.yseg[0], (float*)k.yseg[1], (float*)k.yseg[2]},
-         {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]}, 0};
+         {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]},
+         k.dtype2 ? k.nseg1 : k.nseg};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
   if (k.items && k.item_rows > 8 && !(q8 && gemm_runs(c, k.dtype, mode)))
@@ -419,9 +432,16 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     return launch(c, name, dim3((unsigned)std::max<int64_t>(1, std::min(tiles, hold))), dim3(256), &a,
                   (size_t)xbytes);
   }
-  snprintf(name, sizeof name, "gemv_%s_%s_%s%su%d", fmt_name(k.dtype),
-           mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
-           batch ? "b8" : (k.w2 ? "glu_" : ""), U);
+  if (k.dtype2) {
+    if (!k.nw || k.nseg < 2 || k.nseg1 < 1 || k.nseg1 >= k.nseg || !linear_ok(k.dtype2, k.in))
+      return fail(IHIP_E_ARG, "EnqueueLinear: two types take normed matrices of both");
+    snprintf(name, sizeof name, "gemv_%s_%s_%s_norm_u%d", fmt_name(k.dtype), fmt_name(k.dtype2),
+             mode == IHIP_MODE_Q8 ? "q8" : "f32", U);
+  } else {
+    snprintf(name, sizeof name, "gemv_%s_%s_%s%su%d", fmt_name(k.dtype),
+             mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
+             batch ? "b8" : (k.w2 ? "glu_" : ""), U);
+  }
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
   int64_t tiles_all = tiles;
   if (k.nseg > 1) {

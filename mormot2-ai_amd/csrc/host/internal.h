@@ -124,7 +124,12 @@ struct LinearCall {
   int nseg = 0;
   uint64_t wseg[3] = {}, bseg[3] = {}, yseg[3] = {};
   int64_t oseg[3] = {};
+  // a two-type launch (a kernel for the pair must exist): matrices nseg1..
+  // are of dtype2
+  int dtype2 = 0, nseg1 = 0;
 };
+// whether one launch can take matrices of types a then b (gemv_<a>_<b>_*)
+bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in);
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
 // whether enqueue_linear runs a Q8 chunk of this weight type on the MFMA GEMM
 // (and takes grouped items of up to 64 slots)

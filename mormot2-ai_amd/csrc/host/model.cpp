@@ -283,6 +283,25 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
                      ys[3] = {m->q, m->k, m->v};
       const int64_t os[3] = {qw, kvw, kvw};
       bool done[3] = {false, false, false};
+      // two types with a kernel for the pair (Q4_K_M: q, k Q4_K and v Q6_K)
+      int t2 = 0;
+      for (int j = 1; j < 3; j++)
+        if (dts[j] != dts[0]) t2 = t2 ? (dts[j] == t2 ? t2 : -1) : dts[j];
+      if (t2 > 0 && gemv_pair(m->c, dts[0], t2, m->mode, H)) {
+        LinearCall k;
+        k.x = m->x; k.rows = 1; k.in = H; k.dtype = dts[0]; k.dtype2 = t2; k.mode = m->mode;
+        k.nw = L.input_norm; k.eps = d.rms_eps;
+        for (int pass = 0; pass < 2; pass++)
+          for (int j = 0; j < 3; j++)
+            if ((dts[j] == dts[0]) == (pass == 0)) {
+              k.wseg[k.nseg] = ws[j]; k.bseg[k.nseg] = bs[j]; k.yseg[k.nseg] = ys[j];
+              k.oseg[k.nseg] = os[j]; k.nseg++;
+              if (pass == 0) k.nseg1++;
+              done[j] = true;
+            }
+        k.w = k.wseg[0]; k.y = k.yseg[0]; k.out = k.oseg[0];
+        rc = enqueue_linear(m->c, k);
+      }
       for (int i = 0; i < 3 && !rc; i++) {
         if (done[i]) continue;
         LinearCall k;

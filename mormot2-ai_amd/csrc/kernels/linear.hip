@@ -64,7 +64,8 @@ struct LinArgs {
   const uint8_t* wseg[3];
   const float* bseg[3];
   float* yseg[3];
-  int32_t oseg[3], pad3;
+  int32_t oseg[3];
+  int32_t nseg1;  // a two-type launch: matrices 0..nseg1-1 of the first type, the rest of the second
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
@@ -974,6 +975,17 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   IHIP_CMB(PFX##_cmb_u3, F, M, 3) \
   IHIP_CMB(PFX##_cmb_u4, F, M, 4)
 
+// q, k and v of a Q4_K_M model in one launch: Q4_K matrices, then Q6_K ones
+#define IHIP_GEMV_MIX(NAME, F, F2, M, U)                                              \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a)               \
+  {                                                                                    \
+    if ((int)blockIdx.y < a.nseg1) ihip::gemv<F, M, U, 1, false, true>(a);             \
+    else ihip::gemv<F2, M, U, 1, false, true>(a);                                      \
+  }
+#define IHIP_GEMV_MIX_U(PFX, F, F2, M) \
+  IHIP_GEMV_MIX(PFX##_norm_u1, F, F2, M, 1) IHIP_GEMV_MIX(PFX##_norm_u2, F, F2, M, 2) \
+  IHIP_GEMV_MIX(PFX##_norm_u3, F, F2, M, 3) IHIP_GEMV_MIX(PFX##_norm_u4, F, F2, M, 4)
+
 #define IHIP_GEMV_FMT(NAME, F) \
   IHIP_GEMV_U(gemv_##NAME##_f32, F, 0) \
   IHIP_GEMV_U(gemv_##NAME##_q8, F, 1) \
@@ -1004,6 +1016,8 @@ IHIP_DEQ(q5_1, ihip::DT_Q5_1)
 #endif
 #ifdef IHIP_ONLY_FMT_Q4_K
 IHIP_GEMV_FMT(q4_k, ihip::DT_Q4_K)
+IHIP_GEMV_MIX_U(gemv_q4_k_q6_k_q8, ihip::DT_Q4_K, ihip::DT_Q6_K, 1)
+IHIP_GEMV_MIX_U(gemv_q4_k_q6_k_f32, ihip::DT_Q4_K, ihip::DT_Q6_K, 0)
 IHIP_DEQ(q4_k, ihip::DT_Q4_K)
 #endif
 #ifdef IHIP_ONLY_FMT_Q6_K
