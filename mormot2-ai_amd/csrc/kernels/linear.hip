@@ -257,10 +257,11 @@ __device__ __forceinline__ void group_term(const uint8_t* w, const Raw& raw, int
       }
       accf += p0 + p1;
     } else {
-      double p = 0;
+      // the exact float products summed in double, four chains interleaved
+      double p[4] = {0, 0, 0, 0};
 #pragma unroll
-      for (int k = 0; k < 32; k++) p = __builtin_fma((double)v[k], (double)x.f[k], p);
-      accd += p;
+      for (int k = 0; k < 32; k++) p[k & 3] = __builtin_fma((double)v[k], (double)x.f[k], p[k & 3]);
+      accd += (p[0] + p[1]) + (p[2] + p[3]);
     }
   } else if constexpr (MODE == 0) {
     accf += group_f32<F>(raw, x.f, x.sx, g);
@@ -666,7 +667,8 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     XStage st;
     const bool quantized = !NORM && stage_q8<F, MODE>() && a.xq != nullptr;
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
-                        quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in, a.nw, st);
+                              quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
+                              a.nw, st);
     int64_t tb = wid;
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);

@@ -6,6 +6,7 @@
 // forward pass on the device gives the CPU's logits up to the order of
 // double sums. Sums across lanes run as wave/block reductions.
 #include "common.h"
+#include "route.h"
 
 namespace ihip {
 
@@ -854,71 +855,16 @@ struct RouteArgs {
   int32_t experts, k, norm, rows;
 };
 
-// TDecoderModel.Route (decoder.pas:2901-2949) = route of ops.cu:664-720:
-// softmax in double, the k highest logits (the lower id on a tie), weights
-// rounded to single, renormed in pick order, then sorted by id. One block of
-// 256 per row. The pick order is a rank: logit i is the j-th pick when j
-// logits are higher, or equal with a lower id; each thread counts it for its
-// own logits against the row in LDS, eight 16-byte reads in flight.
+// one block of 256 per row (route_block of route.h)
 extern "C" __global__ __launch_bounds__(256) void route(RouteArgs a)
 {
-  __shared__ __align__(16) float lg[4096 + 32];  // the row's logits, padded to 32
-  __shared__ float pw[64];                       // the picks' weights and ids in pick order
-  __shared__ int pid[64];
-  const int row = blockIdx.x, t = threadIdx.x, l = t & 63, E = a.experts, K = a.k;
-  const int E32 = (E + 31) & ~31;
-  {
-    const float* src = a.logits + (int64_t)row * E;
-    for (int i = t; i < E; i += 256) lg[i] = src[i];
-    // below every logit and never the lower id: the padding is no pick
-    if (E + t < E32) lg[E + t] = -INFINITY;
-    __syncthreads();
-  }
-  // every wave forms the same maximum and sum
-  float mx = -INFINITY;
-  for (int i = l; i < E; i += 64) mx = fmaxf(mx, lg[i]);
-  mx = wave_max(mx);
-  const double m = mx;
-  double sum = 0;
-  for (int i = l; i < E; i += 64) sum = sum + exp((double)lg[i] - m);
-  sum = wave_sum(sum, 64);
-  for (int i = t; i < E; i += 256) {
-    const float v = lg[i];
-    int rank = 0;
-    for (int j = 0; j < E32; j += 32) {
-      float4 u[8];
-#pragma unroll
-      for (int q = 0; q < 8; q++) u[q] = *(const float4*)&lg[j + 4 * q];
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const int jj = j + 4 * q;
-        rank += (u[q].x > v || (u[q].x == v && jj < i)) ? 1 : 0;
-        rank += (u[q].y > v || (u[q].y == v && jj + 1 < i)) ? 1 : 0;
-        rank += (u[q].z > v || (u[q].z == v && jj + 2 < i)) ? 1 : 0;
-        rank += (u[q].w > v || (u[q].w == v && jj + 3 < i)) ? 1 : 0;
-      }
-    }
-    if (rank < K) {
-      pw[rank] = (float)(exp((double)v - m) / sum);
-      pid[rank] = i;
-    }
-  }
-  __syncthreads();
-  if (t >= 64) return;
-  float wt = l < K ? pw[l] : 0.f;
-  const int my_id = l < K ? pid[l] : 0x7fffffff;
-  if (a.norm) {
-    // the picked weights summed in pick order, as the reference's loop does
-    double picked = 0;
-    for (int j = 0; j < K; j++) picked = picked + (double)pw[j];
-    wt = (float)((double)wt / picked);
-  }
-  // sorted by id: a pick's place is the number of smaller ids picked
-  int place = 0;
-  for (int j = 0; j < K; j++) place += pid[j] < my_id ? 1 : 0;
-  if (l < K) {
-    a.ids[(int64_t)row * K + place] = my_id;
-    a.w[(int64_t)row * K + place] = wt;
+  __shared__ int sid[64];
+  __shared__ float sw[64];
+  const int row = blockIdx.x;
+  route_block<4096>(a.logits + (int64_t)row * a.experts, a.experts, a.k, a.norm, sid, sw);
+  if ((int)threadIdx.x < a.k) {
+    a.ids[(int64_t)row * a.k + threadIdx.x] = sid[threadIdx.x];
+    a.w[(int64_t)row * a.k + threadIdx.x] = sw[threadIdx.x];
   }
 }
 
