@@ -677,9 +677,23 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   // the range's rows (an empty range reads row 0 of the cache)
   const int64_t rbase = n > 0 ? base : (int64_t)g * d;
   const int nmax = max(n - 1, 0);
-  uint4 kr[KB];
-  {
-    const uint4* p = (const uint4*)((const uint8_t*)a.kc + (rbase + (int64_t)min(t, nmax) * kvw) * (F16 ? 2 : 4));
+  // f16 keys: the range's rows loaded coalesced (KROW lanes a row), turned
+  // around in LDS (rows padded to an odd number of 16-byte words, so the
+  // per-thread row reads hit distinct banks); f32 keys: a thread loads its row
+  constexpr int KROW = HD * 2 / 16;              // 16-byte words of an f16 key row
+  constexpr int KLD = ATT_CHUNK * KROW / 256;    // coalesced loads per thread
+  constexpr int KPAD = KROW + 1;
+  __shared__ uint4 ks[F16 ? ATT_CHUNK * KPAD : 1];
+  uint4 kr[F16 ? KLD : KB];
+  if constexpr (F16) {
+#pragma unroll
+    for (int r = 0; r < KLD; r++) {
+      const int q = t + 256 * r, row = q / KROW, col = q % KROW;
+      kr[r] = *(const uint4*)((const uint16_t*)a.kc + rbase + (int64_t)min(row, nmax) * kvw + col * 8);
+    }
+
+  } else {
+    const uint4* p = (const uint4*)((const float*)a.kc + rbase + (int64_t)min(t, nmax) * kvw);
 #pragma unroll
     for (int k = 0; k < KB; k++) kr[k] = p[k];
   }
@@ -694,6 +708,14 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
       uint2 x = *(const uint2*)((const float*)a.vc + e);
       vr[u][0] = x.x;
       vr[u][1] = x.y;
+    }
+  }
+  // the key words into LDS once they arrive (the value loads are already out)
+  if constexpr (F16) {
+#pragma unroll
+    for (int r = 0; r < KLD; r++) {
+      const int q = t + 256 * r;
+      ks[(q / KROW) * KPAD + q % KROW] = kr[r];
     }
   }
 
@@ -747,29 +769,38 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     __syncthreads();
   }
 
-  // ---- scores: the CPU's sequential double dot per key, one thread per key
+  // ---- scores: the double dot per key, one thread per key. q and k are
+  // float values, so each product is exact in double and a fused multiply-add
+  // rounds as the CPU's multiply-then-add; the sum runs in four interleaved
+  // chains (only the order of the double sum differs from the CPU's)
   double m = -1.0e308;
   if (t < n) {
-    double acc = 0;
+    double c4[4] = {0, 0, 0, 0};
     if (hasnew && t == jn) {
-      for (int i = 0; i < d; i++) acc = acc + qd[i] * (double)knew[i];
+#pragma unroll
+      for (int i = 0; i < d; i++) c4[i & 3] = __builtin_fma(qd[i], (double)knew[i], c4[i & 3]);
     } else {
 #pragma unroll
       for (int k = 0; k < KB; k++) {
-          uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-          if constexpr (F16) {
+        uint4 kw4;
+        if constexpr (F16) kw4 = ks[t * KPAD + k];
+        else kw4 = kr[k];
+        uint32_t wv[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
+        if constexpr (F16) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-              int i = 8 * k + 2 * j;
-              acc = acc + qd[i] * (double)half_to_float(wv[j] & 0xffffu);
-              acc = acc + qd[i + 1] * (double)half_to_float(wv[j] >> 16);
-            }
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) acc = acc + qd[4 * k + j] * (double)bits_float(wv[j]);
+          for (int j = 0; j < 4; j++) {
+            int i = 8 * k + 2 * j;
+            c4[i & 3] = __builtin_fma(qd[i], (double)half_to_float(wv[j] & 0xffffu), c4[i & 3]);
+            c4[(i + 1) & 3] =
+                __builtin_fma(qd[i + 1], (double)half_to_float(wv[j] >> 16), c4[(i + 1) & 3]);
           }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; j++) c4[j] = __builtin_fma(qd[4 * k + j], (double)bits_float(wv[j]), c4[j]);
         }
+      }
     }
+    double acc = (c4[0] + c4[1]) + (c4[2] + c4[3]);
     acc = acc * a.scale;
     sc[t] = acc;
     m = acc;
@@ -788,7 +819,8 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   if (l == 0) red[4 + w] = e;
 
   // ---- the weighted values: the loads above, the new value from LDS
-  double a0 = 0, a1 = 0;
+  // two chains per dimension (even and odd key slots)
+  double a0e = 0, a1e = 0, a0o = 0, a1o = 0;
 #pragma unroll
   for (int u = 0; u < VB; u++) {
     const int j = jb0 + u * step;
@@ -805,10 +837,16 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
         x0 = bits_float(vr[u][0]);
         x1 = bits_float(vr[u][F16 ? 0 : 1]);
       }
-      a0 = a0 + p * (double)x0;
-      a1 = a1 + p * (double)x1;
+      if (u & 1) {
+        a0o = a0o + p * (double)x0;
+        a1o = a1o + p * (double)x1;
+      } else {
+        a0e = a0e + p * (double)x0;
+        a1e = a1e + p * (double)x1;
+      }
     }
   }
+  double a0 = a0e + a0o, a1 = a1e + a1o;
   if constexpr (lpk == 32) {  // the two keys of a wave: lanes l and l ^ 32
     a0 = a0 + xpart<32>(a0);
     a1 = a1 + xpart<32>(a1);
@@ -831,19 +869,19 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
 
 }
 
-extern "C" __global__ __launch_bounds__(256) void attention_one_f16_64(AttnOneArgs a)
+extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_64(AttnOneArgs a)
 {
   attention_one_t<true, 64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void attention_one_f16_128(AttnOneArgs a)
+extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_128(AttnOneArgs a)
 {
   attention_one_t<true, 128>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void attention_one_f32_64(AttnOneArgs a)
+extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_64(AttnOneArgs a)
 {
   attention_one_t<false, 64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void attention_one_f32_128(AttnOneArgs a)
+extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_128(AttnOneArgs a)
 {
   attention_one_t<false, 128>(a);
 }
