@@ -744,6 +744,10 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
           uint16_t h0 = float_to_half(o0), h1 = float_to_half(o1);
           ((uint16_t*)a.kc)[dst + t] = h0;
           ((uint16_t*)a.kc)[dst + t + half] = h1;
+          // and into the range's key tile, as the cache now holds it
+          uint16_t* kt = (uint16_t*)&ks[jn * KPAD];
+          kt[t] = h0;
+          kt[t + half] = h1;
           o0 = half_to_float(h0);
           o1 = half_to_float(h1);
         } else {
@@ -769,12 +773,37 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     __syncthreads();
   }
 
-  // ---- scores: the double dot per key, one thread per key. q and k are
-  // float values, so each product is exact in double and a fused multiply-add
-  // rounds as the CPU's multiply-then-add; the sum runs in four interleaved
-  // chains (only the order of the double sum differs from the CPU's)
+  // ---- scores: the double dot per key. q and k are float values, so each
+  // product is exact in double and a fused multiply-add rounds as the CPU's
+  // multiply-then-add; the sum runs in interleaved chains (only the order of
+  // the double sum differs from the CPU's). f16 keys: two threads per key,
+  // each half of the dimensions, from the LDS key tile (the new key in it);
+  // f32 keys: a thread per key from its registers.
   double m = -1.0e308;
-  if (t < n) {
+  if constexpr (F16) {
+    const int kk = t >> 1, hh = t & 1;
+    double c4[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < KROW / 2; k++) {
+      const int kw = hh * (KROW / 2) + k;
+      const uint4 kw4 = ks[kk * KPAD + kw];
+      const uint32_t wv[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = 8 * kw + 2 * j;
+        c4[(2 * j) & 3] = __builtin_fma(qd[i], (double)half_to_float(wv[j] & 0xffffu), c4[(2 * j) & 3]);
+        c4[(2 * j + 1) & 3] =
+            __builtin_fma(qd[i + 1], (double)half_to_float(wv[j] >> 16), c4[(2 * j + 1) & 3]);
+      }
+    }
+    double part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+    double acc = part + xpart<1>(part);  // the other half of the key
+    acc = acc * a.scale;
+    if (kk < n) {
+      if (hh == 0) sc[kk] = acc;
+      m = acc;
+    }
+  } else if (t < n) {
     double c4[4] = {0, 0, 0, 0};
     if (hasnew && t == jn) {
 #pragma unroll
@@ -782,22 +811,9 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     } else {
 #pragma unroll
       for (int k = 0; k < KB; k++) {
-        uint4 kw4;
-        if constexpr (F16) kw4 = ks[t * KPAD + k];
-        else kw4 = kr[k];
-        uint32_t wv[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
-        if constexpr (F16) {
+        const uint32_t wv[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
 #pragma unroll
-          for (int j = 0; j < 4; j++) {
-            int i = 8 * k + 2 * j;
-            c4[i & 3] = __builtin_fma(qd[i], (double)half_to_float(wv[j] & 0xffffu), c4[i & 3]);
-            c4[(i + 1) & 3] =
-                __builtin_fma(qd[i + 1], (double)half_to_float(wv[j] >> 16), c4[(i + 1) & 3]);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; j++) c4[j] = __builtin_fma(qd[4 * k + j], (double)bits_float(wv[j]), c4[j]);
-        }
+        for (int j = 0; j < 4; j++) c4[j] = __builtin_fma(qd[4 * k + j], (double)bits_float(wv[j]), c4[j]);
       }
     }
     double acc = (c4[0] + c4[1]) + (c4[2] + c4[3]);
@@ -805,6 +821,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     sc[t] = acc;
     m = acc;
   }
+  __syncthreads();  // sc complete before the softmax reads it
   m = wave_max(m);
   if (l == 0) red[w] = m;
   __syncthreads();
@@ -813,37 +830,41 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   if (t < n) {
     e = exp(sc[t] - m);
     sc[t] = e;
+  } else if (t < ATT_CHUNK) {
+    sc[t] = 0.0;  // no weight past the range: the value loop reads every slot
   }
   e = wave_sum(e, 64);
   __syncthreads();
   if (l == 0) red[4 + w] = e;
 
   // ---- the weighted values: the loads above, the new value from LDS
-  // two chains per dimension (even and odd key slots)
+  // two chains per dimension (even and odd key slots); no branch: a slot
+  // past the range has weight 0, the new key's value is selected
+  const float vn0 = vnew[2 * pair], vn1 = vnew[2 * pair + 1];
+  const int jnew = hasnew ? jn : -1;
   double a0e = 0, a1e = 0, a0o = 0, a1o = 0;
 #pragma unroll
   for (int u = 0; u < VB; u++) {
     const int j = jb0 + u * step;
-    if (j < n) {
-      const double p = sc[j];
-      float x0, x1;
-      if (hasnew && j == jn) {
-        x0 = vnew[2 * pair];
-        x1 = vnew[2 * pair + 1];
-      } else if constexpr (F16) {
-        x0 = half_to_float(vr[u][0] & 0xffffu);
-        x1 = half_to_float(vr[u][0] >> 16);
-      } else {
-        x0 = bits_float(vr[u][0]);
-        x1 = bits_float(vr[u][F16 ? 0 : 1]);
-      }
-      if (u & 1) {
-        a0o = a0o + p * (double)x0;
-        a1o = a1o + p * (double)x1;
-      } else {
-        a0e = a0e + p * (double)x0;
-        a1e = a1e + p * (double)x1;
-      }
+    const double p = sc[j];
+    float x0, x1;
+    if constexpr (F16) {
+      x0 = half_to_float(vr[u][0] & 0xffffu);
+      x1 = half_to_float(vr[u][0] >> 16);
+    } else {
+      x0 = bits_float(vr[u][0]);
+      x1 = bits_float(vr[u][F16 ? 0 : 1]);
+    }
+    // a slot past the range reads a clamped row, which may be the new key's
+    // not yet written one: its value is 0, never the row's bits
+    x0 = j == jnew ? vn0 : (j < n ? x0 : 0.f);
+    x1 = j == jnew ? vn1 : (j < n ? x1 : 0.f);
+    if (u & 1) {
+      a0o = a0o + p * (double)x0;
+      a1o = a1o + p * (double)x1;
+    } else {
+      a0e = a0e + p * (double)x0;
+      a1e = a1e + p * (double)x1;
     }
   }
   double a0 = a0e + a0o, a1 = a1e + a1o;
