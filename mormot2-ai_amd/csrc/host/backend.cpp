@@ -265,11 +265,14 @@ static bool linear_ok(int t, int64_t in)
   return in / 32 <= 256;  // the activation of a lane's groups stays in registers
 }
 
-// lanes per row and groups per lane: the least idle lanes, then wider rows
-static void pick_lpr(int64_t G, int& lpr, int& U)
+// lanes per row and groups per lane, the least idle lanes first. Between
+// equal choices: narrow rows (more groups per lane: a row's lane sums and its
+// addressing are paid once per U groups) when the matrix still gives every CU
+// four tiles of them, else wide rows (more waves for a short matrix)
+static void pick_lpr_order(int64_t G, const int (&order)[4], int& lpr, int& U)
 {
   int best = -1;
-  for (int l : {64, 32, 16, 8}) {
+  for (int l : order) {
     int u = (int)((G + l - 1) / l);
     if (u > 4) continue;
     int waste = l * u - (int)G;
@@ -279,6 +282,13 @@ static void pick_lpr(int64_t G, int& lpr, int& U)
       U = u;
     }
   }
+}
+
+static void pick_lpr(int64_t G, int64_t out, int cus, int& lpr, int& U)
+{
+  static const int narrow_first[4] = {8, 16, 32, 64}, wide_first[4] = {64, 32, 16, 8};
+  pick_lpr_order(G, narrow_first, lpr, U);
+  if (out / (64 / lpr) < 4 * (int64_t)cus) pick_lpr_order(G, wide_first, lpr, U);
 }
 
 uint64_t q8_row_bytes(int64_t in) { return (uint64_t)in + 4 * (uint64_t)(in / 32); }
@@ -310,7 +320,7 @@ bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in)
 {
   if (!linear_ok(a, in) || !linear_ok(b, in)) return false;
   int lpr = 64, U = 1;
-  pick_lpr(in / 32, lpr, U);
+  pick_lpr(in / 32, 1 << 30, 256, lpr, U);  // the name only: every U has a pair kernel
   char name[64];
   snprintf(name, sizeof name, "gemv_%s_%s_%s_norm_u%d", fmt_name(a), fmt_name(b),
            (mode & 1) == IHIP_MODE_Q8 ? "q8" : "f32", U);
@@ -331,7 +341,9 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
                                 " into " + std::to_string(k.out));
   const int64_t G = k.in / 32;
   int lpr = 64, U = 1;
-  pick_lpr(G, lpr, U);
+  int64_t out_max = k.out;
+  for (int i = 0; i < k.nseg && i < 3; i++) out_max = std::max<int64_t>(out_max, k.oseg[i]);
+  pick_lpr(G, out_max, c->cus, lpr, U);
   uint64_t xq = k.xq;
   const int mode = k.mode & 1;
   const bool q8 = mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
