@@ -13,41 +13,50 @@ struct Raw {
   uint32_t a, b, c, d;  // scales, high bits, header words
 };
 
+// the loads of group g of row o. Offsets are 32-bit (a matrix is below
+// 4 GiB): a uniform base plus a 32-bit per-lane offset, the addressing form of
+// the vector memory instructions, with no 64-bit arithmetic per lane
+template <typename T>
+__device__ __forceinline__ T at(const uint8_t* base, uint32_t byte_off)
+{
+  return *(const T*)(base + byte_off);
+}
+
 template <int F>
 __device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, int64_t o,
                                            int G, int g, int64_t in, Raw& r)
 {
-  int64_t og = o * G + g;
+  const uint32_t og = (uint32_t)o * (uint32_t)G + (uint32_t)g;
   if constexpr (F == DT_Q8_0) {
-    const uint4* p = (const uint4*)(w + o * in + (int64_t)g * 32);
-    r.q0 = p[0];
-    r.q1 = p[1];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
+    const uint32_t q = (uint32_t)o * (uint32_t)in + (uint32_t)g * 32u;
+    r.q0 = at<uint4>(w, q);
+    r.q1 = at<uint4>(w, q + 16u);
+    r.a = at<uint16_t>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_Q4_0) {
-    r.q0 = ((const uint4*)w)[og];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
+    r.q0 = at<uint4>(w, og * 16u);
+    r.a = at<uint16_t>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_MXFP4) {
-    r.q0 = ((const uint4*)w)[og];
-    r.a = (w + rg.s)[og];
+    r.q0 = at<uint4>(w, og * 16u);
+    r.a = at<uint8_t>(w + rg.s, og);
   } else if constexpr (F == DT_Q5_0) {
-    r.q0 = ((const uint4*)w)[og];
-    r.b = ((const uint32_t*)(w + rg.h))[og];
-    r.a = ((const uint16_t*)(w + rg.s))[og];
+    r.q0 = at<uint4>(w, og * 16u);
+    r.b = at<uint32_t>(w + rg.h, og * 4u);
+    r.a = at<uint16_t>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_Q5_1) {
-    r.q0 = ((const uint4*)w)[og];
-    r.b = ((const uint32_t*)(w + rg.h))[og];
-    r.a = ((const uint32_t*)(w + rg.s))[og];
+    r.q0 = at<uint4>(w, og * 16u);
+    r.b = at<uint32_t>(w + rg.h, og * 4u);
+    r.a = at<uint32_t>(w + rg.s, og * 4u);
   } else if constexpr (F == DT_Q4_K) {
-    r.q0 = ((const uint4*)w)[og];
-    r.q1 = ((const uint4*)(w + rg.s))[o * (G >> 3) + (g >> 3)];
+    r.q0 = at<uint4>(w, og * 16u);
+    r.q1 = at<uint4>(w + rg.s, ((uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3)) * 16u);
   } else if constexpr (F == DT_Q6_K) {
-    int64_t ob = o * (G >> 3) + (g >> 3);
-    r.q0 = ((const uint4*)w)[og];
-    uint2 h = ((const uint2*)(w + rg.h))[og];
+    const uint32_t ob = (uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3);
+    r.q0 = at<uint4>(w, og * 16u);
+    const uint2 h = at<uint2>(w + rg.h, og * 8u);
     r.b = h.x;
     r.c = h.y;
-    r.a = ((const uint16_t*)(w + rg.s))[ob * 8 + (g & 7)];
-    r.d = ((const uint16_t*)(w + rg.s2))[ob];
+    r.a = at<uint16_t>(w + rg.s, (ob * 8u + (uint32_t)(g & 7)) * 2u);
+    r.d = at<uint16_t>(w + rg.s2, ob * 2u);
   }
 }
 
