@@ -22,41 +22,65 @@ __device__ __forceinline__ T at(const uint8_t* base, uint32_t byte_off)
   return *(const T*)(base + byte_off);
 }
 
-template <int F>
+// a streamed load (NT: non-temporal, the weights of a GEMV read once per
+// pass; the GEMM, which re-reads them per row tile, keeps them cached)
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32 __attribute__((ext_vector_type(2)));
+template <typename T, bool NT>
+__device__ __forceinline__ T ld(const uint8_t* base, uint32_t byte_off)
+{
+  if constexpr (!NT) {
+    return *(const T*)(base + byte_off);
+  } else if constexpr (sizeof(T) == 16) {
+    const v4u32 v = __builtin_nontemporal_load((const v4u32*)(base + byte_off));
+    return __builtin_bit_cast(T, v);
+  } else if constexpr (sizeof(T) == 8) {
+    const v2u32 v = __builtin_nontemporal_load((const v2u32*)(base + byte_off));
+    return __builtin_bit_cast(T, v);
+  } else if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load((const uint32_t*)(base + byte_off)));
+  } else if constexpr (sizeof(T) == 2) {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load((const uint16_t*)(base + byte_off)));
+  } else {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load((const uint8_t*)(base + byte_off)));
+  }
+}
+
+template <int F, bool NT = false>
 __device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, int64_t o,
                                            int G, int g, int64_t in, Raw& r)
 {
   const uint32_t og = (uint32_t)o * (uint32_t)G + (uint32_t)g;
   if constexpr (F == DT_Q8_0) {
     const uint32_t q = (uint32_t)o * (uint32_t)in + (uint32_t)g * 32u;
-    r.q0 = at<uint4>(w, q);
-    r.q1 = at<uint4>(w, q + 16u);
-    r.a = at<uint16_t>(w + rg.s, og * 2u);
+    r.q0 = ld<uint4, NT>(w, q);
+    r.q1 = ld<uint4, NT>(w, q + 16u);
+    r.a = ld<uint16_t, NT>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_Q4_0) {
-    r.q0 = at<uint4>(w, og * 16u);
-    r.a = at<uint16_t>(w + rg.s, og * 2u);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    r.a = ld<uint16_t, NT>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_MXFP4) {
-    r.q0 = at<uint4>(w, og * 16u);
-    r.a = at<uint8_t>(w + rg.s, og);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    r.a = ld<uint8_t, NT>(w + rg.s, og);
   } else if constexpr (F == DT_Q5_0) {
-    r.q0 = at<uint4>(w, og * 16u);
-    r.b = at<uint32_t>(w + rg.h, og * 4u);
-    r.a = at<uint16_t>(w + rg.s, og * 2u);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    r.b = ld<uint32_t, NT>(w + rg.h, og * 4u);
+    r.a = ld<uint16_t, NT>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_Q5_1) {
-    r.q0 = at<uint4>(w, og * 16u);
-    r.b = at<uint32_t>(w + rg.h, og * 4u);
-    r.a = at<uint32_t>(w + rg.s, og * 4u);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    r.b = ld<uint32_t, NT>(w + rg.h, og * 4u);
+    r.a = ld<uint32_t, NT>(w + rg.s, og * 4u);
   } else if constexpr (F == DT_Q4_K) {
-    r.q0 = at<uint4>(w, og * 16u);
-    r.q1 = at<uint4>(w + rg.s, ((uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3)) * 16u);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    r.q1 = ld<uint4, NT>(w + rg.s, ((uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3)) * 16u);
   } else if constexpr (F == DT_Q6_K) {
     const uint32_t ob = (uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3);
-    r.q0 = at<uint4>(w, og * 16u);
-    const uint2 h = at<uint2>(w + rg.h, og * 8u);
+    r.q0 = ld<uint4, NT>(w, og * 16u);
+    const uint2 h = ld<uint2, NT>(w + rg.h, og * 8u);
     r.b = h.x;
     r.c = h.y;
-    r.a = at<uint16_t>(w + rg.s, (ob * 8u + (uint32_t)(g & 7)) * 2u);
-    r.d = at<uint16_t>(w + rg.s2, ob * 2u);
+    r.a = ld<uint16_t, NT>(w + rg.s, (ob * 8u + (uint32_t)(g & 7)) * 2u);
+    r.d = ld<uint16_t, NT>(w + rg.s2, ob * 2u);
   }
 }
 

@@ -581,8 +581,8 @@ __device__ __forceinline__ void load_tiles(const uint8_t* w, const uint8_t* w2, 
 #pragma unroll
     for (int k = 0; k < U; k++) {
       const int g = min(lr + k * lpr, G - 1);
-      load_group<F>(w, rg, o, G, g, in, raw[i][k]);
-      if constexpr (GLU) load_group<F>(w2, rg, o, G, g, in, raw2[i][k]);
+      load_group<F, true>(w, rg, o, G, g, in, raw[i][k]);
+      if constexpr (GLU) load_group<F, true>(w2, rg, o, G, g, in, raw2[i][k]);
     }
   }
 }
@@ -735,7 +735,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         int g = lr + k * lpr;
         bool has = valid && g < G;
         Raw raw;
-        if (has && !is_float_type(F)) load_group<F>(w, rg, o, G, g, a.in, raw);
+        if (has && !is_float_type(F)) load_group<F>(w, rg, o, G, g, a.in, raw);  // re-read per row chunk
 #pragma unroll
         for (int r = 0; r < R; r++) {
           if (r < nrows) {
@@ -813,7 +813,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int k = 0; k < U; k++)
-          load_group<F>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
+          load_group<F, true>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
     }
   };
   load(t);
@@ -897,7 +897,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
       load_fgroup<F>(a.w, o, g, a.in, v);
     } else {
       Raw r;
-      load_group<F>(a.w, rg, o, G, g, a.in, r);
+      load_group<F, true>(a.w, rg, o, G, g, a.in, r);
 #pragma unroll
       for (int hi = 0; hi < 2; hi++)
 #pragma unroll

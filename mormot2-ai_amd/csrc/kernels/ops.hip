@@ -1023,20 +1023,25 @@ struct StreamArgs {
   uint32_t* out;
 };
 
-// reads n16 16-byte words once (grid-stride, 4 in flight per lane) and folds
-// them so the loads are not dropped: the achievable read bandwidth
+// reads n16 16-byte words once (grid-stride, 8 non-temporal 16-byte loads in
+// flight per lane) and folds them so the loads are not dropped: the
+// achievable read bandwidth
 extern "C" __global__ __launch_bounds__(256) void stream_read(StreamArgs a)
 {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
   uint32_t acc = 0;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * stride < a.n16; i += 4 * stride) {
-    uint4 v0 = a.p[i], v1 = a.p[i + stride], v2 = a.p[i + 2 * stride], v3 = a.p[i + 3 * stride];
-    acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
-    acc ^= v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^ v3.w;
+  const v4u* p = (const v4u*)a.p;
+  for (; i + 7 * stride < a.n16; i += 8 * stride) {
+    v4u v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = __builtin_nontemporal_load(p + i + k * stride);
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
   }
   for (; i < a.n16; i += stride) {
-    uint4 v = a.p[i];
+    v4u v = __builtin_nontemporal_load(p + i);
     acc ^= v.x ^ v.y ^ v.z ^ v.w;
   }
   if (acc == 0x9E3779B9u) a.out[0] = acc;
