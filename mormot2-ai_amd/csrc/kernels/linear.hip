@@ -680,15 +680,16 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       int g = lr + k * lpr;
       if (g < G) lds_x<F, MODE>(xs, (const float*)(xs + a.in), g, xg[k]);
     }
-    while (tb < tiles) {
+    // the T tiles of a step from their weight registers
+    auto step = [&](int64_t sb, const Raw (&rw)[T][U], const Raw (&rw2)[T][U]) {
 #pragma unroll
       for (int i = 0; i < T; i++) {
-        const int64_t t = tb + (int64_t)i * nw;
+        const int64_t t = sb + (int64_t)i * nw;
         const int64_t o = t * rpw + rsub;
         const bool valid = t < tiles && o < out;
-        double v = row_value<F, MODE, U>(w, raw[i], o, valid, xg, lr, lpr, G, a.in);
+        double v = row_value<F, MODE, U>(w, rw[i], o, valid, xg, lr, lpr, G, a.in);
         double v2 = 0.0;
-        if constexpr (GLU) v2 = row_value<F, MODE, U>(w2, raw2[i], o, valid, xg, lr, lpr, G, a.in);
+        if constexpr (GLU) v2 = row_value<F, MODE, U>(w2, rw2[i], o, valid, xg, lr, lpr, G, a.in);
         if (lr == 0 && valid) {
           if (bias) v = (double)bias[o] + v;
           float r = (float)v;
@@ -700,10 +701,12 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
           yp[yrow0 * out + o] = r;
         }
       }
+    };
+    while (tb < tiles) {
+      step(tb, raw, raw2);
       tb += (int64_t)T * nw;
       if (tb < tiles)
-        load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out,
-                                 raw, raw2);
+        load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw, raw2);
     }
   } else {
     // the activation and output rows of the batch
