@@ -476,7 +476,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     wgs = std::min(wgs, std::max<int64_t>((tiles_all + 4 * T - 1) / (4 * T), want));
     // and no more blocks than the chip holds at once: the waves walk the
     // rest of the rows, each block stages its row once
-    const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) + share - 1) / share;
+    const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) * c->gemv_hold + share - 1) / share;
     wgs = std::max<int64_t>(1, std::min(wgs, hold));
   }
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
