@@ -30,6 +30,8 @@ sys.path[:0] = [os.path.join(ROOT, "mormot2-ai_amd"), os.path.join(ROOT, "tests"
 METRIC = "decode tok/s + quant GEMV HBM GB/s (% peak), Qwen3-30B-A3B-shape Q4_K_M"
 HBM_PEAK = 8000.0  # GB/s, MI355X published
 INT8_PEAK = 5000.0  # TOP/s, MI355X dense int8 MFMA, published
+PROMPTS = {"qwen3-0.6b-q8_0": 32, "qwen3-0.6b-q4_k_m": 512, "qwen3-30b-a3b-q4_k_m": 1024,
+           "gpt-oss-20b-mxfp4": 2048}
 SWEEP_SHAPES = [(3072, 1024), (1024, 3072), (6144, 2048), (2880, 2880), (151936, 1024)]
 
 
@@ -155,19 +157,27 @@ def copy_calibration(ctx, nbytes=256 << 20):
 
 
 def expert_gemv(ctx, spec, reps=4, graphs=True):
-    """The dominant decode kernel: 8 experts of the gate projection of every
-    MoE layer (Q4_K 768x2048 each), one launch per layer, the 48 launches in
-    one graph timed with events (as the decode step replays them); without
-    graphs (a profiled run) launched directly."""
+    """The dominant decode kernel: the expert GEMV of the MoE layers (the gate
+    projection of 8 experts per launch: Q4_K 768x2048 each for configs[3]),
+    or for a dense model the FFN gate GEMV (3072x1024 for Qwen3-0.6B), one
+    launch per layer, the launches of all layers in one graph timed with
+    events (as the decode step replays them); without graphs (a profiled run)
+    launched directly."""
+    import ctypes
     import infer_hip as H
     L = H.lib()
     c = spec.cfg
-    Hd, FI, E, K = c["hidden"], c["expert_ffn"], c["experts"], c["experts_used"]
+    moe = c.get("moe", False)
+    Hd = c["hidden"]
+    if moe:
+        FI, E, K = c["expert_ffn"], c["experts"], c["experts_used"]
+    else:
+        FI, E, K = c["ffn"], 1, 1
     devs = []
     for li in range(c["layers"]):
-        t = spec.layers[li].exp_gate
-        d = __import__("ctypes").c_uint64()
-        H.check(L.ihip_weight(ctx.h, t.data, t.dtype, FI, Hd, E, __import__("ctypes").byref(d)))
+        t = spec.layers[li].exp_gate if moe else spec.layers[li].gate
+        d = ctypes.c_uint64()
+        H.check(L.ihip_weight(ctx.h, t.data, t.dtype, FI, Hd, E, ctypes.byref(d)))
         devs.append((d.value, t.dtype))
     dtype = devs[0][1]
     rng = np.random.default_rng(3)
@@ -183,22 +193,34 @@ def expert_gemv(ctx, spec, reps=4, graphs=True):
 
     def enq():
         for w, _ in devs:
-            H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr, K,
-                                              0, dy.ptr, 0, H.MODE_Q8 | 2))
+            if moe:
+                H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr,
+                                                  K, 0, dy.ptr, 0, H.MODE_Q8 | 2))
+            else:
+                H.check(L.ihip_enqueue_linear_at(ctx.h, dq.ptr, 1, Hd, dtype, w, FI, dy.ptr, 0,
+                                                 H.MODE_Q8 | 2))
 
     ms = (time_graph(ctx, enq, reps) if graphs else time_direct(ctx, enq, reps)) / len(devs)
-    nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + K * 4 + K * FI * 4
+    nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + (K * 4 if moe else 0) + K * FI * 4
     for b in (dx, dq, ids, dy):
         b.free()
-    return {"kernel": f"gemv_{H.NAMES[dtype].lower()}_q8 (ids, {K} experts {FI}x{Hd})",
+    what = f"ids, {K} experts {FI}x{Hd}" if moe else f"FFN gate {FI}x{Hd}"
+    return {"kernel": f"gemv_{H.NAMES[dtype].lower()}_q8 ({what})",
             "bytes_per_launch": nb, "avg_us": ms * 1e3, "GBps": nb / (ms * 1e-3) / 1e9}
 
 
-def profiled_traffic():
+PROFILED = {  # roofline kernel -> its committed counter profile
+    "gemv_q4_k_q8 (ids, 8 experts 768x2048)": "gemv_q4_k_ids_8x768x2048_traffic.txt",
+}
+
+
+def profiled_traffic(kernel):
     """HBM bytes per launch of the roofline kernel from the committed counter
     profile (FETCH_SIZE + WRITE_SIZE, each scaled by a copy of known size),
-    or None when it is absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_q4_k_ids_8x768x2048_traffic.txt")
+    or None when there is none for this kernel."""
+    if kernel not in PROFILED:
+        return None
+    path = os.path.join(ROOT, "profiles", PROFILED[kernel])
     try:
         with open(path) as f:
             for line in f:
@@ -243,7 +265,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--prompt", type=int, default=1024)
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="prompt tokens (default: the config's BASELINE workload)")
     ap.add_argument("--config", default="qwen3-30b-a3b-q4_k_m")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -251,6 +274,10 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="direct launches per decode step (the profiler cannot trace graphs)")
     args = ap.parse_args()
+    if args.prompt is None:
+        # the BASELINE workloads: configs[0] 32, configs[2] 512, configs[3]
+        # 1024, configs[4] 2048 prompt tokens
+        args.prompt = PROMPTS.get(args.config, 1024)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"{args.gpus}); run with --gpus 1", file=sys.stderr)
@@ -350,7 +377,7 @@ def main():
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
-                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": profiled_traffic(),
+                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": profiled_traffic(dom["kernel"]),
                      "kernel": dom["kernel"], "bytes_per_launch": dom["bytes_per_launch"],
                      "avg_us": round(dom["avg_us"], 3)},
         "stream_read_GBps": round(stream, 1),
