@@ -44,7 +44,8 @@ static void repack_row(const uint8_t* src, uint8_t* dst, int t, int64_t out, int
     for (int64_t b = 0; b < G; b++) {
       const uint8_t* s = src + b * 34;
       memcpy(dst + rg.s + (o * G + b) * 2, s, 2);
-      memcpy(dst + o * in + b * 32, s + 2, 32);
+      memcpy(dst + o * in + b * 16, s + 2, 16);
+      memcpy(dst + o * in + in / 2 + b * 16, s + 18, 16);
     }
     break;
   case DT_Q4_0:
@@ -125,7 +126,8 @@ static void unpack_row(const uint8_t* src, uint8_t* dst, int t, int64_t out, int
   case DT_Q8_0:
     for (int64_t b = 0; b < G; b++) {
       memcpy(dst + b * 34, src + rg.s + (o * G + b) * 2, 2);
-      memcpy(dst + b * 34 + 2, src + o * in + b * 32, 32);
+      memcpy(dst + b * 34 + 2, src + o * in + b * 16, 16);
+      memcpy(dst + b * 34 + 18, src + o * in + in / 2 + b * 16, 16);
     }
     break;
   case DT_Q4_0:

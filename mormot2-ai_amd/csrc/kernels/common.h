@@ -62,17 +62,17 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t s0, uint32_t s1, uint32_t s
   return (w >> ((k & 3) * 8)) & 255u;
 }
 
+// Branch-free (j may differ between the lanes of a wave): both forms use
+// byte j & 3 of each of the three dwords.
 __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
                                              int& sc, int& m)
 {
-  if (j < 4) {
-    sc = (int)(byte_of(s0, s1, s2, j) & 63u);
-    m = (int)(byte_of(s0, s1, s2, j + 4) & 63u);
-  } else {
-    uint32_t a = byte_of(s0, s1, s2, j + 4);
-    sc = (int)((a & 15u) | ((byte_of(s0, s1, s2, j - 4) >> 6) << 4));
-    m = (int)((a >> 4) | ((byte_of(s0, s1, s2, j) >> 6) << 4));
-  }
+  const uint32_t sh = 8u * (uint32_t)(j & 3);
+  const uint32_t b0 = (s0 >> sh) & 255u, b1 = (s1 >> sh) & 255u, b2 = (s2 >> sh) & 255u;
+  const uint32_t lo_sc = b0 & 63u, lo_m = b1 & 63u;
+  const uint32_t hi_sc = (b2 & 15u) | ((b0 & 0xC0u) >> 2), hi_m = (b2 >> 4) | ((b1 & 0xC0u) >> 2);
+  sc = (int)(j < 4 ? lo_sc : hi_sc);
+  m = (int)(j < 4 ? lo_m : hi_m);
 }
 
 // TInferCpuBackend.SwiGlu (backend.cpu.pas:1797-1834) of one value pair:
@@ -106,6 +106,7 @@ __device__ __forceinline__ float swiglu_value(float g, float u, float alpha, flo
 template <int K>
 __device__ __forceinline__ uint32_t xpart_u(uint32_t v)
 {
+  // every lane reads a lane of its own row: no old value is needed
   if constexpr (K == 1) return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);
   else if constexpr (K == 2) return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);
   else if constexpr (K == 4) return __builtin_amdgcn_update_dpp(0u, v, 0x141, 0xF, 0xF, false);

@@ -46,15 +46,21 @@ __device__ __forceinline__ T ld(const uint8_t* base, uint32_t byte_off)
   }
 }
 
-template <int F, bool NT = false>
+// QH (Q4_K): each lane of an aligned quad loads one dword of the 16-byte
+// super-block header (lane & 3), and expand_header() hands every lane all four
+// after the load; the quad's lanes must read one super-block (lanes per row a
+// multiple of 8, whole quads active)
+template <int F, bool NT = false, bool QH = false>
 __device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, int64_t o,
                                            int G, int g, int64_t in, Raw& r)
 {
   const uint32_t og = (uint32_t)o * (uint32_t)G + (uint32_t)g;
   if constexpr (F == DT_Q8_0) {
-    const uint32_t q = (uint32_t)o * (uint32_t)in + (uint32_t)g * 32u;
+    // a row's low halves of its groups, then their high halves: the lanes
+    // of a row read one contiguous run per load
+    const uint32_t q = (uint32_t)o * (uint32_t)in + (uint32_t)g * 16u;
     r.q0 = ld<uint4, NT>(w, q);
-    r.q1 = ld<uint4, NT>(w, q + 16u);
+    r.q1 = ld<uint4, NT>(w, q + (uint32_t)(in >> 1));
     r.a = ld<uint16_t, NT>(w + rg.s, og * 2u);
   } else if constexpr (F == DT_Q4_0) {
     r.q0 = ld<uint4, NT>(w, og * 16u);
@@ -72,7 +78,11 @@ __device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, 
     r.a = ld<uint32_t, NT>(w + rg.s, og * 4u);
   } else if constexpr (F == DT_Q4_K) {
     r.q0 = ld<uint4, NT>(w, og * 16u);
-    r.q1 = ld<uint4, NT>(w + rg.s, ((uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3)) * 16u);
+    const uint32_t hb = ((uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3)) * 16u;
+    if constexpr (QH)
+      r.q1.x = ld<uint32_t, NT>(w + rg.s, hb + 4u * (threadIdx.x & 3u));
+    else
+      r.q1 = ld<uint4, NT>(w + rg.s, hb);
   } else if constexpr (F == DT_Q6_K) {
     const uint32_t ob = (uint32_t)o * (uint32_t)(G >> 3) + (uint32_t)(g >> 3);
     r.q0 = ld<uint4, NT>(w, og * 16u);
@@ -82,6 +92,17 @@ __device__ __forceinline__ void load_group(const uint8_t* w, const Regions& rg, 
     r.a = ld<uint16_t, NT>(w + rg.s, (ob * 8u + (uint32_t)(g & 7)) * 2u);
     r.d = ld<uint16_t, NT>(w + rg.s2, ob * 2u);
   }
+}
+
+// the header dwords of a QH load: dword i from lane i of the quad (DPP quad
+// broadcasts)
+__device__ __forceinline__ void expand_header(Raw& r)
+{
+  const uint32_t v = r.q1.x;
+  r.q1.x = __builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, false);
+  r.q1.y = __builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, false);
+  r.q1.z = __builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, false);
+  r.q1.w = __builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, false);
 }
 
 // float weights: 32 values of row o, group g (F32 128 bytes, BF16/F16 64)

@@ -171,11 +171,12 @@ __device__ __forceinline__ void group_q8k(const Raw& r, const int (&xw)[8], int 
   if constexpr (F == DT_Q4_K) {
     int sc, m;
     scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, m);
-    isum = sc * (sl + sh);
-    msum = m * (sxl + sxh);
+    // |sums| < 2^16 and scales < 64: 24-bit products (full-rate multiplies)
+    isum = __mul24(sc, sl + sh);
+    msum = __mul24(m, sxl + sxh);
   } else {
     int sa = (int)(int8_t)(r.a & 255u), sb = (int)(int8_t)(r.a >> 8);
-    isum = sa * (sl - 32 * sxl) + sb * (sh - 32 * sxh);
+    isum = __mul24(sa, sl - 32 * sxl) + __mul24(sb, sh - 32 * sxh);
     msum = 0;
   }
 }
@@ -202,7 +203,48 @@ struct XGroup {
   int w[8];
   float dx;
   int sl, sh;
+  // MXFP4 one-row path: the codes as f16 pairs (value j, value j + 16)
+  uint32_t h[16];
 };
+
+// the activation codes of a group as f16 pairs (x_j, x_16+j), j = 4d + i:
+// the operand order of the MXFP4 code bytes (value j low, j + 16 high nibble)
+__device__ __forceinline__ void half_pairs(XGroup& x)
+{
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float lo = (float)(int)(int8_t)(x.w[d] >> (8 * i));
+      const float hi = (float)(int)(int8_t)(x.w[4 + d] >> (8 * i));
+      x.h[4 * d + i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+    }
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Q8 mode, MXFP4, codes converted by the matrix-core-era conversion: every
+// code byte to two f16 (the doubled E2M1 values, scale 2), dotted with the f16
+// activation pairs. Every value is an integer below 2^11 and every partial sum
+// one below 2^24, so the float sum is the exact integer group sum.
+__device__ __forceinline__ double group_mxfp4_h(const Raw& r, const XGroup& x)
+{
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const uint32_t q = comp(r.q0, d);
+    const half2_t w0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 2.0f, 0);
+    const half2_t w1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 2.0f, 1);
+    const half2_t w2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 2.0f, 2);
+    const half2_t w3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 2.0f, 3);
+    s0 = __builtin_amdgcn_fdot2(w0, __builtin_bit_cast(half2_t, x.h[4 * d]), s0, false);
+    s1 = __builtin_amdgcn_fdot2(w1, __builtin_bit_cast(half2_t, x.h[4 * d + 1]), s1, false);
+    s0 = __builtin_amdgcn_fdot2(w2, __builtin_bit_cast(half2_t, x.h[4 * d + 2]), s0, false);
+    s1 = __builtin_amdgcn_fdot2(w3, __builtin_bit_cast(half2_t, x.h[4 * d + 3]), s1, false);
+  }
+  const int s = (int)s0 + (int)s1;
+  return (double)s * (mxfp4_q8_scale(r.a) * (double)x.dx);
+}
 
 template <int F, int MODE>
 __device__ __forceinline__ void load_x(const LinArgs& a, int64_t xrow, int g, int G, XGroup& x)
@@ -295,26 +337,73 @@ __device__ __forceinline__ double row_total(int lpr, const Raw& hdr, float dxsb,
 
 // the value of row o against the lane's activation groups: the lanes of the
 // row meet in row_total (lane 0 of the row segment holds it)
-template <int F, int MODE, int U>
-__device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&raw)[U], int64_t o,
+template <int F, int MODE, int U, bool HX = false>
+__device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&rawin)[U], int64_t o,
                                             bool valid, const XGroup (&xg)[U], int lr, int lpr,
                                             int G, int64_t in)
 {
-  float accf = 0.f;
-  double accd = 0.0, tot = 0.0;
+  Raw raw[U];
 #pragma unroll
   for (int k = 0; k < U; k++) {
-    int g = lr + k * lpr;
-    int isum = 0, msum = 0;
-    if (valid && g < G) group_term<F, MODE>(w, raw[k], o, g, in, xg[k], accf, accd, isum, msum);
-    if constexpr (MODE == 1 && is_k_quant(F)) {
-      // every k-th group set of the lanes forms whole super-blocks
-      bool lead = (g & 7) == 0 && valid && g < G;
-      tot += row_total<F, MODE>(lpr, raw[k], xg[k].dx, lead, 0.f, 0.0, isum, msum, g);
-    }
+    raw[k] = rawin[k];
+    if constexpr (F == DT_Q4_K) expand_header(raw[k]);  // the rows' loads are QH loads
   }
-  if constexpr (MODE == 1 && is_k_quant(F)) return tot;
-  return row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
+  if constexpr (HX) {
+    static_assert(F == DT_MXFP4 && MODE == 1, "f16 pairs: MXFP4 in the Q8 arithmetic");
+    double accd = 0.0;
+#pragma unroll
+    for (int k = 0; k < U; k++)
+    {
+      // every group is formed (a group past the row reads clamped codes and
+      // a zeroed activation), its term kept or dropped by a select
+      const double t = group_mxfp4_h(raw[k], xg[k]);
+      accd += (valid && lr + k * lpr < G) ? t : 0.0;
+    }
+    return wave_sum(accd, lpr);
+  } else if constexpr (MODE == 1 && is_k_quant(F)) {
+    // lpr is a multiple of 8 and G of 8: the k-th groups of 8 aligned lanes
+    // form one super-block. Its exact integer sums meet in all 8 lanes, each
+    // lane forms the super-block's double term, adds its super-blocks in
+    // order, and the super-block sets of a row (lpr / 8 of them) meet last.
+    int is[U], ms[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      const int g = lr + k * lpr;
+      float af = 0.f;
+      double ad = 0.0;
+      is[k] = ms[k] = 0;
+      group_term<F, MODE>(w, raw[k], o, g, in, xg[k], af, ad, is[k], ms[k]);
+      const bool ok = valid && g < G;
+      is[k] = ok ? is[k] : 0;
+      ms[k] = ok ? ms[k] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      is[k] = wave_sum(is[k], 8);
+      ms[k] = wave_sum(ms[k], 8);
+    }
+    double tot = 0.0;
+#pragma unroll
+    for (int k = 0; k < U; k++)
+    {
+      const double t = superblock_q8k<F>(raw[k], is[k], ms[k], xg[k].dx);
+      tot += (valid && lr + k * lpr < G) ? t : 0.0;
+    }
+    if (lpr > 8) tot = tot + xpart<8>(tot);
+    if (lpr > 16) tot = tot + xpart<16>(tot);
+    if (lpr > 32) tot = tot + xpart<32>(tot);
+    return tot;
+  } else {
+    float accf = 0.f;
+    double accd = 0.0;
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      int g = lr + k * lpr;
+      int isum = 0, msum = 0;
+      if (valid && g < G) group_term<F, MODE>(w, raw[k], o, g, in, xg[k], accf, accd, isum, msum);
+    }
+    return row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
+  }
 }
 
 // ------------------------------------------------- activation row in LDS
@@ -581,8 +670,8 @@ __device__ __forceinline__ void load_tiles(const uint8_t* w, const uint8_t* w2, 
 #pragma unroll
     for (int k = 0; k < U; k++) {
       const int g = min(lr + k * lpr, G - 1);
-      load_group<F, true>(w, rg, o, G, g, in, raw[i][k]);
-      if constexpr (GLU) load_group<F, true>(w2, rg, o, G, g, in, raw2[i][k]);
+      load_group<F, true, F == DT_Q4_K>(w, rg, o, G, g, in, raw[i][k]);
+      if constexpr (GLU) load_group<F, true, F == DT_Q4_K>(w2, rg, o, G, g, in, raw2[i][k]);
     }
   }
 }
@@ -662,6 +751,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     XGroup xg[U];
     Raw raw[T][U], raw2[T][U];
     __shared__ __align__(16) uint8_t xs[xs_bytes<F, MODE>()];
+    constexpr bool HXP = F == DT_MXFP4 && MODE == 1;  // f16 activation pairs
     // the activation row's global loads first, then the first step's weight
     // loads, so the row is staged while the weights are on their way
     XStage st;
@@ -678,7 +768,9 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
 #pragma unroll
     for (int k = 0; k < U; k++) {
       int g = lr + k * lpr;
+      xg[k] = XGroup{};
       if (g < G) lds_x<F, MODE>(xs, (const float*)(xs + a.in), g, xg[k]);
+      if constexpr (HXP) half_pairs(xg[k]);
     }
     // the T tiles of a step from their weight registers
     auto step = [&](int64_t sb, const Raw (&rw)[T][U], const Raw (&rw2)[T][U]) {
@@ -687,9 +779,9 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         const int64_t t = sb + (int64_t)i * nw;
         const int64_t o = t * rpw + rsub;
         const bool valid = t < tiles && o < out;
-        double v = row_value<F, MODE, U>(w, rw[i], o, valid, xg, lr, lpr, G, a.in);
+        double v = row_value<F, MODE, U, HXP>(w, rw[i], o, valid, xg, lr, lpr, G, a.in);
         double v2 = 0.0;
-        if constexpr (GLU) v2 = row_value<F, MODE, U>(w2, rw2[i], o, valid, xg, lr, lpr, G, a.in);
+        if constexpr (GLU) v2 = row_value<F, MODE, U, HXP>(w2, rw2[i], o, valid, xg, lr, lpr, G, a.in);
         if (lr == 0 && valid) {
           if (bias) v = (double)bias[o] + v;
           float r = (float)v;
@@ -816,7 +908,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int k = 0; k < U; k++)
-          load_group<F, true>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
+          load_group<F, true, F == DT_Q4_K>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
     }
   };
   load(t);
@@ -839,6 +931,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
 #pragma unroll
         for (int k = 0; k < U; k++) {
           const int g = lr + k * lpr;
+          xg[k] = XGroup{};
           if (g < G) lds_x<F, MODE>(cmb_xs, dxs, sl * G + g, xg[k]);
         }
         double v = row_value<F, MODE, U>(wi[i], raw[i], o, valid && ok[i], xg, lr, lpr, G, a.in);

@@ -15,7 +15,8 @@
 // value j in its low and value j + 16 in its high nibble (the Q4_0 order);
 // Q4_K and Q6_K are reordered into it from their GGUF super-block order.
 //
-//   Q8_0 : Q int8 [out][in]               | S fp16 [out][G]
+//   Q8_0 : Q int8 [out][2][G][16] (per row: the first 16 values of every
+//          group, then their last 16)  | S fp16 [out][G]
 //   Q4_0 : Q u8 [out][G][16]              | S fp16 [out][G]
 //   MXFP4: Q u8 [out][G][16]              | S e8m0 u8 [out][G]
 //   Q5_0 : Q u8 [out][G][16] | H u32 [out][G] (bit v: 5th bit of value v)

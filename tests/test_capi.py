@@ -61,7 +61,9 @@ def test_repack_layout_regions(dtype):
     packed = H.repack(src, dtype, rows, cols)
     G = cols // 32
     if dtype == H.Q8_0:
-        codes = packed[:rows * cols].view(np.int8).reshape(rows, cols)
+        # per row: the first 16 values of every group, then their last 16
+        codes = packed[:rows * cols].view(np.int8).reshape(rows, 2, G, 16)
+        codes = codes.transpose(0, 2, 1, 3).reshape(rows, cols)
         d = packed[rows * cols:].view(np.float16).reshape(rows, G).astype(np.float32)
         assert np.array_equal(codes * np.repeat(d, 32, axis=1), deq)
     elif dtype == H.Q4_0:
