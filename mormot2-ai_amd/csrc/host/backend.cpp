@@ -862,15 +862,17 @@ int enqueue_attention_one(ihip_ctx* c, const AttnOne& o)
     double* part;
     double scale, eps;
     int32_t heads, kvh, hd, past, window, splits;
+    int* done;
   } a = {(const float*)o.q, (const float*)o.k, (const float*)o.v, (const float*)o.qn,
          (const float*)o.kn, (const float*)o.cs, (void*)o.kc, (void*)o.vc, (float*)o.y,
          (const float*)o.sinks, (const int*)o.pastp, (double*)o.part,
          o.scale > 0 ? o.scale : 1.0 / std::sqrt((double)o.hd), o.eps, (int32_t)o.heads,
-         (int32_t)o.kvh, (int32_t)o.hd, (int32_t)o.past, (int32_t)o.window, o.splits};
+         (int32_t)o.kvh, (int32_t)o.hd, (int32_t)o.past, (int32_t)o.window, o.splits,
+         (int*)o.done};
   char name[32];
   snprintf(name, sizeof name, "attention_one_%s_%d", o.f16 ? "f16" : "f32", (int)o.hd);
   int rc = launch(c, name, dim3((unsigned)o.heads, 1, (unsigned)o.splits), dim3(256), &a);
-  if (rc) return rc;
+  if (rc || o.done) return rc;
   struct {
     const float* q;
     const void* kc;

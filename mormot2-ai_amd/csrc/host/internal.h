@@ -153,6 +153,7 @@ int enqueue_addnorm_moe(ihip_ctx* c, uint64_t x, uint64_t cd, uint64_t cw, int64
 struct AttnOne {
   uint64_t q = 0, k = 0, v = 0, qn = 0, kn = 0, cs = 0, kc = 0, vc = 0, y = 0, sinks = 0;
   uint64_t pastp = 0, part = 0;
+  uint64_t done = 0;  // [heads] zeroed counters: the merge in the kernel's last block per head
   double scale = 0, eps = 0;
   int64_t heads = 0, kvh = 0, hd = 0, past = 0, window = 0;
   int splits = 1, f16 = 0;

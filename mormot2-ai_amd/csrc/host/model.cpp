@@ -48,6 +48,9 @@ struct ihip_model {
   uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
   uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
   uint64_t attn_part = 0;               // flash-decoding partials
+  // zeroed counters of the decode attention's heads (the last range block of
+  // a head merges the head)
+  uint64_t done = 0;
   uint64_t logits_all = 0;
   int64_t logits_all_rows = 0;
   std::vector<uint64_t> owned;
@@ -330,6 +333,7 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
       o.part = m->attn_part; o.scale = 1.0 / std::sqrt((double)hd);
       o.eps = d.rms_eps; o.heads = d.heads; o.kvh = d.kv_heads; o.hd = hd; o.past = past;
       o.window = L.window; o.f16 = m->kv_f16;
+      if (d.heads <= 256) o.done = m->done;  // the merge in the last range block of a head
       int64_t maxkeys = graph ? m->max_tokens : past + 1;
       if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
       o.splits = attention_splits(maxkeys);
@@ -696,6 +700,11 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
                    m->items)))
     return bad(rc);
   if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
+  if ((rc = dalloc(m, 4096, m->done))) return bad(rc);
+  {
+    const hipError_t e = hipMemsetAsync((void*)m->done, 0, 4096, m->c->stream);
+    if (e != hipSuccess) return bad(hip_fail(e, "model: counters"));
+  }
   if ((rc = dalloc(m, (uint64_t)d.heads * N * attention_splits(max_tokens) * (hd + 2) * 8,
                    m->attn_part)))
     return bad(rc);

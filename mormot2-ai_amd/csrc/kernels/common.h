@@ -96,6 +96,49 @@ __device__ __forceinline__ float swiglu_value(float g, float u, float alpha, flo
   return b * u;
 }
 
+// ------------------------------------------- results handed between blocks
+// A block that hands results to the launch's last block (which counts the
+// others in with an atomic counter) writes them with agent-scope stores and
+// the last block reads them with agent-scope loads: both go through to the
+// device's coherence point, so the blocks of different XCDs (each with its
+// own L2) meet without an L2 write-back and invalidation per block (the
+// cost of a device-scope fence). wait_stores() completes a block's stores
+// before it counts itself.
+__device__ __forceinline__ void store_agent(float* p, float v)
+{
+  __hip_atomic_store((uint32_t*)p, __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(double* p, double v)
+{
+  __hip_atomic_store((uint64_t*)p, __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p)
+{
+  return __builtin_bit_cast(float, __hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ double load_agent(const double* p)
+{
+  return __builtin_bit_cast(double, __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void wait_stores() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// the launch's last block to arrive (all of the block's stores complete
+// first); every thread calls it, every thread gets the answer
+__device__ __forceinline__ bool last_block(int* counter, int blocks)
+{
+  __shared__ int last;
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == blocks - 1;
+  __syncthreads();
+  return last;
+}
+
 // ------------------------------------------------ wave reductions in VGPRs
 // xpart<K>(v): the value of a lane in the sibling block of K lanes (the block
 // that differs in lane bit K), moved inside the register file: DPP quad

@@ -556,22 +556,27 @@ extern "C" __global__ __launch_bounds__(256) void attention_part_f32(AttnArgs a)
 }
 
 // y = sum_s exp(m_s - M) acc_s / (sum_s exp(m_s - M) l_s + exp(sink - M)),
-// M the largest range maximum (and the sink); one block per (head, row)
-extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
+// M the largest range maximum (and the sink), over the splits ranges of one
+// (head, row) at b (each hd values, its maximum, its sum); y the head's hd
+// outputs. Every thread of the block calls it (at least 64 threads, splits
+// <= 256).
+template <bool AG = false>
+__device__ __forceinline__ void merge_ranges(const double* b, int splits, int d, const float* sink,
+                                             float* y)
 {
+  // AG: the ranges were written by other blocks of this launch
+  auto rd = [&](int i) { return AG ? load_agent(b + i) : b[i]; };
   // the range weights exp(m_s - M) once, in LDS; the sums in range order
   __shared__ double wts[256];
   __shared__ double dsh[2];
-  const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-  const int d = a.hd;
-  const double* b = a.part + ((int64_t)h * a.rows + r) * a.splits * (d + 2);
+  const int t = threadIdx.x;
   if (t < 64) {
     double M = -1.0e308;
-    for (int s = t; s < a.splits; s += 64) M = fmax(M, b[s * (d + 2) + d]);
+    for (int s = t; s < splits; s += 64) M = fmax(M, rd(s * (d + 2) + d));
     M = wave_max(M);
-    if (a.sinks && (double)a.sinks[h] > M) M = a.sinks[h];
-    for (int s = t; s < a.splits; s += 64) {
-      double ms = b[s * (d + 2) + d];
+    if (sink && (double)*sink > M) M = *sink;
+    for (int s = t; s < splits; s += 64) {
+      double ms = rd(s * (d + 2) + d);
       wts[s] = ms > -1.0e308 ? exp(ms - M) : 0.0;
     }
     if (t == 0) dsh[0] = M;
@@ -579,17 +584,26 @@ extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
   __syncthreads();
   if (t == 0) {
     double den = 0;
-    for (int s = 0; s < a.splits; s++) den = den + wts[s] * b[s * (d + 2) + d + 1];
-    if (a.sinks) den = den + exp((double)a.sinks[h] - dsh[0]);
+    for (int s = 0; s < splits; s++) den = den + wts[s] * rd(s * (d + 2) + d + 1);
+    if (sink) den = den + exp((double)*sink - dsh[0]);
     dsh[1] = 1.0 / den;
   }
   __syncthreads();
   const double inv = dsh[1];
   for (int i = t; i < d; i += blockDim.x) {
     double acc = 0;
-    for (int s = 0; s < a.splits; s++) acc = acc + wts[s] * b[s * (d + 2) + i];
-    a.y[(int64_t)r * a.heads * d + (int64_t)h * d + i] = (float)(acc * inv);
+    for (int s = 0; s < splits; s++) acc = acc + wts[s] * rd(s * (d + 2) + i);
+    y[i] = (float)(acc * inv);
   }
+}
+
+// one block per (head, row)
+extern "C" __global__ __launch_bounds__(256) void attention_merge(AttnArgs a)
+{
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int d = a.hd;
+  merge_ranges(a.part + ((int64_t)h * a.rows + r) * a.splits * (d + 2), a.splits, d,
+               a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)r * a.heads * d + (int64_t)h * d);
 }
 
 // ------------------------------------------------------------------- MoE
@@ -615,6 +629,10 @@ struct AttnOneArgs {
   double* part;      // [heads, splits, hd + 2]
   double scale, eps;
   int32_t heads, kvh, hd, past, window, splits;
+  // [heads] counters, zero between launches, or null: with them the last
+  // range block of a head to finish merges the head's ranges (and sets its
+  // counter back to zero), else attention_merge does
+  int* done;
 };
 
 // the sums of two values over a block of 256 (wave sums, then 4 waves)
@@ -877,17 +895,24 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     accs[w][2 * pair + 1] = a1;
   }
   __syncthreads();
+  // agent-scope stores: the head's last range block may read them
   if (n > 0) {
-    for (int i = t; i < d; i += 256) out[i] = (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]);
+    for (int i = t; i < d; i += 256)
+      store_agent(out + i, (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]));
     if (t == 0) {
-      out[d] = m;
-      out[d + 1] = (red[4] + red[5]) + (red[6] + red[7]);
+      store_agent(out + d, m);
+      store_agent(out + d + 1, (red[4] + red[5]) + (red[6] + red[7]));
     }
   } else if (t == 0) {  // an empty range: weight 0 in the merge
-    out[d] = -1.0e308;
-    out[d + 1] = 0.0;
+    store_agent(out + d, -1.0e308);
+    store_agent(out + d + 1, 0.0);
   }
-
+  // the head's last range block to finish merges the head's ranges
+  if (a.done && last_block(a.done + h, a.splits)) {
+    merge_ranges<true>(a.part + (int64_t)h * a.splits * (d + 2), a.splits, d,
+                       a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d);
+    if (t == 0) a.done[h] = 0;
+  }
 }
 
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_64(AttnOneArgs a)
