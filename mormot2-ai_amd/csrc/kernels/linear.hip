@@ -25,6 +25,22 @@
 // are added exactly before the one double product of the super-block.
 #include "formats.h"
 
+// IHIP_STAMP(i): with IHIP_TRACE defined (a timing build that defines
+// ihip_trace), wave 0 of a block records the 100 MHz clock at phase i of the
+// one-row GEMV; compiled out otherwise
+#ifdef IHIP_TRACE
+#define IHIP_STAMP(i)                                                                       \
+  do {                                                                                      \
+    if (threadIdx.x == 0)                                                                   \
+      ihip_trace[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + (i)] =                \
+          __builtin_amdgcn_s_memrealtime();                                                 \
+  } while (0)
+#else
+#define IHIP_STAMP(i) \
+  do {                \
+  } while (0)
+#endif
+
 namespace ihip {
 
 struct LinArgs {
@@ -740,6 +756,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
+    IHIP_STAMP(0);
     if ((int64_t)blockIdx.x * (blockDim.x >> 6) >= tiles) return;  // the whole block: no tile
     // T tiles per wave step, their weight loads issued together (and the
     // first ones before the activation row is read), so a wave keeps several
@@ -762,9 +779,11 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     int64_t tb = wid;
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
+    IHIP_STAMP(1);
     stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
                          1 + (int)xrow0);
     __syncthreads();
+    IHIP_STAMP(2);
 #pragma unroll
     for (int k = 0; k < U; k++) {
       int g = lr + k * lpr;
@@ -794,12 +813,15 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         }
       }
     };
+    IHIP_STAMP(3);
     while (tb < tiles) {
       step(tb, raw, raw2);
+      IHIP_STAMP(4);
       tb += (int64_t)T * nw;
       if (tb < tiles)
         load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw, raw2);
     }
+    IHIP_STAMP(5);
   } else {
     // the activation and output rows of the batch
     int64_t xr[R], yr[R];
