@@ -345,6 +345,9 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   int lpr = 64, U = 1;
   int64_t out_max = k.out;
   for (int i = 0; i < k.nseg && i < 3; i++) out_max = std::max<int64_t>(out_max, k.oseg[i]);
+  // the experts of one token's slots share the launch: their rows together
+  // decide between narrow and wide rows
+  if (k.ids && !k.cw && !k.items) out_max *= std::max<int64_t>(1, k.rows);
   pick_lpr(G, out_max, c->cus, lpr, U);
   uint64_t xq = k.xq;
   const int mode = k.mode & 1;

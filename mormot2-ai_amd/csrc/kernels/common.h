@@ -8,6 +8,22 @@
 
 #include "../layout.h"
 
+// IHIP_STAMP(i): with IHIP_TRACE defined (a timing build that defines
+// ihip_trace), thread 0 of a block records the 100 MHz clock at phase i of
+// an instrumented kernel; compiled out otherwise
+#ifdef IHIP_TRACE
+#define IHIP_STAMP(i)                                                                            \
+  do {                                                                                           \
+    if (threadIdx.x == 0)                                                                        \
+      ihip_trace[(((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8 + \
+                 (i)] = __builtin_amdgcn_s_memrealtime();                                        \
+  } while (0)
+#else
+#define IHIP_STAMP(i) \
+  do {                \
+  } while (0)
+#endif
+
 namespace ihip {
 
 __device__ __forceinline__ float half_to_float(uint32_t h)

@@ -25,22 +25,6 @@
 // are added exactly before the one double product of the super-block.
 #include "formats.h"
 
-// IHIP_STAMP(i): with IHIP_TRACE defined (a timing build that defines
-// ihip_trace), wave 0 of a block records the 100 MHz clock at phase i of the
-// one-row GEMV; compiled out otherwise
-#ifdef IHIP_TRACE
-#define IHIP_STAMP(i)                                                                       \
-  do {                                                                                      \
-    if (threadIdx.x == 0)                                                                   \
-      ihip_trace[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + (i)] =                \
-          __builtin_amdgcn_s_memrealtime();                                                 \
-  } while (0)
-#else
-#define IHIP_STAMP(i) \
-  do {                \
-  } while (0)
-#endif
-
 namespace ihip {
 
 struct LinArgs {
@@ -777,8 +761,21 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
                               quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
                               a.nw, st);
     int64_t tb = wid;
+    // the epilogue operands of a step's rows (bias, up bias, residual), loaded
+    // with its weights rather than after its sums (a null operand reads x[0])
+    float eb[T], eb2[T], er[T];
+    auto load_epi = [&](int64_t sb) {
+#pragma unroll
+      for (int i = 0; i < T; i++) {
+        const int64_t o = min((sb + (int64_t)i * nw) * rpw + rsub, (int64_t)out - 1);
+        eb[i] = *(bias ? bias + o : a.x);
+        if constexpr (GLU) eb2[i] = *(bias2 ? bias2 + o : a.x);
+        er[i] = *(a.res ? a.res + o : a.x);
+      }
+    };
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
+    load_epi(tb);
     IHIP_STAMP(1);
     stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
                          1 + (int)xrow0);
@@ -802,13 +799,13 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
         double v2 = 0.0;
         if constexpr (GLU) v2 = row_value<F, MODE, U, HXP>(w2, rw2[i], o, valid, xg, lr, lpr, G, a.in);
         if (lr == 0 && valid) {
-          if (bias) v = (double)bias[o] + v;
+          if (bias) v = (double)eb[i] + v;
           float r = (float)v;
           if constexpr (GLU) {
-            if (bias2) v2 = (double)bias2[o] + v2;
+            if (bias2) v2 = (double)eb2[i] + v2;
             r = swiglu_value(r, (float)v2, a.alpha, a.limit);
           }
-          if (a.res) r = a.res[o] + r;
+          if (a.res) r = er[i] + r;
           yp[yrow0 * out + o] = r;
         }
       }
@@ -818,8 +815,10 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       step(tb, raw, raw2);
       IHIP_STAMP(4);
       tb += (int64_t)T * nw;
-      if (tb < tiles)
+      if (tb < tiles) {
         load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw, raw2);
+        load_epi(tb);
+      }
     }
     IHIP_STAMP(5);
   } else {
@@ -922,16 +921,20 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
     wi[i] = a.w + e[i] * a.stride;
   }
   Raw raw[2][U];
+  float eb[2], er;  // the tile row's expert biases and residual, loaded with its weights
   int64_t t = blockIdx.x;
   auto load = [&](int64_t tt) {
+    const int64_t o = min(tt * rpw + rsub, (int64_t)a.out - 1);
     if constexpr (!is_float_type(F)) {
-      const int64_t o = min(tt * rpw + rsub, (int64_t)a.out - 1);
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int k = 0; k < U; k++)
           load_group<F, true, F == DT_Q4_K>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
     }
+#pragma unroll
+    for (int i = 0; i < 2; i++) eb[i] = *(a.bias ? a.bias + e[i] * a.out + o : a.x);
+    er = *(a.res ? a.res + o : a.x);
   };
   load(t);
   for (int c0 = 0; c0 < n; c0 += XN) {
@@ -960,7 +963,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
         if (lr == 0) {
           float d = 0.f;
           if (valid && ok[i]) {
-            if (a.bias) v = (double)a.bias[e[i] * a.out + o] + v;
+            if (a.bias) v = (double)eb[i] + v;
             d = (float)v;
           }
           dv[sl][rsub] = d;
@@ -968,6 +971,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
       }
     }
     __syncthreads();
+    const float res = er;  // this tile's residual, before the next tile's loads
     const int64_t tn = t + gridDim.x;
     if (tn < tiles) load(tn);
     if (wave == 0 && lr == 0 && valid) {
@@ -976,7 +980,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
         float p = a.cw[sl] * dv[sl][rsub];
         add = add + p;
       }
-      a.y[o] = a.res ? a.res[o] + add : add;
+      a.y[o] = a.res ? res + add : add;
     }
     __syncthreads();
     t = tn;

@@ -661,6 +661,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   __shared__ double accs[4][HD];
   const int h = blockIdx.x, s = blockIdx.z, t = threadIdx.x;
   constexpr int d = HD, half = HD / 2;
+  IHIP_STAMP(0);
   const int64_t kvw = (int64_t)a.kvh * d;
   const int g = h / (a.heads / a.kvh);
   const int past = a.pastp ? *a.pastp : a.past;
@@ -737,6 +738,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     }
   }
 
+  IHIP_STAMP(1);
   // ---- the head norms (qkrope's arithmetic) and RoPE of q and the new key
   {
     double sq = (double)qv * (double)qv, sk = (double)kv * (double)kv;
@@ -797,6 +799,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   // the double sum differs from the CPU's). f16 keys: two threads per key,
   // each half of the dimensions, from the LDS key tile (the new key in it);
   // f32 keys: a thread per key from its registers.
+  IHIP_STAMP(2);
   double m = -1.0e308;
   if constexpr (F16) {
     const int kk = t >> 1, hh = t & 1;
@@ -855,6 +858,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   __syncthreads();
   if (l == 0) red[4 + w] = e;
 
+  IHIP_STAMP(3);
   // ---- the weighted values: the loads above, the new value from LDS
   // two chains per dimension (even and odd key slots); no branch: a slot
   // past the range has weight 0, the new key's value is selected
@@ -895,6 +899,7 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     accs[w][2 * pair + 1] = a1;
   }
   __syncthreads();
+  IHIP_STAMP(4);
   // agent-scope stores: the head's last range block may read them
   if (n > 0) {
     for (int i = t; i < d; i += 256)
@@ -909,8 +914,10 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   }
   // the head's last range block to finish merges the head's ranges
   if (a.done && last_block(a.done + h, a.splits)) {
+    IHIP_STAMP(5);
     merge_ranges<true>(a.part + (int64_t)h * a.splits * (d + 2), a.splits, d,
                        a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d);
+    IHIP_STAMP(6);
     if (t == 0) a.done[h] = 0;
   }
 }
