@@ -46,7 +46,7 @@ struct GemmArgs {
   int32_t x_per_slot, pad2;
 };
 
-constexpr int GBM = 64, GBN = 64, GKC = 8;  // tile rows, outputs, groups per LDS stage
+constexpr int GBM = 64, GBN = 64, GKC = 8;  // tile rows, outputs, groups per chunk
 
 // the weight codes of lane half h (values 8h..8h+7 and 16+8h..16+8h+7 of the
 // group) as 16 int8 in the Q8 arithmetic's value (centred where the format
@@ -54,8 +54,21 @@ constexpr int GBM = 64, GBN = 64, GKC = 8;  // tile rows, outputs, groups per LD
 template <int F>
 __device__ __forceinline__ v4i b_operand(const Raw& r, int h)
 {
-  uint32_t c[4] = {code_bytes<F>(r, 2 * h, 0), code_bytes<F>(r, 2 * h + 1, 0),
-                   code_bytes<F>(r, 2 * h, 1), code_bytes<F>(r, 2 * h + 1, 1)};
+  // the lane half's view of the group: code dwords 2h and 2h + 1 moved to
+  // dwords 0 and 1, chosen by masks (values, never an index into registers)
+  const uint32_t m = 0u - (uint32_t)h;
+  Raw v = r;
+  v.q0.x = (r.q0.x & ~m) | (r.q0.z & m);
+  v.q0.y = (r.q0.y & ~m) | (r.q0.w & m);
+  v.q1.x = (r.q1.x & ~m) | (r.q1.z & m);
+  v.q1.y = (r.q1.y & ~m) | (r.q1.w & m);
+  if constexpr (F == DT_Q5_0 || F == DT_Q5_1) v.b = r.b >> (8 * h);  // 4 bits per code dword
+  if constexpr (F == DT_Q6_K) {  // 2 bits per code dword
+    v.b = r.b >> (4 * h);
+    v.c = r.c >> (4 * h);
+  }
+  uint32_t c[4] = {code_bytes<F>(v, 0, 0), code_bytes<F>(v, 1, 0), code_bytes<F>(v, 0, 1),
+                   code_bytes<F>(v, 1, 1)};
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     uint32_t t = c[k];
@@ -78,11 +91,123 @@ __device__ __forceinline__ v4i b_operand(const Raw& r, int h)
 // minimum / offset the CPU applies with it)
 constexpr bool needs_xsum(int F) { return F == DT_Q4_K || F == DT_Q5_1; }
 
+// The fields of Raw a format uses, as dwords: how a weight group sits in LDS.
+template <int F>
+constexpr int raw_dwords()
+{
+  return F == DT_Q8_0 ? 9 : (F == DT_Q4_K || F == DT_Q6_K) ? 8 : (F == DT_Q5_0 || F == DT_Q5_1) ? 6 : 5;
+}
+
+template <int F>
+__device__ __forceinline__ void raw_put(uint32_t* d, int stride, const Raw& r)
+{
+  uint32_t v[9] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, 0, 0, 0, 0, 0};
+  if constexpr (F == DT_Q8_0 || F == DT_Q4_K) {
+    v[4] = r.q1.x; v[5] = r.q1.y; v[6] = r.q1.z; v[7] = r.q1.w;
+    v[8] = r.a;
+  } else if constexpr (F == DT_Q6_K) {
+    v[4] = r.a; v[5] = r.b; v[6] = r.c; v[7] = r.d;
+  } else {
+    v[4] = r.a;
+    v[5] = r.b;
+  }
+#pragma unroll
+  for (int k = 0; k < raw_dwords<F>(); k++) d[k * stride] = v[k];
+}
+
+template <int F>
+__device__ __forceinline__ Raw raw_get(const uint32_t* d, int stride)
+{
+  uint32_t v[9];
+#pragma unroll
+  for (int k = 0; k < raw_dwords<F>(); k++) v[k] = d[k * stride];
+  Raw r{};
+  r.q0 = make_uint4(v[0], v[1], v[2], v[3]);
+  if constexpr (F == DT_Q8_0 || F == DT_Q4_K) {
+    r.q1 = make_uint4(v[4], v[5], v[6], v[7]);
+    if constexpr (F == DT_Q8_0) r.a = v[8];
+  } else if constexpr (F == DT_Q6_K) {
+    r.a = v[4]; r.b = v[5]; r.c = v[6]; r.d = v[7];
+  } else {
+    r.a = v[4];
+    if constexpr (F == DT_Q5_0 || F == DT_Q5_1) r.b = v[5];
+  }
+  return r;
+}
+
+// A chunk of GKC groups of a block's tile, loaded cooperatively with
+// coalesced accesses (each group of 8 lanes reads 8 consecutive groups of one
+// weight row; each 4 lanes one activation row's 256 code bytes) into
+// registers, then stored to LDS: the operands reach the lanes that feed
+// the MFMAs from LDS, never as 32 scattered rows per load instruction.
+struct ChunkRegs {
+  Raw wr[2];      // weight groups: column t / 8 (+ 32), group t % 8
+  v4u32 xc[4];    // activation codes: row t / 4, groups 2 (t % 4) and 2 (t % 4) + 1
+  float dx[2];    // and their scales
+};
+
+template <int F>
+__device__ __forceinline__ void chunk_load(const GemmArgs& a, const uint8_t* wb, const Regions& rg,
+                                           int col0, const int* sxr, int64_t xstride, int G, int gc,
+                                           ChunkRegs& cr)
+{
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int64_t o = min(col0 + (t >> 3) + 32 * p, a.out - 1);
+    load_group<F>(wb, rg, o, G, min(gc + (t & 7), G - 1), a.in, cr.wr[p]);
+  }
+  const uint8_t* xr = a.xq + (int64_t)sxr[t >> 2] * xstride;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int g = min(gc + 2 * (t & 3) + k, G - 1);
+    const v4u32* q = (const v4u32*)(xr + (int64_t)g * 32);
+    cr.xc[2 * k] = q[0];
+    cr.xc[2 * k + 1] = q[1];
+    cr.dx[k] = ((const float*)(xr + a.in))[g];
+  }
+}
+
+constexpr int GSW = GKC * raw_dwords<DT_Q8_0>() + 1;  // LDS dwords per weight column (odd)
+constexpr int GSA = GKC * 8 + 2;                     // LDS dwords per activation row
+
+template <int F>
+__device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, uint32_t* sa, float* sdx,
+                                            int* sbs)
+{
+  const int t = threadIdx.x;
+  constexpr int WS = GKC * raw_dwords<F>() + 1;  // this format's column stride
+#pragma unroll
+  for (int p = 0; p < 2; p++) raw_put<F>(sw + ((t >> 3) + 32 * p) * WS + (t & 7), GKC, cr.wr[p]);
+  const int row = t >> 2;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int j = 2 * (t & 3) + k;
+    uint32_t* d = sa + row * GSA + j * 8;
+    *(v4u32*)d = cr.xc[2 * k];
+    *(v4u32*)(d + 4) = cr.xc[2 * k + 1];
+    sdx[j * GBM + row] = cr.dx[k];
+    if constexpr (needs_xsum(F)) {
+      const v4u32 u0 = cr.xc[2 * k], u1 = cr.xc[2 * k + 1];
+      int sm = 0;
+      sm = sdot4((int)u0.x, 0x01010101, sm); sm = sdot4((int)u0.y, 0x01010101, sm);
+      sm = sdot4((int)u0.z, 0x01010101, sm); sm = sdot4((int)u0.w, 0x01010101, sm);
+      sm = sdot4((int)u1.x, 0x01010101, sm); sm = sdot4((int)u1.y, 0x01010101, sm);
+      sm = sdot4((int)u1.z, 0x01010101, sm); sm = sdot4((int)u1.w, 0x01010101, sm);
+      sbs[j * GBM + row] = sm;
+    }
+  }
+}
+
 template <int F>
 __device__ __forceinline__ void gemm(const GemmArgs& a)
 {
-  __shared__ float sdx[GKC][GBM];  // activation scales of the chunk's groups
-  __shared__ int sbs[GKC][GBM];    // activation code sums (Q4_K, Q5_1)
+  // one chunk's operands: weight groups by column, activation codes by row,
+  // the rows' scales and code sums
+  __shared__ uint32_t sw_[GBN * GSW];
+  __shared__ __align__(16) uint32_t sa_[GBM * GSA];
+  __shared__ __align__(16) float sdx_[GKC * GBM];
+  __shared__ int sbs_[needs_xsum(F) ? GKC * GBM : 1];
   __shared__ int sxr[GBM], syr[GBM];
   const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5;
   const int wm = w & 1, wn = w >> 1;
@@ -109,10 +234,13 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
   }
   __syncthreads();
   const Regions rg = regions(F, a.out, a.in);
-  const int o_real = blockIdx.x * GBN + 32 * wn + (l & 31);
+  const int col0 = blockIdx.x * GBN;
+  const int o_real = col0 + 32 * wn + (l & 31);
   const int64_t o = min(o_real, a.out - 1);
-  const uint8_t* xa = a.xq + (int64_t)sxr[32 * wm + (l & 31)] * xstride;  // this lane's A row
   const int rb = 32 * wm + 4 * h;  // tile row of result register i: rb + 8 (i / 4) + i % 4
+  constexpr int WS = GKC * raw_dwords<F>() + 1;
+  const uint32_t* myw = sw_ + (32 * wn + (l & 31)) * WS;     // this lane's weight column
+  const uint32_t* mya = sa_ + (32 * wm + (l & 31)) * GSA;    // this lane's activation row
 
   double acc[16];
   int isum[16], msum[16];
@@ -122,99 +250,109 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
     isum[i] = msum[i] = 0;
   }
 
-  for (int gc = 0; gc < G; gc += GKC) {
-    __syncthreads();  // the previous chunk's LDS reads are done
-    for (int e = t; e < GKC * GBM; e += 256) {
-      const int j = e / GBM, rt = e % GBM, g = min(gc + j, G - 1);
-      const uint8_t* xr = a.xq + (int64_t)sxr[rt] * xstride;
-      sdx[j][rt] = ((const float*)(xr + a.in))[g];
-      if constexpr (needs_xsum(F)) {
-        const uint4* p = (const uint4*)(xr + (int64_t)g * 32);
-        uint4 u0 = p[0], u1 = p[1];
-        int sm = 0;
-        sm = sdot4((int)u0.x, 0x01010101, sm); sm = sdot4((int)u0.y, 0x01010101, sm);
-        sm = sdot4((int)u0.z, 0x01010101, sm); sm = sdot4((int)u0.w, 0x01010101, sm);
-        sm = sdot4((int)u1.x, 0x01010101, sm); sm = sdot4((int)u1.y, 0x01010101, sm);
-        sm = sdot4((int)u1.z, 0x01010101, sm); sm = sdot4((int)u1.w, 0x01010101, sm);
-        sbs[j][rt] = sm;
-      }
-    }
-    __syncthreads();
-    const int nj = min(GKC, G - gc);
-    for (int j = 0; j < nj; j++) {
+  // chunk c + 1 is in registers (its loads issued during chunk c - 1) while
+  // chunk c is computed from LDS; loads past the last group read the last
+  // group (values unused)
+  const int nch = (G + GKC - 1) / GKC;
+  ChunkRegs cr;
+  chunk_load<F>(a, wb, rg, col0, sxr, xstride, G, 0, cr);
+  chunk_store<F>(cr, sw_, sa_, sdx_, sbs_);
+  chunk_load<F>(a, wb, rg, col0, sxr, xstride, G, GKC, cr);
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    const int gc = c * GKC;
+#pragma unroll
+    for (int j = 0; j < GKC; j++) {
       const int g = gc + j;
-      Raw r;
-      load_group<F>(wb, rg, o, G, g, a.in, r);
-      const uint2 x0 = *(const uint2*)(xa + (int64_t)g * 32 + 8 * h);
-      const uint2 x1 = *(const uint2*)(xa + (int64_t)g * 32 + 16 + 8 * h);
-      const v4i bv = b_operand<F>(r, h);
-      v16i s;
-      v16i s2 = {};
-      if constexpr (F == DT_Q6_K) {
-        // the two 16-value sub-blocks of the group, each its own sum
-        const v16i z = {};
-        s = __builtin_amdgcn_mfma_i32_32x32x16_i8(
-            (long)(((uint64_t)x0.y << 32) | x0.x),
-            (long)(((uint64_t)(uint32_t)bv.y << 32) | (uint32_t)bv.x), z, 0, 0, 0);
-        s2 = __builtin_amdgcn_mfma_i32_32x32x16_i8(
-            (long)(((uint64_t)x1.y << 32) | x1.x),
-            (long)(((uint64_t)(uint32_t)bv.w << 32) | (uint32_t)bv.z), z, 0, 0, 0);
-      } else {
-        const v4i av = {(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
-        const v16i z = {};
-        s = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z, 0, 0, 0);
-      }
-      // the group's terms (group_q8 / group_q8k / superblock_q8k)
-      if constexpr (F == DT_Q4_K) {
-        int sc, mn;
-        scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, mn);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          isum[i] += sc * s[i];
-          msum[i] += mn * sbs[j][rb + 8 * (i >> 2) + (i & 3)];
-        }
-        if ((g & 7) == 7) {
-          const double hd = half_to_float(r.q1.x & 0xffffu), hm = half_to_float(r.q1.x >> 16);
-#pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
-            acc[i] = acc[i] + ((hd * dx) * (double)isum[i] - (hm * dx) * (double)msum[i]);
-            isum[i] = msum[i] = 0;
+      if (g < G) {
+        const Raw r = raw_get<F>(myw + j, GKC);
+        const uint2 x0 = *(const uint2*)(mya + j * 8 + 2 * h);
+        const uint2 x1 = *(const uint2*)(mya + j * 8 + 4 + 2 * h);
+        float (*sdx)[GBM] = (float (*)[GBM])sdx_;
+        int (*sbs)[GBM] = (int (*)[GBM])sbs_;
+        const int buf = 0;
+        (void)buf;
+          const v4i bv = b_operand<F>(r, h);
+          v16i s;
+          v16i s2 = {};
+          if constexpr (F == DT_Q6_K) {
+            // the two 16-value sub-blocks of the group, each its own sum
+            const v16i z = {};
+            s = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                (long)(((uint64_t)x0.y << 32) | x0.x),
+                (long)(((uint64_t)(uint32_t)bv.y << 32) | (uint32_t)bv.x), z, 0, 0, 0);
+            s2 = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                (long)(((uint64_t)x1.y << 32) | x1.x),
+                (long)(((uint64_t)(uint32_t)bv.w << 32) | (uint32_t)bv.z), z, 0, 0, 0);
+          } else {
+            const v4i av = {(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+            const v16i z = {};
+            s = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z, 0, 0, 0);
           }
-        }
-      } else if constexpr (F == DT_Q6_K) {
-        const int sa = (int)(int8_t)(r.a & 255u), sb = (int)(int8_t)(r.a >> 8);
+          // the group's terms (group_q8 / group_q8k / superblock_q8k)
+          if constexpr (F == DT_Q4_K) {
+            int sc, mn;
+            scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, mn);
 #pragma unroll
-        for (int i = 0; i < 16; i++) isum[i] += sa * s[i] + sb * s2[i];
-        if ((g & 7) == 7) {
-          const double d = half_to_float(r.d);
+            for (int i = 0; i < 16; i++) {
+              // |sums| < 2^16, scales < 64: 24-bit multiplies
+              isum[i] += __mul24(sc, s[i]);
+              msum[i] += __mul24(mn, sbs[j][rb + 8 * (i >> 2) + (i & 3)]);
+            }
+            if ((g & 7) == 7) {
+              const double hd = half_to_float(r.q1.x & 0xffffu), hm = half_to_float(r.q1.x >> 16);
 #pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
-            acc[i] = acc[i] + (d * dx) * (double)isum[i];
-            isum[i] = 0;
+              for (int i = 0; i < 16; i++) {
+                const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
+                acc[i] = acc[i] + ((hd * dx) * (double)isum[i] - (hm * dx) * (double)msum[i]);
+                isum[i] = msum[i] = 0;
+              }
+            }
+          } else if constexpr (F == DT_Q6_K) {
+            const int sa = (int)(int8_t)(r.a & 255u), sb = (int)(int8_t)(r.a >> 8);
+#pragma unroll
+            for (int i = 0; i < 16; i++) isum[i] += __mul24(sa, s[i]) + __mul24(sb, s2[i]);
+            if ((g & 7) == 7) {
+              const double d = half_to_float(r.d);
+#pragma unroll
+              for (int i = 0; i < 16; i++) {
+                const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
+                acc[i] = acc[i] + (d * dx) * (double)isum[i];
+                isum[i] = 0;
+              }
+            }
+          } else if constexpr (F == DT_Q5_1) {
+            const double d = half_to_float(r.a & 0xffffu), m = half_to_float(r.a >> 16);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+              const int ri = rb + 8 * (i >> 2) + (i & 3);
+              const double dx = sdx[j][ri];
+              const double tt = (double)s[i] * (d * dx);
+              acc[i] = acc[i] + (tt + m * (dx * (double)sbs[j][ri]));
+            }
+          } else {
+            double dw;
+            if constexpr (F == DT_MXFP4) dw = mxfp4_q8_scale(r.a);
+            else dw = half_to_float(r.a);
+            // s * dw * dx is exact in double (at most 19 + 11 + 11 significant
+            // bits), so one fused multiply-add rounds as the CPU's multiply-then-add
+            // the 16 rows' scales: four 16-byte LDS reads, all issued first
+            float4 dq[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) dq[q] = *(const float4*)&sdx[j][rb + 8 * q];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+              const float4 d4 = dq[i >> 2];
+              const double dx = (i & 3) == 0 ? d4.x : (i & 3) == 1 ? d4.y : (i & 3) == 2 ? d4.z : d4.w;
+              acc[i] = __builtin_fma((double)s[i], dw * dx, acc[i]);
+            }
           }
-        }
-      } else if constexpr (F == DT_Q5_1) {
-        const double d = half_to_float(r.a & 0xffffu), m = half_to_float(r.a >> 16);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const int ri = rb + 8 * (i >> 2) + (i & 3);
-          const double dx = sdx[j][ri];
-          const double tt = (double)s[i] * (d * dx);
-          acc[i] = acc[i] + (tt + m * (dx * (double)sbs[j][ri]));
-        }
-      } else {
-        double dw;
-        if constexpr (F == DT_MXFP4) dw = mxfp4_q8_scale(r.a);
-        else dw = half_to_float(r.a);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-          const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
-          acc[i] = acc[i] + ((double)s[i] * dw) * dx;
-        }
       }
     }
+    __syncthreads();  // the chunk's LDS reads are done
+    chunk_store<F>(cr, sw_, sa_, sdx_, sbs_);
+    chunk_load<F>(a, wb, rg, col0, sxr, xstride, G, gc + 2 * GKC, cr);
+    __syncthreads();
   }
   if (o_real >= a.out) return;
   const double b = bias ? (double)bias[o] : 0.0;
