@@ -911,9 +911,16 @@ int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_
   } a = {(const float*)q, (const void*)kc, (const void*)vc, (float*)y, (const float*)sinks,
          (const int*)pastp, (double*)part, scale, (int32_t)rows, (int32_t)heads, (int32_t)kvh,
          (int32_t)hd, (int32_t)past, (int32_t)window, f16, splits};
-  int rc = launch(c, f16 ? "attention_part_f16" : "attention_part_f32",
-                  dim3((unsigned)heads, (unsigned)rows, (unsigned)splits),
-                  dim3(256), &a);
+  int rc;
+  if ((hd == 64 || hd == 128) && rows > 1) {
+    // tiles of 8 rows sharing each range's keys
+    char name[32];
+    snprintf(name, sizeof name, "attention_rows_%s_%d", f16 ? "f16" : "f32", (int)hd);
+    rc = launch(c, name, dim3((unsigned)heads, (unsigned)((rows + 7) / 8), (unsigned)splits), dim3(256), &a);
+  } else {
+    rc = launch(c, f16 ? "attention_part_f16" : "attention_part_f32",
+                dim3((unsigned)heads, (unsigned)rows, (unsigned)splits), dim3(256), &a);
+  }
   if (rc) return rc;
   return launch(c, "attention_merge", dim3((unsigned)heads, (unsigned)rows), dim3(128), &a);
 }

@@ -545,6 +545,197 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   }
 }
 
+// The ranges of ATTR rows at once (prompt chunks, head_dim HD = 64 or 128):
+// one block per (head, tile of ATTR consecutive rows, range s). Row r's
+// range s is its keys first_r + s * ATT_CHUNK .. (its own window start and
+// causal end); the tile's rows together need at most ATT_CHUNK + ATTR - 1
+// keys, loaded once for all of them (attention_part loads them per row).
+// The arithmetic of a row is attention_part's: every score the CPU's
+// sequential double dot product, exp(score - range max) and the weighted
+// values in double, here summed in key order per row.
+constexpr int ATTR = 8;
+constexpr int ATTK = ATT_CHUNK + ATTR - 1;  // keys of a tile's range
+template <bool F16, int HD>
+__device__ __forceinline__ void attention_rows_t(const AttnArgs& a)
+{
+  __shared__ double qd[ATTR][HD];
+  __shared__ double sc[ATTR][ATTK + 1];
+  __shared__ double stat[ATTR][2];  // a row's range maximum and sum
+  const int h = blockIdx.x, r0 = blockIdx.y * ATTR, s = blockIdx.z, t = threadIdx.x;
+  constexpr int d = HD;
+  const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
+  const int g = h / (a.heads / a.kvh);
+  const int past = a.pastp ? *a.pastp : a.past;
+  // row r (tile row, r0 + r < rows): absolute keys [k0[r], k1[r]) of range s
+  auto range = [&](int r, int& k0, int& k1) {
+    const int total = past + r0 + r + 1;
+    const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
+    const int cnt = total - first;
+    const int j0 = min(cnt, s * ATT_CHUNK), j1 = min(cnt, j0 + ATT_CHUNK);
+    k0 = first + j0;
+    k1 = first + j1;
+    if (r0 + r >= a.rows) k0 = k1 = 0;
+  };
+  int kb, dummy;
+  range(0, kb, dummy);  // the tile's first key (row 0 starts earliest)
+  for (int i = t; i < ATTR * d; i += 256) {
+    const int r = i / d, c = i % d;
+    qd[r][c] = r0 + r < a.rows ? (double)a.q[(int64_t)(r0 + r) * qw + (int64_t)h * d + c] : 0.0;
+  }
+  __syncthreads();
+  // ---- scores: a thread per key of the tile, the rows' dots in key-row order
+  if (t < ATTK) {
+    const int key = kb + t;
+    bool in[ATTR];
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < ATTR; r++) {
+      int k0, k1;
+      range(r, k0, k1);
+      in[r] = key >= k0 && key < k1;
+      any |= in[r];
+    }
+    double acc[ATTR];
+#pragma unroll
+    for (int r = 0; r < ATTR; r++) acc[r] = 0.0;
+    if (any) {
+      const int64_t kr = (int64_t)key * kvw + (int64_t)g * d;
+      if constexpr (F16) {
+        const uint4* p = (const uint4*)((const uint16_t*)a.kc + kr);
+        uint4 u[d / 8];
+#pragma unroll
+        for (int k = 0; k < d / 8; k++) u[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < d / 8; k++) {
+          const uint32_t wv[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int i = 8 * k + 2 * j;
+            const double k0v = (double)half_to_float(wv[j] & 0xffffu), k1v = (double)half_to_float(wv[j] >> 16);
+            // q * k is exact in double: a fused multiply-add rounds as the
+            // CPU's multiply-then-add
+#pragma unroll
+            for (int r = 0; r < ATTR; r++) {
+              acc[r] = __builtin_fma(qd[r][i], k0v, acc[r]);
+              acc[r] = __builtin_fma(qd[r][i + 1], k1v, acc[r]);
+            }
+          }
+        }
+      } else {
+        const float4* p = (const float4*)((const float*)a.kc + kr);
+#pragma unroll 4
+        for (int k = 0; k < d / 4; k++) {
+          const float4 u = p[k];
+          const double kv[4] = {(double)u.x, (double)u.y, (double)u.z, (double)u.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < ATTR; r++) acc[r] = __builtin_fma(qd[r][4 * k + j], kv[j], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < ATTR; r++) sc[r][t] = in[r] ? acc[r] * a.scale : -1.0e308;
+  }
+  __syncthreads();
+  // ---- per row: the range maximum, the weights exp(score - max), their sum
+  // (wave w takes rows 2w and 2w + 1)
+  const int w = t >> 6, l = t & 63;
+#pragma unroll
+  for (int rr = 0; rr < 2; rr++) {
+    const int r = 2 * w + rr;
+    double m = -1.0e308;
+    for (int j = l; j < ATTK; j += 64) m = fmax(m, sc[r][j]);
+    m = wave_max(m);
+    double e = 0;
+    for (int j = l; j < ATTK; j += 64) {
+      const double x = sc[r][j];
+      const double p = x > -1.0e308 ? exp(x - m) : 0.0;
+      sc[r][j] = p;
+      e += p;
+    }
+    e = wave_sum(e, 64);
+    if (l == 0) {
+      stat[r][0] = m;
+      stat[r][1] = e;
+    }
+  }
+  __syncthreads();
+  // ---- the weighted values: wave w, rows 2w and 2w + 1; a lane holds a
+  // dimension pair (HD 64: lanes 32.. take every other key, added at the end)
+  constexpr int LPK = HD / 2;               // lanes per key
+  constexpr int KPW = 64 / LPK;             // keys side by side in a wave
+  const int pair = l % LPK, ks = l / LPK;
+  double a00 = 0, a01 = 0, a10 = 0, a11 = 0;  // [row][dim]
+  const int64_t vb = (int64_t)kb * kvw + (int64_t)g * d + 2 * pair;
+  constexpr int VB = 16;  // value loads in flight per lane
+  for (int j0 = ks; j0 < ATTK; j0 += VB * KPW) {
+    float2 v[VB];
+#pragma unroll
+    for (int u = 0; u < VB; u++) {
+      const int j = min(j0 + u * KPW, ATTK - 1);
+      // a key past the cache's end reads the tile's first key (weight 0)
+      const int64_t e = (kb + j < (int64_t)past + a.rows) ? vb + (int64_t)j * kvw : vb;
+      if constexpr (F16) {
+        const uint32_t x = *(const uint32_t*)((const uint16_t*)a.vc + e);
+        v[u] = make_float2(half_to_float(x & 0xffffu), half_to_float(x >> 16));
+      } else {
+        v[u] = *(const float2*)((const float*)a.vc + e);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VB; u++) {
+      const int j = j0 + u * KPW;
+      if (j < ATTK) {
+        const double p0 = sc[2 * w][j], p1 = sc[2 * w + 1][j];
+        a00 = a00 + p0 * (double)v[u].x;
+        a01 = a01 + p0 * (double)v[u].y;
+        a10 = a10 + p1 * (double)v[u].x;
+        a11 = a11 + p1 * (double)v[u].y;
+      }
+    }
+  }
+  if constexpr (KPW == 2) {
+    a00 = a00 + xpart<32>(a00);
+    a01 = a01 + xpart<32>(a01);
+    a10 = a10 + xpart<32>(a10);
+    a11 = a11 + xpart<32>(a11);
+  }
+#pragma unroll
+  for (int rr = 0; rr < 2; rr++) {
+    const int r = 2 * w + rr;
+    if (r0 + r >= a.rows) continue;
+    double* out = a.part + (((int64_t)h * a.rows + r0 + r) * a.splits + s) * (d + 2);
+    if (ks == 0) {
+      out[2 * pair] = rr ? a10 : a00;
+      out[2 * pair + 1] = rr ? a11 : a01;
+    }
+    if (l == 0) {
+      // an empty range: weight 0 in the merge
+      const bool empty = !(stat[r][1] > 0.0);
+      out[d] = empty ? -1.0e308 : stat[r][0];
+      out[d + 1] = empty ? 0.0 : stat[r][1];
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_rows_f16_64(AttnArgs a)
+{
+  attention_rows_t<true, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_rows_f16_128(AttnArgs a)
+{
+  attention_rows_t<true, 128>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_rows_f32_64(AttnArgs a)
+{
+  attention_rows_t<false, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_rows_f32_128(AttnArgs a)
+{
+  attention_rows_t<false, 128>(a);
+}
+
 extern "C" __global__ __launch_bounds__(256) void attention_part_f16(AttnArgs a)
 {
   attention_part_t<true>(a);
