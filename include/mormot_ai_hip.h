@@ -301,6 +301,9 @@ int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_
  * [rows, rope/2] cos then sin (TDecoderModel.Rotary, decoder.pas:2539-2561) */
 int ihip_model_rotary(const ihip_model_desc* desc, int64_t first, int64_t rows,
                       float* cs);
+/* prompt rows per chunk of a forward pass: 1..1024 (default 1024); the
+ * reference's CHUNK_MAX (model.qwen3.cuda.pas:308) is a constant 256 */
+int ihip_model_chunk(ihip_model* m, int64_t rows);
 /* decode steps as one replayed HIP graph (on, the default) or as direct
  * launches (TQwen3Cuda.UseGraphs, model.qwen3.cuda.pas:253-262) */
 int ihip_model_use_graphs(ihip_model* m, int on);

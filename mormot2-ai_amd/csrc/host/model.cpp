@@ -4,8 +4,9 @@
 // Qwen3 dense, Qwen3-MoE and gpt-oss shapes: per-head q/k norms, biases,
 // sinks, sliding windows, clamped SwiGLU, experts chosen on the device.
 //
-// A prompt runs in chunks of up to CHUNK rows (the 256 of CHUNK_MAX,
-// model.qwen3.cuda.pas:308); a decode step (one row) is one HIP graph,
+// A prompt runs in chunks of up to CHUNK rows (CHUNK_MAX of
+// model.qwen3.cuda.pas:308 is 256; here 1024 by default, so that a prompt
+// chunk's GEMMs fill the 256 CUs, ihip_model_chunk sets fewer); a decode step (one row) is one HIP graph,
 // captured once and replayed: the position lives in device memory, the
 // token id and the cos/sin of the position are copied in before each launch,
 // and the argmax runs on the device, so one int32 comes back per token.
@@ -18,7 +19,7 @@
 
 namespace ihip {
 
-static const int64_t CHUNK = 256;
+static const int64_t CHUNK = 1024;
 
 struct DevLayer {
   uint64_t input_norm = 0, post_norm = 0, q = 0, k = 0, v = 0, o = 0;
@@ -60,6 +61,7 @@ struct ihip_model {
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
   bool graph_ready = false;
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
+  int64_t chunk_rows = ihip::CHUNK;  // prompt rows per chunk (ihip_model_chunk), at most CHUNK
   int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
   double prefill_ms = 0, decode_ms = 0;
 };
@@ -708,8 +710,10 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
   if ((rc = dalloc(m, (uint64_t)d.heads * N * attention_splits(max_tokens) * (hd + 2) * 8,
                    m->attn_part)))
     return bad(rc);
-  if (any_moe && (d.experts > 4096 || N * d.experts_used > 4096))
-    return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or slots per chunk"));
+  // moe_plan counts the slots per expert in LDS (4096 experts); a chunk's
+  // work items stay within one grid dimension
+  if (any_moe && (d.experts > 4096 || N * d.experts_used > 65535))
+    return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or 65535 slots per chunk"));
   // a prompt chunk's experts on the MFMA GEMM when every expert matrix can
   // run there: work items of 64 slots
   bool all_gemm = any_moe;
@@ -753,8 +757,8 @@ int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count, float* 
   for (int64_t i = 0; i < count; i++)
     if (ids[i] < 0 || ids[i] >= m->d.vocab) return fail(IHIP_E_ARG, "token id outside the vocabulary");
   std::lock_guard<std::mutex> g(m->c->lock);
-  for (int64_t s = 0; s < count; s += CHUNK) {
-    int64_t n = std::min(CHUNK, count - s);
+  for (int64_t s = 0; s < count; s += m->chunk_rows) {
+    int64_t n = std::min(m->chunk_rows, count - s);
     bool last = s + n == count;
     bool want = logits && (all_logits || last);
     uint64_t ldev = m->logits;
@@ -792,8 +796,8 @@ int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n, int64_t m
   {
     // the prompt: every chunk, logits of the last row only, argmax on device
     std::lock_guard<std::mutex> g(c->lock);
-    for (int64_t s = 0; s < n && !rc; s += CHUNK) {
-      int64_t k = std::min(CHUNK, n - s);
+    for (int64_t s = 0; s < n && !rc; s += m->chunk_rows) {
+      int64_t k = std::min(m->chunk_rows, n - s);
       rc = chunk(m, prompt + s, k, s + k == n, false, m->logits);
     }
     if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
@@ -826,6 +830,13 @@ int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_
   int rc = decode_steps(m, first, steps, out_ids);
   m->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   return rc;
+}
+
+int ihip_model_chunk(ihip_model* m, int64_t rows)
+{
+  if (!m || rows < 1 || rows > CHUNK) return fail(IHIP_E_ARG, "ihip_model_chunk: 1.." + std::to_string(CHUNK) + " rows");
+  m->chunk_rows = rows;
+  return 0;
 }
 
 int ihip_model_use_graphs(ihip_model* m, int on)

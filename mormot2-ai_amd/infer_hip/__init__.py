@@ -94,6 +94,7 @@ def lib():
             "ihip_model_greedy": (i32, [vp, vp, i64, i64, vp]),
             "ihip_model_decode": (i32, [vp, C.c_int32, i64, vp]),
             "ihip_model_use_graphs": (i32, [vp, i32]),
+            "ihip_model_chunk": (i32, [vp, i64]),
             "ihip_enqueue_stream_read": (i32, [vp, u64, u64, u64]),
             "ihip_model_rotary": (i32, [vp, i64, i64, vp]),
             "ihip_model_timing": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -310,6 +311,9 @@ class Model:
         out = np.empty(max_new, np.int32)
         check(lib().ihip_model_greedy(self.h, _p(p), len(p), max_new, _p(out)), "greedy")
         return out
+
+    def chunk(self, rows):
+        check(lib().ihip_model_chunk(self.h, int(rows)), "chunk")
 
     def use_graphs(self, on):
         check(lib().ihip_model_use_graphs(self.h, int(on)), "use_graphs")

@@ -90,13 +90,17 @@ LONG = [
 ]
 
 
+@pytest.mark.parametrize("chunk", [1024, 100])
 @pytest.mark.parametrize("name,over", LONG)
-def test_tiny_greedy_long_context(ctx, name, over):
+def test_tiny_greedy_long_context(ctx, name, over, chunk):
     # a context of several 128-key ranges (and a window across them): the
-    # decode attention's ranges and their merge, replayed by the graph
+    # decode attention's ranges and their merge, replayed by the graph; the
+    # prompt in one chunk, or in chunks of 100 rows (a chunk's rows start
+    # inside a range and partway through the window)
     spec = models.Spec(models.tiny(name, **over), seed=57)
     prompt = np.random.default_rng(9).integers(0, spec.vocab, 300).astype(np.int32)
     dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=True, max_tokens=512)
+    dev.chunk(chunk)
     cpu = O.Model(spec, 512, kv_f16=True, threads=16)
     got = dev.greedy(prompt, 24)
     ref, margins = cpu.greedy(prompt, 24)
