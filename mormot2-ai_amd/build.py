@@ -15,7 +15,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 # linear.hip is built once per weight type (IHIP_ONLY_FMT), in parallel
 LINEAR_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf16", "f16"]
 # gemm.hip (the MFMA prefill GEMM) once per quantized weight type
-GEMM_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k"]
+GEMM_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf16", "f16"]
 KERNELS = ([("ops", "ops", [])] +
            [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in LINEAR_FMTS] +
            [("gemm_" + f, "gemm", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in GEMM_FMTS])

@@ -315,8 +315,10 @@ int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind
 static bool gemm_fmt(int t)
 {
   return t == DT_Q8_0 || t == DT_Q4_0 || t == DT_MXFP4 || t == DT_Q5_0 || t == DT_Q5_1 ||
-         t == DT_Q4_K || t == DT_Q6_K;
+         t == DT_Q4_K || t == DT_Q6_K || t == DT_F32 || t == DT_BF16 || t == DT_F16;
 }
+
+static bool float_fmt(int t) { return t == DT_F32 || t == DT_BF16 || t == DT_F16; }
 
 bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in)
 {
@@ -407,10 +409,12 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          k.dtype2 ? k.nseg1 : k.nseg};
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
-  if (k.items && k.item_rows > 8 && !(q8 && gemm_runs(c, k.dtype, mode)))
+  // (float weights in the Q8 arithmetic: the float activations as they are,
+  // on the f64 matrix cores)
+  const bool gemm_q8 = (q8 || float_fmt(k.dtype)) && gemm_runs(c, k.dtype, mode);
+  if (k.items && k.item_rows > 8 && !gemm_q8)
     return fail(IHIP_E_ARG, "EnqueueLinear: items of more than 8 slots need the GEMM");
-  if (batch && q8 && gemm_runs(c, k.dtype, mode) &&
-      (k.items ? k.item_rows > 8 : k.rows >= GEMM_MIN_ROWS)) {
+  if (batch && gemm_q8 && (k.items ? k.item_rows > 8 : k.rows >= GEMM_MIN_ROWS)) {
     struct {
       const uint8_t* w;
       const uint8_t* xq;
@@ -421,9 +425,10 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       const void* items;
       const int* perm;
       int32_t x_per_slot, pad2;
+      const float* x;
     } g = {(const uint8_t*)k.w, (const uint8_t*)xq, (const float*)k.bias, (float*)k.y, k.stride,
            (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, (const void*)k.items,
-           (const int*)k.perm, k.x_per_slot, 0};
+           (const int*)k.perm, k.x_per_slot, 0, (const float*)k.x};
     if (k.items && k.item_rows > 64) return fail(IHIP_E_ARG, "EnqueueLinear: items of at most 64 slots");
     char gname[32];
     snprintf(gname, sizeof gname, "gemm_%s", fmt_name(k.dtype));

@@ -44,6 +44,7 @@ struct GemmArgs {
   const int4* items;
   const int* perm;
   int32_t x_per_slot, pad2;
+  const float* x;  // float rows [*, in] (float weights)
 };
 
 constexpr int GBM = 64, GBN = 64, GKC = 8;  // tile rows, outputs, groups per chunk
@@ -367,13 +368,149 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
   }
 }
 
+// ------------------------------------------------------- float weights
+// y[r, o] = bias[o] + sum_i x[r, i] w[o, i] for F32 / BF16 / F16 weights in
+// the Q8 arithmetic of TInferCpuBackend.Linear's float branch
+// (backend.cpu.pas:1548-1565): every product of a float activation and a
+// float weight is exact in double, and the sum runs in double, here on the
+// f64 matrix cores (v_mfma_f64_16x16x4_f64; only the order of the double sum
+// differs from the CPU's). A block owns 64 rows x 64 outputs, each wave
+// 32 x 32 as 2 x 2 tiles of 16 x 16; chunks of FKC values of x and w are
+// loaded coalesced into LDS (the next chunk's loads in flight while one is
+// computed).
+typedef double v4d __attribute__((ext_vector_type(4)));
+constexpr int FKC = 32;  // values of the sum per chunk
+
+template <int F>
+__device__ __forceinline__ float wval(const void* w, int64_t i)
+{
+  if constexpr (F == DT_F32) return ((const float*)w)[i];
+  else if constexpr (F == DT_BF16) return bits_float((uint32_t)((const uint16_t*)w)[i] << 16);
+  else return half_to_float(((const uint16_t*)w)[i]);
+}
+
+template <int F>
+__device__ __forceinline__ void gemm_flt(const GemmArgs& a)
+{
+  __shared__ float xs[2][GBM][FKC + 1];
+  __shared__ float ws[2][GBN][FKC + 1];
+  __shared__ int sxr[GBM], syr[GBM];
+  const int t = threadIdx.x, l = t & 63, w = t >> 6;
+  const int wm = w & 1, wn = w >> 1;
+  const uint8_t* wb = a.w;
+  const float* bias = a.bias;
+  int nrows;
+  if (a.items) {
+    const int4 it = a.items[blockIdx.y];
+    if (it.z <= 0) return;
+    wb += (int64_t)it.x * a.stride;
+    if (bias) bias += (int64_t)it.x * a.out;
+    nrows = min(GBM, it.z);
+    if (t < GBM) {
+      const int sl = a.perm[it.y + min(t, nrows - 1)];
+      sxr[t] = a.x_per_slot ? sl / a.x_per_slot : 0;
+      syr[t] = sl;
+    }
+  } else {
+    const int r0 = blockIdx.y * GBM;
+    nrows = min(GBM, a.rows - r0);
+    if (t < GBM) sxr[t] = syr[t] = r0 + min(t, nrows - 1);
+  }
+  __syncthreads();
+  const int col0 = blockIdx.x * GBN;
+  // a thread's share of a chunk: 8 consecutive values of row (t / 4) of x
+  // and of column (t / 4) of w
+  const int lr = t >> 2, lk = 8 * (t & 3);
+  const float* xrow = a.x + (int64_t)sxr[lr] * a.in;
+  const int64_t wrow = (int64_t)min(col0 + lr, a.out - 1) * a.in;
+  float xv[8], wv[8];
+  auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int k = min(k0 + lk + u, a.in - 1);
+      xv[u] = xrow[k];
+      wv[u] = wval<F>(wb, wrow + k);
+    }
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      xs[buf][lr][lk + u] = xv[u];
+      ws[buf][lr][lk + u] = wv[u];
+    }
+  };
+  v4d acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
+  const int nch = (a.in + FKC - 1) / FKC;
+  load(0);
+  store(0);
+  __syncthreads();
+  // operand lane mapping of v_mfma_f64_16x16x4_f64 (probed on gfx950): A
+  // lane l = row l % 16, k = l / 16; B lane l = column l % 16, k = l / 16;
+  // result register e of lane l = row 4 e + l / 16, column l % 16
+  const int ar = l & 15, ak = l >> 4;
+  for (int c = 0; c < nch; c++) {
+    const int buf = c & 1, k0 = c * FKC;
+    if (c + 1 < nch) load(k0 + FKC);
+#pragma unroll
+    for (int kk = 0; kk < FKC; kk += 4) {
+      // a chunk past the end of the sum: values beyond in read 0 weight
+      const bool kin = k0 + kk + ak < a.in;
+      double av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) av[i] = (double)xs[buf][32 * wm + 16 * i + ar][kk + ak];
+#pragma unroll
+      for (int j = 0; j < 2; j++) bv[j] = kin ? (double)ws[buf][32 * wn + 16 * j + ar][kk + ak] : 0.0;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+    if (c + 1 < nch) store(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int o = col0 + 32 * wn + 16 * j + ar;
+    if (o >= a.out) continue;
+    const double b = bias ? (double)bias[o] : 0.0;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int rt = 32 * wm + 16 * i + 4 * e + ak;
+        if (rt < nrows) {
+          double v = acc[i][j][e];
+          if (bias) v = b + v;
+          a.y[(int64_t)syr[rt] * a.out + o] = (float)v;
+        }
+      }
+  }
+}
+
 }  // namespace ihip
 
 #define IHIP_GEMM(NAME, F) \
   extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm<F>(a); }
 
+#define IHIP_GEMM_FLT(NAME, F) \
+  extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm_flt<F>(a); }
+
 #ifdef IHIP_ONLY_FMT_Q8_0
 IHIP_GEMM(q8_0, ihip::DT_Q8_0)
+#endif
+#ifdef IHIP_ONLY_FMT_F32
+IHIP_GEMM_FLT(f32, ihip::DT_F32)
+#endif
+#ifdef IHIP_ONLY_FMT_BF16
+IHIP_GEMM_FLT(bf16, ihip::DT_BF16)
+#endif
+#ifdef IHIP_ONLY_FMT_F16
+IHIP_GEMM_FLT(f16, ihip::DT_F16)
 #endif
 #ifdef IHIP_ONLY_FMT_Q4_0
 IHIP_GEMM(q4_0, ihip::DT_Q4_0)

@@ -118,14 +118,15 @@ def test_linear_q8_mode_cpu_bits(ctx, dtype):
     assert differ <= max(2, total // 1000), (differ, total)
 
 
-GEMM_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K]
-GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100)]
+GEMM_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K, H.F32, H.BF16, H.F16]
+GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100), (40, 2880, 70)]
 
 
 @pytest.mark.parametrize("dtype", GEMM_FMTS)
 def test_gemm_q8_mode_cpu_bits(ctx, dtype):
     # chunks of >= 16 rows run on the MFMA GEMM: exact int32 group sums from
-    # the int8 matrix cores, the scales in double, as the CPU
+    # the int8 matrix cores, the scales in double, as the CPU; float weights
+    # on the f64 matrix cores (exact products, double sums)
     rng = np.random.default_rng(19)
     total, differ = 0, 0
     for rows, cols, out in GEMM_SHAPES:
