@@ -97,7 +97,14 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     (128, 32, 4, 300, 3, 0, False, False),
     (64, 64, 8, 200, 2, 128, True, False),
     (64, 64, 8, 20, 5, 0, True, False),
-    (128, 16, 8, 100, 1, 0, False, True)])
+    (128, 16, 8, 100, 1, 0, False, True),
+    # tiles of 8 prompt rows: from position 0 (two ranges, the causal end
+    # inside a tile), a window moving across a tile's rows, one whole tile,
+    # a partial last tile under a window
+    (128, 32, 4, 0, 130, 0, False, True),
+    (64, 64, 8, 150, 20, 128, True, True),
+    (128, 16, 8, 7, 8, 0, False, False),
+    (64, 8, 2, 300, 33, 100, False, False)])
 def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     rng = np.random.default_rng(past + rows)
     T = past + rows
