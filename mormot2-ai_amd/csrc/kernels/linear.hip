@@ -887,6 +887,120 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   }
 }
 
+// ------------------------------------------------------------ float rows
+// One activation row against F32 / BF16 / F16 weights in the Q8 arithmetic
+// (TInferCpuBackend.Linear's float branch, backend.cpu.pas:1548-1565: the
+// exact float products summed in double). A wave takes RW rows per step;
+// its 64 lanes read each row as consecutive 16-byte chunks (one contiguous
+// kilobyte per load instruction, every load of the step issued before the
+// first use); the activation row is staged in LDS once per block (normed
+// with NORM) and read per chunk. Rows of up to 3 matrices (nseg) as the
+// one-row GEMV.
+constexpr int FRW = 2;  // rows per wave step
+
+template <int F>
+constexpr int f_bytes() { return F == DT_F32 ? 4 : 2; }
+
+// the 16-byte chunks lane + 64 j of rows sp * RW .. (a row past the matrix
+// reads its last row; chunks past the row its last chunk: values unused)
+template <int RW, int NJ>
+__device__ __forceinline__ void flt_load(const uint8_t* w, int64_t rb, int64_t sp, int out, int lane,
+                                         int nj, int NC, uint4 (&wv)[RW][NJ])
+{
+#pragma unroll
+  for (int r = 0; r < RW; r++) {
+    const int64_t o = min(sp * RW + r, (int64_t)out - 1);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      if (j < nj) {  // the same for the whole launch
+        const int c = min(lane + 64 * j, NC - 1);
+        wv[r][j] = ld<uint4, true>(w + o * rb, (uint32_t)c * 16u);
+      }
+    }
+  }
+}
+
+template <int F, bool NORM, int NJ>
+__device__ __forceinline__ void gemv_flt(const LinArgs& a)
+{
+  constexpr int ES = f_bytes<F>(), VPC = 16 / ES;  // values per 16-byte chunk
+  const int lane = threadIdx.x & 63;
+  const uint8_t* w = a.w;
+  const float* bias = a.bias;
+  int out = a.out;
+  float* yp = a.y;
+  if (a.nseg > 1) {
+    // (selected, not indexed: an index into the argument block would move it
+    // to scratch memory)
+    const int sg = blockIdx.y;
+    w = sg == 0 ? a.wseg[0] : (sg == 1 ? a.wseg[1] : a.wseg[2]);
+    bias = sg == 0 ? a.bseg[0] : (sg == 1 ? a.bseg[1] : a.bseg[2]);
+    out = sg == 0 ? a.oseg[0] : (sg == 1 ? a.oseg[1] : a.oseg[2]);
+    yp = sg == 0 ? a.yseg[0] : (sg == 1 ? a.yseg[1] : a.yseg[2]);
+  }
+  const int NC = a.in / VPC;  // chunks per row: at most 64 NJ
+  const int nj = (NC + 63) / 64;
+  const int64_t rb = (int64_t)a.in * ES;  // row bytes
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t steps = ((int64_t)out + FRW - 1) / FRW;
+  __shared__ __align__(16) float xs[XN];
+  if ((int64_t)blockIdx.x * (blockDim.x >> 6) >= steps) return;  // the whole block: no rows
+  XStage st;
+  stage_load<F, 1, NORM>(a.x, nullptr, a.in, a.nw, st);
+  // the first step's weights while the row is staged
+  uint4 wv[FRW][NJ];
+  int64_t sp = wid;
+  flt_load<FRW, NJ>(w, rb, sp, out, lane, nj, NC, wv);
+  stage_store<F, 1, NORM>(st, false, a.in, a.eps, (uint8_t*)xs, nullptr, a.bad, 1);
+  __syncthreads();
+  while (sp < steps) {
+#pragma unroll
+    for (int r = 0; r < FRW; r++) {
+      double p[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const int c = lane + 64 * j;
+        if (j < nj && c < NC) {
+          const uint32_t q[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            if constexpr (F == DT_F32) {
+              v[i] = bits_float(q[i]);
+            } else if constexpr (F == DT_BF16) {
+              v[2 * i] = bits_float(q[i] << 16);
+              v[2 * i + 1] = bits_float(q[i] & 0xffff0000u);
+            } else {
+              v[2 * i] = half_to_float(q[i] & 0xffffu);
+              v[2 * i + 1] = half_to_float(q[i] >> 16);
+            }
+          }
+          const float4* xp = (const float4*)(xs + c * VPC);
+#pragma unroll
+          for (int h = 0; h < VPC / 4; h++) {
+            const float4 xv = xp[h];
+            p[0] = __builtin_fma((double)v[4 * h], (double)xv.x, p[0]);
+            p[1] = __builtin_fma((double)v[4 * h + 1], (double)xv.y, p[1]);
+            p[2] = __builtin_fma((double)v[4 * h + 2], (double)xv.z, p[2]);
+            p[3] = __builtin_fma((double)v[4 * h + 3], (double)xv.w, p[3]);
+          }
+        }
+      }
+      double v = wave_sum((p[0] + p[1]) + (p[2] + p[3]), 64);
+      const int64_t o = sp * FRW + r;
+      if (lane == 0 && o < out) {
+        if (bias) v = (double)bias[o] + v;
+        float rr = (float)v;
+        if (a.res) rr = a.res[o] + rr;
+        yp[o] = rr;
+      }
+    }
+    sp += nw;
+    if (sp < steps) flt_load<FRW, NJ>(w, rb, sp, out, lane, nj, NC, wv);
+  }
+}
+
 // ------------------------------------------------------------------ combine
 // The down projection of one token's experts, added into the residual:
 // TDecoderModel.Experts (decoder.pas:3140-3148) - every expert row as a float
@@ -1110,6 +1224,18 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   IHIP_GEMV_MIX(PFX##_norm_u1, F, F2, M, 1) IHIP_GEMV_MIX(PFX##_norm_u2, F, F2, M, 2) \
   IHIP_GEMV_MIX(PFX##_norm_u3, F, F2, M, 3) IHIP_GEMV_MIX(PFX##_norm_u4, F, F2, M, 4)
 
+#define IHIP_FLT1(NAME, F, NORM, NJ)                                          \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a)       \
+  {                                                                             \
+    ihip::gemv_flt<F, NORM, NJ>(a);                                             \
+  }
+// rows of at most 512 (j8) or 1024 (j16) 16-byte chunks
+#define IHIP_FLT(NAME, F)                                       \
+  IHIP_FLT1(gemv_##NAME##_q8_rows_j8, F, false, 8)              \
+  IHIP_FLT1(gemv_##NAME##_q8_rows_j16, F, false, 16)            \
+  IHIP_FLT1(gemv_##NAME##_q8_norm_rows_j8, F, true, 8)          \
+  IHIP_FLT1(gemv_##NAME##_q8_norm_rows_j16, F, true, 16)
+
 #define IHIP_GEMV_FMT(NAME, F) \
   IHIP_GEMV_U(gemv_##NAME##_f32, F, 0) \
   IHIP_GEMV_U(gemv_##NAME##_q8, F, 1) \
@@ -1150,13 +1276,16 @@ IHIP_DEQ(q6_k, ihip::DT_Q6_K)
 #endif
 #ifdef IHIP_ONLY_FMT_F32
 IHIP_GEMV_FMT(f32, ihip::DT_F32)
+IHIP_FLT(f32, ihip::DT_F32)
 IHIP_DEQ(f32, ihip::DT_F32)
 #endif
 #ifdef IHIP_ONLY_FMT_BF16
 IHIP_GEMV_FMT(bf16, ihip::DT_BF16)
+IHIP_FLT(bf16, ihip::DT_BF16)
 IHIP_DEQ(bf16, ihip::DT_BF16)
 #endif
 #ifdef IHIP_ONLY_FMT_F16
 IHIP_GEMV_FMT(f16, ihip::DT_F16)
+IHIP_FLT(f16, ihip::DT_F16)
 IHIP_DEQ(f16, ihip::DT_F16)
 #endif
