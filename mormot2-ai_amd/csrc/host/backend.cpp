@@ -456,7 +456,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   }
   if (float_fmt(k.dtype) && mode == IHIP_MODE_Q8 && !batch && !k.ids && !k.w2 && !k.dtype2) {
     // float weights, one row: a wave reads each row as consecutive 16-byte
-    // chunks (gemv_flt), 2 rows per wave step
+    // chunks (gemv_flt), one row per wave step
     const int64_t chunks = k.in * (k.dtype == DT_F32 ? 4 : 2) / 16;
     if (chunks <= 1024) {
       snprintf(name, sizeof name, "gemv_%s_q8_%srows_j%d", fmt_name(k.dtype), k.nw ? "norm_" : "",
@@ -464,7 +464,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       int64_t rows_max = k.out;
       if (k.nseg > 1)
         for (int i = 0; i < k.nseg; i++) rows_max = std::max<int64_t>(rows_max, k.oseg[i]);
-      const int64_t waves = (rows_max + 1) / 2;
+      const int64_t waves = rows_max;  // one row per wave step
       const int64_t hold = (int64_t)c->cus * resident_blocks(c, name, 256) * c->gemv_hold;
       const int64_t wgs = std::max<int64_t>(1, std::min((waves + 3) / 4, hold));
       return launch(c, name, dim3((unsigned)wgs, (unsigned)(k.nseg > 1 ? k.nseg : 1)), dim3(256), &a);

@@ -890,13 +890,13 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
 // ------------------------------------------------------------ float rows
 // One activation row against F32 / BF16 / F16 weights in the Q8 arithmetic
 // (TInferCpuBackend.Linear's float branch, backend.cpu.pas:1548-1565: the
-// exact float products summed in double). A wave takes RW rows per step;
+// exact float products summed in double). A wave takes FRW rows per step;
 // its 64 lanes read each row as consecutive 16-byte chunks (one contiguous
 // kilobyte per load instruction, every load of the step issued before the
 // first use); the activation row is staged in LDS once per block (normed
 // with NORM) and read per chunk. Rows of up to 3 matrices (nseg) as the
 // one-row GEMV.
-constexpr int FRW = 2;  // rows per wave step
+constexpr int FRW = 1;  // rows per wave step
 
 template <int F>
 constexpr int f_bytes() { return F == DT_F32 ? 4 : 2; }
