@@ -762,15 +762,18 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
                               a.nw, st);
     int64_t tb = wid;
     // the epilogue operands of a step's rows (bias, up bias, residual), loaded
-    // with its weights rather than after its sums (a null operand reads x[0])
+    // with its weights rather than after its sums; a launch without them
+    // issues no load for them (a uniform branch)
     float eb[T], eb2[T], er[T];
     auto load_epi = [&](int64_t sb) {
 #pragma unroll
       for (int i = 0; i < T; i++) {
         const int64_t o = min((sb + (int64_t)i * nw) * rpw + rsub, (int64_t)out - 1);
-        eb[i] = *(bias ? bias + o : a.x);
-        if constexpr (GLU) eb2[i] = *(bias2 ? bias2 + o : a.x);
-        er[i] = *(a.res ? a.res + o : a.x);
+        eb[i] = eb2[i] = er[i] = 0.f;
+        if (bias) eb[i] = bias[o];
+        if constexpr (GLU)
+          if (bias2) eb2[i] = bias2[o];
+        if (a.res) er[i] = a.res[o];
       }
     };
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
