@@ -757,17 +757,30 @@ __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d,
 {
   // AG: the ranges were written by other blocks of this launch
   auto rd = [&](int i) { return AG ? load_agent(b + i) : b[i]; };
-  // the range weights exp(m_s - M) once, in LDS; the sums in range order
-  __shared__ double wts[256];
+  // the range weights exp(m_s - M) and the range sums in LDS; the sums in
+  // range order. Every load of the first MU ranges (a thread's dimension of
+  // each, the maxima and sums) is issued before the first arithmetic: one
+  // memory round trip.
+  constexpr int MU = 16;
+  __shared__ double wts[256], lsum[256];
   __shared__ double dsh[2];
   const int t = threadIdx.x;
+  const int ic = min(t, d - 1);
+  double pv[MU];
+#pragma unroll
+  for (int u = 0; u < MU; u++) pv[u] = rd(min(u, splits - 1) * (d + 2) + ic);
   if (t < 64) {
     double M = -1.0e308;
-    for (int s = t; s < splits; s += 64) M = fmax(M, rd(s * (d + 2) + d));
+    for (int s = t; s < splits; s += 64) {
+      const double ms = rd(s * (d + 2) + d);
+      wts[s] = ms;
+      lsum[s] = rd(s * (d + 2) + d + 1);
+      M = fmax(M, ms);
+    }
     M = wave_max(M);
     if (sink && (double)*sink > M) M = *sink;
     for (int s = t; s < splits; s += 64) {
-      double ms = rd(s * (d + 2) + d);
+      const double ms = wts[s];
       wts[s] = ms > -1.0e308 ? exp(ms - M) : 0.0;
     }
     if (t == 0) dsh[0] = M;
@@ -775,7 +788,7 @@ __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d,
   __syncthreads();
   if (t == 0) {
     double den = 0;
-    for (int s = 0; s < splits; s++) den = den + wts[s] * rd(s * (d + 2) + d + 1);
+    for (int s = 0; s < splits; s++) den = den + wts[s] * lsum[s];
     if (sink) den = den + exp((double)*sink - dsh[0]);
     dsh[1] = 1.0 / den;
   }
@@ -783,7 +796,14 @@ __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d,
   const double inv = dsh[1];
   for (int i = t; i < d; i += blockDim.x) {
     double acc = 0;
-    for (int s = 0; s < splits; s++) acc = acc + wts[s] * rd(s * (d + 2) + i);
+    if (i == t) {
+#pragma unroll
+      for (int u = 0; u < MU; u++)
+        if (u < splits) acc = acc + wts[u] * pv[u];
+      for (int s = MU; s < splits; s++) acc = acc + wts[s] * rd(s * (d + 2) + i);
+    } else {
+      for (int s = 0; s < splits; s++) acc = acc + wts[s] * rd(s * (d + 2) + i);
+    }
     y[i] = (float)(acc * inv);
   }
 }
