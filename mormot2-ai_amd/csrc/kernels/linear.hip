@@ -69,64 +69,55 @@ struct LinArgs {
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
-// sx their sum.
+// sx their sum. Every code is turned into its exact value (signed, offset
+// removed) before it multiplies x, as InferRowToF32 dequantizes it: a bias
+// taken out afterwards through sx would leave the rounding of two large sums,
+// which a large scale (an E8M0 exponent up to 255: 2^127) turns into garbage
+// for a block of zero codes.
 template <int F>
 __device__ __forceinline__ float group_f32(const Raw& r, const float (&x)[32], float sx, int g)
 {
-  // sum over the 32 values of the code (as float) times x: signed codes are
-  // read biased by 128 (byte ^ 0x80) and the bias removed through sx
+  // the offset of the unsigned codes: q - 8 (Q4_0), q - 16 (Q5_0), q - 32
+  // (Q6_K); Q8_0 and MXFP4 codes are signed bytes; Q5_1 and Q4_K keep their
+  // unsigned codes and an affine term in sx (w = d q + m, d q - m)
+  constexpr float off = F == DT_Q4_0 ? 8.0f : (F == DT_Q5_0 ? 16.0f : (F == DT_Q6_K ? 32.0f : 0.0f));
   constexpr bool sgn = (F == DT_Q8_0 || F == DT_MXFP4);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float accl = 0.f, acch = 0.f;  // Q6_K: the two scale halves
 #pragma unroll
   for (int hi = 0; hi < 2; hi++) {
     float part[2] = {0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 4; d++) {
-      uint32_t c = code_bytes<F>(r, d, hi);
-      if (sgn) c ^= 0x80808080u;
+      const uint32_t c = code_bytes<F>(r, d, hi);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        float cf = (float)((c >> (8 * i)) & 255u);
+        const uint32_t b = (c >> (8 * i)) & 255u;
+        const float cf = sgn ? (float)(int)(int8_t)b : (float)b - off;
         part[i & 1] = __builtin_fmaf(cf, x[16 * hi + 4 * d + i], part[i & 1]);
       }
     }
-    if (F == DT_Q6_K) {
-      if (hi) acch = part[0] + part[1];
-      else accl = part[0] + part[1];
-    } else {
-      acc[2 * hi] = part[0];
-      acc[2 * hi + 1] = part[1];
-    }
+    acc[2 * hi] = part[0];
+    acc[2 * hi + 1] = part[1];
   }
-  float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-  if constexpr (F == DT_Q8_0) {
-    return half_to_float(r.a) * (s - 128.0f * sx);
+  if constexpr (F == DT_Q6_K) {  // (d * sc) * (q - 32) per half of 16 values
+    const float d = half_to_float(r.d);
+    const float ta = d * (float)(int)(int8_t)(r.a & 255u);
+    const float tb = d * (float)(int)(int8_t)(r.a >> 8);
+    return ta * (acc[0] + acc[1]) + tb * (acc[2] + acc[3]);
+  }
+  const float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  if constexpr (F == DT_Q8_0 || F == DT_Q4_0 || F == DT_Q5_0) {
+    return half_to_float(r.a) * s;
   } else if constexpr (F == DT_MXFP4) {
-    return e8m0_half(r.a) * (s - 128.0f * sx);
-  } else if constexpr (F == DT_Q4_0) {
-    return half_to_float(r.a) * (s - 8.0f * sx);
-  } else if constexpr (F == DT_Q5_0) {
-    return half_to_float(r.a) * (s - 16.0f * sx);
+    return e8m0_half(r.a) * s;
   } else if constexpr (F == DT_Q5_1) {
     return half_to_float(r.a & 0xffffu) * s + half_to_float(r.a >> 16) * sx;
-  } else if constexpr (F == DT_Q4_K) {
+  } else {  // Q4_K
     int sc, m;
     scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, m);
-    float d1 = half_to_float(r.q1.x & 0xffffu) * (float)sc;
-    float m1 = half_to_float(r.q1.x >> 16) * (float)m;
+    const float d1 = half_to_float(r.q1.x & 0xffffu) * (float)sc;
+    const float m1 = half_to_float(r.q1.x >> 16) * (float)m;
     return d1 * s - m1 * sx;
-  } else {  // Q6_K: (d * sc) * (q - 32) per half of 16 values
-    float d = half_to_float(r.d);
-    float ta = d * (float)(int)(int8_t)(r.a & 255u);
-    float tb = d * (float)(int)(int8_t)(r.a >> 8);
-    float sxl = 0.f, sxh = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      sxl += x[i];
-      sxh += x[16 + i];
-    }
-    return ta * (accl - 32.0f * sxl) + tb * (acch - 32.0f * sxh);
   }
 }
 

@@ -462,15 +462,20 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   e = wave_sum(e, 64);
   __syncthreads();
   if ((t & 63) == 0) red[4 + (t >> 6)] = e;
-  // the weighted values: a key takes hd / 2 lanes, each a dimension pair;
-  // the 4 waves and the key slots of a wave split the range
-  const int lpk = d >> 1;                      // lanes per key (32 or 64 for hd 64/128)
-  const int kpw = lpk >= 64 ? 1 : 64 / lpk;    // keys side by side in a wave
+  // the weighted values: a key takes a slot of lps lanes (hd / 2 rounded up
+  // to a power of two, at most 64), each lane a dimension pair (two for
+  // hd > 128); lanes past the key's pairs hold zeros. The 4 waves and the
+  // key slots of a wave split the range.
+  const int lpk = d >> 1;                                      // dimension pairs of a key
+  const int lps = lpk >= 64 ? 64 : 1 << (32 - __clz(lpk - 1));  // lanes per key slot
+  const int kpw = 64 / lps;                                    // keys side by side in a wave
   const int w = t >> 6, l = t & 63;
-  const int lane_key = lpk >= 64 ? 0 : l / lpk, pair = lpk >= 64 ? l : l % lpk;
+  const int lane_key = l / lps, pair = l % lps;
   const int step = 4 * kpw;
   double a0[2] = {0, 0}, a1[2] = {0, 0};  // two dimension pairs (hd 256)
-  const int npair = d > 128 ? 2 : 1;
+  // the lane's pairs inside the key (pair, pair + 64)
+  const bool live0 = pair < lpk, live1 = pair + 64 < lpk;
+  const int npair = live1 ? 2 : (live0 ? 1 : 0);
   constexpr int VB = F16 ? 32 : 16;  // value loads in flight per lane
   for (int jb = w * kpw + lane_key; jb < n; jb += VB * step) {
     if constexpr (F16) {
@@ -524,7 +529,7 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
     }
   }
   // the key slots of a wave, then the waves
-  for (int o = lpk; o < 64; o <<= 1)
+  for (int o = lps; o < 64; o <<= 1)
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       a0[c] += __shfl_xor(a0[c], o);

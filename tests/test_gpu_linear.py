@@ -73,6 +73,41 @@ def test_mxfp4_edge_exponents(ctx, dtype):
     assert np.array_equal(y, ref)
 
 
+@pytest.mark.parametrize("mode", [H.MODE_F32, H.MODE_Q8])
+def test_zero_codes_at_extreme_scales(ctx, mode):
+    # blocks whose values are all zero (-0 included) under the largest scales
+    # - MXFP4 exponents 255, 254, 200, 0, 1 (the tiny gpt-oss checkpoint holds
+    # a -0 block with exponent 255), Q8_0 / Q4_0 / Q5_0 at fp16 scale 65504 -
+    # give exact zero rows, with random activations; the other rows as the CPU
+    rng = np.random.default_rng(11)
+    cols = 64
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    cases = []
+    w = H.synth_blocks(H.MXFP4, 6, cols, 5).reshape(6, 2, 17)
+    for i, e in enumerate((255, 254, 200, 0, 1)):
+        w[i, :, 0] = e
+        w[i, :, 1:] = 0x88 if i % 2 == 0 else 0x00  # -0 or +0 codes
+    cases.append((H.MXFP4, w.ravel().copy(), 6))
+    for dt, zero in ((H.Q8_0, 0x00), (H.Q4_0, 0x88)):
+        bs = H.BLOCK[dt][1]
+        w = H.synth_blocks(dt, 4, cols, 6).reshape(4, 2, bs)
+        w[:2, :, 0:2] = np.frombuffer(np.float16(65504).tobytes(), np.uint8)
+        w[:2, :, 2:] = zero
+        cases.append((dt, w.ravel().copy(), 4))
+    w = H.synth_blocks(H.Q5_0, 4, cols, 7).reshape(4, 2, 22)
+    w[:2, :, 0:2] = np.frombuffer(np.float16(65504).tobytes(), np.uint8)
+    w[:2, :, 2:6] = 0xFF   # the fifth bits set and nibbles 0: q = 16, value 0
+    w[:2, :, 6:] = 0x00
+    cases.append((H.Q5_0, w.ravel().copy(), 4))
+    for dt, w, out in cases:
+        y = ctx.linear(x, w, dt, out, mode=mode)
+        ref = O.linear(x, w, dt, out, f32=(mode == H.MODE_F32))
+        zero_rows = 5 if dt == H.MXFP4 else 2
+        assert np.all(y[:, :zero_rows] == 0), (H.NAMES[dt], y[:, :zero_rows])
+        assert np.all(ref[:, :zero_rows] == 0)
+        assert rel_error(y, ref) <= 1e-5, (H.NAMES[dt], mode)
+
+
 @pytest.mark.parametrize("dtype", ALL_FMTS)
 def test_linear_f32_mode(ctx, dtype):
     rng = np.random.default_rng(7)

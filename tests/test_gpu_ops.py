@@ -104,7 +104,12 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     (128, 32, 4, 0, 130, 0, False, True),
     (64, 64, 8, 150, 20, 128, True, True),
     (128, 16, 8, 7, 8, 0, False, False),
-    (64, 8, 2, 300, 33, 100, False, False)])
+    (64, 8, 2, 300, 33, 100, False, False),
+    # other head sizes (the ranges kernel): 24 (12 pairs in a 16-lane slot, the
+    # tiny gpt-oss), 32, 96 and 192 (a second pair for half the lanes)
+    (24, 4, 2, 10, 6, 5, True, True), (24, 4, 2, 150, 1, 0, True, False),
+    (32, 4, 2, 200, 3, 0, False, True), (96, 8, 4, 130, 2, 0, False, False),
+    (192, 4, 1, 60, 2, 0, True, True)])
 def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     rng = np.random.default_rng(past + rows)
     T = past + rows
