@@ -65,7 +65,8 @@ enum {
   IHIP_E_UNSUPPORTED = -3, /* this dtype/shape has no kernel: CPU fallback */
   IHIP_E_NONFINITE = -4,   /* a NaN/Inf activation where Q8 refuses it */
   IHIP_E_CAPTURE = -5,     /* not allowed while capturing, or capture misuse */
-  IHIP_E_NOMEM = -6        /* a fixed maximum size exceeded */
+  IHIP_E_NOMEM = -6,       /* a fixed maximum size exceeded */
+  IHIP_E_FORMAT = -7       /* a damaged, hostile or unsupported file (EInferError) */
 };
 
 typedef struct ihip_ctx ihip_ctx;
@@ -309,6 +310,85 @@ int ihip_model_chunk(ihip_model* m, int64_t rows);
 int ihip_model_use_graphs(ihip_model* m, int on);
 /* timings of the last greedy call: prefill and decode milliseconds */
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
+
+/* ======================================================================
+ * GGUF v3 files (TGgufFile, src/infer/mormot.ai.infer.loader.gguf.pas:94-170)
+ * and the decoder description of a llama.cpp file
+ * (NewDecoderModelFromGguf, decoder.pas:3491-3510)
+ * ==================================================================== */
+typedef struct ihip_gguf ihip_gguf;
+
+/* the metadata value types (TGgufType, loader.gguf.pas:57-70) */
+enum {
+  IHIP_GGUF_UINT8 = 0, IHIP_GGUF_INT8, IHIP_GGUF_UINT16, IHIP_GGUF_INT16, IHIP_GGUF_UINT32,
+  IHIP_GGUF_INT32, IHIP_GGUF_FLOAT32, IHIP_GGUF_BOOL, IHIP_GGUF_STRING, IHIP_GGUF_ARRAY,
+  IHIP_GGUF_UINT64, IHIP_GGUF_INT64, IHIP_GGUF_FLOAT64
+};
+
+/* one key/value pair, a view into the file (TGgufValue, loader.gguf.pas:73-87):
+ * data is the value or the first array element; a string starts with its
+ * 8-byte length */
+typedef struct {
+  const char* key;
+  int32_t vtype, etype;
+  int64_t count;
+  const void* data;
+} ihip_gguf_value;
+
+/* one tensor (TInferTensor): row-major shape (GGUF lists ne0 first), dtype as
+ * TInferDType, data inside the mapped file */
+typedef struct {
+  const char* name;
+  int32_t dtype, ndim;
+  int64_t shape[4];
+  int64_t count, bytes;
+  const void* data;
+} ihip_gguf_tensor;
+
+/* map and validate a file (TGgufFile.Create, loader.gguf.pas:318-323): every
+ * defect of TGgufFile.Parse (:405-585) returns IHIP_E_FORMAT with the reason
+ * in ihip_last_error(), nothing is read past the end */
+int ihip_gguf_open(const char* path, ihip_gguf** out);
+/* validate a copy of an in-memory content (TGgufFile.CreateFromContent, :325-330) */
+int ihip_gguf_open_mem(const void* data, int64_t size, ihip_gguf** out);
+/* unmap (TGgufFile.Destroy): the desc of ihip_gguf_model_desc dies with it */
+void ihip_gguf_close(ihip_gguf* g);
+/* TGgufFile.Alignment, length(Values), length(Tensors) */
+int64_t ihip_gguf_alignment(const ihip_gguf* g);
+int64_t ihip_gguf_value_count(const ihip_gguf* g);
+int64_t ihip_gguf_tensor_count(const ihip_gguf* g);
+/* Values[i] in file order */
+int ihip_gguf_value_at(const ihip_gguf* g, int64_t i, ihip_gguf_value* out);
+/* the index of a key, -1 when absent (Find / Has, :595-609) */
+int64_t ihip_gguf_find(const ihip_gguf* g, const char* key);
+/* typed access, IHIP_E_FORMAT when missing or of another type (Str, Int,
+ * Float, Bool, BoolDef, :622-710); a string is a view of len bytes */
+int ihip_gguf_str(const ihip_gguf* g, const char* key, const char** s, int64_t* len);
+int ihip_gguf_int(const ihip_gguf* g, const char* key, int64_t* v);
+int ihip_gguf_float(const ihip_gguf* g, const char* key, double* v);
+int ihip_gguf_bool(const ihip_gguf* g, const char* key, int* v);
+int ihip_gguf_bool_def(const ihip_gguf* g, const char* key, int def, int* v);
+/* an array of fixed-size elements of type elem, count elements expected
+ * (-1 = any): a view into the file (Floats32, Ints32, Bytes, :727-760) */
+int ihip_gguf_array(const ihip_gguf* g, const char* key, int32_t elem, int64_t count,
+                    const void** data, int64_t* n);
+/* strings [first, first + n) of a string array (Strings, :712-725) */
+int ihip_gguf_strings(const ihip_gguf* g, const char* key, int64_t first, int64_t n,
+                      const char** s, int64_t* len);
+/* Tensors[i] in file order; the index of a tensor or -1 (FindTensor, :762) */
+int ihip_gguf_tensor_at(const ihip_gguf* g, int64_t i, ihip_gguf_tensor* out);
+int64_t ihip_gguf_find_tensor(const ihip_gguf* g, const char* name);
+/* the tensor checked against a type and row-major dims (Weight, :778-797) */
+int ihip_gguf_weight(const ihip_gguf* g, const char* name, int32_t dtype, int32_t ndim,
+                     const int64_t* dims, const void** data);
+/* the decoder of a qwen3, qwen3moe or gpt-oss file, its settings from the
+ * metadata and its tensors checked by name, shape, type and scales as
+ * TQwen3Model / TQwen3MoeModel / TGptOssModel.LoadGgufConfig + LoadWeights do
+ * (model.qwen3.pas:419-620, :797-846; model.gptoss.pas:331-475, :700-760):
+ * block matrices point into the mapped file, norms and biases are F32 (BF16
+ * and F16 ones widened exactly into memory of g). Valid while g is open;
+ * pass it to ihip_model_create. */
+int ihip_gguf_model_desc(ihip_gguf* g, const ihip_model_desc** out);
 
 /* ======================================================================
  * seeded synthetic weights, written on the host (the generators of

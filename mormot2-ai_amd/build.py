@@ -19,7 +19,7 @@ GEMM_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf
 KERNELS = ([("ops", "ops", [])] +
            [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in LINEAR_FMTS] +
            [("gemm_" + f, "gemm", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in GEMM_FMTS])
-HOST = ["runtime", "backend", "model", "synth"]
+HOST = ["runtime", "backend", "model", "synth", "gguf"]
 HIP_FLAGS = ["--genco", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", CSRC]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

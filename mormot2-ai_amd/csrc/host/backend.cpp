@@ -791,8 +791,8 @@ int ihip_enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, ui
                            int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                            int64_t window, uint64_t sinks, double scale, int kv_f16)
 {
-  if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 1 || hd > 256 || 256 % hd ||
-      past < 0 || window < 0)
+  if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 8 || hd > 256 || past < 0 ||
+      window < 0)
     return fail(IHIP_E_ARG, "ihip_enqueue_attention");
   if (hd % 8) return fail(IHIP_E_ARG, "attention: head size not a multiple of 8");
   int64_t maxkeys = past + rows;

@@ -27,6 +27,24 @@ class HipError(RuntimeError):
     pass
 
 
+class FormatError(HipError):
+    """A damaged, hostile or unsupported file (IHIP_E_FORMAT, EInferError)."""
+
+
+IHIP_E_FORMAT = -7
+
+
+class GgufValue(C.Structure):
+    _fields_ = [("key", C.c_char_p), ("vtype", C.c_int32), ("etype", C.c_int32),
+                ("count", C.c_int64), ("data", C.c_void_p)]
+
+
+class GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
+                ("shape", C.c_int64 * 4), ("count", C.c_int64), ("bytes", C.c_int64),
+                ("data", C.c_void_p)]
+
+
 def row_bytes(dtype, cols):
     bv, bs = BLOCK[dtype]
     return cols // bv * bs
@@ -100,6 +118,26 @@ def lib():
             "ihip_model_timing": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
             "ihip_synth_blocks": (i32, [vp, i32, i64, i64, u64, i32, i32, i32]),
             "ihip_synth_normal": (i32, [vp, i32, i64, i64, u64, C.c_float, i32]),
+            "ihip_gguf_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+            "ihip_gguf_open_mem": (i32, [vp, i64, C.POINTER(vp)]),
+            "ihip_gguf_close": (None, [vp]),
+            "ihip_gguf_alignment": (i64, [vp]),
+            "ihip_gguf_value_count": (i64, [vp]),
+            "ihip_gguf_tensor_count": (i64, [vp]),
+            "ihip_gguf_value_at": (i32, [vp, i64, C.POINTER(GgufValue)]),
+            "ihip_gguf_find": (i64, [vp, C.c_char_p]),
+            "ihip_gguf_str": (i32, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(i64)]),
+            "ihip_gguf_int": (i32, [vp, C.c_char_p, C.POINTER(i64)]),
+            "ihip_gguf_float": (i32, [vp, C.c_char_p, C.POINTER(C.c_double)]),
+            "ihip_gguf_bool": (i32, [vp, C.c_char_p, C.POINTER(i32)]),
+            "ihip_gguf_bool_def": (i32, [vp, C.c_char_p, i32, C.POINTER(i32)]),
+            "ihip_gguf_array": (i32, [vp, C.c_char_p, i32, i64, C.POINTER(vp), C.POINTER(i64)]),
+            "ihip_gguf_strings": (i32, [vp, C.c_char_p, i64, i64, C.POINTER(vp),
+                                        C.POINTER(i64)]),
+            "ihip_gguf_tensor_at": (i32, [vp, i64, C.POINTER(GgufTensor)]),
+            "ihip_gguf_find_tensor": (i64, [vp, C.c_char_p]),
+            "ihip_gguf_weight": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(i64), C.POINTER(vp)]),
+            "ihip_gguf_model_desc": (i32, [vp, C.POINTER(vp)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -120,7 +158,7 @@ def header_symbols():
 def check(rc, what=""):
     if rc != 0:
         msg = lib().ihip_last_error().decode(errors="replace")
-        raise HipError(f"{what}: status {rc}: {msg}")
+        raise (FormatError if rc == IHIP_E_FORMAT else HipError)(f"{what}: status {rc}: {msg}")
 
 
 def _p(a):
@@ -327,3 +365,145 @@ class Model:
         a, b = C.c_double(), C.c_double()
         check(lib().ihip_model_timing(self.h, C.byref(a), C.byref(b)), "timing")
         return a.value, b.value
+
+
+# ---------------------------------------------------------------- GGUF
+GGUF_UINT8, GGUF_INT8, GGUF_UINT16, GGUF_INT16, GGUF_UINT32, GGUF_INT32, GGUF_FLOAT32, \
+    GGUF_BOOL, GGUF_STRING, GGUF_ARRAY, GGUF_UINT64, GGUF_INT64, GGUF_FLOAT64 = range(13)
+
+
+class Gguf:
+    """A validated, memory-mapped GGUF v3 file (TGgufFile,
+    src/infer/mormot.ai.infer.loader.gguf.pas:94-170): path, or content=bytes
+    for CreateFromContent. A defect raises FormatError."""
+
+    def __init__(self, path=None, content=None):
+        h = C.c_void_p()
+        if content is not None:
+            buf = C.create_string_buffer(bytes(content), len(content))
+            rc = lib().ihip_gguf_open_mem(buf, len(content), C.byref(h))
+        else:
+            rc = lib().ihip_gguf_open(os.fsencode(path), C.byref(h))
+        check(rc, "gguf")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ihip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def alignment(self):
+        return lib().ihip_gguf_alignment(self.h)
+
+    def keys(self):
+        out = []
+        v = GgufValue()
+        for i in range(lib().ihip_gguf_value_count(self.h)):
+            check(lib().ihip_gguf_value_at(self.h, i, C.byref(v)), "value_at")
+            out.append(v.key.decode())
+        return out
+
+    def has(self, key):
+        return lib().ihip_gguf_find(self.h, key.encode()) >= 0
+
+    def str(self, key):
+        p, n = C.c_void_p(), C.c_int64()
+        check(lib().ihip_gguf_str(self.h, key.encode(), C.byref(p), C.byref(n)), "str")
+        return C.string_at(p, n.value).decode()
+
+    def int(self, key):
+        v = C.c_int64()
+        check(lib().ihip_gguf_int(self.h, key.encode(), C.byref(v)), "int")
+        return v.value
+
+    def float(self, key):
+        v = C.c_double()
+        check(lib().ihip_gguf_float(self.h, key.encode(), C.byref(v)), "float")
+        return v.value
+
+    def bool(self, key, default=None):
+        v = C.c_int()
+        if default is None:
+            check(lib().ihip_gguf_bool(self.h, key.encode(), C.byref(v)), "bool")
+        else:
+            check(lib().ihip_gguf_bool_def(self.h, key.encode(), int(default), C.byref(v)), "bool")
+        return bool(v.value)
+
+    def array(self, key, elem, count=-1):
+        """A fixed-size element array as numpy (a copy)."""
+        dt = {GGUF_UINT8: np.uint8, GGUF_INT8: np.int8, GGUF_UINT16: np.uint16,
+              GGUF_INT16: np.int16, GGUF_UINT32: np.uint32, GGUF_INT32: np.int32,
+              GGUF_FLOAT32: np.float32, GGUF_BOOL: np.uint8, GGUF_UINT64: np.uint64,
+              GGUF_INT64: np.int64, GGUF_FLOAT64: np.float64}[elem]
+        p, n = C.c_void_p(), C.c_int64()
+        check(lib().ihip_gguf_array(self.h, key.encode(), elem, count, C.byref(p), C.byref(n)),
+              "array")
+        return np.frombuffer(C.string_at(p, n.value * np.dtype(dt).itemsize), dt).copy()
+
+    def strings(self, key):
+        v = GgufValue()
+        i = lib().ihip_gguf_find(self.h, key.encode())
+        n = 0
+        if i >= 0:
+            check(lib().ihip_gguf_value_at(self.h, i, C.byref(v)), "value_at")
+            n = v.count if v.vtype == GGUF_ARRAY else 0
+        ptrs, lens = (C.c_void_p * max(n, 1))(), (C.c_int64 * max(n, 1))()
+        check(lib().ihip_gguf_strings(self.h, key.encode(), 0, n, ptrs, lens), "strings")
+        return [C.string_at(ptrs[j], lens[j]).decode(errors="surrogateescape") for j in range(n)]
+
+    def tensors(self):
+        out = []
+        t = GgufTensor()
+        for i in range(lib().ihip_gguf_tensor_count(self.h)):
+            check(lib().ihip_gguf_tensor_at(self.h, i, C.byref(t)), "tensor_at")
+            out.append(dict(name=t.name.decode(), dtype=t.dtype, shape=tuple(t.shape[:t.ndim]),
+                            count=t.count, bytes=t.bytes, data=t.data))
+        return out
+
+    def tensor(self, name):
+        """The tensor named name, or None (FindTensor)."""
+        i = lib().ihip_gguf_find_tensor(self.h, name.encode())
+        if i < 0:
+            return None
+        t = GgufTensor()
+        check(lib().ihip_gguf_tensor_at(self.h, i, C.byref(t)), "tensor_at")
+        return dict(name=name, dtype=t.dtype, shape=tuple(t.shape[:t.ndim]), count=t.count,
+                    bytes=t.bytes, data=t.data)
+
+    def weight(self, name, dtype, dims):
+        d = (C.c_int64 * len(dims))(*dims)
+        p = C.c_void_p()
+        check(lib().ihip_gguf_weight(self.h, name.encode(), dtype, len(dims), d, C.byref(p)),
+              "weight")
+        return p.value
+
+
+class GgufSpec:
+    """The decoder of a qwen3 / qwen3moe / gpt-oss GGUF file as a model
+    description (NewDecoderModelFromGguf, decoder.pas:3491-3510): pass it to
+    Model (the device) or to the CPU oracle like a synthetic Spec."""
+
+    def __init__(self, path=None, content=None):
+        self.file = Gguf(path, content)
+        p = C.c_void_p()
+        check(lib().ihip_gguf_model_desc(self.file.h, C.byref(p)), "gguf model")
+        self.struct = ModelDesc.from_address(p.value)
+        self.vocab = self.struct.vocab
+        self.layers = [self.struct.layer[i] for i in range(self.struct.layers)]
+        d = self.struct
+        self.cfg = dict(vocab=d.vocab, hidden=d.hidden, layers=d.layers, heads=d.heads,
+                        kv_heads=d.kv_heads, head_dim=d.head_dim, ffn=d.ffn, experts=d.experts,
+                        experts_used=d.experts_used, expert_ffn=d.expert_ffn)
+
+    def close(self):
+        self.file.close()
