@@ -269,6 +269,8 @@ def main():
                     help="prompt tokens (default: the config's BASELINE workload)")
     ap.add_argument("--config", default="qwen3-30b-a3b-q4_k_m")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sample-steps", type=int, default=32,
+                    help="decode steps with device sampling after the greedy ones (0: none)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kv-f32", action="store_true")
     ap.add_argument("--no-graphs", action="store_true",
@@ -297,7 +299,7 @@ def main():
     t = time.time()
     spec = models.Spec(models.CONFIGS[args.config], seed=1)
     log(f"synthetic {args.config} built in {time.time() - t:.1f}s")
-    max_tokens = args.prompt + args.warmup + args.steps + 8
+    max_tokens = args.prompt + args.warmup + args.steps + args.sample_steps + 16
     t = time.time()
     model = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=not args.kv_f32, max_tokens=max_tokens)
     log(f"uploaded in {time.time() - t:.1f}s")
@@ -318,6 +320,21 @@ def main():
     dt = time.perf_counter() - t0
     tok_s = args.steps / dt
     log(f"decode {args.steps} steps: {dt * 1e3 / args.steps:.3f} ms/token, {tok_s:.1f} tok/s")
+    # the same decode with draws of a TInferSampler (temperature 0.8, top-k 40,
+    # top-p 0.95) made on the device inside the graph: the sampler's cost
+    sampled = None
+    if args.sample_steps > 0:
+        model.sampling(temperature=0.8, top_k=40, top_p=0.95, seed=1)
+        ids3 = model.decode(int(ids2[-1]), 4)
+        ctx.sync()
+        t0 = time.perf_counter()
+        model.decode(int(ids3[-1]), args.sample_steps)
+        ctx.sync()
+        st = (time.perf_counter() - t0) / args.sample_steps
+        sampled = {"tok_s": round(1.0 / st, 1), "ms_per_token": round(st * 1e3, 4),
+                   "settings": "temperature 0.8, top_k 40, top_p 0.95", "steps": args.sample_steps}
+        log(f"sampled decode {args.sample_steps} steps: {st * 1e3:.3f} ms/token, {1.0 / st:.1f} tok/s")
+        model.sampling()
     wbytes = spec.weight_bytes_per_token()
     # the model's own device copies (same host tensors)
     dom = expert_gemv(ctx, spec, graphs=not args.no_graphs)
@@ -375,6 +392,7 @@ def main():
                    "weight_bytes_per_token": wbytes, "parallelism": "single GPU",
                    "graphs": not args.no_graphs},
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
+        "sampled_decode": sampled,
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
                      "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": profiled_traffic(dom["kernel"]),

@@ -232,6 +232,31 @@ int ihip_enqueue_argmax(ihip_ctx* ctx, uint64_t v, int64_t n, uint64_t out);
 int ihip_enqueue_stream_read(ihip_ctx* ctx, uint64_t p, uint64_t bytes, uint64_t out);
 
 /* ======================================================================
+ * TInferSampler (src/infer/mormot.ai.infer.sampler.pas:52-435) on the device
+ * ==================================================================== */
+typedef struct ihip_sampler ihip_sampler;
+
+/* TInferSampling (sampler.pas:46-59): temperature <= 0 is greedy; top_k 0,
+ * top_p 1 and min_p 0 filter nothing; the seed starts the splitmix64 stream */
+typedef struct {
+  double temperature;
+  int32_t top_k;
+  int32_t reserved;
+  double top_p, min_p;
+  int64_t seed;
+} ihip_sampling;
+
+/* the settings checked as TInferSampler.Create (sampler.pas:210-223), the
+ * generator state and buffers for rows of up to n_max (at most 2^22) logits
+ * on the device */
+int ihip_sampler_create(ihip_ctx* ctx, const ihip_sampling* s, int64_t n_max, ihip_sampler** out);
+void ihip_sampler_destroy(ihip_sampler* s);
+/* the next token of n logits at `logits`, written as int32 to `out`
+ * (TInferSampler.Next, sampler.pas:269-435): the argmax when greedy, else one
+ * draw that advances the sampler's stream on the device (graph-capturable) */
+int ihip_enqueue_sample(ihip_ctx* ctx, ihip_sampler* s, uint64_t logits, int64_t n, uint64_t out);
+
+/* ======================================================================
  * TQwen3Cuda (src/infer/mormot.ai.infer.model.qwen3.cuda.pas:150-301):
  * the whole decoder on the device, behind TDecoderDevice
  * (src/infer/mormot.ai.infer.decoder.pas:907-928)
@@ -305,6 +330,11 @@ int ihip_model_rotary(const ihip_model_desc* desc, int64_t first, int64_t rows,
 /* prompt rows per chunk of a forward pass: 1..1024 (default 1024); the
  * reference's CHUNK_MAX (model.qwen3.cuda.pas:308) is a constant 256 */
 int ihip_model_chunk(ihip_model* m, int64_t rows);
+/* how ihip_model_greedy and ihip_model_decode choose each next token: the
+ * argmax (s NULL or temperature <= 0), or draws of a TInferSampler with these
+ * settings, made on the device inside the decode graph (TNativeLlmClient's
+ * sampling, llm.native.pas; the logits never leave the device) */
+int ihip_model_sampling(ihip_model* m, const ihip_sampling* s);
 /* decode steps as one replayed HIP graph (on, the default) or as direct
  * launches (TQwen3Cuda.UseGraphs, model.qwen3.cuda.pas:253-262) */
 int ihip_model_use_graphs(ihip_model* m, int on);

@@ -852,6 +852,117 @@ int ihip_enqueue_argmax(ihip_ctx* c, uint64_t v, int64_t n, uint64_t out)
 
 }  // extern "C"
 
+// TInferSampler (sampler.pas:52-435) on the device: the settings, the
+// splitmix64 state and the buffers of sample_probs / _compact / _pick
+struct ihip_sampler {
+  ihip_ctx* c = nullptr;
+  double temperature = 0, top_p = 1, min_p = 0;
+  int32_t top_k = 0;
+  int64_t n_max = 0;
+  std::vector<void*> mem;
+  uint64_t state = 0, p = 0, bsum = 0, bq = 0, bcnt = 0, bmass = 0, cid = 0, ckey = 0, cp = 0;
+};
+
+namespace {
+constexpr int SAMPLE_BUCKETS = 128, SAMPLE_MAX_BLOCKS = 256;
+// tokens per block of sample_probs / sample_compact: a multiple of 256, at
+// least 1024, at most SAMPLE_MAX_BLOCKS blocks
+int64_t sample_per(int64_t n)
+{
+  int64_t per = std::max<int64_t>(1024, (n + SAMPLE_MAX_BLOCKS - 1) / SAMPLE_MAX_BLOCKS);
+  return (per + 255) / 256 * 256;
+}
+}  // namespace
+
+extern "C" {
+
+int ihip_sampler_create(ihip_ctx* c, const ihip_sampling* s, int64_t n_max, ihip_sampler** out)
+{
+  // n_max up to 2^22: the 2^40 fixed-point masses of p <= 1 sum below 2^63
+  if (!c || !s || !out || n_max < 1 || n_max > (1 << 22)) return fail(IHIP_E_ARG, "ihip_sampler_create");
+  *out = nullptr;
+  // TInferSampler.Create (sampler.pas:210-223): NaN, infinities and settings
+  // out of range refused
+  if (!std::isfinite(s->temperature) || !std::isfinite(s->top_p) || !std::isfinite(s->min_p) ||
+      s->top_k < 0 || s->top_p <= 0 || s->top_p > 1 || s->min_p < 0 || s->min_p >= 1)
+    return fail(IHIP_E_ARG, "ihip_sampler_create: temperature, top_k, top_p or min_p out of range");
+  if (c->capturing) return fail(IHIP_E_CAPTURE, "ihip_sampler_create while capturing");
+  auto* k = new ihip_sampler;
+  k->c = c;
+  k->temperature = s->temperature;
+  k->top_p = s->top_p;
+  k->min_p = s->min_p;
+  k->top_k = s->top_k;
+  k->n_max = n_max;
+  const int64_t nb = (n_max + sample_per(n_max) - 1) / sample_per(n_max);
+  hipError_t e = hipSetDevice(c->device);
+  auto get = [&](uint64_t& dst, size_t bytes) {
+    void* q = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&q, std::max<size_t>(bytes, 256));
+    if (q) k->mem.push_back(q);
+    dst = (uint64_t)q;
+  };
+  get(k->state, 8);
+  get(k->p, (size_t)n_max * 8);
+  get(k->bsum, (size_t)nb * 8);
+  get(k->bq, (size_t)nb * 8);
+  get(k->bcnt, (size_t)nb * SAMPLE_BUCKETS * 4);
+  get(k->bmass, (size_t)nb * SAMPLE_BUCKETS * 8);
+  get(k->cid, (size_t)n_max * 4);
+  get(k->ckey, (size_t)n_max * 4);
+  get(k->cp, (size_t)n_max * 8);
+  const uint64_t seed = (uint64_t)s->seed;
+  if (e == hipSuccess) e = hipMemcpy((void*)k->state, &seed, 8, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    ihip_sampler_destroy(k);
+    return hip_fail(e, "ihip_sampler_create");
+  }
+  *out = k;
+  return 0;
+}
+
+void ihip_sampler_destroy(ihip_sampler* k)
+{
+  if (!k) return;
+  (void)hipStreamSynchronize(k->c->stream);
+  for (void* q : k->mem) (void)hipFree(q);
+  delete k;
+}
+
+int ihip_enqueue_sample(ihip_ctx* c, ihip_sampler* k, uint64_t logits, int64_t n, uint64_t out)
+{
+  if (!c || !k || k->c != c || !logits || !out || n < 1 || n > k->n_max)
+    return fail(IHIP_E_ARG, "ihip_enqueue_sample");
+  // the argmax first: greedy, or the best token of the draw
+  int rc = ihip_enqueue_argmax(c, logits, n, out);
+  if (rc || !(k->temperature > 0)) return rc;
+  const int64_t per = sample_per(n), nb = (n + per - 1) / per;
+  struct {
+    const float* logits;
+    const int* best;
+    int* out;
+    uint64_t* state;
+    double* p;
+    double* bsum;
+    double* bq;
+    uint32_t* bcnt;
+    uint64_t* bmass;
+    int* cid;
+    uint32_t* ckey;
+    double* cp;
+    double temperature, top_p, min_p;
+    int32_t n, top_k, nb, per;
+  } a = {(const float*)logits, (const int*)out, (int*)out, (uint64_t*)k->state, (double*)k->p,
+         (double*)k->bsum, (double*)k->bq, (uint32_t*)k->bcnt, (uint64_t*)k->bmass, (int*)k->cid,
+         (uint32_t*)k->ckey, (double*)k->cp, k->temperature, k->top_p, k->min_p, (int32_t)n, k->top_k,
+         (int32_t)nb, (int32_t)per};
+  if ((rc = launch(c, "sample_probs", dim3((unsigned)nb), dim3(256), &a))) return rc;
+  if ((rc = launch(c, "sample_compact", dim3((unsigned)nb), dim3(256), &a))) return rc;
+  return launch(c, "sample_pick", dim3(1), dim3(1024), &a);
+}
+
+}  // extern "C"
+
 extern "C" int ihip_enqueue_stream_read(ihip_ctx* c, uint64_t p, uint64_t bytes, uint64_t out)
 {
   if (!c || !p || bytes < 16 || bytes % 16 || !out) return fail(IHIP_E_ARG, "ihip_enqueue_stream_read");

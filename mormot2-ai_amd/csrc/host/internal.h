@@ -69,6 +69,7 @@ struct ihip_ctx {
   bool capturing = false;
   hipGraph_t graphs[16] = {};
   hipGraphExec_t execs[16] = {};
+  const void* slot_owner[16] = {};  // the model whose decode graph a slot holds
   hipEvent_t events[64] = {};
   std::mutex lock;
 };

@@ -60,6 +60,7 @@ struct ihip_model {
   // tensors at a reused address must not meet the stale device copy
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
   bool graph_ready = false;
+  ihip_sampler* sampler = nullptr;  // null: the argmax
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
   int64_t chunk_rows = ihip::CHUNK;  // prompt rows per chunk (ihip_model_chunk), at most CHUNK
   int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
@@ -551,14 +552,21 @@ static int chunk(ihip_model* m, const int32_t* ids, int64_t n, bool want_logits,
   return rc;
 }
 
-// the decode step as a graph: embed(tok) -> layers(pos) -> head -> argmax
+// the next id from the logits: the argmax, or a draw of the sampler
+static int next_token(ihip_model* m)
+{
+  return m->sampler ? ihip_enqueue_sample(m->c, m->sampler, m->logits, m->d.vocab, m->next)
+                    : ihip_enqueue_argmax(m->c, m->logits, m->d.vocab, m->next);
+}
+
+// the decode step as a graph: embed(tok) -> layers(pos) -> head -> next id
 static int decode_body(ihip_model* m)
 {
   ihip_ctx* c = m->c;
   int rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, m->tok, 1, m->x);
   if (!rc) rc = layers(m, 1, 0, true);
   if (!rc) rc = head(m, 1, false, m->logits);
-  if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+  if (!rc) rc = next_token(m);
   return rc;
 }
 
@@ -572,6 +580,7 @@ static int decode_graph(ihip_model* m)
   if (rc) return rc;
   if (rc2) return rc2;
   m->graph_ready = true;
+  c->slot_owner[0] = m;
   return 0;
 }
 
@@ -581,7 +590,9 @@ static int decode_steps(ihip_model* m, int32_t first, int64_t steps, int32_t* ou
 {
   ihip_ctx* c = m->c;
   int rc = 0;
-  if (m->use_graphs && !m->graph_ready && (rc = decode_graph(m))) return rc;
+  // slot 0 holds one model's decode graph: another model of this context
+  // may have captured into it since
+  if (m->use_graphs && (!m->graph_ready || c->slot_owner[0] != m) && (rc = decode_graph(m))) return rc;
   std::vector<float> cs(m->d.head_dim);
   int32_t tok = first;
   for (int64_t i = 0; i < steps; i++) {
@@ -737,7 +748,9 @@ void ihip_model_destroy(ihip_model* m)
   (void)hipStreamSynchronize(m->c->stream);
   for (auto p : m->owned) (void)hipFree((void*)p);
   if (m->logits_all) (void)hipFree((void*)m->logits_all);
+  ihip_sampler_destroy(m->sampler);
   for (auto& u : m->uploaded) ihip_forget_weights(m->c, u.first, u.first + u.second);
+  if (m->c->slot_owner[0] == m) m->c->slot_owner[0] = nullptr;
   delete m;
 }
 
@@ -765,6 +778,7 @@ int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count, float* 
     if (want && all_logits) {
       if (m->logits_all_rows < n) {
         if (m->logits_all) (void)hipFree((void*)m->logits_all);
+  ihip_sampler_destroy(m->sampler);
         void* p = nullptr;
         IHIP_CHECK(hipMalloc(&p, (uint64_t)CHUNK * m->d.vocab * 4));
         m->logits_all = (uint64_t)p;
@@ -800,7 +814,7 @@ int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n, int64_t m
       int64_t k = std::min(m->chunk_rows, n - s);
       rc = chunk(m, prompt + s, k, s + k == n, false, m->logits);
     }
-    if (!rc) rc = ihip_enqueue_argmax(c, m->logits, m->d.vocab, m->next);
+    if (!rc) rc = next_token(m);
     if (!rc) {
       IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[0], (hipDeviceptr_t)m->next, 4, c->stream));
       IHIP_CHECK(hipStreamSynchronize(c->stream));
@@ -836,6 +850,29 @@ int ihip_model_chunk(ihip_model* m, int64_t rows)
 {
   if (!m || rows < 1 || rows > CHUNK) return fail(IHIP_E_ARG, "ihip_model_chunk: 1.." + std::to_string(CHUNK) + " rows");
   m->chunk_rows = rows;
+  return 0;
+}
+
+int ihip_model_sampling(ihip_model* m, const ihip_sampling* s)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_sampling");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  ihip_sampler* k = nullptr;
+  if (s && s->temperature > 0) {
+    int rc = ihip_sampler_create(m->c, s, m->d.vocab, &k);
+    if (rc) return rc;
+  } else if (s) {
+    // greedy: the settings are still checked as TInferSampler.Create does
+    ihip_sampling chk = *s;
+    chk.temperature = 0;
+    ihip_sampler* probe = nullptr;
+    int rc = ihip_sampler_create(m->c, &chk, 1, &probe);
+    ihip_sampler_destroy(probe);
+    if (rc) return rc;
+  }
+  ihip_sampler_destroy(m->sampler);
+  m->sampler = k;
+  m->graph_ready = false;  // the decode graph is captured again with it
   return 0;
 }
 

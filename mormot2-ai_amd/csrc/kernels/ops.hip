@@ -1262,6 +1262,594 @@ extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxArgs a)
   if (threadIdx.x == 0) a.out[0] = best ? (int)(0xffffffffu - (uint32_t)best) : 0;
 }
 
+// ------------------------------------------------------------------ sampling
+// TInferSampler.Next (sampler.pas:269-435) for one row of logits: the softmax
+// of logits / temperature in double, then either one draw over every token in
+// id order, or the warpers in the order of generate() - top-k keeping the ties
+// of the k-th logit, top-p over what top-k kept, min-p - and one draw from
+// what is left, all in the order (logit descending, id ascending).
+//
+// The reference lowers a probability threshold until its candidates hold
+// what the filters keep, sorts them and cuts the sorted list. What it keeps
+// depends only on the filters, so here the candidates are any superset, and
+// nothing is sorted:
+// - sample_probs (a block per 'per' tokens): p = exp((l - max) / T), the
+//   block's sum of p, and a histogram of p over 128 buckets (the binary
+//   exponent and the first mantissa bit: larger p, lower bucket) with each
+//   bucket's count and 40-bit fixed-point mass;
+// - sample_compact: the bucket level L that surely holds what the filters
+//   keep (k tokens, top_p of the mass, or the min-p cut), the same in every
+//   block; each block writes its candidates (bucket <= L) in id order at its
+//   offset. Without filters, each block's sum of p / sum instead.
+// - sample_pick (one block): top-k is the key of the k-th logit (a radix
+//   select), min-p the smallest key whose p / sum reaches min_p times the
+//   best's (p grows with the logit), the top-p cut and the draw radix
+//   searches of the running probability in (key descending, id ascending)
+//   order over 8-bit key digits, with 62-bit fixed-point sums (exact integer
+//   sums: the result does not depend on the order of atomics).
+constexpr int SNT = 1024;   // threads of sample_pick
+constexpr int SBT = 256;    // threads of sample_probs / sample_compact
+constexpr int SBK = 128;    // buckets of p
+struct SampleArgs {
+  const float* logits;
+  const int* best;     // the argmax of the row (InferArgMax)
+  int* out;            // the drawn id (may be best)
+  uint64_t* state;     // the splitmix64 state, advanced once per draw
+  double* p;           // [n] exp((logit - max) / temperature), 0 for NaN / Inf
+  double* bsum;        // [nb] the blocks' sums of p
+  double* bq;          // [nb] the blocks' sums of p / sum (the unfiltered draw)
+  uint32_t* bcnt;      // [nb][SBK] counts per bucket
+  uint64_t* bmass;     // [nb][SBK] fixed-point masses per bucket (2^40 = p of 1)
+  int* cid;            // [n] the candidates: id, logit key, p
+  uint32_t* ckey;
+  double* cp;
+  double temperature, top_p, min_p;
+  int32_t n, top_k, nb, per;
+};
+
+// the logit as an order-preserving key (-0 as +0), as argmax_pack
+__device__ __forceinline__ uint32_t logit_key(float f)
+{
+  const uint32_t b = float_bits(f);
+  int k = (int)(b ^ ((b >> 31) * 0x7fffffffu));
+  if (k == -1) k = 0;
+  return (uint32_t)k ^ 0x80000000u;
+}
+
+__device__ __forceinline__ bool finite_bits(float f) { return (float_bits(f) & 0x7f800000u) != 0x7f800000u; }
+
+// the bucket of p in (0, 1] (2 per binary exponent, larger p lower); 0 in the last
+__device__ __forceinline__ int p_bucket(double p)
+{
+  const uint64_t b = __builtin_bit_cast(uint64_t, p);
+  const int e = 1023 - (int)((b >> 52) & 2047);  // 0 for [1, 2)
+  const int hi = (int)((b >> 51) & 1);
+  return p > 0.0 ? min(SBK - 1, max(0, 2 * e + 1 - hi)) : SBK - 1;
+}
+
+// splitmix64 (the published generator of Vigna): 53 random bits in [0, 1)
+__device__ __forceinline__ double splitmix_next(uint64_t* state)
+{
+  uint64_t st = *state + 0x9E3779B97F4A7C15ull;
+  *state = st;
+  uint64_t z = st;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z = z ^ (z >> 31);
+  return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// block-wide sums, minima and exclusive prefixes in a fixed order (NT threads)
+template <int NT, typename T>
+__device__ __forceinline__ T sblock_sum(T v, T* sh)
+{
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = NT / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] = sh[threadIdx.x] + sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  const T r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+template <int NT, typename T>
+__device__ __forceinline__ T sblock_min(T v, T* sh)
+{
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = NT / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] = min(sh[threadIdx.x], sh[threadIdx.x + o]);
+    __syncthreads();
+  }
+  const T r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+template <int NT, typename T>
+__device__ __forceinline__ T sblock_exclusive(T v, T* sh)
+{
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = 1; o < NT; o <<= 1) {
+    const T a = (int)threadIdx.x >= o ? sh[threadIdx.x - o] : T(0);
+    __syncthreads();
+    sh[threadIdx.x] = sh[threadIdx.x] + a;
+    __syncthreads();
+  }
+  const T r = sh[threadIdx.x] - v;
+  __syncthreads();
+  return r;
+}
+
+constexpr double FX_ONE = 4611686018427387904.0;  // 2^62: a probability of 1
+constexpr double MX_ONE = 1099511627776.0;        // 2^40: a p of 1 (bucket masses)
+
+// the normalised probability p / sum as a 62-bit fixed-point weight: one
+// definition for every sum and search, so their totals agree to the bit
+__device__ __forceinline__ uint64_t wfx(double p, double sum) { return (uint64_t)(p / sum * FX_ONE); }
+
+// no finite best, or a temperature too close to 0 to divide by: greedy
+__device__ __forceinline__ bool sample_greedy(const SampleArgs& a, int best)
+{
+  return !finite_bits(a.logits[best]) || !(a.temperature >= 1e-30);
+}
+
+__device__ __forceinline__ bool sample_filters(const SampleArgs& a)
+{
+  return a.top_k > 0 || a.top_p < 1.0 || a.min_p > 0.0;
+}
+
+extern "C" __global__ __launch_bounds__(256) void sample_probs(SampleArgs a)
+{
+  __shared__ double shd[SBT];
+  __shared__ uint32_t hc[SBK];
+  __shared__ unsigned long long hm[SBK];
+  const int t = threadIdx.x, b = blockIdx.x;
+  const int best = *a.best;
+  if (sample_greedy(a, best)) return;
+  const bool filters = sample_filters(a);
+  if (t < SBK) {
+    hc[t] = 0;
+    hm[t] = 0;
+  }
+  __syncthreads();
+  const double m = a.logits[best], inv = 1.0 / a.temperature;
+  const int ept = a.per / SBT;  // a contiguous run per thread
+  const int i0 = min(a.n, b * a.per + t * ept), i1 = min(a.n, i0 + ept);
+  double s = 0;
+  for (int i = i0; i < i1; i++) {
+    const float l = a.logits[i];
+    const bool fin = finite_bits(l);
+    const double p = fin ? exp(((double)l - m) * inv) : 0.0;
+    a.p[i] = p;
+    s = s + p;
+    if (filters && fin) {
+      const int k = p_bucket(p);
+      atomicAdd(&hc[k], 1u);
+      atomicAdd(&hm[k], (unsigned long long)(p * MX_ONE));
+    }
+  }
+  s = sblock_sum<SBT>(s, shd);
+  if (t == 0) a.bsum[b] = s;
+  if (filters && t < SBK) {
+    a.bcnt[(int64_t)b * SBK + t] = hc[t];
+    a.bmass[(int64_t)b * SBK + t] = hm[t];
+  }
+}
+
+// the sum of p over the blocks (at most 256): a tree in a fixed order over
+// the block sums, the same value in every kernel that takes it
+template <int NT>
+__device__ __forceinline__ double blocks_sum(const SampleArgs& a, double* sh)
+{
+  if ((int)threadIdx.x < 256) sh[threadIdx.x] = (int)threadIdx.x < a.nb ? a.bsum[threadIdx.x] : 0.0;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] = sh[threadIdx.x] + sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  const double r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+// the count and fixed-point mass of every bucket over the blocks: each
+// thread reads whole rows of blocks (16-byte loads, all in flight) and adds
+// them into LDS (integer sums: the order does not matter)
+template <int NT>
+__device__ __forceinline__ void bucket_totals(const SampleArgs& a, uint32_t* cnt, uint64_t* mass, uint64_t* shu)
+{
+  (void)shu;
+  const int t = threadIdx.x;
+  if (t < SBK) {
+    cnt[t] = 0;
+    mass[t] = 0;
+  }
+  __syncthreads();
+  // (block, quarter of its row): 32 buckets per item
+  for (int it = t; it < a.nb * 4; it += NT) {
+    const int b = it >> 2, k0 = (it & 3) * 32;
+    const uint4* pc = (const uint4*)(a.bcnt + (int64_t)b * SBK + k0);
+    const uint4* pm = (const uint4*)(a.bmass + (int64_t)b * SBK + k0);
+    uint4 c[8], m[16];
+#pragma unroll
+    for (int x = 0; x < 8; x++) c[x] = pc[x];
+#pragma unroll
+    for (int x = 0; x < 16; x++) m[x] = pm[x];
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+      const uint32_t v[4] = {c[x].x, c[x].y, c[x].z, c[x].w};
+#pragma unroll
+      for (int y = 0; y < 4; y++)
+        if (v[y]) atomicAdd(&cnt[k0 + 4 * x + y], v[y]);
+    }
+#pragma unroll
+    for (int x = 0; x < 16; x++) {
+      const uint64_t v0 = ((uint64_t)m[x].y << 32) | m[x].x, v1 = ((uint64_t)m[x].w << 32) | m[x].z;
+      if (v0) atomicAdd((unsigned long long*)&mass[k0 + 2 * x], (unsigned long long)v0);
+      if (v1) atomicAdd((unsigned long long*)&mass[k0 + 2 * x + 1], (unsigned long long)v1);
+    }
+  }
+  __syncthreads();
+}
+
+// the candidate bucket level (thread 0's loops; the same in every kernel):
+// top-k: the first bucket whose running count reaches k; top-p alone: whose
+// running mass reaches top_p of the sum (a margin for the fixed point); min-p
+// alone: the bucket of its cut; else every finite token
+__device__ int sample_level(const SampleArgs& a, const uint32_t* cnt, const uint64_t* mass, double sum)
+{
+  if (a.top_k > 0) {
+    uint64_t c = 0;
+    for (int k = 0; k < SBK; k++)
+      if ((c += cnt[k]) >= (uint64_t)a.top_k) return k;
+    return SBK - 1;
+  }
+  if (a.top_p < 1.0) {
+    uint64_t c = 0;
+    // the truncation of each token's fixed-point mass: at most n units short
+    const double want = a.top_p * sum * (1.0 + 1e-9) * MX_ONE + (double)a.n + 1.0;
+    for (int k = 0; k < SBK; k++)
+      if ((double)(c += mass[k]) >= want) return k;
+    return SBK - 1;
+  }
+  return p_bucket(a.min_p * (1.0 - 1e-9));
+}
+
+extern "C" __global__ __launch_bounds__(256) void sample_compact(SampleArgs a)
+{
+  __shared__ uint32_t cnt[SBK];
+  __shared__ uint64_t mass[SBK];
+  __shared__ uint64_t shu[SBT];
+  __shared__ double shd[SBT];
+  __shared__ int level;
+  __shared__ uint64_t at0;
+  const int t = threadIdx.x, b = blockIdx.x;
+  const int best = *a.best;
+  if (sample_greedy(a, best)) return;
+  const int ept = a.per / SBT;
+  const int i0 = min(a.n, b * a.per + t * ept), i1 = min(a.n, i0 + ept);
+  const double sum = blocks_sum<SBT>(a, shd);
+  if (!sample_filters(a)) {
+    double q = 0;
+    for (int i = i0; i < i1; i++) q = q + a.p[i] / sum;
+    q = sblock_sum<SBT>(q, shd);
+    if (t == 0) a.bq[b] = q;
+    return;
+  }
+  // the totals per bucket over the blocks, then the level
+  bucket_totals<SBT>(a, cnt, mass, shu);
+  if (t == 0) level = sample_level(a, cnt, mass, sum);
+  __syncthreads();
+  const int L = level;
+  // this block's offset: the candidates of the blocks before it
+  uint64_t before = 0;
+  for (int k = t; k < b; k += SBT) {
+#pragma unroll 8
+    for (int j = 0; j <= L; j++) before += a.bcnt[(int64_t)k * SBK + j];
+  }
+  before = sblock_sum<SBT>(before, shu);
+  if (t == 0) at0 = before;
+  __syncthreads();
+  uint64_t mine = 0;
+  for (int i = i0; i < i1; i++)
+    if (finite_bits(a.logits[i]) && p_bucket(a.p[i]) <= L) mine++;
+  uint64_t at = at0 + sblock_exclusive<SBT>(mine, shu);
+  for (int i = i0; i < i1; i++) {
+    const float l = a.logits[i];
+    if (finite_bits(l) && p_bucket(a.p[i]) <= L) {
+      a.cid[at] = i;
+      a.ckey[at] = logit_key(l);
+      a.cp[at] = a.p[i];
+      at++;
+    }
+  }
+}
+
+// what the warpers kept: a key at or above kmin (top-k, min-p) and, after a
+// top-p cut at (kp, ip), a key above kp or kp with an id up to ip
+struct Kept {
+  uint32_t kmin = 0;
+  bool cut = false;
+  uint32_t kp = 0;
+  int ip = 0;
+  __device__ bool operator()(uint32_t key, int id) const
+  {
+    return key >= kmin && !(cut && (key < kp || (key == kp && id > ip)));
+  }
+};
+
+// the first candidate, in (key descending, id ascending) order among the kept
+// ones, at which the running sum of the weights (the count 1 when ONE, else
+// the fixed-point probability) reaches rem (>= rem, or > rem when strict).
+// Returns the id, or -1 when the total stays short of rem. Per-wave
+// histograms of the 256 digit values, added in wave order.
+template <bool ONE>
+__device__ int radix_search(const SampleArgs& a, const Kept& k, int nc, uint64_t rem, bool strict, double sum,
+                            uint64_t (*hist)[256], uint64_t* shu, int* shi, uint32_t* found_key)
+{
+  __shared__ int choice;
+  __shared__ uint64_t rem_sh;
+  const int t = threadIdx.x, w = t >> 6;
+  uint32_t prefix = 0, mask = 0;
+  for (int d = 0; d < 4; d++) {
+    const int shift = 24 - 8 * d;
+    for (int x = t; x < 16 * 256; x += SNT) hist[x >> 8][x & 255] = 0;
+    __syncthreads();
+    for (int c = t; c < nc; c += SNT) {
+      const uint32_t key = a.ckey[c];
+      if ((key & mask) != prefix || !k(key, a.cid[c])) continue;
+      const uint64_t wt = ONE ? 1ull : wfx(a.cp[c], sum);
+      atomicAdd((unsigned long long*)&hist[w][(key >> shift) & 255u], (unsigned long long)wt);
+    }
+    __syncthreads();
+    // the bins over the waves, then their sums from the top digit down
+    // (S[d] = sum of bins >= d): the digit is the largest d whose S[d]
+    // reaches rem, the rest carries S[d + 1]
+    uint64_t h = 0;
+    if (t < 256)
+      for (int x = 0; x < 16; x++) h += hist[x][t];
+    if (t == 0) choice = -1;
+    __syncthreads();
+    if (t < 256) hist[0][255 - t] = h;  // reversed: a prefix sum gives S
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const uint64_t v = (t < 256 && t >= o) ? hist[0][t - o] : 0ull;
+      __syncthreads();
+      if (t < 256) hist[0][t] += v;
+      __syncthreads();
+    }
+    if (t < 256) {
+      const uint64_t sd = hist[0][t], above = t > 0 ? hist[0][t - 1] : 0ull;  // S[d], S[d + 1]
+      const bool reach = strict ? sd > rem : sd >= rem, before = strict ? above > rem : above >= rem;
+      if (reach && !before) {
+        choice = 255 - t;
+        rem_sh = rem - above;
+      }
+    }
+    __syncthreads();
+    if (choice < 0) return -1;
+    rem = rem_sh;
+    prefix |= (uint32_t)choice << shift;
+    mask |= 255u << shift;
+    __syncthreads();
+  }
+  *found_key = prefix;
+  // the ties of that key in id order (the candidates are in id order): each
+  // thread a contiguous run, its sum, the prefix over the threads
+  const int per = (nc + SNT - 1) / SNT;
+  const int c0 = min(nc, t * per), c1 = min(nc, c0 + per);
+  uint64_t part = 0;
+  for (int c = c0; c < c1; c++)
+    if (a.ckey[c] == prefix && k(prefix, a.cid[c])) part += ONE ? 1ull : wfx(a.cp[c], sum);
+  uint64_t cum = sblock_exclusive<SNT>(part, shu);
+  int hit = INT_MAX;
+  for (int c = c0; c < c1; c++) {
+    if (a.ckey[c] != prefix || !k(prefix, a.cid[c])) continue;
+    cum += ONE ? 1ull : wfx(a.cp[c], sum);
+    if (strict ? cum > rem : cum >= rem) {
+      hit = a.cid[c];
+      break;
+    }
+  }
+  hit = sblock_min<SNT>(hit, shi);
+  return hit == INT_MAX ? -1 : hit;
+}
+
+// the warpers and the draw over at most SNT candidates sorted in LDS (a
+// bitonic sort of key << 32 | ~id, descending: the logit descending, the id
+// ascending), each thread one of them: top-k, top-p, min-p and the draw are
+// prefixes of that order, their sums a scan in it (sampler.pas:397-449)
+__device__ void sorted_pick(const SampleArgs& a, int nc, double sum, uint64_t* sk, double* shd, int* shi)
+{
+  __shared__ double qh[SNT];
+  __shared__ double u_sh2;
+  const int t = threadIdx.x;
+  sk[t] = t < nc ? ((uint64_t)a.ckey[t] << 32) | (uint64_t)(0xffffffffu - (uint32_t)a.cid[t]) : 0ull;
+  for (int k = 2; k <= SNT; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      __syncthreads();
+      const int x = t ^ j;
+      if (x > t) {
+        const uint64_t p = sk[t], q = sk[x];
+        if (((t & k) == 0) ? p < q : p > q) {
+          sk[t] = q;
+          sk[x] = p;
+        }
+      }
+    }
+  __syncthreads();
+  const uint64_t me = sk[t];
+  const uint32_t key = (uint32_t)(me >> 32);
+  const int id = (int)(0xffffffffu - (uint32_t)me);
+  const double q = t < nc ? a.p[id] / sum : 0.0;
+  qh[t] = q;
+  // top-k: the first k and every tie of the k-th logit
+  int n = nc;
+  if (a.top_k > 0 && nc > a.top_k) {
+    const uint32_t kk = (uint32_t)(sk[a.top_k - 1] >> 32);
+    n = sblock_sum<SNT>((t < nc && key >= kk) ? 1 : 0, shi);
+  }
+  // the running probability in sorted order over the first n
+  double cum = sblock_exclusive<SNT>(t < n ? q : 0.0, shd) + (t < n ? q : 0.0);
+  // top-p over what top-k kept: the shortest prefix reaching top_p of its mass
+  if (a.top_p < 1.0) {
+    double mass = 1.0;
+    if (a.top_k > 0) mass = sblock_sum<SNT>(t < n ? q : 0.0, shd);
+    const int first = sblock_min<SNT>((t < n && cum >= a.top_p * mass) ? t : INT_MAX, shi);
+    if (first != INT_MAX) n = first + 1;
+  }
+  // min-p: while the probability reaches min_p times the best's
+  if (a.min_p > 0.0) {
+    const double q0 = qh[0];
+    const int fail_at = sblock_min<SNT>((t >= 1 && t < n && !(q >= a.min_p * q0)) ? t : INT_MAX, shi);
+    if (fail_at != INT_MAX) n = fail_at;
+  }
+  // one draw: u times the mass of the first n (the running sum at n - 1),
+  // the first whose running sum passes it
+  if (t == n - 1) qh[0] = cum;
+  __syncthreads();
+  if (t == 0) u_sh2 = splitmix_next(a.state) * qh[0];
+  __syncthreads();
+  const int hit = sblock_min<SNT>((t < n && u_sh2 < cum) ? t : INT_MAX, shi);
+  if (t == 0) {
+    const int pick = hit == INT_MAX ? 0 : hit;
+    *a.out = (int)(0xffffffffu - (uint32_t)sk[pick]);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(1024) void sample_pick(SampleArgs a)
+{
+  __shared__ double shd[SNT];
+  __shared__ uint64_t shu[SNT];
+  __shared__ int shi[SNT];
+  __shared__ uint64_t hist[16][256];
+  __shared__ double u_sh;
+  __shared__ int level, blk;
+  __shared__ uint32_t cnt[SBK];
+  __shared__ uint64_t mass[SBK];
+  const int t = threadIdx.x;
+  IHIP_STAMP(0);
+  const int best = *a.best;
+  __syncthreads();  // every thread has read best before it may be overwritten
+  if (sample_greedy(a, best)) {
+    if (t == 0) *a.out = best;
+    return;
+  }
+  const double sum = blocks_sum<SNT>(a, shd);
+  IHIP_STAMP(1);
+  if (!sample_filters(a)) {
+    // one draw over every token in id order (sampler.pas:326-342): the block
+    // whose running sum passes u, then its tokens
+    if (t < a.nb) shd[t] = a.bq[t];
+    __syncthreads();
+    if (t == 0) {
+      const double u = splitmix_next(a.state);
+      double cum = 0;
+      int bk = -1;
+      for (int b = 0; b < a.nb; b++) {
+        if (u < cum + shd[b]) {
+          bk = b;
+          break;
+        }
+        cum = cum + shd[b];
+      }
+      blk = bk;
+      u_sh = u;
+      shd[SNT - 1] = cum;
+    }
+    __syncthreads();
+    const int bk = blk;
+    const double u = u_sh, base = shd[SNT - 1];
+    __syncthreads();
+    int hit = INT_MAX;
+    if (bk >= 0) {
+      const int per = (a.per + SNT - 1) / SNT;
+      const int i0 = min(a.n, bk * a.per + min(a.per, t * per)), i1 = min(min(a.n, (bk + 1) * a.per), i0 + per);
+      double part = 0;
+      for (int i = i0; i < i1; i++) part = part + a.p[i] / sum;
+      double cum = base + sblock_exclusive<SNT>(part, shd);
+      for (int i = i0; i < i1; i++) {
+        const double q = a.p[i] / sum;
+        cum = cum + q;
+        if (q > 0 && u < cum) {
+          hit = i;
+          break;
+        }
+      }
+    }
+    hit = sblock_min<SNT>(hit, shi);
+    if (t == 0) *a.out = hit == INT_MAX ? best : hit;
+    return;
+  }
+  // the level and the number of candidates (as sample_compact found them)
+  bucket_totals<SNT>(a, cnt, mass, shu);
+  if (t == 0) {
+    const int L = sample_level(a, cnt, mass, sum);
+    uint32_t nc = 0;
+    for (int k = 0; k <= L; k++) nc += cnt[k];
+    level = (int)nc;
+  }
+  __syncthreads();
+  const int nc = level;
+  IHIP_STAMP(2);
+  if (nc <= SNT) {
+    sorted_pick(a, nc, sum, shu, shd, shi);
+    return;
+  }
+  const double qbest = a.p[best] / sum;
+  Kept k;
+  uint32_t key;
+  // top-k: the k-th largest logit; its ties stay (sampler.pas:400-408)
+  if (a.top_k > 0 && nc > a.top_k) {
+    if (radix_search<true>(a, k, nc, (uint64_t)a.top_k, false, sum, hist, shu, shi, &key) >= 0) k.kmin = key;
+  }
+  IHIP_STAMP(3);
+  // top-p over what top-k kept: the shortest prefix reaching top_p of its
+  // mass (sampler.pas:409-428)
+  if (a.top_p < 1.0) {
+    uint64_t mfx = (uint64_t)FX_ONE;
+    if (a.top_k > 0) {
+      uint64_t part = 0;
+      for (int c = t; c < nc; c += SNT)
+        if (k(a.ckey[c], a.cid[c])) part += wfx(a.cp[c], sum);
+      mfx = sblock_sum<SNT>(part, shu);
+    }
+    const uint64_t target = (uint64_t)ceil(a.top_p * (double)mfx);
+    const int id = radix_search<false>(a, k, nc, target, false, sum, hist, shu, shi, &key);
+    if (id >= 0) {
+      k.cut = true;
+      k.kp = key;
+      k.ip = id;
+    }
+  }
+  IHIP_STAMP(4);
+  // min-p, relative to the best token (sampler.pas:429-434): p grows with the
+  // logit, so what it keeps is every key from the smallest that passes
+  if (a.min_p > 0.0) {
+    uint32_t kmin = 0xffffffffu;
+    for (int c = t; c < nc; c += SNT)
+      if (k(a.ckey[c], a.cid[c]) && a.cp[c] / sum >= a.min_p * qbest) kmin = min(kmin, a.ckey[c]);
+    kmin = sblock_min<SNT>(kmin, (uint32_t*)shi);
+    k.kmin = max(k.kmin, kmin);
+  }
+  // one draw from what is left (sampler.pas:435-449)
+  uint64_t part = 0;
+  for (int c = t; c < nc; c += SNT)
+    if (k(a.ckey[c], a.cid[c])) part += wfx(a.cp[c], sum);
+  const uint64_t total = sblock_sum<SNT>(part, shu);
+  IHIP_STAMP(5);
+  if (t == 0) u_sh = splitmix_next(a.state);
+  __syncthreads();
+  const uint64_t target = (uint64_t)(u_sh * (double)total);
+  const int id = radix_search<false>(a, k, nc, target, true, sum, hist, shu, shi, &key);
+  IHIP_STAMP(6);
+  if (t == 0) *a.out = id >= 0 ? id : best;
+}
+
 }  // namespace ihip
 
 // ---------------------------------------------------------- HBM streaming

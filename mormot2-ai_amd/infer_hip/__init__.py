@@ -34,6 +34,16 @@ class FormatError(HipError):
 IHIP_E_FORMAT = -7
 
 
+class Sampling(C.Structure):
+    """TInferSampling (sampler.pas:46-59)."""
+    _fields_ = [("temperature", C.c_double), ("top_k", C.c_int32), ("reserved", C.c_int32),
+                ("top_p", C.c_double), ("min_p", C.c_double), ("seed", C.c_int64)]
+
+
+def sampling(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, seed=0):
+    return Sampling(temperature, top_k, 0, top_p, min_p, seed)
+
+
 class GgufValue(C.Structure):
     _fields_ = [("key", C.c_char_p), ("vtype", C.c_int32), ("etype", C.c_int32),
                 ("count", C.c_int64), ("data", C.c_void_p)]
@@ -138,6 +148,10 @@ def lib():
             "ihip_gguf_find_tensor": (i64, [vp, C.c_char_p]),
             "ihip_gguf_weight": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(i64), C.POINTER(vp)]),
             "ihip_gguf_model_desc": (i32, [vp, C.POINTER(vp)]),
+            "ihip_sampler_create": (i32, [vp, C.POINTER(Sampling), i64, C.POINTER(vp)]),
+            "ihip_sampler_destroy": (None, [vp]),
+            "ihip_enqueue_sample": (i32, [vp, vp, u64, i64, u64]),
+            "ihip_model_sampling": (i32, [vp, C.POINTER(Sampling)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -356,6 +370,11 @@ class Model:
     def use_graphs(self, on):
         check(lib().ihip_model_use_graphs(self.h, int(on)), "use_graphs")
 
+    def sampling(self, **kw):
+        """Draw the next tokens with these settings (None: the argmax)."""
+        s = sampling(**kw) if kw else None
+        check(lib().ihip_model_sampling(self.h, C.byref(s) if s is not None else None), "sampling")
+
     def decode(self, first, steps):
         out = np.empty(steps, np.int32)
         check(lib().ihip_model_decode(self.h, int(first), steps, _p(out)), "decode")
@@ -507,3 +526,26 @@ class GgufSpec:
 
     def close(self):
         self.file.close()
+
+
+class Sampler:
+    """TInferSampler on the device (ihip_sampler): draws with its own
+    splitmix64 stream, kept on the device."""
+
+    def __init__(self, ctx, n_max, **kw):
+        self.ctx = ctx
+        h = C.c_void_p()
+        s = sampling(**kw)
+        check(lib().ihip_sampler_create(ctx.h, C.byref(s), n_max, C.byref(h)), "sampler")
+        self.h = h
+
+    def enqueue(self, logits_ptr, n, out_ptr):
+        check(lib().ihip_enqueue_sample(self.ctx.h, self.h, logits_ptr, n, out_ptr), "sample")
+
+    def close(self):
+        if getattr(self, "h", None) and getattr(self.ctx, "h", None):
+            lib().ihip_sampler_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        self.close()

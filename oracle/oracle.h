@@ -111,6 +111,13 @@ int orc_model_forward(orc_model* m, const int32_t* ids, int64_t count,
 int orc_model_greedy(orc_model* m, const int32_t* prompt, int64_t n,
                      int64_t max_new, int32_t* out_ids, float* margins);
 
+/* sampler.c: TInferSampler (sampler.pas:52-435) */
+double orc_splitmix_next(uint64_t* state);
+int orc_sampler_create(double temperature, int32_t top_k, double top_p, double min_p,
+                       int64_t seed, void** out);
+void orc_sampler_destroy(void* s);
+int64_t orc_sampler_next(void* s, const float* logits, int64_t count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,14 @@ def lib():
         L.orc_model_set_f32.restype = None
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
         L.orc_model_greedy.argtypes = [vp, vp, i64, i64, vp, vp]
+        L.orc_splitmix_next.restype = C.c_double
+        L.orc_splitmix_next.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_sampler_create.argtypes = [C.c_double, C.c_int32, C.c_double, C.c_double,
+                                         C.c_int64, C.POINTER(vp)]
+        L.orc_sampler_destroy.argtypes = [vp]
+        L.orc_sampler_destroy.restype = None
+        L.orc_sampler_next.restype = i64
+        L.orc_sampler_next.argtypes = [vp, vp, i64]
         _lib = L
     return _lib
 
@@ -150,6 +158,31 @@ def route(logits, k, norm_topk=True):
     w = np.empty(k, np.float32)
     lib().orc_route(_p(lg), lg.size, k, int(norm_topk), _p(ids), _p(w))
     return ids, w
+
+
+class Sampler:
+    """TInferSampler (sampler.pas:52-435) on the CPU: temperature, top_k,
+    top_p, min_p, seed."""
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, seed=0):
+        self.h = None
+        h = C.c_void_p()
+        rc = lib().orc_sampler_create(temperature, top_k, top_p, min_p, seed, C.byref(h))
+        if rc:
+            raise ValueError("sampling settings out of range")
+        self.h = h
+
+    def next(self, logits):
+        v = np.ascontiguousarray(logits, np.float32)
+        return int(lib().orc_sampler_next(self.h, _p(v), v.size))
+
+    def close(self):
+        if self.h:
+            lib().orc_sampler_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 def argmax(v):
