@@ -129,6 +129,12 @@ struct LinearCall {
   // a two-type launch (a kernel for the pair must exist): matrices nseg1..
   // are of dtype2
   int dtype2 = 0, nseg1 = 0;
+  // self-routing (one token's expert slots, rows = rk, one row per block):
+  // rl the router logits [rexp]; each block takes its slot's expert by rank,
+  // one block writes the picks (by id) to ids and their weights to rw
+  uint64_t rl = 0, rw = 0;
+  int rexp = 0, rk = 0, rnorm = 0;
+  bool batch_rows() const { return items != 0; }
 };
 // whether one launch can take matrices of types a then b (gemv_<a>_<b>_*)
 bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in);

@@ -368,19 +368,28 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
     // MoeBlock (decoder.pas:3037-3053), the experts chosen on the device
     const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
     if ((rc = normed(L.post_norm, L.rd, L.router, E, L.router_b, m->route))) return rc;
-    struct {
-      const float* logits;
-      int* ids;
-      float* w;
-      int32_t experts, k, norm, rows;
-    } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
-            d.norm_topk, 1};
-    if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
+    // the route (TDecoderModel.Route) inside the gate/up launch: each block
+    // ranks the logits for its slot's expert, one writes the picks and
+    // weights for the down launch (up to 256 experts); else its own launch
+    const bool self_route = E <= 256 && K <= E && K <= 8;
+    if (!self_route) {
+      struct {
+        const float* logits;
+        int* ids;
+        float* w;
+        int32_t experts, k, norm, rows;
+      } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
+              d.norm_topk, 1};
+      if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
+    }
     LinearCall k;
     k.x = m->x; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
     k.y = m->gate; k.mode = m->mode; k.ids = m->ids; k.stride = L.eg_stride; k.x_per_slot = 0;
     k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
     k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
+    if (self_route) {
+      k.rl = m->route; k.rw = m->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
+    }
     if ((rc = enqueue_linear(m->c, k))) return rc;
     LinearCall dn;
     dn.x = m->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;

@@ -24,6 +24,7 @@
 // groups of a super-block sit in 8 neighbouring lanes, whose integer sums
 // are added exactly before the one double product of the super-block.
 #include "formats.h"
+#include "route.h"
 
 namespace ihip {
 
@@ -66,6 +67,14 @@ struct LinArgs {
   float* yseg[3];
   int32_t oseg[3];
   int32_t nseg1;  // a two-type launch: matrices 0..nseg1-1 of the first type, the rest of the second
+  // self-routing (a token's one-row expert launch): rl the row's router
+  // logits, rexp experts, rk picks, rnorm NormTopK; each block takes the
+  // expert of its slot by rank (ids unused as input), and block (0, 0) writes
+  // the picks sorted by id to ids and their weights to rw (route of
+  // TDecoderModel.Route) for the down projection
+  const float* rl;
+  float* rw;
+  int32_t rexp, rk, rnorm, rpad;
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
@@ -698,8 +707,11 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     xrow0 = yrow0 = 0;
   } else if (a.ids) {
     int slot = blockIdx.y;
-    int e = a.ids[slot];
-    if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
+    // a self-routed token (one row) takes its expert below, once the
+    // activation row is on its way
+    const bool later = R == 1 && a.rl != nullptr;
+    const int e = later ? 0 : a.ids[slot];
+    if (!later && (e < 0 || (a.nexp > 0 && e >= a.nexp))) {
       for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
            o += (int64_t)gridDim.x * blockDim.x)
         a.y[(int64_t)slot * a.out + o] = 0.f;
@@ -737,13 +749,6 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     // first ones before the activation row is read), so a wave keeps several
     // 16-byte loads per lane in flight
     constexpr int T = GLU ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
-    // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
-    const uint8_t* w2 = GLU ? a.w2 + (w - a.w) : nullptr;
-    const float* bias2 = a.bias2 ? a.bias2 + expert * out : nullptr;
-    XGroup xg[U];
-    Raw raw[T][U], raw2[T][U];
-    __shared__ __align__(16) uint8_t xs[xs_bytes<F, MODE>()];
-    constexpr bool HXP = F == DT_MXFP4 && MODE == 1;  // f16 activation pairs
     // the activation row's global loads first, then the first step's weight
     // loads, so the row is staged while the weights are on their way
     XStage st;
@@ -751,6 +756,34 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
                               quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
                               a.nw, st);
+    if (a.ids && a.rl) {
+      // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
+      // of this block's slot; the blocks of column 0 hand it to the down launch
+      int sid[8];
+      float sw[8];
+      if (a.rexp <= 64) route_wave<1, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      else if (a.rexp <= 128) route_wave<2, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      else route_wave<4, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      int e = -1;
+#pragma unroll
+      for (int s = 0; s < 8; s++) e = s == (int)blockIdx.y ? sid[s] : e;
+      if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
+        for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
+             o += (int64_t)gridDim.x * blockDim.x)
+          a.y[(int64_t)blockIdx.y * a.out + o] = 0.f;
+        return;
+      }
+      expert = e;
+      w += (int64_t)e * a.stride;
+      if (bias) bias += (int64_t)e * a.out;
+    }
+    // gate + up + SwiGLU in one pass: w2 the up matrices, the same expert
+    const uint8_t* w2 = GLU ? a.w2 + (w - a.w) : nullptr;
+    const float* bias2 = a.bias2 ? a.bias2 + expert * out : nullptr;
+    XGroup xg[U];
+    Raw raw[T][U], raw2[T][U];
+    __shared__ __align__(16) uint8_t xs[xs_bytes<F, MODE>()];
+    constexpr bool HXP = F == DT_MXFP4 && MODE == 1;  // f16 activation pairs
     int64_t tb = wid;
     // the epilogue operands of a step's rows (bias, up bias, residual), loaded
     // with its weights rather than after its sums; a launch without them
@@ -770,6 +803,26 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
     load_epi(tb);
+    if (a.ids && a.rl && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+      // a self-routed token: wave 0 of one block writes the picks (by id) and
+      // their weights for the down launch while its own loads are on their way
+      int sid[8];
+      float sw[8];
+      if (a.rexp <= 64) route_wave<1, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      else if (a.rexp <= 128) route_wave<2, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      else route_wave<4, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      int myid = -1;
+      float myw = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < 8; s2++) {
+        myid = (int)threadIdx.x == s2 ? sid[s2] : myid;
+        myw = (int)threadIdx.x == s2 ? sw[s2] : myw;
+      }
+      if ((int)threadIdx.x < a.rk) {
+        ((int*)a.ids)[threadIdx.x] = myid;
+        a.rw[threadIdx.x] = myw;
+      }
+    }
     IHIP_STAMP(1);
     stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
                          1 + (int)xrow0);
