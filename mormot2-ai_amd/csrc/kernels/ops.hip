@@ -366,6 +366,16 @@ __device__ __forceinline__ double cache_at(const void* c, int64_t i, int f16)
   return f16 ? (double)half_to_float(((const uint16_t*)c)[i]) : (double)((const float*)c)[i];
 }
 
+// the head of block x of an attention launch over (heads, ...): consecutive
+// heads - one KV group's query heads, which read the same key and value
+// tiles - on one XCD. The workgroups of a launch go to the 8 XCDs in turn by
+// block id (x first), each XCD with its own L2; with heads a multiple of 8,
+// block x runs on XCD x % 8 whatever its y and z.
+__device__ __forceinline__ int xcd_head(unsigned x, int heads)
+{
+  return (heads & 7) ? (int)x : (int)(x & 7) * (heads >> 3) + (int)(x >> 3);
+}
+
 // the keys of one (head, row) cut into `splits` ranges of at most ATT_CHUNK
 // keys (flash-decoding): each block scores its range - every score the CPU's
 // sequential double dot product (CausalRows, backend.cpu.pas:1305-1354) -
@@ -383,7 +393,7 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   __shared__ double sc[ATT_CHUNK];
   __shared__ double red[8];
   __shared__ double accs[4][256];
-  const int h = blockIdx.x, r = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
+  const int h = xcd_head(blockIdx.x, a.heads), r = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
   const int d = a.hd;
   const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
   const int g = h / (a.heads / a.kvh);
@@ -566,7 +576,7 @@ __device__ __forceinline__ void attention_rows_t(const AttnArgs& a)
   __shared__ double qd[ATTR][HD];
   __shared__ double sc[ATTR][ATTK + 1];
   __shared__ double stat[ATTR][2];  // a row's range maximum and sum
-  const int h = blockIdx.x, r0 = blockIdx.y * ATTR, s = blockIdx.z, t = threadIdx.x;
+  const int h = xcd_head(blockIdx.x, a.heads), r0 = blockIdx.y * ATTR, s = blockIdx.z, t = threadIdx.x;
   constexpr int d = HD;
   const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
   const int g = h / (a.heads / a.kvh);
@@ -875,7 +885,8 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   __shared__ double sc[ATT_CHUNK];
   __shared__ double red[8];
   __shared__ double accs[4][HD];
-  const int h = blockIdx.x, s = blockIdx.z, t = threadIdx.x;
+  const int h = xcd_head(blockIdx.x, a.heads);
+  const int s = blockIdx.z, t = threadIdx.x;
   constexpr int d = HD, half = HD / 2;
   IHIP_STAMP(0);
   const int64_t kvw = (int64_t)a.kvh * d;
