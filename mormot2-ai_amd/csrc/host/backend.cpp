@@ -411,9 +411,9 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]},
          k.dtype2 ? k.nseg1 : k.nseg, (const float*)k.rl, (float*)k.rw, (int32_t)k.rexp,
          (int32_t)k.rk, (int32_t)k.rnorm, 0};
-  if (k.rl && (!k.ids || !k.rw || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
+  if (k.rl && (!k.ids || !k.rw || !k.w2 || !k.nw || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
                k.rk > std::min<int64_t>(k.rexp, 8) || k.rk != k.rows))
-    return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts");
+    return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts, gate/up with a norm");
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
   // (float weights in the Q8 arithmetic: the float activations as they are,

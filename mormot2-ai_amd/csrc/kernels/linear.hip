@@ -709,7 +709,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     int slot = blockIdx.y;
     // a self-routed token (one row) takes its expert below, once the
     // activation row is on its way
-    const bool later = R == 1 && a.rl != nullptr;
+    const bool later = R == 1 && GLU && NORM && a.rl != nullptr;
     const int e = later ? 0 : a.ids[slot];
     if (!later && (e < 0 || (a.nexp > 0 && e >= a.nexp))) {
       for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
@@ -756,7 +756,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
                               quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
                               a.nw, st);
-    if (a.ids && a.rl) {
+    if (GLU && NORM && a.ids && a.rl) {
       // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
       // of this block's slot; the blocks of column 0 hand it to the down launch
       int sid[8];
@@ -803,7 +803,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
     load_epi(tb);
-    if (a.ids && a.rl && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
+    if (GLU && NORM && a.ids && a.rl && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
       // a self-routed token: wave 0 of one block writes the picks (by id) and
       // their weights for the down launch while its own loads are on their way
       int sid[8];
