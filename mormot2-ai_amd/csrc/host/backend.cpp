@@ -487,7 +487,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
              mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
              batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   }
-  unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows : (batch ? (k.rows + 7) / 8 : 1)));
+  // a self-routed token: one row more, whose first block forms the weights
+  unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows + (k.rl ? 1 : 0) : (batch ? (k.rows + 7) / 8 : 1)));
   int64_t tiles_all = tiles;
   if (k.nseg > 1) {
     gy = (unsigned)k.nseg;

@@ -707,6 +707,30 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     xrow0 = yrow0 = 0;
   } else if (a.ids) {
     int slot = blockIdx.y;
+    if (R == 1 && GLU && NORM && a.rl && slot == a.rk) {
+      // the launch's extra row of a self-routed token: wave 0 of its first
+      // block writes the picks (by id) and their weights for the down
+      // launch, beside the blocks of the slots
+      if (blockIdx.x == 0 && threadIdx.x < 64) {
+        int sid[8];
+        float sw[8];
+        if (a.rexp <= 64) route_wave<1, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+        else if (a.rexp <= 128) route_wave<2, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+        else route_wave<4, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+        int myid = -1;
+        float myw = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++) {
+          myid = (int)threadIdx.x == s2 ? sid[s2] : myid;
+          myw = (int)threadIdx.x == s2 ? sw[s2] : myw;
+        }
+        if ((int)threadIdx.x < a.rk) {
+          ((int*)a.ids)[threadIdx.x] = myid;
+          a.rw[threadIdx.x] = myw;
+        }
+      }
+      return;
+    }
     // a self-routed token (one row) takes its expert below, once the
     // activation row is on its way
     const bool later = R == 1 && GLU && NORM && a.rl != nullptr;
@@ -758,7 +782,8 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
                               a.nw, st);
     if (GLU && NORM && a.ids && a.rl) {
       // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
-      // of this block's slot; the blocks of column 0 hand it to the down launch
+      // of this block's slot; the launch's extra row writes the picks and
+      // weights for the down launch
       int sid[8];
       float sw[8];
       if (a.rexp <= 64) route_wave<1, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
@@ -803,26 +828,6 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     load_tiles<F, U, T, GLU>(w, w2, rg, tb, nw, rpw, rsub, lr, lpr, G, a.in, out, raw,
                              raw2);
     load_epi(tb);
-    if (GLU && NORM && a.ids && a.rl && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 64) {
-      // a self-routed token: wave 0 of one block writes the picks (by id) and
-      // their weights for the down launch while its own loads are on their way
-      int sid[8];
-      float sw[8];
-      if (a.rexp <= 64) route_wave<1, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-      else if (a.rexp <= 128) route_wave<2, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-      else route_wave<4, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-      int myid = -1;
-      float myw = 0.f;
-#pragma unroll
-      for (int s2 = 0; s2 < 8; s2++) {
-        myid = (int)threadIdx.x == s2 ? sid[s2] : myid;
-        myw = (int)threadIdx.x == s2 ? sw[s2] : myw;
-      }
-      if ((int)threadIdx.x < a.rk) {
-        ((int*)a.ids)[threadIdx.x] = myid;
-        a.rw[threadIdx.x] = myw;
-      }
-    }
     IHIP_STAMP(1);
     stage_store<F, MODE, NORM>(st, quantized, a.in, a.eps, xs, (float*)(xs + a.in), a.bad,
                          1 + (int)xrow0);
