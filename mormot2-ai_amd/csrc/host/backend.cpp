@@ -487,7 +487,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
              mode == IHIP_MODE_Q8 ? "q8" : "f32", k.nw ? "norm_" : "",
              batch ? "b8" : (k.w2 ? "glu_" : ""), U);
   }
-  // a self-routed token: one row more, whose first block forms the weights
+  // a self-routed token: one row more (row 0), whose first block forms the route
   unsigned gy = (unsigned)(k.items ? k.nitems : (k.ids ? k.rows + (k.rl ? 1 : 0) : (batch ? (k.rows + 7) / 8 : 1)));
   int64_t tiles_all = tiles;
   if (k.nseg > 1) {
@@ -505,7 +505,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     // about two blocks per CU. Matrices of one launch (nseg) are sized by
     // the largest; the blocks of a smaller one past its rows end at once.
     const int T = k.w2 ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
-    const unsigned share = k.nseg > 1 ? 1u : gy;
+    // (the route row of a self-routed token is not a share: one block works)
+    const unsigned share = k.nseg > 1 ? 1u : gy - (k.ids && k.rl ? 1u : 0u);
     const int64_t want = ((int64_t)c->cus * c->gemv_blocks_per_cu + share - 1) / share;
     wgs = std::min(wgs, std::max<int64_t>((tiles_all + 4 * T - 1) / (4 * T), want));
     // and no more blocks than the chip holds at once: the waves walk the

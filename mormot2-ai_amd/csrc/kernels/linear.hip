@@ -706,11 +706,14 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     nrows = min(R, it.z);
     xrow0 = yrow0 = 0;
   } else if (a.ids) {
-    int slot = blockIdx.y;
-    if (R == 1 && GLU && NORM && a.rl && slot == a.rk) {
-      // the launch's extra row of a self-routed token: wave 0 of its first
-      // block writes the picks (by id) and their weights for the down
-      // launch, beside the blocks of the slots
+    const bool routed = R == 1 && GLU && NORM && a.rl != nullptr;
+    // a self-routed token: row 0 of the launch forms the route, row 1 + s
+    // computes slot s
+    const int slot = routed ? (int)blockIdx.y - 1 : (int)blockIdx.y;
+    if (routed && slot < 0) {
+      // the route row (dispatched first): wave 0 of its first block writes
+      // the picks (by id) and their weights for the down launch, beside the
+      // blocks of the slots
       if (blockIdx.x == 0 && threadIdx.x < 64) {
         int sid[8];
         float sw[8];
@@ -733,7 +736,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     }
     // a self-routed token (one row) takes its expert below, once the
     // activation row is on its way
-    const bool later = R == 1 && GLU && NORM && a.rl != nullptr;
+    const bool later = routed;
     const int e = later ? 0 : a.ids[slot];
     if (!later && (e < 0 || (a.nexp > 0 && e >= a.nexp))) {
       for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
@@ -791,11 +794,11 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       else route_wave<4, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
       int e = -1;
 #pragma unroll
-      for (int s = 0; s < 8; s++) e = s == (int)blockIdx.y ? sid[s] : e;
+      for (int s = 0; s < 8; s++) e = s == (int)yrow0 ? sid[s] : e;
       if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
         for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
              o += (int64_t)gridDim.x * blockDim.x)
-          a.y[(int64_t)blockIdx.y * a.out + o] = 0.f;
+          a.y[yrow0 * a.out + o] = 0.f;
         return;
       }
       expert = e;
