@@ -50,8 +50,8 @@ struct ihip_ctx {
   int device = 0;
   int cus = 256;
   bool use_gemm = true;        // Q8 chunks of >= GEMM_MIN_ROWS rows on the MFMA GEMM (IHIP_GEMM=0: off)
-  int gemv_blocks_per_cu = 2;
-  int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
+  int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
+  int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
   hipStream_t stream = nullptr;
   std::vector<ihip::Module> modules;
   std::unordered_map<std::string, hipFunction_t> kernels;
