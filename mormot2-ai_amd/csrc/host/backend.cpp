@@ -421,7 +421,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   const bool gemm_q8 = (q8 || float_fmt(k.dtype)) && gemm_runs(c, k.dtype, mode);
   if (k.items && k.item_rows > 8 && !gemm_q8)
     return fail(IHIP_E_ARG, "EnqueueLinear: items of more than 8 slots need the GEMM");
-  if (batch && gemm_q8 && (k.items ? k.item_rows > 8 : k.rows >= GEMM_MIN_ROWS)) {
+  if (batch && gemm_q8 && (k.items ? k.item_rows > 8 : k.rows >= c->gemm_min_rows)) {
     struct {
       const uint8_t* w;
       const uint8_t* xq;

@@ -10,6 +10,8 @@ tests/test.infer.cuda.pas:714-967, 2333-2447):
   integer sums, double scaling), allowing a 1-ulp difference only where the
   order of a double sum differs - counted and bounded.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -157,11 +159,25 @@ GEMM_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K, H.F32, H.B
 GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100), (40, 2880, 70)]
 
 
+@pytest.fixture(scope="module")
+def gemm_ctx():
+    # a context that sends every chunk of 16 rows or more to the GEMM (the
+    # default sends chunks of 80 or more; smaller ones go to 8-row GEMVs)
+    os.environ["IHIP_GEMM_MIN_ROWS"] = "16"
+    try:
+        c = H.Context(0)
+    finally:
+        del os.environ["IHIP_GEMM_MIN_ROWS"]
+    yield c
+    c.close()
+
+
 @pytest.mark.parametrize("dtype", GEMM_FMTS)
-def test_gemm_q8_mode_cpu_bits(ctx, dtype):
-    # chunks of >= 16 rows run on the MFMA GEMM: exact int32 group sums from
-    # the int8 matrix cores, the scales in double, as the CPU; float weights
-    # on the f64 matrix cores (exact products, double sums)
+def test_gemm_q8_mode_cpu_bits(gemm_ctx, dtype):
+    # chunks of >= 16 rows run on the MFMA GEMM here: exact int32 group sums
+    # from the int8 matrix cores, the scales in double, as the CPU; float
+    # weights on the f64 matrix cores (exact products, double sums)
+    ctx = gemm_ctx
     rng = np.random.default_rng(19)
     total, differ = 0, 0
     for rows, cols, out in GEMM_SHAPES:
