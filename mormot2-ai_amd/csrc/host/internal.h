@@ -15,6 +15,13 @@
 
 namespace ihip {
 
+// rows from which a Q8 Linear runs on the MFMA GEMM instead of 8-row GEMVs:
+// below 80 rows the GEMVs are faster (a 32-token prompt of Qwen3-0.6B
+// prefills 1.6x faster on them, a 128-token one 7% slower)
+constexpr int GEMM_MIN_ROWS = 80;
+// the GEMM's smallest chunk (one 16-row tile)
+constexpr int GEMM_TILE_ROWS = 16;
+
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int hip_fail(hipError_t e, const char* what);
@@ -50,7 +57,7 @@ struct ihip_ctx {
   int device = 0;
   int cus = 256;
   bool use_gemm = true;        // Q8 chunks of >= GEMM_MIN_ROWS rows on the MFMA GEMM (IHIP_GEMM=0: off)
-  int gemm_min_rows = 80;      // the smallest chunk on the GEMM, GEMM_MIN_ROWS (IHIP_GEMM_MIN_ROWS)
+  int gemm_min_rows = ihip::GEMM_MIN_ROWS;  // the smallest chunk on the GEMM (IHIP_GEMM_MIN_ROWS)
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
   hipStream_t stream = nullptr;
@@ -92,12 +99,6 @@ void unpack(const void* src, void* dst, int dtype, int64_t out, int64_t in, int6
 // the Linear dispatch shared by the public entry points and the model
 // block results of the two-stage argmax
 constexpr int ARGMAX_PARTS = 1024;
-// rows from which a Q8 Linear runs on the MFMA GEMM instead of 8-row GEMVs:
-// below 80 rows the GEMVs are faster (a 32-token prompt of Qwen3-0.6B
-// prefills 1.6x faster on them, a 128-token one 7% slower)
-constexpr int GEMM_MIN_ROWS = 80;
-// the GEMM's smallest chunk (one 16-row tile)
-constexpr int GEMM_TILE_ROWS = 16;
 
 struct LinearCall {
   uint64_t x = 0;      // float activations [rows, in]

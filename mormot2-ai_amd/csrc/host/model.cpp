@@ -787,7 +787,6 @@ int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count, float* 
     if (want && all_logits) {
       if (m->logits_all_rows < n) {
         if (m->logits_all) (void)hipFree((void*)m->logits_all);
-  ihip_sampler_destroy(m->sampler);
         void* p = nullptr;
         IHIP_CHECK(hipMalloc(&p, (uint64_t)CHUNK * m->d.vocab * 4));
         m->logits_all = (uint64_t)p;

@@ -13,6 +13,10 @@ struct orc_model {
   ihip_layer_desc* layer;
   int64_t max_tokens, length;
   int kv_f16, threads, f32;
+  /* the smallest gap between the k-th and (k+1)-th router logit of any
+   * routed row since the last orc_model_route_gap (a near tie there could
+   * pick another expert on another arithmetic) */
+  double route_gap;
   float** keys;
   float** values;
 };
@@ -32,6 +36,7 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
   m->max_tokens = max_tokens;
   m->kv_f16 = kv_f16;
   m->threads = threads > 0 ? threads : 1;
+  m->route_gap = INFINITY;
   int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   m->keys = (float**)calloc(d->layers, sizeof(float*));
   m->values = (float**)calloc(d->layers, sizeof(float*));
@@ -44,6 +49,28 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
 }
 
 void orc_model_set_f32(orc_model* m, int f32) { m->f32 = f32; }
+
+double orc_model_route_gap(orc_model* m)
+{
+  double g = m->route_gap;
+  m->route_gap = INFINITY;
+  return g;
+}
+
+/* logit of the k-th pick minus the largest logit not picked */
+static double route_gap(const float* lg, int64_t e, const int32_t* chosen, int64_t k)
+{
+  double kth = INFINITY, next = -INFINITY;
+  for (int64_t j = 0; j < k; j++)
+    if (lg[chosen[j]] < kth) kth = lg[chosen[j]];
+  for (int64_t i = 0; i < e; i++) {
+    int taken = 0;
+    for (int64_t j = 0; j < k; j++)
+      if (chosen[j] == i) taken = 1;
+    if (!taken && lg[i] > next) next = lg[i];
+  }
+  return kth - next;
+}
 
 void orc_model_destroy(orc_model* m)
 {
@@ -147,8 +174,13 @@ int orc_model_forward(orc_model* m, const int32_t* ids, int64_t n, float* logits
     } else {
       int64_t fi = d->expert_ffn;
       err |= lin(m, hh, n, h, L->router, 0, E, (const float*)L->router_bias.data, route);
-      for (int64_t r = 0; r < n; r++)
+      for (int64_t r = 0; r < n; r++) {
         orc_route(route + r * E, E, K, d->norm_topk, chosen + r * K, cw + r * K);
+        if (K < E) {
+          double g = route_gap(route + r * E, E, chosen + r * K, K);
+          if (g < m->route_gap) m->route_gap = g;
+        }
+      }
       memset(tmp, 0, n * h * 4);
       uint64_t gb = row_bytes(L->exp_gate.dtype, h) * fi;
       uint64_t db = row_bytes(L->exp_down.dtype, fi) * h;

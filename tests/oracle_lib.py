@@ -56,6 +56,8 @@ def lib():
         L.orc_model_destroy.restype = None
         L.orc_model_set_f32.argtypes = [vp, C.c_int]
         L.orc_model_set_f32.restype = None
+        L.orc_model_route_gap.restype = C.c_double
+        L.orc_model_route_gap.argtypes = [vp]
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
         L.orc_model_greedy.argtypes = [vp, vp, i64, i64, vp, vp]
         L.orc_splitmix_next.restype = C.c_double
@@ -220,6 +222,11 @@ class Model:
         if rc:
             raise RuntimeError(rc)
         return lg if all_logits else lg[0]
+
+    def route_gap(self):
+        """The smallest k-th vs (k+1)-th router logit gap of the rows routed
+        since the last call (inf for a dense model)."""
+        return float(lib().orc_model_route_gap(self.h))
 
     def greedy(self, prompt, max_new):
         p = np.ascontiguousarray(prompt, np.int32)

@@ -163,11 +163,19 @@ GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100
 def gemm_ctx():
     # a context that sends every chunk of 16 rows or more to the GEMM (the
     # default sends chunks of 80 or more; smaller ones go to 8-row GEMVs)
+    # (the settings are read when a context is created; the caller's own
+    # values come back afterwards)
+    saved = {k: os.environ.get(k) for k in ("IHIP_GEMM_MIN_ROWS", "IHIP_GEMM")}
     os.environ["IHIP_GEMM_MIN_ROWS"] = "16"
+    os.environ["IHIP_GEMM"] = "1"
     try:
         c = H.Context(0)
     finally:
-        del os.environ["IHIP_GEMM_MIN_ROWS"]
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     yield c
     c.close()
 

@@ -1,0 +1,92 @@
+"""Tier 3 at the BASELINE shapes themselves: greedy decode on the device is
+token-identical to the CPU decoder (the oracle) for 64 tokens, with the
+full layer count, expert count, vocabulary and widths of each model config:
+
+- configs[3], Qwen3-30B-A3B Q4_K_M (48 layers, 128 experts top-8);
+- configs[4], gpt-oss-20b (MXFP4 experts, bf16 attention, windows, sinks,
+  YaRN);
+- configs[2], Qwen3-0.6B Q4_K_M after its own 512-token prompt;
+- configs[0], Qwen3-0.6B Q8_0 after a 96-token prompt.
+
+Every prompt here is at least 80 rows, so the prefill runs on the MFMA GEMM
+(the MoE prompts on its grouped-expert items), not on the 8-row GEMVs. The
+MoE prompts are 96 tokens rather than the configs' 1024/2048: the oracle's
+attention is a scalar loop, and 96 rows keep each case near a minute of CPU
+time (the reference's own 30B-A3B device test, tests/test.infer.cuda.pas:
+2100-2232, also decodes a short prompt at the real shape).
+
+Each step records the top-1/top-2 logit margin of the CPU logits and, for
+the MoE models, the smallest gap between the k-th and (k+1)-th router logit
+of any row routed in that step: a near tie in either would be reported, not
+hidden behind a pass."""
+import gc
+import os
+
+import numpy as np
+import pytest
+
+import infer_hip as H
+import oracle_lib as O
+from infer_hip import models
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(16, os.cpu_count() or 1)
+STEPS = 64
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = H.Context(0)
+    yield c
+    c.close()
+
+
+def cpu_greedy(cpu, prompt, steps, vocab):
+    """TDecoderModel.Greedy on the oracle, one Forward per step, so each
+    step's margin and router gap are seen."""
+    ids, margins, gaps = [], [], []
+    lg = cpu.forward(prompt)
+    gaps.append(cpu.route_gap())
+    for i in range(steps):
+        t = O.argmax(lg)
+        ids.append(t)
+        second = np.max(np.delete(lg, t))
+        margins.append(float(lg[t] - second))
+        if i + 1 < steps:
+            lg = cpu.forward([t])
+            gaps.append(cpu.route_gap())
+    return np.array(ids, np.int32), np.array(margins), np.array(gaps)
+
+
+FULL = [
+    ("qwen3-30b-a3b-q4_k_m", 96),
+    ("gpt-oss-20b-mxfp4", 96),
+    ("qwen3-0.6b-q4_k_m", 512),
+    ("qwen3-0.6b-q8_0", 96),
+]
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name,prompt_len", FULL)
+def test_full_shape_greedy_64(ctx, name, prompt_len):
+    print(f"\n[{name}] building the seeded weights", flush=True)
+    spec = models.Spec(models.CONFIGS[name], seed=1)
+    prompt = np.random.default_rng(2024).integers(0, spec.vocab, prompt_len).astype(np.int32)
+    max_tokens = prompt_len + STEPS + 16
+    print(f"[{name}] device: prompt {prompt_len}, greedy {STEPS}", flush=True)
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=True, max_tokens=max_tokens)
+    got = dev.greedy(prompt, STEPS)
+    dev.close()
+    print(f"[{name}] cpu oracle ({THREADS} threads)", flush=True)
+    cpu = O.Model(spec, max_tokens, kv_f16=True, threads=THREADS)
+    ref, margins, gaps = cpu_greedy(cpu, prompt, STEPS, spec.vocab)
+    cpu.close()
+    print(f"[{name}] min top-1/top-2 margin {margins.min():.3e} (step {int(margins.argmin())}); "
+          f"min router gap {gaps.min():.3e} (step {int(gaps.argmin())}); tokens {got[:8].tolist()}",
+          flush=True)
+    bad = np.nonzero(got != ref)[0]
+    del spec
+    gc.collect()
+    assert bad.size == 0, (f"first difference at step {bad[0]}", got[bad[0]], ref[bad[0]],
+                           margins[bad[0]], gaps[bad[0]])
