@@ -149,6 +149,19 @@ int ihip_gpu_linear(int dtype, int64_t in);
 int ihip_enqueue_linear_at(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
                            int dtype, uint64_t w, int64_t out, uint64_t y,
                            uint64_t bias, int mode);
+/* ihip_enqueue_linear_at without any allocation: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * Q8 quantized activations of a multi-row call go to a fixed device array of
+ * IHIP_STATIC_SCRATCH_BYTES per GPU instead of the context's growable
+ * scratch: rows * (in + in / 8) must fit (else IHIP_E_NOMEM, nothing
+ * enqueued). Every call on one GPU shares that array, so calls that overlap
+ * on one GPU (two contexts' streams) race; one context's stream orders its
+ * own calls. Same arguments and results as ihip_enqueue_linear_at. */
+#define IHIP_STATIC_SCRATCH_BYTES (8u << 20)
+int ihip_enqueue_linear_at_static(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
+                                  int dtype, uint64_t w, int64_t out, uint64_t y,
+                                  uint64_t bias, int mode);
 /* one token row through `slots` experts chosen on the device
  * (EnqueueLinearIds, backend.cuda.pas:386-412): slot s reads expert ids[s]
  * (int32 at a device address), its matrix at w + ids[s] * stride bytes

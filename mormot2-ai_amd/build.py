@@ -20,6 +20,8 @@ KERNELS = ([("ops", "ops", [])] +
            [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in LINEAR_FMTS] +
            [("gemm_" + f, "gemm", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in GEMM_FMTS])
 HOST = ["runtime", "backend", "model", "synth", "gguf"]
+# host sources compiled as HIP (a device array registered with the runtime)
+HOST_HIP = ["static_scratch"]
 HIP_FLAGS = ["--genco", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", CSRC]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
@@ -48,11 +50,20 @@ def _host(name):
     return out
 
 
+def _host_hip(name):
+    src = os.path.join(CSRC, "host", name + ".hip")
+    out = os.path.join(BUILD, name + ".o")
+    _run([HIPCC, "-c", "-fPIC", "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall",
+          "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", CSRC, src, "-o", out])
+    return out
+
+
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 8)) as ex:
         kfut = {k[0]: ex.submit(_kernel, k) for k in KERNELS}
-        hfut = [ex.submit(_host, h) for h in HOST]
+        hfut = [ex.submit(_host, h) for h in HOST] + [ex.submit(_host_hip, h) for h in HOST_HIP]
         cos = {k: f.result() for k, f in kfut.items()}
         objs = [f.result() for f in hfut]
     embed = os.path.join(BUILD, "embed.S")

@@ -260,7 +260,7 @@ int q8_kind(int t)
   return 0;
 }
 
-static bool linear_ok(int t, int64_t in)
+bool linear_ok(int t, int64_t in)
 {
   if (!fmt_name(t) || in <= 0 || in % 32) return false;
   if ((t == DT_Q4_K || t == DT_Q6_K) && in % 256) return false;

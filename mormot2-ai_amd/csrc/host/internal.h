@@ -74,6 +74,9 @@ struct ihip_ctx {
   uint64_t scratch_bad = 0;
   uint64_t scratch_argmax = 0;  // [ARGMAX_PARTS] block results of argmax_part
   uint64_t scratch_attn = 0, scratch_attn_bytes = 0;
+  // the device address of static_scratch.hip's array on this device
+  // (ihip_enqueue_linear_at_static), read once at ihip_create
+  uint64_t static_scratch = 0;
   bool capturing = false;
   hipGraph_t graphs[16] = {};
   hipGraphExec_t execs[16] = {};
@@ -145,6 +148,12 @@ struct LinearCall {
 // whether one launch can take matrices of types a then b (gemv_<a>_<b>_*)
 bool gemv_pair(ihip_ctx* c, int a, int b, int mode, int64_t in);
 int enqueue_linear(ihip_ctx* c, const LinearCall& call);
+// whether a weight type with `in` inputs has a Linear kernel
+bool linear_ok(int dtype, int64_t in);
+// bytes of one quantized activation row (Q8_0 or Q8_K) of `in` values
+uint64_t q8_row_bytes(int64_t in);
+// reads the device address of the static scratch array for the current device
+int static_scratch_init(ihip_ctx* c);
 // whether enqueue_linear runs a Q8 chunk of this weight type on the MFMA GEMM
 // (and takes grouped items of up to 64 slots)
 bool gemm_runs(const ihip_ctx* c, int dtype, int mode);

@@ -170,6 +170,10 @@ int ihip_create(int device, ihip_ctx** out)
     return fail(IHIP_E_NOMEM, "hipMalloc");
   }
   c->scratch_argmax = (uint64_t)am;
+  if (int rc = static_scratch_init(c)) {
+    ihip_destroy(c);
+    return rc;
+  }
   *out = c;
   return 0;
 }

@@ -31,7 +31,7 @@ class FormatError(HipError):
     """A damaged, hostile or unsupported file (IHIP_E_FORMAT, EInferError)."""
 
 
-IHIP_E_FORMAT = -7
+IHIP_E_ARG, IHIP_E_NOMEM, IHIP_E_FORMAT = -1, -6, -7
 
 
 class Sampling(C.Structure):
@@ -97,6 +97,8 @@ def lib():
             "ihip_clear_weights": (i32, [vp]),
             "ihip_gpu_linear": (i32, [i32, i64]),
             "ihip_enqueue_linear_at": (i32, [vp, u64, i64, i64, i32, u64, i64, u64, u64, i32]),
+            "ihip_enqueue_linear_at_static": (i32, [vp, u64, i64, i64, i32, u64, i64, u64, u64,
+                                                    i32]),
             "ihip_enqueue_linear_ids": (i32, [vp, u64, i64, i32, u64, i64, i64, u64, i64, i32,
                                               u64, u64, i32]),
             "ihip_linear": (i32, [vp, vp, i64, i64, vp, i32, i64, vp, vp, i32]),
