@@ -6,9 +6,10 @@ Q4_K_M weights (seeded synthetic bytes), a 1024-token prompt, then greedy
 decode. A step is one decode token (batch 1); `value` is decode tokens/s.
 
 Beside it, on the same process and device:
-- roofline: the dominant decode kernel (the Q4_K expert GEMV of the MoE
-  layers, 8 experts of 768x2048 per launch, expert matrices of all 48 layers
-  cycled so they come from HBM) timed with HIP events on the library's stream;
+- roofline: the decode step's dominant kernel (the MoE layers' gate+up+SwiGLU
+  GEMV of the 8 routed experts, Q4_K 768x2048 each, which also routes the
+  token), every launch of 32 decode steps timed by its own dispatch's start
+  and end events on the library's stream; the decode attention beside it;
 - gemv: the configs[1] sweep (Q8_0, Q4_0, Q4_K, Q6_K, MXFP4 over the five
   shapes, batch 1 and 8) in GB/s of algorithmic bytes, each timed group
   cycling > 512 MB of distinct weight copies (beyond the 256 MB MALL);
@@ -156,61 +157,76 @@ def copy_calibration(ctx, nbytes=256 << 20):
     return nbytes, 2 * nbytes / (ms * 1e-3) / 1e9
 
 
-def expert_gemv(ctx, spec, reps=4, graphs=True):
-    """The dominant decode kernel: the expert GEMV of the MoE layers (the gate
-    projection of 8 experts per launch: Q4_K 768x2048 each for configs[3]),
-    or for a dense model the FFN gate GEMV (3072x1024 for Qwen3-0.6B), one
-    launch per layer, the launches of all layers in one graph timed with
-    events (as the decode step replays them); without graphs (a profiled run)
-    launched directly."""
-    import ctypes
+def decode_kernels(ctx, model, spec, first, steps, past):
+    """The decode step's own kernels, timed live: `steps` decode steps with
+    direct launches (the graph's kernels, launched one by one), every launch
+    of the dominant kernel - the MoE layers' gate+up+SwiGLU expert GEMV that
+    also routes the token (or, for a dense model, the FFN gate+up+SwiGLU
+    GEMV) - timed by its own dispatch's start and end events on the
+    library's stream; then the same for the decode attention. Returns the
+    per-launch averages and the algorithmic bytes per launch."""
     import infer_hip as H
-    L = H.lib()
     c = spec.cfg
     moe = c.get("moe", False)
-    Hd = c["hidden"]
+    Hd, hd = c["hidden"], c["head_dim"]
+    L0 = spec.layers[0]
     if moe:
-        FI, E, K = c["expert_ffn"], c["experts"], c["experts_used"]
+        E, K, FI = c["experts"], c["experts_used"], c["expert_ffn"]
+        gt = L0.exp_gate.dtype
+        # both matrices of K experts, the residual row and its norm weights,
+        # the router logits, the K x FI outputs, the picks and their weights
+        wb = 2 * K * FI * H.row_bytes(gt, Hd)
+        nb = wb + 2 * Hd * 4 + E * 4 + K * FI * 4 + K * 8
+        if L0.exp_gate_bias.data:
+            nb += 2 * K * FI * 4
+        what = f"gate+up+SwiGLU of {K} routed experts ({FI}x{Hd}, {H.NAMES[gt]}), route in-launch"
     else:
-        FI, E, K = c["ffn"], 1, 1
-    devs = []
-    for li in range(c["layers"]):
-        t = spec.layers[li].exp_gate if moe else spec.layers[li].gate
-        d = ctypes.c_uint64()
-        H.check(L.ihip_weight(ctx.h, t.data, t.dtype, FI, Hd, E, ctypes.byref(d)))
-        devs.append((d.value, t.dtype))
-    dtype = devs[0][1]
-    rng = np.random.default_rng(3)
-    x = rng.standard_normal((1, Hd)).astype(np.float32)
-    dx = ctx.array(x)
-    kq = 1 if dtype in (H.Q4_K, H.Q6_K) else 0
-    dq = ctx.alloc(int(L.ihip_q8_bytes(Hd, kq)))
-    H.check(L.ihip_enqueue_quantize(ctx.h, dx.ptr, 1, Hd, kq, dq.ptr, 0))
-    ids = ctx.array(np.sort(rng.choice(E, K, replace=False)).astype(np.int32))
-    dy = ctx.alloc(K * FI * 4)
-    stride = FI * H.row_bytes(dtype, Hd)
-    ctx.sync()
-
-    def enq():
-        for w, _ in devs:
-            if moe:
-                H.check(L.ihip_enqueue_linear_ids(ctx.h, dq.ptr, Hd, dtype, w, stride, FI, ids.ptr,
-                                                  K, 0, dy.ptr, 0, H.MODE_Q8 | 2))
-            else:
-                H.check(L.ihip_enqueue_linear_at(ctx.h, dq.ptr, 1, Hd, dtype, w, FI, dy.ptr, 0,
-                                                 H.MODE_Q8 | 2))
-
-    ms = (time_graph(ctx, enq, reps) if graphs else time_direct(ctx, enq, reps)) / len(devs)
-    nb = K * FI * H.row_bytes(dtype, Hd) + (Hd + Hd // 8) + (K * 4 if moe else 0) + K * FI * 4
-    for b in (dx, dq, ids, dy):
-        b.free()
-    what = f"ids, {K} experts {FI}x{Hd}" if moe else f"FFN gate {FI}x{Hd}"
-    return {"kernel": f"gemv_{H.NAMES[dtype].lower()}_q8 ({what})",
-            "bytes_per_launch": nb, "avg_us": ms * 1e3, "GBps": nb / (ms * 1e-3) / 1e9}
+        FI, gt = c["ffn"], L0.gate.dtype
+        wb = 2 * FI * H.row_bytes(gt, Hd)
+        nb = wb + 2 * Hd * 4 + FI * 4
+        what = f"FFN gate+up+SwiGLU ({FI}x{Hd}, {H.NAMES[gt]})"
+    dom_name = f"gemv_{H.NAMES[gt].lower()}_q8_norm_glu"
+    kvw = c["kv_heads"] * hd
+    out = {}
+    model.use_graphs(False)
+    tok = first
+    for key, prefix in (("dominant", dom_name), ("attention", "attention_one")):
+        ctx.kernel_timer(prefix, capacity=steps * c["layers"] + 64)
+        ids = model.decode(tok, steps)
+        n, ms = ctx.kernel_timer_read()
+        ctx.kernel_timer(None)
+        # the cache length averaged over the timed steps (keys read per launch)
+        keys = past + 1 + (steps - 1) / 2.0
+        past += steps
+        tok = int(ids[-1])
+        out[key] = {"prefix": prefix, "launches": n, "avg_us": ms * 1e3 / max(n, 1)}
+        if key == "attention":
+            # the window layers read fewer keys; configs without windows read all
+            out[key]["keys_avg"] = keys
+    # every kernel of `steps` steps: the per-token breakdown
+    ctx.kernel_timer("*", capacity=steps * (8 * c["layers"] + 16))
+    ids = model.decode(tok, steps)
+    rep = ctx.kernel_timer_report()
+    ctx.kernel_timer(None)
+    past += steps
+    tok = int(ids[-1])
+    out["per_token"] = {k: {"launches": round(n / steps, 2), "avg_us": round(ms * 1e3 / n, 2),
+                            "us_per_token": round(ms * 1e3 / steps, 1)}
+                        for k, (n, ms) in sorted(rep.items(), key=lambda kv: -kv[1][1])}
+    model.use_graphs(True)
+    d = out["dominant"]
+    d.update({"kernel": dom_name, "what": what, "bytes_per_launch": nb, "weight_bytes": wb,
+              "GBps": nb / (d["avg_us"] * 1e-6) / 1e9})
+    a = out["attention"]
+    qw = c["heads"] * hd
+    abytes = int(a["keys_avg"] * kvw * 2 * 2 + qw * 4 * 2 + kvw * 4 * 2)
+    if not c.get("window"):
+        a.update({"bytes_per_launch": abytes, "GBps": abytes / (a["avg_us"] * 1e-6) / 1e9})
+    return out, tok, past
 
 
 PROFILED = {  # roofline kernel -> its committed counter profile
-    "gemv_q4_k_q8 (ids, 8 experts 768x2048)": "gemv_q4_k_ids_8x768x2048_traffic.txt",
+    "gemv_q4_k_q8_norm_glu": "gemv_q4_k_q8_norm_glu_route_8x768x2048_traffic.txt",
 }
 
 
@@ -299,7 +315,7 @@ def main():
     t = time.time()
     spec = models.Spec(models.CONFIGS[args.config], seed=1)
     log(f"synthetic {args.config} built in {time.time() - t:.1f}s")
-    max_tokens = args.prompt + args.warmup + args.steps + args.sample_steps + 16
+    max_tokens = args.prompt + args.warmup + args.steps + args.sample_steps + 4 + 96 + 16
     t = time.time()
     model = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=not args.kv_f32, max_tokens=max_tokens)
     log(f"uploaded in {time.time() - t:.1f}s")
@@ -343,9 +359,14 @@ def main():
         log(f"sampled decode {args.sample_steps} steps: {st * 1e3:.3f} ms/token, {1.0 / st:.1f} tok/s")
         model.sampling()
     wbytes = spec.weight_bytes_per_token()
-    # the model's own device copies (same host tensors)
-    dom = expert_gemv(ctx, spec, graphs=not args.no_graphs)
+    # the decode step's dominant kernel and its attention, timed live
+    past = args.prompt + args.warmup + args.steps + (4 + args.sample_steps if sampled else 0)
+    kt, _, _ = decode_kernels(ctx, model, spec, int(ids2[-1]), 32, past)
+    dom = kt["dominant"]
     log("dominant kernel", dom)
+    log("attention", kt["attention"])
+    for k, v in kt["per_token"].items():
+        log(f"  {k:40s} {v}")
     model.close()
 
     sweep = {}
@@ -403,9 +424,14 @@ def main():
         "sampled_decode": sampled,
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
-                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4), "traffic": profiled_traffic(dom["kernel"]),
-                     "kernel": dom["kernel"], "bytes_per_launch": dom["bytes_per_launch"],
-                     "avg_us": round(dom["avg_us"], 3)},
+                     "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4),
+                     "traffic": profiled_traffic(dom["kernel"]),
+                     "kernel": dom["kernel"] + "*", "what": dom["what"],
+                     "bytes_per_launch": dom["bytes_per_launch"], "avg_us": round(dom["avg_us"], 3),
+                     "launches_timed": dom["launches"]},
+        "attention": {k: (round(v, 3) if isinstance(v, float) else v)
+                      for k, v in kt["attention"].items()},
+        "decode_kernels": kt["per_token"],
         "stream_read_GBps": round(stream, 1),
         "copy_GBps": round(copy_gbps, 1),
         "gemv_head_151936x1024_b1_GBps": big,

@@ -112,6 +112,23 @@ int ihip_graph_launch(ihip_ctx* ctx, int slot);
  * events on that stream: ihip_event_record(ctx, i) marks point i (0..63) */
 int ihip_event_record(ihip_ctx* ctx, int index);
 int ihip_event_elapsed(ihip_ctx* ctx, int from, int to, float* ms);
+/* the kernel timer (measurement; no counterpart in the reference, whose
+ * benchmarks time whole passes): every later direct launch (not under
+ * capture) of a kernel whose name starts with `prefix` is timed by the
+ * start and end of its own dispatch, the durations a profiler reports;
+ * NULL or "" stops it; at most `capacity` launches between two reads.
+ * _read waits for the stream, returns the launches timed and their total
+ * milliseconds since the last read, and starts over. */
+int ihip_kernel_timer(ihip_ctx* ctx, const char* prefix, int64_t capacity);
+int ihip_kernel_timer_read(ihip_ctx* ctx, int64_t* launches, double* total_ms);
+/* the same, per kernel name (prefix "*" times every kernel): one line
+ * "name launches total_ms" per kernel, in first-launch order, into text */
+int ihip_kernel_timer_report(ihip_ctx* ctx, char* text, int64_t len);
+/* a timing build (IHIP_TRACE) records phase clocks (100 MHz) of instrumented
+ * kernels: launch k (k < count) of a kernel named prefix* into dev + k *
+ * stride ([blocks][8] uint64); dev 0 stops; ignored by other builds */
+int ihip_trace_buffer(ihip_ctx* ctx, uint64_t dev, uint64_t stride, int64_t count,
+                      const char* prefix);
 
 /* ======================================================================
  * TInferCudaBackend (src/infer/mormot.ai.infer.backend.cuda.pas:51-148)

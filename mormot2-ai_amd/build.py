@@ -10,6 +10,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmormot_ai_hip.so")
+# IHIP_TRACE=1: a timing build (IHIP_STAMP phase clocks in the kernels) into
+# its own library and build folder, loaded when IHIP_LIB names it
+TRACE = os.environ.get("IHIP_TRACE") == "1"
+if TRACE:
+    BUILD = os.path.join(HERE, "_build_trace")
+    LIB = os.path.join(HERE, "libmormot_ai_hip_trace.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 # linear.hip is built once per weight type (IHIP_ONLY_FMT), in parallel
@@ -37,6 +43,8 @@ def _run(cmd):
 
 def _kernel(spec):
     name, src, defs = spec
+    if TRACE:
+        defs = defs + ["-DIHIP_TRACE"]
     src = os.path.join(CSRC, "kernels", src + ".hip")
     out = os.path.join(BUILD, name + ".hsaco")
     _run([HIPCC] + HIP_FLAGS + defs + [src, "-o", out])

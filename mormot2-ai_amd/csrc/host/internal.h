@@ -82,6 +82,16 @@ struct ihip_ctx {
   hipGraphExec_t execs[16] = {};
   const void* slot_owner[16] = {};  // the model whose decode graph a slot holds
   hipEvent_t events[64] = {};
+  // the kernel timer (ihip_kernel_timer): launches whose name starts with
+  // timer_prefix carry a start and a stop event of their own dispatch
+  std::string timer_prefix;
+  std::vector<hipEvent_t> timer_events;  // pairs: start, stop
+  std::vector<std::string> timer_names;  // the kernel of each pair in use
+  size_t timer_used = 0;                 // pairs in use since the last read
+  // a timing build's stamp buffers (ihip_trace_buffer)
+  std::string trace_prefix;
+  std::vector<uint64_t> trace_ptrs, trace_globals;
+  size_t trace_used = 0;
   std::mutex lock;
 };
 

@@ -722,9 +722,9 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
                    m->items)))
     return bad(rc);
   if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
-  if ((rc = dalloc(m, 4096, m->done))) return bad(rc);
+  if ((rc = dalloc(m, 256 * 128, m->done))) return bad(rc);
   {
-    const hipError_t e = hipMemsetAsync((void*)m->done, 0, 4096, m->c->stream);
+    const hipError_t e = hipMemsetAsync((void*)m->done, 0, 256 * 128, m->c->stream);
     if (e != hipSuccess) return bad(hip_fail(e, "model: counters"));
   }
   if ((rc = dalloc(m, (uint64_t)d.heads * N * attention_splits(max_tokens) * (hd + 2) * 8,

@@ -7,6 +7,13 @@
 
 #include "internal.h"
 
+// hip_ext.h's launch with per-dispatch timing events (the header itself needs
+// the HIP compiler; the library is built by the host one)
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t gx, uint32_t gy, uint32_t gz,
+                                               uint32_t lx, uint32_t ly, uint32_t lz, size_t shmem,
+                                               hipStream_t stream, void** params, void** extra,
+                                               hipEvent_t start, hipEvent_t stop, uint32_t flags);
+
 // the code objects, linked in by embed.S (.incbin of the built .hsaco
 // files): ihip_co_count pairs of (begin, end)
 extern "C" const char* const ihip_co_table[];
@@ -68,9 +75,35 @@ int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, siz
   if (grid.x == 0 || grid.y == 0 || grid.z == 0)
     return fail(IHIP_E_ARG, std::string("empty grid for ") + name);
   void* params[] = {args};
-  hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
-                                       (unsigned)shmem, c->stream, params, nullptr);
+  hipError_t e;
+  // a timing build: this launch's stamps into its own buffer
+  const bool traced = !c->trace_prefix.empty() && !c->capturing &&
+                      c->trace_used + 1 < c->trace_ptrs.size() &&
+                      strncmp(name, c->trace_prefix.c_str(), c->trace_prefix.size()) == 0;
+  if (traced)
+    for (uint64_t g : c->trace_globals) {
+      e = hipMemcpyHtoDAsync((hipDeviceptr_t)g, &c->trace_ptrs[c->trace_used], 8, c->stream);
+      if (e != hipSuccess) return hip_fail(e, "trace");
+    }
+  if (!c->timer_prefix.empty() && !c->capturing && c->timer_used * 2 < c->timer_events.size() &&
+      (c->timer_prefix == "*" || strncmp(name, c->timer_prefix.c_str(), c->timer_prefix.size()) == 0)) {
+    // the dispatch's own start and end (the times a profiler reports)
+    c->timer_names[c->timer_used] = name;
+    hipEvent_t* ev = &c->timer_events[2 * c->timer_used++];
+    e = hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
+                                 block.y, block.z, shmem, c->stream, params, nullptr, ev[0], ev[1], 0);
+  } else {
+    e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, (unsigned)shmem,
+                              c->stream, params, nullptr);
+  }
   if (e != hipSuccess) return hip_fail(e, name);
+  if (traced) {
+    c->trace_used++;
+    for (uint64_t g : c->trace_globals) {
+      e = hipMemcpyHtoDAsync((hipDeviceptr_t)g, &c->trace_ptrs.back(), 8, c->stream);
+      if (e != hipSuccess) return hip_fail(e, "trace");
+    }
+  }
   return 0;
 }
 
@@ -194,6 +227,7 @@ void ihip_destroy(ihip_ctx* c)
     if (b) (void)hipFree((void*)b);
   for (auto ev : c->events)
     if (ev) (void)hipEventDestroy(ev);
+  for (auto ev : c->timer_events) (void)hipEventDestroy(ev);
   for (auto& m : c->modules)
     if (m.mod) (void)hipModuleUnload(m.mod);
   if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -329,6 +363,98 @@ int ihip_event_record(ihip_ctx* c, int i)
 {
   if (!c || i < 0 || i >= 64) return fail(IHIP_E_ARG, "ihip_event_record");
   IHIP_CHECK(hipEventRecord(c->events[i], c->stream));
+  return 0;
+}
+
+// the kernel timer: every later direct launch (not under capture) of a
+// kernel whose name starts with prefix is timed by its own dispatch's start
+// and end; NULL or "" stops it. At most `capacity` launches are timed
+// between two reads.
+int ihip_kernel_timer(ihip_ctx* c, const char* prefix, int64_t capacity)
+{
+  if (!c || capacity < 0 || capacity > 65536) return fail(IHIP_E_ARG, "ihip_kernel_timer");
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  c->timer_used = 0;
+  c->timer_prefix = prefix ? prefix : "";
+  while ((int64_t)c->timer_events.size() < 2 * capacity) {
+    hipEvent_t ev = nullptr;
+    IHIP_CHECK(hipEventCreate(&ev));
+    c->timer_events.push_back(ev);
+  }
+  c->timer_names.resize(c->timer_events.size() / 2);
+  return 0;
+}
+
+// a timing build's stamp buffers (IHIP_STAMP): launch k of a kernel named
+// prefix* records into dev + k * stride, for k < count (the module's
+// ihip_trace pointer is set before the launch and cleared after it); an
+// ordinary build has no ihip_trace and ignores the call
+int ihip_trace_buffer(ihip_ctx* c, uint64_t dev, uint64_t stride, int64_t count, const char* prefix)
+{
+  if (!c || count < 0) return fail(IHIP_E_ARG, "ihip_trace_buffer");
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  c->trace_ptrs.clear();
+  c->trace_globals.clear();
+  c->trace_prefix = (dev && prefix) ? prefix : "";
+  c->trace_used = 0;
+  if (c->trace_prefix.empty()) return 0;
+  for (auto& m : c->modules) {
+    hipDeviceptr_t p = nullptr;
+    size_t bytes = 0;
+    if (hipModuleGetGlobal(&p, &bytes, m.mod, "ihip_trace") != hipSuccess) {
+      (void)hipGetLastError();
+      continue;
+    }
+    c->trace_globals.push_back((uint64_t)p);
+  }
+  // the pointer values the copies read: k = 0..count-1, then the null
+  c->trace_ptrs.resize((size_t)count + 1);
+  for (int64_t k = 0; k < count; k++) c->trace_ptrs[k] = dev + (uint64_t)k * stride;
+  c->trace_ptrs[count] = 0;
+  return 0;
+}
+
+int ihip_kernel_timer_report(ihip_ctx* c, char* text, int64_t len)
+{
+  if (!c || !text || len < 1) return fail(IHIP_E_ARG, "ihip_kernel_timer_report");
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  std::vector<std::string> order;
+  std::unordered_map<std::string, std::pair<int64_t, double>> agg;
+  for (size_t i = 0; i < c->timer_used; i++) {
+    float ms = 0;
+    IHIP_CHECK(hipEventElapsedTime(&ms, c->timer_events[2 * i], c->timer_events[2 * i + 1]));
+    auto it = agg.find(c->timer_names[i]);
+    if (it == agg.end()) {
+      order.push_back(c->timer_names[i]);
+      it = agg.emplace(c->timer_names[i], std::make_pair((int64_t)0, 0.0)).first;
+    }
+    it->second.first++;
+    it->second.second += ms;
+  }
+  std::string out;
+  char line[160];
+  for (auto& n : order) {
+    snprintf(line, sizeof line, "%s %lld %.6f\n", n.c_str(), (long long)agg[n].first, agg[n].second);
+    out += line;
+  }
+  snprintf(text, (size_t)len, "%s", out.c_str());
+  c->timer_used = 0;
+  return 0;
+}
+
+int ihip_kernel_timer_read(ihip_ctx* c, int64_t* launches, double* total_ms)
+{
+  if (!c || !launches || !total_ms) return fail(IHIP_E_ARG, "ihip_kernel_timer_read");
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  double t = 0;
+  for (size_t i = 0; i < c->timer_used; i++) {
+    float ms = 0;
+    IHIP_CHECK(hipEventElapsedTime(&ms, c->timer_events[2 * i], c->timer_events[2 * i + 1]));
+    t += ms;
+  }
+  *launches = (int64_t)c->timer_used;
+  *total_ms = t;
+  c->timer_used = 0;
   return 0;
 }
 

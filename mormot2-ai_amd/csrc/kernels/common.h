@@ -12,11 +12,15 @@
 // ihip_trace), thread 0 of a block records the 100 MHz clock at phase i of
 // an instrumented kernel; compiled out otherwise
 #ifdef IHIP_TRACE
+// the stamp buffer of a timing build ([blocks][8] clocks), set by
+// ihip_trace_buffer through hipModuleGetGlobal
+__device__ uint64_t* ihip_trace;
 #define IHIP_STAMP(i)                                                                            \
   do {                                                                                           \
     if (threadIdx.x == 0)                                                                        \
-      ihip_trace[(((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8 + \
-                 (i)] = __builtin_amdgcn_s_memrealtime();                                        \
+      if (ihip_trace)                                                                            \
+        ihip_trace[(((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8 + \
+                   (i)] = __builtin_amdgcn_s_memrealtime();                                      \
   } while (0)
 #else
 #define IHIP_STAMP(i) \
@@ -143,16 +147,30 @@ __device__ __forceinline__ double load_agent(const double* p)
 __device__ __forceinline__ void wait_stores() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // the launch's last block to arrive (all of the block's stores complete
-// first); every thread calls it, every thread gets the answer
-__device__ __forceinline__ bool last_block(int* counter, int blocks)
+// first); every thread calls it, every thread gets the answer. XCD: the
+// blocks that count on this counter all run on one XCD (their launch-order
+// ids are equal modulo 8, and workgroups are dispatched to the 8 XCDs in
+// turn), so the XCD's L2 is their point of coherence: their plain stores and
+// an atomic executed in that L2 suffice, with no round trip to memory;
+// otherwise the stores and the count are agent-scope (memory).
+__device__ __forceinline__ bool last_block(int* counter, int blocks, bool xcd = false)
 {
   __shared__ int last;
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == blocks - 1;
+    last = (xcd ? __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                : __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) ==
+           blocks - 1;
   __syncthreads();
   return last;
+}
+// a load of another block's store on the same XCD (through the L2, after
+// last_block with xcd)
+__device__ __forceinline__ double load_xcd(const double* p)
+{
+  return __builtin_bit_cast(double, __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
 }
 
 // ------------------------------------------------ wave reductions in VGPRs

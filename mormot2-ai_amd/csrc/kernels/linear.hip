@@ -783,6 +783,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
                               quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
                               a.nw, st);
+    IHIP_STAMP(6);
     if (GLU && NORM && a.ids && a.rl) {
       // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
       // of this block's slot; the launch's extra row writes the picks and
@@ -792,6 +793,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       if (a.rexp <= 64) route_wave<1, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
       else if (a.rexp <= 128) route_wave<2, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
       else route_wave<4, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      IHIP_STAMP(7);
       int e = -1;
 #pragma unroll
       for (int s = 0; s < 8; s++) e = s == (int)yrow0 ? sid[s] : e;

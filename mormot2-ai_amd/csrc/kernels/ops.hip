@@ -768,10 +768,11 @@ extern "C" __global__ __launch_bounds__(256) void attention_part_f32(AttnArgs a)
 // <= 256).
 template <bool AG = false>
 __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d, const float* sink,
-                                             float* y)
+                                             float* y, bool xcd = false)
 {
-  // AG: the ranges were written by other blocks of this launch
-  auto rd = [&](int i) { return AG ? load_agent(b + i) : b[i]; };
+  // AG: the ranges were written by other blocks of this launch (xcd: blocks
+  // of this XCD, through its L2; else agent-scope)
+  auto rd = [&](int i) { return AG ? (xcd ? load_xcd(b + i) : load_agent(b + i)) : b[i]; };
   // the range weights exp(m_s - M) and the range sums in LDS; the sums in
   // range order. Every load of the first MU ranges (a thread's dimension of
   // each, the maxima and sums) is issued before the first arithmetic: one
@@ -855,7 +856,8 @@ struct AttnOneArgs {
   double* part;      // [heads, splits, hd + 2]
   double scale, eps;
   int32_t heads, kvh, hd, past, window, splits;
-  // [heads] counters, zero between launches, or null: with them the last
+  // [heads] counters 128 bytes apart (h * 32: one L2 line each), zero between
+  // launches, or null: with them the last
   // range block of a head to finish merges the head's ranges (and sets its
   // counter back to zero), else attention_merge does
   int* done;
@@ -1127,25 +1129,31 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   }
   __syncthreads();
   IHIP_STAMP(4);
-  // agent-scope stores: the head's last range block may read them
+  // the head's last range block may read these: with a multiple of 8 heads
+  // every range block of head h runs on one XCD (launch-order ids h' + heads
+  // * s, xcd_head), so plain stores meet in that XCD's L2; else agent-scope
+  const bool xcd = (a.heads & 7) == 0;
+  auto put = [&](double* p, double v) {
+    if (xcd) *p = v;
+    else store_agent(p, v);
+  };
   if (n > 0) {
-    for (int i = t; i < d; i += 256)
-      store_agent(out + i, (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]));
+    for (int i = t; i < d; i += 256) put(out + i, (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]));
     if (t == 0) {
-      store_agent(out + d, m);
-      store_agent(out + d + 1, (red[4] + red[5]) + (red[6] + red[7]));
+      put(out + d, m);
+      put(out + d + 1, (red[4] + red[5]) + (red[6] + red[7]));
     }
   } else if (t == 0) {  // an empty range: weight 0 in the merge
-    store_agent(out + d, -1.0e308);
-    store_agent(out + d + 1, 0.0);
+    put(out + d, -1.0e308);
+    put(out + d + 1, 0.0);
   }
   // the head's last range block to finish merges the head's ranges
-  if (a.done && last_block(a.done + h, a.splits)) {
+  if (a.done && last_block(a.done + h * 32, a.splits, xcd)) {
     IHIP_STAMP(5);
     merge_ranges<true>(a.part + (int64_t)h * a.splits * (d + 2), a.splits, d,
-                       a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d);
+                       a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d, xcd);
     IHIP_STAMP(6);
-    if (t == 0) a.done[h] = 0;
+    if (t == 0) a.done[h * 32] = 0;
   }
 }
 

@@ -11,7 +11,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(HERE), "libmormot_ai_hip.so")
+LIB_PATH = os.environ.get("IHIP_LIB") or os.path.join(os.path.dirname(HERE), "libmormot_ai_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "mormot_ai_hip.h")
 
 # TInferDType ordinals
@@ -89,6 +89,10 @@ def lib():
             "ihip_graph_launch": (i32, [vp, i32]),
             "ihip_event_record": (i32, [vp, i32]),
             "ihip_event_elapsed": (i32, [vp, i32, i32, C.POINTER(C.c_float)]),
+            "ihip_kernel_timer": (i32, [vp, C.c_char_p, i64]),
+            "ihip_kernel_timer_read": (i32, [vp, C.POINTER(i64), C.POINTER(C.c_double)]),
+            "ihip_kernel_timer_report": (i32, [vp, C.c_char_p, i64]),
+            "ihip_trace_buffer": (i32, [vp, u64, u64, i64, C.c_char_p]),
             "ihip_type_bytes": (u64, [i32, u64]),
             "ihip_weight": (i32, [vp, vp, i32, i64, i64, i64, C.POINTER(u64)]),
             "ihip_repack": (i32, [vp, vp, i32, i64, i64, i64, i32]),
@@ -258,6 +262,28 @@ class Context:
 
     def alloc(self, nbytes):
         return Buffer(self, nbytes)
+
+    def kernel_timer(self, prefix, capacity=4096):
+        """Time every later direct launch of kernels named prefix* by their
+        own dispatch (None: stop)."""
+        check(lib().ihip_kernel_timer(self.h, prefix.encode() if prefix else None, capacity),
+              "kernel_timer")
+
+    def kernel_timer_read(self):
+        """(launches, total ms) since the last read."""
+        n, ms = C.c_int64(), C.c_double()
+        check(lib().ihip_kernel_timer_read(self.h, C.byref(n), C.byref(ms)), "kernel_timer_read")
+        return n.value, ms.value
+
+    def kernel_timer_report(self):
+        """{kernel: (launches, total ms)} since the last read."""
+        buf = C.create_string_buffer(1 << 16)
+        check(lib().ihip_kernel_timer_report(self.h, buf, len(buf)), "kernel_timer_report")
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, n, ms = line.split()
+            out[name] = (int(n), float(ms))
+        return out
 
     def array(self, a):
         a = np.ascontiguousarray(a)
