@@ -334,7 +334,9 @@ typedef struct {
 
 /* the model on the device: every weight uploaded (UploadWeights,
  * model.qwen3.cuda.pas:602-828); mode: the Linear arithmetic; kv_f16: a
- * half-float KV cache (TQwen3Cuda.KvF16); the host tensors must outlive it */
+ * half-float KV cache (TQwen3Cuda.KvF16); max_tokens: the capacity of the
+ * model's own context's cache up front (it grows beyond, up to
+ * max_positions); the host tensors must outlive it */
 int ihip_model_create(ihip_ctx* ctx, const ihip_model_desc* desc, int mode,
                       int kv_f16, int64_t max_tokens, ihip_model** out);
 void ihip_model_destroy(ihip_model* m);
@@ -370,6 +372,46 @@ int ihip_model_sampling(ihip_model* m, const ihip_sampling* s);
 int ihip_model_use_graphs(ihip_model* m, int on);
 /* timings of the last greedy call: prefill and decode milliseconds */
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
+
+/* ---- contexts of a model (TDecoderDevice, decoder.pas:907-928) ----
+ * A context is one sequence on the device: its KV cache (grown as tokens
+ * come: doubled, at least a quarter beyond them, up to max_positions -
+ * Prepare, model.qwen3.cuda.pas:856-940), the id of each cached position, the
+ * activations of a chunk and its own decode graph; the weights are the
+ * model's, shared by all of its contexts. The ihip_model_* calls above use
+ * the model's own context (ihip_model_context). One context at a time per
+ * device (the calls take the device's lock). */
+typedef struct ihip_mctx ihip_mctx;
+/* a new, empty context (NewDeviceContext, model.qwen3.cuda.pas:229-231) */
+int ihip_model_new_context(ihip_model* m, ihip_mctx** out);
+/* free a context made by ihip_model_new_context (the model's own goes with it) */
+void ihip_context_destroy(ihip_mctx* s);
+/* the model's own context */
+ihip_mctx* ihip_model_context(ihip_model* m);
+/* Forward (model.qwen3.cuda.pas:1722-1730): count ids after the cached
+ * tokens; logits [vocab] of the last one, or [count, vocab] with all_logits,
+ * or NULL */
+int ihip_context_forward(ihip_mctx* s, const int32_t* ids, int64_t count, float* logits,
+                         int all_logits);
+/* ForwardEmbeds (model.qwen3.cuda.pas:237-245, :1732-1739): count rows of
+ * [hidden] floats in place of token embeddings; normed (or NULL) receives the
+ * last row after the final norm [hidden]; head: the head of the logits (0,
+ * the one head of these models; another is refused) */
+int ihip_context_forward_embeds(ihip_mctx* s, const float* embeds, int64_t count, float* logits,
+                                int all_logits, float* normed, int head);
+/* Reuse (model.qwen3.cuda.pas:1741-1752): keep the cached tokens that start
+ * ids, at most count - 1 of them (a position fed an embedding row matches no
+ * id), drop the rest; *kept = the tokens kept */
+int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t* kept);
+/* TDecoderContext.Truncate (decoder.pas:996-1016): keep the first length
+ * tokens (the device keeps every row, so any length is restorable) */
+int ihip_context_truncate(ihip_mctx* s, int64_t length);
+/* cached tokens and the cache's capacity (either pointer may be NULL) */
+int ihip_context_length(ihip_mctx* s, int64_t* length, int64_t* capacity);
+/* ihip_model_greedy and ihip_model_decode on a context */
+int ihip_context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                        int32_t* out_ids);
+int ihip_context_decode(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out_ids);
 
 /* ======================================================================
  * GGUF v3 files (TGgufFile, src/infer/mormot.ai.infer.loader.gguf.pas:94-170)

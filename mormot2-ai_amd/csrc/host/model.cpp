@@ -28,11 +28,42 @@ struct DevLayer {
   uint64_t eg = 0, eu = 0, ed = 0, egb = 0, eub = 0, edb = 0;
   int qd = 0, kd = 0, vd = 0, od = 0, gd = 0, ud = 0, dd = 0, rd = 0, egd = 0, eud = 0, edd = 0;
   int64_t eg_stride = 0, ed_stride = 0;
-  uint64_t kc = 0, vc = 0;
   int window = 0, moe = 0;
 };
 
 }  // namespace ihip
+
+// a context of a model on the device (TQwen3CuContext,
+// model.qwen3.cuda.pas:150-198): its KV cache, which grows as tokens come
+// (Prepare, :856-940), the activations of one chunk, the id of every cached
+// position and its own decode graph
+struct ihip_mctx {
+  ihip_model* m = nullptr;
+  int64_t capacity = 0, length = 0;
+  std::vector<int32_t> ids;         // the token of each cached position, -1: an embedding row
+  std::vector<uint64_t> kc, vc;     // per layer [capacity, kvw] (f16 or f32)
+  // activations for CHUNK rows
+  uint64_t x = 0, h = 0, tmp = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0;
+  uint64_t route = 0, ids_dev = 0, rw = 0, eout = 0, cs = 0, tok = 0, logits = 0, next = 0, pos = 0;
+  uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
+  uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
+  uint64_t attn_part = 0, attn_part_bytes = 0;  // flash-decoding partials
+  // zeroed counters of the decode attention's heads (the last range block of
+  // a head merges the head)
+  uint64_t done = 0;
+  uint64_t logits_all = 0;
+  int64_t logits_all_rows = 0;
+  std::vector<uint64_t> owned;
+  // the decode step's graph (one per context: it holds this context's
+  // buffers), captured for a capacity and a sampler
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_ready = false;
+  int64_t graph_capacity = 0;
+  int graph_sampler = -1;
+  double prefill_ms = 0, decode_ms = 0;
+  bool is_default = false;  // the model's own context (ihip_model_*), freed with it
+};
 
 struct ihip_model {
   ihip_ctx* c = nullptr;
@@ -40,31 +71,20 @@ struct ihip_model {
   std::vector<ihip_layer_desc> layer_desc;
   std::vector<ihip::DevLayer> L;
   int mode = IHIP_MODE_Q8, kv_f16 = 0;
-  int64_t max_tokens = 0, length = 0;
   uint64_t embed = 0, final_norm = 0, head = 0;
   int embed_dt = 0, head_dt = 0;
-  // activations for CHUNK rows
-  uint64_t x = 0, h = 0, tmp = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0;
-  uint64_t route = 0, ids = 0, rw = 0, eout = 0, cs = 0, tok = 0, logits = 0, next = 0, pos = 0;
-  uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
-  uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
-  uint64_t attn_part = 0;               // flash-decoding partials
-  // zeroed counters of the decode attention's heads (the last range block of
-  // a head merges the head)
-  uint64_t done = 0;
-  uint64_t logits_all = 0;
-  int64_t logits_all_rows = 0;
-  std::vector<uint64_t> owned;
+  bool any_moe = false;
   // the host ranges of the uploaded weights: forgotten when the model goes,
   // as a model does in its destructor (backend.pas:151-158) - new host
   // tensors at a reused address must not meet the stale device copy
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
-  bool graph_ready = false;
   ihip_sampler* sampler = nullptr;  // null: the argmax
+  int sampler_epoch = 0;            // bumped by ihip_model_sampling (graphs captured again)
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
   int64_t chunk_rows = ihip::CHUNK;  // prompt rows per chunk (ihip_model_chunk), at most CHUNK
   int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
-  double prefill_ms = 0, decode_ms = 0;
+  ihip_mctx* def = nullptr;  // the context of the ihip_model_* calls
+  std::vector<ihip_mctx*> contexts;  // every live context (freed with the model)
 };
 
 namespace ihip {
@@ -136,15 +156,6 @@ static void rotary(const ihip_model_desc& d, int64_t first, int64_t rows, float*
     }
 }
 
-static int dalloc(ihip_model* m, uint64_t bytes, uint64_t& p)
-{
-  void* q = nullptr;
-  IHIP_CHECK(hipMalloc(&q, bytes ? (bytes + 255) & ~(uint64_t)255 : 256));
-  m->owned.push_back((uint64_t)q);
-  p = (uint64_t)q;
-  return 0;
-}
-
 static int upw(ihip_model* m, const ihip_tensor& t, int64_t out, int64_t in, int64_t count,
                uint64_t& dev, int& dt)
 {
@@ -170,9 +181,10 @@ struct QCache {
   bool have0 = false, havek = false;
 };
 
-static int lin(ihip_model* m, uint64_t x, QCache* qc, int64_t rows, int64_t in, int dt,
+static int lin(ihip_mctx* s, uint64_t x, QCache* qc, int64_t rows, int64_t in, int dt,
                uint64_t w, int64_t out, uint64_t bias, uint64_t y)
 {
+  ihip_model* m = s->m;
   LinearCall k;
   k.x = x; k.rows = rows; k.in = in; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
   k.y = y; k.mode = m->mode;
@@ -190,10 +202,11 @@ static int lin(ihip_model* m, uint64_t x, QCache* qc, int64_t rows, int64_t in, 
   return enqueue_linear(m->c, k);
 }
 
-static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int64_t in, int dt,
+static int lin_ids(ihip_mctx* s, uint64_t x, uint64_t xqbuf, int64_t xrows, int64_t in, int dt,
                    uint64_t w, int64_t stride, int64_t out, uint64_t ids, int64_t slots,
                    int x_div, uint64_t bias, uint64_t y, bool quantized)
 {
+  ihip_model* m = s->m;
   LinearCall k;
   k.x = x; k.rows = slots; k.in = in; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
   k.y = y; k.mode = m->mode; k.ids = ids; k.stride = stride; k.x_per_slot = x_div;
@@ -203,8 +216,8 @@ static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int
     // item_rows rows per work item (8 for the 8-row GEMV, 64 for the GEMM),
     // so an expert's matrix is read once per that many of its tokens
     k.ids = 0;
-    k.items = m->items;
-    k.perm = m->perm;
+    k.items = s->items;
+    k.perm = s->perm;
     k.item_rows = m->item_rows;
     k.nitems = (slots + m->item_rows - 1) / m->item_rows + m->d.experts;
   }
@@ -218,9 +231,11 @@ static int lin_ids(ihip_model* m, uint64_t x, uint64_t xqbuf, int64_t xrows, int
   return enqueue_linear(m->c, k);
 }
 
-static int rope_attn(ihip_model* m, const DevLayer& L, int64_t n, int64_t past, bool graph)
+static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
 {
+  ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
+  const DevLayer& L = m->L[l];
   struct {
     float* q;
     const float* k;
@@ -233,17 +248,17 @@ static int rope_attn(ihip_model* m, const DevLayer& L, int64_t n, int64_t past, 
     const int* pastp;
     double eps;
     int32_t rows, heads, kvh, hd, past, f16;
-  } ra = {(float*)m->q, (const float*)m->k, (const float*)m->v, (const float*)L.qn,
-          (const float*)L.kn, (const float*)m->cs, (void*)L.kc, (void*)L.vc,
-          graph ? (const int*)m->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads,
+  } ra = {(float*)s->q, (const float*)s->k, (const float*)s->v, (const float*)L.qn,
+          (const float*)L.kn, (const float*)s->cs, (void*)s->kc[l], (void*)s->vc[l],
+          graph ? (const int*)s->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads,
           d.kv_heads, d.head_dim, (int32_t)past, m->kv_f16};
   int rc = launch(m->c, "qkrope", dim3((unsigned)(d.heads + d.kv_heads), (unsigned)n), dim3(64), &ra);
   if (rc) return rc;
-  int64_t maxkeys = graph ? m->max_tokens : past + n;
+  int64_t maxkeys = graph ? s->capacity : past + n;
   if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
   // a graph replays one grid for every position: splits for the longest
-  return enqueue_attention(m->c, m->q, L.kc, L.vc, m->attn, m->attn_part, n, d.heads, d.kv_heads,
-                           d.head_dim, past, graph ? m->pos : 0, L.window, L.sinks,
+  return enqueue_attention(m->c, s->q, s->kc[l], s->vc[l], s->attn, s->attn_part, n, d.heads, d.kv_heads,
+                           d.head_dim, past, graph ? s->pos : 0, L.window, L.sinks,
                            1.0 / std::sqrt((double)d.head_dim), m->kv_f16,
                            attention_splits(maxkeys));
 }
@@ -267,15 +282,16 @@ static bool one_row_fused(const ihip_model* m)
 // combine), so the row costs no norm or add launches. The arithmetic is that
 // of layers() step for step. Leaves x = the residual (the final norm is the
 // head's).
-static int layers_one(ihip_model* m, int64_t past, bool graph)
+static int layers_one(ihip_mctx* s, int64_t past, bool graph)
 {
+  ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
   const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
                 kvw = (int64_t)d.kv_heads * hd;
   int rc = 0;
   auto normed = [&](uint64_t nw, int dt, uint64_t w, int64_t out, uint64_t bias, uint64_t y) {
     LinearCall k;
-    k.x = m->x; k.rows = 1; k.in = H; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
+    k.x = s->x; k.rows = 1; k.in = H; k.dtype = dt; k.w = w; k.out = out; k.bias = bias;
     k.y = y; k.mode = m->mode; k.nw = nw; k.eps = d.rms_eps;
     return enqueue_linear(m->c, k);
   };
@@ -286,7 +302,7 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
       // q, k and v: the matrices of one weight type in one launch
       const int dts[3] = {L.qd, L.kd, L.vd};
       const uint64_t ws[3] = {L.q, L.k, L.v}, bs[3] = {L.qb, L.kb, L.vb},
-                     ys[3] = {m->q, m->k, m->v};
+                     ys[3] = {s->q, s->k, s->v};
       const int64_t os[3] = {qw, kvw, kvw};
       bool done[3] = {false, false, false};
       // two types with a kernel for the pair (Q4_K_M: q, k Q4_K and v Q6_K)
@@ -295,7 +311,7 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
         if (dts[j] != dts[0]) t2 = t2 ? (dts[j] == t2 ? t2 : -1) : dts[j];
       if (t2 > 0 && gemv_pair(m->c, dts[0], t2, m->mode, H)) {
         LinearCall k;
-        k.x = m->x; k.rows = 1; k.in = H; k.dtype = dts[0]; k.dtype2 = t2; k.mode = m->mode;
+        k.x = s->x; k.rows = 1; k.in = H; k.dtype = dts[0]; k.dtype2 = t2; k.mode = m->mode;
         k.nw = L.input_norm; k.eps = d.rms_eps;
         for (int pass = 0; pass < 2; pass++)
           for (int j = 0; j < 3; j++)
@@ -311,7 +327,7 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
       for (int i = 0; i < 3 && !rc; i++) {
         if (done[i]) continue;
         LinearCall k;
-        k.x = m->x; k.rows = 1; k.in = H; k.dtype = dts[i]; k.mode = m->mode;
+        k.x = s->x; k.rows = 1; k.in = H; k.dtype = dts[i]; k.mode = m->mode;
         k.nw = L.input_norm; k.eps = d.rms_eps;
         for (int j = i; j < 3; j++)
           if (!done[j] && dts[j] == dts[i]) {
@@ -331,23 +347,23 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
     if (hd == 64 || hd == 128) {
       // head norms, RoPE, cache store and the ranges in one launch, then the merge
       AttnOne o;
-      o.q = m->q; o.k = m->k; o.v = m->v; o.qn = L.qn; o.kn = L.kn; o.cs = m->cs;
-      o.kc = L.kc; o.vc = L.vc; o.y = m->attn; o.sinks = L.sinks; o.pastp = graph ? m->pos : 0;
-      o.part = m->attn_part; o.scale = 1.0 / std::sqrt((double)hd);
+      o.q = s->q; o.k = s->k; o.v = s->v; o.qn = L.qn; o.kn = L.kn; o.cs = s->cs;
+      o.kc = s->kc[l]; o.vc = s->vc[l]; o.y = s->attn; o.sinks = L.sinks; o.pastp = graph ? s->pos : 0;
+      o.part = s->attn_part; o.scale = 1.0 / std::sqrt((double)hd);
       o.eps = d.rms_eps; o.heads = d.heads; o.kvh = d.kv_heads; o.hd = hd; o.past = past;
       o.window = L.window; o.f16 = m->kv_f16;
-      if (d.heads <= 256) o.done = m->done;  // the merge in the last range block of a head
-      int64_t maxkeys = graph ? m->max_tokens : past + 1;
+      if (d.heads <= 256) o.done = s->done;  // the merge in the last range block of a head
+      int64_t maxkeys = graph ? s->capacity : past + 1;
       if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
       o.splits = attention_splits(maxkeys);
       if ((rc = enqueue_attention_one(m->c, o))) return rc;
-    } else if ((rc = rope_attn(m, L, 1, past, graph))) {
+    } else if ((rc = rope_attn(s, l, 1, past, graph))) {
       return rc;
     }
     {
       LinearCall k;
-      k.x = m->attn; k.rows = 1; k.in = qw; k.dtype = L.od; k.w = L.o; k.out = H; k.bias = L.ob;
-      k.y = m->x; k.res = m->x; k.mode = m->mode;
+      k.x = s->attn; k.rows = 1; k.in = qw; k.dtype = L.od; k.w = L.o; k.out = H; k.bias = L.ob;
+      k.y = s->x; k.res = s->x; k.mode = m->mode;
       if ((rc = enqueue_linear(m->c, k))) return rc;
     }
     if (!L.moe) {
@@ -355,19 +371,19 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
       const int64_t F = d.ffn;
       if (L.gd != L.ud) return fail(IHIP_E_ARG, "model: gate and up of one type");
       LinearCall k;
-      k.x = m->x; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
-      k.y = m->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
+      k.x = s->x; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
+      k.y = s->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
       k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
       if ((rc = enqueue_linear(m->c, k))) return rc;
       LinearCall dn;
-      dn.x = m->gate; dn.rows = 1; dn.in = F; dn.dtype = L.dd; dn.w = L.down; dn.out = H;
-      dn.y = m->x; dn.res = m->x; dn.mode = m->mode;
+      dn.x = s->gate; dn.rows = 1; dn.in = F; dn.dtype = L.dd; dn.w = L.down; dn.out = H;
+      dn.y = s->x; dn.res = s->x; dn.mode = m->mode;
       if ((rc = enqueue_linear(m->c, dn))) return rc;
       continue;
     }
     // MoeBlock (decoder.pas:3037-3053), the experts chosen on the device
     const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
-    if ((rc = normed(L.post_norm, L.rd, L.router, E, L.router_b, m->route))) return rc;
+    if ((rc = normed(L.post_norm, L.rd, L.router, E, L.router_b, s->route))) return rc;
     // the route (TDecoderModel.Route) inside the gate/up launch: each block
     // ranks the logits for its slot's expert, one writes the picks and
     // weights for the down launch (up to 256 experts); else its own launch
@@ -378,22 +394,22 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
         int* ids;
         float* w;
         int32_t experts, k, norm, rows;
-      } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
+      } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, 1};
       if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
     }
     LinearCall k;
-    k.x = m->x; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
-    k.y = m->gate; k.mode = m->mode; k.ids = m->ids; k.stride = L.eg_stride; k.x_per_slot = 0;
+    k.x = s->x; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
+    k.y = s->gate; k.mode = m->mode; k.ids = s->ids_dev; k.stride = L.eg_stride; k.x_per_slot = 0;
     k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
     k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
     if (self_route) {
-      k.rl = m->route; k.rw = m->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
+      k.rl = s->route; k.rw = s->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
     }
     if ((rc = enqueue_linear(m->c, k))) return rc;
     LinearCall dn;
-    dn.x = m->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
-    dn.y = m->x; dn.res = m->x; dn.cw = m->rw; dn.mode = m->mode; dn.ids = m->ids;
+    dn.x = s->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
+    dn.y = s->x; dn.res = s->x; dn.cw = s->rw; dn.mode = m->mode; dn.ids = s->ids_dev;
     dn.stride = L.ed_stride; dn.x_per_slot = 1; dn.nexp = (int)E; dn.bias = L.edb;
     if ((rc = enqueue_linear(m->c, dn))) return rc;
   }
@@ -402,33 +418,34 @@ static int layers_one(ihip_model* m, int64_t past, bool graph)
 
 // the layers of one chunk of n rows at positions past.., x holding the
 // embeddings; leaves h = the final norm of x. graph: the position is read
-// from m->pos (decode step under capture)
-static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
+// from s->pos (decode step under capture)
+static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
 {
+  ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
   const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
                 kvw = (int64_t)d.kv_heads * hd;
   // one row (decode): every GEMV quantizes its activation row in registers;
   // a chunk: the rows are quantized once per activation buffer
   const bool one = n == 1;
-  if (one && one_row_fused(m)) return layers_one(m, past, graph);
-  int rc = ihip_enqueue_rmsnorm(m->c, m->x, m->L[0].input_norm, m->h, n, H, d.rms_eps);
+  if (one && one_row_fused(m)) return layers_one(s, past, graph);
+  int rc = ihip_enqueue_rmsnorm(m->c, s->x, m->L[0].input_norm, s->h, n, H, d.rms_eps);
   if (rc) return rc;
   for (int l = 0; l < d.layers; l++) {
     const DevLayer& L = m->L[l];
-    QCache qh{m->xq0, m->xqk};
+    QCache qh{s->xq0, s->xqk};
     QCache* qhp = one ? nullptr : &qh;
     // attention block (decoder.pas:2625-2702)
-    if ((rc = lin(m, m->h, qhp, n, H, L.qd, L.q, qw, L.qb, m->q))) return rc;
-    if ((rc = lin(m, m->h, qhp, n, H, L.kd, L.k, kvw, L.kb, m->k))) return rc;
-    if ((rc = lin(m, m->h, qhp, n, H, L.vd, L.v, kvw, L.vb, m->v))) return rc;
-    if ((rc = rope_attn(m, L, n, past, graph))) return rc;
-    QCache qa{m->xq0, m->xqk};
-    if ((rc = lin(m, m->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, m->tmp))) return rc;
+    if ((rc = lin(s, s->h, qhp, n, H, L.qd, L.q, qw, L.qb, s->q))) return rc;
+    if ((rc = lin(s, s->h, qhp, n, H, L.kd, L.k, kvw, L.kb, s->k))) return rc;
+    if ((rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
+    if ((rc = rope_attn(s, l, n, past, graph))) return rc;
+    QCache qa{s->xq0, s->xqk};
+    if ((rc = lin(s, s->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, s->tmp))) return rc;
     // residual, then the pre-FFN norm
-    if ((rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, L.post_norm, m->h, n, H, d.rms_eps)))
+    if ((rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, L.post_norm, s->h, n, H, d.rms_eps)))
       return rc;
-    QCache qf{m->xq0, m->xqk};
+    QCache qf{s->xq0, s->xqk};
     QCache* qfp = one ? nullptr : &qf;
     bool moe_out = false;  // the FFN output is the expert rows (added by the next norm)
     if (!L.moe) {
@@ -437,45 +454,45 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
       if (one) {
         // gate, up and SwiGLU in one pass
         LinearCall k;
-        k.x = m->h; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
-        k.y = m->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
+        k.x = s->h; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
+        k.y = s->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
         k.limit = d.swiglu_limit;
         if (L.gd != L.ud) return fail(IHIP_E_ARG, "model: gate and up of one type");
         if ((rc = enqueue_linear(m->c, k))) return rc;
       } else {
-        if ((rc = lin(m, m->h, qfp, n, H, L.gd, L.gate, F, 0, m->gate))) return rc;
-        if ((rc = lin(m, m->h, qfp, n, H, L.ud, L.up, F, 0, m->up))) return rc;
-        if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * F, d.swiglu_alpha,
+        if ((rc = lin(s, s->h, qfp, n, H, L.gd, L.gate, F, 0, s->gate))) return rc;
+        if ((rc = lin(s, s->h, qfp, n, H, L.ud, L.up, F, 0, s->up))) return rc;
+        if ((rc = ihip_enqueue_swiglu(m->c, s->gate, s->up, n * F, d.swiglu_alpha,
                                       d.swiglu_limit)))
           return rc;
       }
-      QCache qg{m->xqf, m->xqf};
-      if ((rc = lin(m, m->gate, one ? nullptr : &qg, n, F, L.dd, L.down, H, 0, m->tmp))) return rc;
+      QCache qg{s->xqf, s->xqf};
+      if ((rc = lin(s, s->gate, one ? nullptr : &qg, n, F, L.dd, L.down, H, 0, s->tmp))) return rc;
     } else {
       // MoeBlock (decoder.pas:3037-3053) with the experts chosen on the
       // device (model.qwen3.cuda.pas:1152-1205)
       const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
-      if ((rc = lin(m, m->h, qfp, n, H, L.rd, L.router, E, L.router_b, m->route))) return rc;
+      if ((rc = lin(s, s->h, qfp, n, H, L.rd, L.router, E, L.router_b, s->route))) return rc;
       struct {
         const float* logits;
         int* ids;
         float* w;
         int32_t experts, k, norm, rows;
-      } ra = {(const float*)m->route, (int*)m->ids, (float*)m->rw, (int32_t)E, (int32_t)K,
+      } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n};
       if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
       if (one) {
         // the token's K experts: gate, up and SwiGLU in one pass per slot,
         // then down per slot; the weighted sum goes into the next norm
         LinearCall k;
-        k.x = m->h; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
-        k.y = m->gate; k.mode = m->mode; k.ids = m->ids; k.stride = L.eg_stride; k.x_per_slot = 0;
+        k.x = s->h; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
+        k.y = s->gate; k.mode = m->mode; k.ids = s->ids_dev; k.stride = L.eg_stride; k.x_per_slot = 0;
         k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
         k.limit = d.swiglu_limit;
         if ((rc = enqueue_linear(m->c, k))) return rc;
         LinearCall dn;
-        dn.x = m->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
-        dn.y = m->eout; dn.mode = m->mode; dn.ids = m->ids; dn.stride = L.ed_stride;
+        dn.x = s->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
+        dn.y = s->eout; dn.mode = m->mode; dn.ids = s->ids_dev; dn.stride = L.ed_stride;
         dn.x_per_slot = 1; dn.nexp = (int)E; dn.bias = L.edb;
         if ((rc = enqueue_linear(m->c, dn))) return rc;
       } else {
@@ -484,7 +501,7 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
           int* perm;
           void* items;
           int32_t slots, experts, max_items, chunk;
-        } pa = {(const int*)m->ids, (int*)m->perm, (void*)m->items, (int32_t)(n * K), (int32_t)E,
+        } pa = {(const int*)s->ids_dev, (int*)s->perm, (void*)s->items, (int32_t)(n * K), (int32_t)E,
                 (int32_t)((n * K + m->item_rows - 1) / m->item_rows + E), m->item_rows};
         if ((rc = launch(m->c, "moe_plan", dim3(1), dim3(256), &pa))) return rc;
         // gate and up: slot s = row s / K, expert ids[s], grouped by expert
@@ -493,25 +510,25 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
           bool& hv = q8_kind(L.egd) ? qf.havek : qf.have0;
           uint64_t buf = q8_kind(L.egd) ? qf.bufk : qf.buf0;
           if (!hv) {
-            if ((rc = enqueue_quantize(m->c, m->h, n, H, q8_kind(L.egd), buf))) return rc;
+            if ((rc = enqueue_quantize(m->c, s->h, n, H, q8_kind(L.egd), buf))) return rc;
             hv = true;
           }
           q0 = true;
         }
         uint64_t xqg = q8_kind(L.egd) == 1 ? qf.bufk : qf.buf0;
-        if ((rc = lin_ids(m, m->h, xqg, n, H, L.egd, L.eg, L.eg_stride, FI, m->ids, n * K, (int)K,
-                          L.egb, m->gate, q0)))
+        if ((rc = lin_ids(s, s->h, xqg, n, H, L.egd, L.eg, L.eg_stride, FI, s->ids_dev, n * K, (int)K,
+                          L.egb, s->gate, q0)))
           return rc;
         bool qu = q0 && q8_kind(L.eud) == q8_kind(L.egd);
         uint64_t xqu = q8_kind(L.eud) == 1 ? qf.bufk : qf.buf0;
-        if ((rc = lin_ids(m, m->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, m->ids, n * K, (int)K,
-                          L.eub, m->up, qu)))
+        if ((rc = lin_ids(s, s->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, s->ids_dev, n * K, (int)K,
+                          L.eub, s->up, qu)))
           return rc;
-        if ((rc = ihip_enqueue_swiglu(m->c, m->gate, m->up, n * K * FI, d.swiglu_alpha,
+        if ((rc = ihip_enqueue_swiglu(m->c, s->gate, s->up, n * K * FI, d.swiglu_alpha,
                                       d.swiglu_limit)))
           return rc;
-        if ((rc = lin_ids(m, m->gate, m->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, m->ids,
-                          n * K, 1, L.edb, m->eout, false)))
+        if ((rc = lin_ids(s, s->gate, s->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, s->ids_dev,
+                          n * K, 1, L.edb, s->eout, false)))
           return rc;
       }
       moe_out = true;
@@ -519,104 +536,441 @@ static int layers(ihip_model* m, int64_t n, int64_t past, bool graph)
     // residual, then the next layer's input norm (or the final norm)
     uint64_t nw = l + 1 < d.layers ? m->L[l + 1].input_norm : m->final_norm;
     if (moe_out)
-      rc = enqueue_addnorm_moe(m->c, m->x, m->eout, m->rw, d.experts_used, nw, m->h, n, H, d.rms_eps);
+      rc = enqueue_addnorm_moe(m->c, s->x, s->eout, s->rw, d.experts_used, nw, s->h, n, H, d.rms_eps);
     else
-      rc = ihip_enqueue_addnorm(m->c, m->x, m->tmp, nw, m->h, n, H, d.rms_eps);
+      rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, nw, s->h, n, H, d.rms_eps);
     if (rc) return rc;
   }
   return 0;
 }
 
-static int head(ihip_model* m, int64_t n, bool all, uint64_t y)
+static int head(ihip_mctx* s, int64_t n, bool all, uint64_t y)
 {
+  ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
-  QCache qh{m->xq0, m->xqk};
+  QCache qh{s->xq0, s->xqk};
   if (n == 1 && one_row_fused(m)) {
     // layers_one left the residual: the final norm is staged by the head
     LinearCall k;
-    k.x = m->x; k.rows = 1; k.in = d.hidden; k.dtype = m->head_dt; k.w = m->head;
+    k.x = s->x; k.rows = 1; k.in = d.hidden; k.dtype = m->head_dt; k.w = m->head;
     k.out = d.vocab; k.y = y; k.mode = m->mode; k.nw = m->final_norm; k.eps = d.rms_eps;
     return enqueue_linear(m->c, k);
   }
-  if (all) return lin(m, m->h, &qh, n, d.hidden, m->head_dt, m->head, d.vocab, 0, y);
-  return lin(m, m->h + (uint64_t)(n - 1) * d.hidden * 4, nullptr, 1, d.hidden, m->head_dt,
+  if (all) return lin(s, s->h, &qh, n, d.hidden, m->head_dt, m->head, d.vocab, 0, y);
+  return lin(s, s->h + (uint64_t)(n - 1) * d.hidden * 4, nullptr, 1, d.hidden, m->head_dt,
              m->head, d.vocab, 0, y);
 }
 
-// one chunk: ids and cos/sin uploaded, embeddings, layers, head
-static int chunk(ihip_model* m, const int32_t* ids, int64_t n, bool want_logits, bool all,
-                 uint64_t logits_dev)
+// one chunk: ids (or embedding rows) and cos/sin uploaded, embeddings,
+// layers, head; normed (host, or null): the last row after the final norm
+static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t n,
+                 bool want_logits, bool all, uint64_t logits_dev, float* normed)
 {
+  ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
+  ihip_ctx* c = m->c;
   std::vector<float> cs((size_t)n * d.head_dim);
-  rotary(d, m->length, n, cs.data());
-  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, (void*)ids, n * 4, m->c->stream));
-  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, m->c->stream));
-  int rc = ihip_enqueue_embed(m->c, m->embed, m->embed_dt, d.vocab, d.hidden, m->tok, n, m->x);
-  if (!rc) rc = layers(m, n, m->length, false);
-  if (!rc && want_logits) rc = head(m, n, all, logits_dev);
+  rotary(d, s->length, n, cs.data());
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
+  int rc = 0;
+  if (ids) {
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, (void*)ids, n * 4, c->stream));
+    rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, d.vocab, d.hidden, s->tok, n, s->x);
+  } else {
+    // ForwardEmbeds: the caller's rows in place of the token embeddings
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->x, (void*)embeds, (size_t)n * d.hidden * 4,
+                                  c->stream));
+  }
+  if (!rc) rc = layers(s, n, s->length, false);
+  if (!rc && normed) {
+    // one row leaves the residual in x (the head stages the final norm):
+    // the norm of that row; a chunk leaves h = the final norm of every row
+    uint64_t src = s->h + (uint64_t)(n - 1) * d.hidden * 4;
+    if (n == 1 && one_row_fused(m)) {
+      rc = ihip_enqueue_rmsnorm(c, s->x, m->final_norm, s->h, 1, d.hidden, d.rms_eps);
+      src = s->h;
+    }
+    if (!rc)
+      IHIP_CHECK(hipMemcpyDtoHAsync(normed, (hipDeviceptr_t)src, (size_t)d.hidden * 4, c->stream));
+  }
+  if (!rc && want_logits) rc = head(s, n, all, logits_dev);
   // the host vectors must outlive the copies
-  IHIP_CHECK(hipStreamSynchronize(m->c->stream));
-  if (!rc) m->length += n;
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  if (!rc) {
+    for (int64_t i = 0; i < n; i++) s->ids[s->length + i] = ids ? ids[i] : -1;
+    s->length += n;
+  }
   return rc;
 }
 
 // the next id from the logits: the argmax, or a draw of the sampler
-static int next_token(ihip_model* m)
+static int next_token(ihip_mctx* s)
 {
-  return m->sampler ? ihip_enqueue_sample(m->c, m->sampler, m->logits, m->d.vocab, m->next)
-                    : ihip_enqueue_argmax(m->c, m->logits, m->d.vocab, m->next);
+  ihip_model* m = s->m;
+  return m->sampler ? ihip_enqueue_sample(m->c, m->sampler, s->logits, m->d.vocab, s->next)
+                    : ihip_enqueue_argmax(m->c, s->logits, m->d.vocab, s->next);
 }
 
 // the decode step as a graph: embed(tok) -> layers(pos) -> head -> next id
-static int decode_body(ihip_model* m)
+static int decode_body(ihip_mctx* s)
 {
+  ihip_model* m = s->m;
   ihip_ctx* c = m->c;
-  int rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, m->tok, 1, m->x);
-  if (!rc) rc = layers(m, 1, 0, true);
-  if (!rc) rc = head(m, 1, false, m->logits);
-  if (!rc) rc = next_token(m);
+  int rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, s->tok, 1, s->x);
+  if (!rc) rc = layers(s, 1, 0, true);
+  if (!rc) rc = head(s, 1, false, s->logits);
+  if (!rc) rc = next_token(s);
   return rc;
 }
 
-static int decode_graph(ihip_model* m)
+// the context's decode graph, captured for its capacity (the attention's
+// ranges) and the model's sampler; updated in place when the topology allows
+static int decode_graph(ihip_mctx* s)
 {
+  ihip_model* m = s->m;
   ihip_ctx* c = m->c;
-  int rc = ihip_capture_begin(c);
-  if (rc) return rc;
-  rc = decode_body(m);
-  int rc2 = ihip_capture_end(c, 0);
-  if (rc) return rc;
-  if (rc2) return rc2;
-  m->graph_ready = true;
-  c->slot_owner[0] = m;
+  if (c->capturing) return fail(IHIP_E_CAPTURE, "decode graph: the context is capturing");
+  IHIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  c->capturing = true;
+  int rc = decode_body(s);
+  c->capturing = false;
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  bool updated = false;
+  if (s->exec) {
+    hipGraphExecUpdateResult res;
+    hipGraphNode_t err_node = nullptr;
+    updated = hipGraphExecUpdate(s->exec, g, &err_node, &res) == hipSuccess &&
+              res == hipGraphExecUpdateSuccess;
+    if (!updated) {
+      (void)hipGetLastError();
+      (void)hipGraphExecDestroy(s->exec);
+      s->exec = nullptr;
+    }
+  }
+  if (s->graph) (void)hipGraphDestroy(s->graph);
+  s->graph = g;
+  if (!updated) IHIP_CHECK(hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0));
+  s->graph_ready = true;
+  s->graph_capacity = s->capacity;
+  s->graph_sampler = m->sampler_epoch;
+  return 0;
+}
+
+static int dalloc_ctx(ihip_mctx* s, uint64_t bytes, uint64_t& p)
+{
+  void* q = nullptr;
+  IHIP_CHECK(hipMalloc(&q, bytes ? (bytes + 255) & ~(uint64_t)255 : 256));
+  s->owned.push_back((uint64_t)q);
+  p = (uint64_t)q;
+  return 0;
+}
+
+static void free_owned(ihip_mctx* s, uint64_t& p)
+{
+  if (!p) return;
+  for (size_t i = 0; i < s->owned.size(); i++)
+    if (s->owned[i] == p) {
+      s->owned.erase(s->owned.begin() + i);
+      break;
+    }
+  (void)hipFree((void*)p);
+  p = 0;
+}
+
+// the most bytes of attention partials a chunk may use: the rows of a chunk
+// are cut down so a long context stays within it
+static const uint64_t ATTN_PART_MAX = 1ull << 30;
+
+static uint64_t part_bytes(const ihip_model* m, int64_t rows, int64_t keys)
+{
+  return (uint64_t)m->d.heads * rows * attention_splits(keys) * (m->d.head_dim + 2) * 8;
+}
+
+// rows of the next chunk after `past` cached tokens, at most `want`
+static int64_t chunk_rows(const ihip_mctx* s, int64_t past, int64_t want)
+{
+  int64_t n = std::min(want, s->m->chunk_rows);
+  while (n > 1 && part_bytes(s->m, n, past + n) > ATTN_PART_MAX) n = (n + 1) / 2;
+  return n;
+}
+
+// Prepare (model.qwen3.cuda.pas:856-940): the KV cache grown to hold
+// `tokens` (doubled, at least a quarter beyond them and 64, at most the
+// model's positions; the cached rows copied over), and the attention
+// partials for chunks of up to CHUNK rows over it
+static int prepare(ihip_mctx* s, int64_t tokens)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  ihip_ctx* c = m->c;
+  const int64_t maxpos = d.max_positions > 0 ? d.max_positions : ((int64_t)1 << 30);
+  if (tokens > maxpos)
+    return fail(IHIP_E_ARG, "forward: " + std::to_string(tokens) + " tokens exceed the " +
+                                std::to_string(maxpos) + " positions");
+  if (tokens > s->capacity) {
+    int64_t cap = s->capacity * 2;
+    if (cap < tokens + tokens / 4) cap = tokens + tokens / 4;
+    if (cap < 64) cap = 64;
+    if (cap > maxpos) cap = maxpos;
+    const uint64_t es = m->kv_f16 ? 2 : 4, kvw = (uint64_t)d.kv_heads * d.head_dim;
+    std::vector<uint64_t> nk(d.layers, 0), nv(d.layers, 0);
+    int rc = 0;
+    for (int l = 0; l < d.layers && !rc; l++) {
+      void* a = nullptr;
+      void* b = nullptr;
+      hipError_t e = hipMalloc(&a, (uint64_t)cap * kvw * es);
+      if (e == hipSuccess) e = hipMalloc(&b, (uint64_t)cap * kvw * es);
+      nk[l] = (uint64_t)a;
+      nv[l] = (uint64_t)b;
+      if (e != hipSuccess) {
+        rc = hip_fail(e, "KV cache");
+        break;
+      }
+      if (s->length > 0) {
+        e = hipMemcpyDtoDAsync((hipDeviceptr_t)nk[l], (hipDeviceptr_t)s->kc[l], s->length * kvw * es,
+                               c->stream);
+        if (e == hipSuccess)
+          e = hipMemcpyDtoDAsync((hipDeviceptr_t)nv[l], (hipDeviceptr_t)s->vc[l],
+                                 s->length * kvw * es, c->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "KV cache copy");
+      }
+    }
+    (void)hipStreamSynchronize(c->stream);
+    if (rc) {
+      for (int l = 0; l < d.layers; l++) {
+        if (nk[l]) (void)hipFree((void*)nk[l]);
+        if (nv[l]) (void)hipFree((void*)nv[l]);
+      }
+      return rc;
+    }
+    for (int l = 0; l < (int)s->kc.size(); l++) {
+      if (s->kc[l]) (void)hipFree((void*)s->kc[l]);
+      if (s->vc[l]) (void)hipFree((void*)s->vc[l]);
+    }
+    s->kc = nk;
+    s->vc = nv;
+    s->ids.resize(cap, -1);
+    s->capacity = cap;
+  }
+  // partials for a chunk of up to CHUNK rows over the cache (or fewer rows:
+  // chunk_rows), and for the decode step's ranges over the whole capacity
+  const uint64_t want = std::max(part_bytes(m, chunk_rows(s, 0, CHUNK), s->capacity),
+                                 part_bytes(m, 1, s->capacity));
+  if (s->attn_part_bytes < want) {
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    free_owned(s, s->attn_part);
+    s->attn_part_bytes = 0;
+    int rc = dalloc_ctx(s, want, s->attn_part);
+    if (rc) return rc;
+    s->attn_part_bytes = want;
+    s->graph_ready = false;
+  }
   return 0;
 }
 
 // steps decode steps from token `first` (not yet in the cache): each one
 // graph launch that writes the next id; out_ids[i] the id after step i
-static int decode_steps(ihip_model* m, int32_t first, int64_t steps, int32_t* out_ids)
+static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out_ids)
 {
+  ihip_model* m = s->m;
   ihip_ctx* c = m->c;
-  int rc = 0;
-  // slot 0 holds one model's decode graph: another model of this context
-  // may have captured into it since
-  if (m->use_graphs && (!m->graph_ready || c->slot_owner[0] != m) && (rc = decode_graph(m))) return rc;
+  int rc = prepare(s, s->length + steps);
+  if (rc) return rc;
+  // a graph holds this context's cache and ranges: captured again when the
+  // cache grew or the sampler changed since
+  if (m->use_graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
+                        s->graph_sampler != m->sampler_epoch) &&
+      (rc = decode_graph(s)))
+    return rc;
   std::vector<float> cs(m->d.head_dim);
   int32_t tok = first;
   for (int64_t i = 0; i < steps; i++) {
-    int32_t pos = (int32_t)m->length;
+    int32_t pos = (int32_t)s->length;
     rotary(m->d, pos, 1, cs.data());
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->tok, &tok, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->pos, &pos, 4, c->stream));
-    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)m->cs, cs.data(), cs.size() * 4, c->stream));
-    if ((rc = m->use_graphs ? ihip_graph_launch(c, 0) : decode_body(m))) return rc;
-    IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)m->next, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, &tok, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->pos, &pos, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
+    if (m->use_graphs) {
+      IHIP_CHECK(hipGraphLaunch(s->exec, c->stream));
+    } else if ((rc = decode_body(s))) {
+      return rc;
+    }
+    IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[i], (hipDeviceptr_t)s->next, 4, c->stream));
     IHIP_CHECK(hipStreamSynchronize(c->stream));
-    m->length++;
+    s->ids[s->length] = tok;
+    s->length++;
     tok = out_ids[i];
   }
   return 0;
+}
+
+static void context_free(ihip_mctx* s)
+{
+  if (!s) return;
+  ihip_ctx* c = s->m->c;
+  (void)hipStreamSynchronize(c->stream);
+  if (s->exec) (void)hipGraphExecDestroy(s->exec);
+  if (s->graph) (void)hipGraphDestroy(s->graph);
+  for (auto p : s->owned) (void)hipFree((void*)p);
+  if (s->logits_all) (void)hipFree((void*)s->logits_all);
+  for (size_t l = 0; l < s->kc.size(); l++) {
+    if (s->kc[l]) (void)hipFree((void*)s->kc[l]);
+    if (s->vc[l]) (void)hipFree((void*)s->vc[l]);
+  }
+  delete s;
+}
+
+// a new context: the activations of one chunk, the attention counters, and a
+// KV cache of `capacity` tokens (0: none until the first tokens come)
+static int context_new(ihip_model* m, int64_t capacity, ihip_mctx** out)
+{
+  *out = nullptr;
+  ihip_mctx* s = new ihip_mctx();
+  s->m = m;
+  const ihip_model_desc& d = m->d;
+  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
+                kvw = (int64_t)d.kv_heads * hd;
+  const int64_t N = CHUNK;
+  int64_t F = std::max<int64_t>(d.ffn, 1);
+  int64_t EK = m->any_moe ? (int64_t)d.experts_used * d.expert_ffn : 0;
+  int64_t wide = std::max<int64_t>({F, EK, qw, H, (int64_t)d.experts});
+  const int64_t K1 = std::max(d.experts_used, 1), E1 = std::max(d.experts, 1);
+  const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
+  const uint64_t qrow = qin + 4 * (qin / 32);
+  int rc = 0;
+  auto bad = [&](int r) {
+    context_free(s);
+    return r;
+  };
+  s->kc.assign(d.layers, 0);
+  s->vc.assign(d.layers, 0);
+  if ((rc = dalloc_ctx(s, N * H * 4, s->x)) || (rc = dalloc_ctx(s, N * H * 4, s->h)) ||
+      (rc = dalloc_ctx(s, N * H * 4, s->tmp)) || (rc = dalloc_ctx(s, N * qw * 4, s->q)) ||
+      (rc = dalloc_ctx(s, N * kvw * 4, s->k)) || (rc = dalloc_ctx(s, N * kvw * 4, s->v)) ||
+      (rc = dalloc_ctx(s, N * qw * 4, s->attn)) || (rc = dalloc_ctx(s, N * wide * 4, s->gate)) ||
+      (rc = dalloc_ctx(s, N * wide * 4, s->up)) || (rc = dalloc_ctx(s, N * E1 * 4, s->route)) ||
+      (rc = dalloc_ctx(s, N * K1 * 4, s->ids_dev)) || (rc = dalloc_ctx(s, N * K1 * 4, s->rw)) ||
+      (rc = dalloc_ctx(s, N * K1 * H * 4, s->eout)) || (rc = dalloc_ctx(s, N * hd * 4, s->cs)) ||
+      (rc = dalloc_ctx(s, N * 4, s->tok)) || (rc = dalloc_ctx(s, (uint64_t)d.vocab * 4, s->logits)) ||
+      (rc = dalloc_ctx(s, 256, s->next)) || (rc = dalloc_ctx(s, 256, s->pos)) ||
+      (rc = dalloc_ctx(s, N * K1 * 4, s->perm)) ||
+      (rc = dalloc_ctx(s, (N * K1 / 8 + 1 + E1) * 16, s->items)) ||
+      (rc = dalloc_ctx(s, N * qrow, s->xq0)) || (rc = dalloc_ctx(s, N * qrow, s->xqk)) ||
+      (rc = dalloc_ctx(s, N * K1 * qrow, s->xqf)) || (rc = dalloc_ctx(s, 256 * 128, s->done)))
+    return bad(rc);
+  // the attention counters start at zero (a fill kernel would do under
+  // capture; this runs once, outside any capture)
+  {
+    const hipError_t e = hipMemsetAsync((void*)s->done, 0, 256 * 128, m->c->stream);
+    if (e != hipSuccess) return bad(hip_fail(e, "model: counters"));
+  }
+  if (capacity > 0 && (rc = prepare(s, capacity))) return bad(rc);
+  m->contexts.push_back(s);
+  *out = s;
+  return 0;
+}
+
+// TDecoderModel.Forward / ForwardEmbeds on a context (ForwardRows,
+// model.qwen3.cuda.pas:1656-1720): chunks of the rows, logits of the last
+// row (or of every row), the last row's final norm into normed
+static int context_forward(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t count,
+                           float* logits, int all_logits, float* normed, int head_index)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  if (count < 1 || (!ids && !embeds)) return fail(IHIP_E_ARG, "forward: no tokens");
+  if (head_index != 0) return fail(IHIP_E_ARG, "forward: no head " + std::to_string(head_index) + " (1 head)");
+  if (ids)
+    for (int64_t i = 0; i < count; i++)
+      if (ids[i] < 0 || ids[i] >= d.vocab)
+        return fail(IHIP_E_ARG, "forward: token id " + std::to_string(ids[i]) + " outside the vocabulary");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  int rc = prepare(s, s->length + count);
+  if (rc) return rc;
+  for (int64_t done = 0; done < count;) {
+    const int64_t n = chunk_rows(s, s->length, count - done);
+    const bool last = done + n == count;
+    const bool want = logits && (all_logits || last);
+    uint64_t ldev = s->logits;
+    if (want && all_logits) {
+      if (s->logits_all_rows < n) {
+        if (s->logits_all) (void)hipFree((void*)s->logits_all);
+        s->logits_all = 0;
+        s->logits_all_rows = 0;
+        void* p = nullptr;
+        IHIP_CHECK(hipMalloc(&p, (uint64_t)CHUNK * d.vocab * 4));
+        s->logits_all = (uint64_t)p;
+        s->logits_all_rows = CHUNK;
+      }
+      ldev = s->logits_all;
+    }
+    rc = chunk(s, ids ? ids + done : nullptr, embeds ? embeds + done * d.hidden : nullptr, n, want,
+               all_logits != 0, ldev, last ? normed : nullptr);
+    if (rc) return rc;
+    if (want) {
+      float* dst = all_logits ? logits + done * d.vocab : logits;
+      const uint64_t rows = all_logits ? n : 1;
+      IHIP_CHECK(hipMemcpyDtoHAsync(dst, (hipDeviceptr_t)ldev, rows * d.vocab * 4, m->c->stream));
+      IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+    }
+    done += n;
+  }
+  return 0;
+}
+
+// TDecoderModel.Greedy (decoder.pas:3390-3426) on a context
+static int context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                          int32_t* out_ids)
+{
+  ihip_model* m = s->m;
+  ihip_ctx* c = m->c;
+  for (int64_t i = 0; i < n; i++)
+    if (prompt[i] < 0 || prompt[i] >= m->d.vocab) return fail(IHIP_E_ARG, "greedy: token id outside the vocabulary");
+  auto t0 = std::chrono::steady_clock::now();
+  int rc = 0;
+  {
+    // the prompt: every chunk, logits of the last row only, argmax on device
+    std::lock_guard<std::mutex> g(c->lock);
+    if ((rc = prepare(s, s->length + n + max_new))) return rc;
+    for (int64_t done = 0; done < n && !rc;) {
+      const int64_t k = chunk_rows(s, s->length, n - done);
+      rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr);
+      done += k;
+    }
+    if (!rc) rc = next_token(s);
+    if (!rc) {
+      IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[0], (hipDeviceptr_t)s->next, 4, c->stream));
+      IHIP_CHECK(hipStreamSynchronize(c->stream));
+    }
+  }
+  if (rc) return rc;
+  auto t1 = std::chrono::steady_clock::now();
+  std::lock_guard<std::mutex> g(c->lock);
+  // the new ids, then the last one into the cache too (TDecoderModel.Greedy:
+  // a Forward without logits after the last step), through the same graph
+  if (max_new > 1 && (rc = decode_steps(s, out_ids[0], max_new - 1, out_ids + 1))) return rc;
+  int32_t spare;
+  if ((rc = decode_steps(s, out_ids[max_new - 1], 1, &spare))) return rc;
+  auto t2 = std::chrono::steady_clock::now();
+  s->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+  s->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+  return 0;
+}
+
+static int context_decode(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out_ids)
+{
+  if (first < 0 || first >= s->m->d.vocab) return fail(IHIP_E_ARG, "decode: token id outside the vocabulary");
+  std::lock_guard<std::mutex> g(s->m->c->lock);
+  auto t0 = std::chrono::steady_clock::now();
+  int rc = decode_steps(s, first, steps, out_ids);
+  s->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  return rc;
 }
 
 }  // namespace ihip
@@ -645,7 +999,6 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
   m->d.layer = m->layer_desc.data();
   m->mode = mode;
   m->kv_f16 = kv_f16;
-  m->max_tokens = max_tokens;
   const ihip_model_desc& d = m->d;
   const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
                 kvw = (int64_t)d.kv_heads * hd;
@@ -664,7 +1017,7 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
   }
   if ((rc = upf(m, d.final_norm, H, m->final_norm))) return bad(rc);
   m->L.resize(d.layers);
-  bool any_moe = false;
+  bool& any_moe = m->any_moe;
   for (int l = 0; l < d.layers; l++) {
     const ihip_layer_desc& s = m->layer_desc[l];
     DevLayer& L = m->L[l];
@@ -697,42 +1050,11 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       L.eg_stride = (int64_t)row_bytes(L.egd, H) * FI;
       L.ed_stride = (int64_t)row_bytes(L.edd, FI) * H;
     }
-    const uint64_t kvbytes = (uint64_t)max_tokens * kvw * (kv_f16 ? 2 : 4);
-    if ((rc = dalloc(m, kvbytes, L.kc)) || (rc = dalloc(m, kvbytes, L.vc))) return bad(rc);
   }
-  // activations of one chunk
-  const int64_t N = CHUNK;
-  int64_t F = std::max<int64_t>(d.ffn, 1);
-  int64_t EK = any_moe ? (int64_t)d.experts_used * d.expert_ffn : 0;
-  int64_t wide = std::max<int64_t>({F, EK, qw, H, (int64_t)d.experts});
-  if ((rc = dalloc(m, N * H * 4, m->x)) || (rc = dalloc(m, N * H * 4, m->h)) ||
-      (rc = dalloc(m, N * H * 4, m->tmp)) || (rc = dalloc(m, N * qw * 4, m->q)) ||
-      (rc = dalloc(m, N * kvw * 4, m->k)) || (rc = dalloc(m, N * kvw * 4, m->v)) ||
-      (rc = dalloc(m, N * qw * 4, m->attn)) || (rc = dalloc(m, N * wide * 4, m->gate)) ||
-      (rc = dalloc(m, N * wide * 4, m->up)) ||
-      (rc = dalloc(m, N * std::max<int64_t>(d.experts, 1) * 4, m->route)) ||
-      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->ids)) ||
-      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->rw)) ||
-      (rc = dalloc(m, N * std::max(d.experts_used, 1) * H * 4, m->eout)) ||
-      (rc = dalloc(m, N * hd * 4, m->cs)) || (rc = dalloc(m, N * 4, m->tok)) ||
-      (rc = dalloc(m, (uint64_t)d.vocab * 4, m->logits)) || (rc = dalloc(m, 256, m->next)) ||
-      (rc = dalloc(m, 256, m->pos)) ||
-      (rc = dalloc(m, N * std::max(d.experts_used, 1) * 4, m->perm)) ||
-      (rc = dalloc(m, (N * std::max(d.experts_used, 1) / 8 + 1 + std::max(d.experts, 1)) * 16,
-                   m->items)))
-    return bad(rc);
   if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
-  if ((rc = dalloc(m, 256 * 128, m->done))) return bad(rc);
-  {
-    const hipError_t e = hipMemsetAsync((void*)m->done, 0, 256 * 128, m->c->stream);
-    if (e != hipSuccess) return bad(hip_fail(e, "model: counters"));
-  }
-  if ((rc = dalloc(m, (uint64_t)d.heads * N * attention_splits(max_tokens) * (hd + 2) * 8,
-                   m->attn_part)))
-    return bad(rc);
   // moe_plan counts the slots per expert in LDS (4096 experts); a chunk's
   // work items stay within one grid dimension
-  if (any_moe && (d.experts > 4096 || N * d.experts_used > 65535))
+  if (any_moe && (d.experts > 4096 || CHUNK * d.experts_used > 65535))
     return bad(fail(IHIP_E_ARG, "model: more than 4096 experts or 65535 slots per chunk"));
   // a prompt chunk's experts on the MFMA GEMM when every expert matrix can
   // run there: work items of 64 slots
@@ -742,11 +1064,9 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       all_gemm = all_gemm && gemm_runs(c, L.egd, mode) && gemm_runs(c, L.eud, mode) &&
                  gemm_runs(c, L.edd, mode);
   m->item_rows = all_gemm ? 64 : 8;
-  const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
-  const uint64_t qrow = qin + 4 * (qin / 32);
-  if ((rc = dalloc(m, N * qrow, m->xq0)) || (rc = dalloc(m, N * qrow, m->xqk)) ||
-      (rc = dalloc(m, N * std::max(d.experts_used, 1) * qrow, m->xqf)))
-    return bad(rc);
+  // the model's own context, its cache sized for max_tokens up front
+  if ((rc = context_new(m, max_tokens, &m->def))) return bad(rc);
+  m->def->is_default = true;
   *out = m;
   return 0;
 }
@@ -755,18 +1075,17 @@ void ihip_model_destroy(ihip_model* m)
 {
   if (!m) return;
   (void)hipStreamSynchronize(m->c->stream);
-  for (auto p : m->owned) (void)hipFree((void*)p);
-  if (m->logits_all) (void)hipFree((void*)m->logits_all);
+  for (ihip_mctx* s : m->contexts) context_free(s);
+  m->contexts.clear();
   ihip_sampler_destroy(m->sampler);
   for (auto& u : m->uploaded) ihip_forget_weights(m->c, u.first, u.first + u.second);
-  if (m->c->slot_owner[0] == m) m->c->slot_owner[0] = nullptr;
   delete m;
 }
 
 int ihip_model_reset(ihip_model* m)
 {
   if (!m) return fail(IHIP_E_ARG, "ihip_model_reset");
-  m->length = 0;
+  m->def->length = 0;
   return 0;
 }
 
@@ -774,84 +1093,100 @@ int ihip_model_forward(ihip_model* m, const int32_t* ids, int64_t count, float* 
                        int all_logits)
 {
   if (!m || !ids || count < 1) return fail(IHIP_E_ARG, "ihip_model_forward: no tokens");
-  if (m->length + count > m->max_tokens)
-    return fail(IHIP_E_ARG, "ihip_model_forward: beyond the KV cache");
-  for (int64_t i = 0; i < count; i++)
-    if (ids[i] < 0 || ids[i] >= m->d.vocab) return fail(IHIP_E_ARG, "token id outside the vocabulary");
-  std::lock_guard<std::mutex> g(m->c->lock);
-  for (int64_t s = 0; s < count; s += m->chunk_rows) {
-    int64_t n = std::min(m->chunk_rows, count - s);
-    bool last = s + n == count;
-    bool want = logits && (all_logits || last);
-    uint64_t ldev = m->logits;
-    if (want && all_logits) {
-      if (m->logits_all_rows < n) {
-        if (m->logits_all) (void)hipFree((void*)m->logits_all);
-        void* p = nullptr;
-        IHIP_CHECK(hipMalloc(&p, (uint64_t)CHUNK * m->d.vocab * 4));
-        m->logits_all = (uint64_t)p;
-        m->logits_all_rows = CHUNK;
-      }
-      ldev = m->logits_all;
-    }
-    int rc = chunk(m, ids + s, n, want, all_logits != 0, ldev);
-    if (rc) return rc;
-    if (want) {
-      float* dst = all_logits ? logits + s * m->d.vocab : logits;
-      uint64_t rows = all_logits ? n : 1;
-      IHIP_CHECK(hipMemcpyDtoHAsync(dst, (hipDeviceptr_t)ldev, rows * m->d.vocab * 4, m->c->stream));
-      IHIP_CHECK(hipStreamSynchronize(m->c->stream));
-    }
-  }
-  return 0;
+  return context_forward(m->def, ids, nullptr, count, logits, all_logits, nullptr, 0);
 }
 
 int ihip_model_greedy(ihip_model* m, const int32_t* prompt, int64_t n, int64_t max_new,
                       int32_t* out_ids)
 {
   if (!m || !prompt || n < 1 || max_new < 1 || !out_ids) return fail(IHIP_E_ARG, "ihip_model_greedy");
-  if (m->length + n + max_new > m->max_tokens)
-    return fail(IHIP_E_ARG, "ihip_model_greedy: beyond the KV cache");
-  ihip_ctx* c = m->c;
-  auto t0 = std::chrono::steady_clock::now();
-  int rc = 0;
-  {
-    // the prompt: every chunk, logits of the last row only, argmax on device
-    std::lock_guard<std::mutex> g(c->lock);
-    for (int64_t s = 0; s < n && !rc; s += m->chunk_rows) {
-      int64_t k = std::min(m->chunk_rows, n - s);
-      rc = chunk(m, prompt + s, k, s + k == n, false, m->logits);
-    }
-    if (!rc) rc = next_token(m);
-    if (!rc) {
-      IHIP_CHECK(hipMemcpyDtoHAsync(&out_ids[0], (hipDeviceptr_t)m->next, 4, c->stream));
-      IHIP_CHECK(hipStreamSynchronize(c->stream));
-    }
-  }
-  if (rc) return rc;
-  auto t1 = std::chrono::steady_clock::now();
-  std::lock_guard<std::mutex> g(c->lock);
-  // the new ids, then the last one into the cache too (TDecoderModel.Greedy:
-  // a Forward without logits after the last step), through the same graph
-  if (max_new > 1 && (rc = decode_steps(m, out_ids[0], max_new - 1, out_ids + 1))) return rc;
-  int32_t spare;
-  if ((rc = decode_steps(m, out_ids[max_new - 1], 1, &spare))) return rc;
-  auto t2 = std::chrono::steady_clock::now();
-  m->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
-  m->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
-  return 0;
+  return context_greedy(m->def, prompt, n, max_new, out_ids);
 }
 
 int ihip_model_decode(ihip_model* m, int32_t first, int64_t steps, int32_t* out_ids)
 {
-  if (!m || steps < 1 || !out_ids || first < 0 || first >= m->d.vocab)
-    return fail(IHIP_E_ARG, "ihip_model_decode");
-  if (m->length + steps > m->max_tokens) return fail(IHIP_E_ARG, "ihip_model_decode: beyond the KV cache");
+  if (!m || steps < 1 || !out_ids) return fail(IHIP_E_ARG, "ihip_model_decode");
+  return context_decode(m->def, first, steps, out_ids);
+}
+
+/* ---- contexts (TDecoderDevice.NewDeviceContext and the calls on one) ---- */
+
+int ihip_model_new_context(ihip_model* m, ihip_mctx** out)
+{
+  if (!m || !out) return fail(IHIP_E_ARG, "ihip_model_new_context");
   std::lock_guard<std::mutex> g(m->c->lock);
-  auto t0 = std::chrono::steady_clock::now();
-  int rc = decode_steps(m, first, steps, out_ids);
-  m->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-  return rc;
+  return context_new(m, 0, out);
+}
+
+void ihip_context_destroy(ihip_mctx* s)
+{
+  if (!s || s->is_default) return;  // the model's own context goes with the model
+  ihip_model* m = s->m;
+  std::lock_guard<std::mutex> g(m->c->lock);
+  for (size_t i = 0; i < m->contexts.size(); i++)
+    if (m->contexts[i] == s) {
+      m->contexts.erase(m->contexts.begin() + i);
+      break;
+    }
+  context_free(s);
+}
+
+ihip_mctx* ihip_model_context(ihip_model* m) { return m ? m->def : nullptr; }
+
+int ihip_context_forward(ihip_mctx* s, const int32_t* ids, int64_t count, float* logits,
+                         int all_logits)
+{
+  if (!s || !ids || count < 1) return fail(IHIP_E_ARG, "ihip_context_forward: no ids");
+  return context_forward(s, ids, nullptr, count, logits, all_logits, nullptr, 0);
+}
+
+int ihip_context_forward_embeds(ihip_mctx* s, const float* embeds, int64_t count, float* logits,
+                                int all_logits, float* normed, int head)
+{
+  if (!s || !embeds || count < 1) return fail(IHIP_E_ARG, "ihip_context_forward_embeds: no rows");
+  return context_forward(s, nullptr, embeds, count, logits, all_logits, normed, head);
+}
+
+int ihip_context_truncate(ihip_mctx* s, int64_t length)
+{
+  if (!s || length < 0 || length > s->length)
+    return fail(IHIP_E_ARG, "ihip_context_truncate(" + std::to_string(length) + ") of " +
+                                std::to_string(s ? s->length : 0) + " tokens");
+  s->length = length;  // the cache keeps every row: any length is restorable
+  return 0;
+}
+
+int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t* kept)
+{
+  if (!s || (!ids && count > 0) || !kept) return fail(IHIP_E_ARG, "ihip_context_reuse");
+  // the common prefix, at most count - 1 tokens (the last one is computed
+  // again for its logits); a position fed an embedding row matches no id
+  int64_t n = 0, lim = std::min<int64_t>(count > 0 ? count - 1 : 0, s->length);
+  while (n < lim && s->ids[n] >= 0 && s->ids[n] == ids[n]) n++;
+  s->length = n;
+  *kept = n;
+  return 0;
+}
+
+int ihip_context_length(ihip_mctx* s, int64_t* length, int64_t* capacity)
+{
+  if (!s) return fail(IHIP_E_ARG, "ihip_context_length");
+  if (length) *length = s->length;
+  if (capacity) *capacity = s->capacity;
+  return 0;
+}
+
+int ihip_context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                        int32_t* out_ids)
+{
+  if (!s || !prompt || n < 1 || max_new < 1 || !out_ids) return fail(IHIP_E_ARG, "ihip_context_greedy");
+  return context_greedy(s, prompt, n, max_new, out_ids);
+}
+
+int ihip_context_decode(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out_ids)
+{
+  if (!s || steps < 1 || !out_ids) return fail(IHIP_E_ARG, "ihip_context_decode");
+  return context_decode(s, first, steps, out_ids);
 }
 
 int ihip_model_chunk(ihip_model* m, int64_t rows)
@@ -880,7 +1215,7 @@ int ihip_model_sampling(ihip_model* m, const ihip_sampling* s)
   }
   ihip_sampler_destroy(m->sampler);
   m->sampler = k;
-  m->graph_ready = false;  // the decode graph is captured again with it
+  m->sampler_epoch++;  // every context's decode graph is captured again with it
   return 0;
 }
 
@@ -894,8 +1229,8 @@ int ihip_model_use_graphs(ihip_model* m, int on)
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms)
 {
   if (!m) return fail(IHIP_E_ARG, "ihip_model_timing");
-  if (prefill_ms) *prefill_ms = m->prefill_ms;
-  if (decode_ms) *decode_ms = m->decode_ms;
+  if (prefill_ms) *prefill_ms = m->def->prefill_ms;
+  if (decode_ms) *decode_ms = m->def->decode_ms;
   return 0;
 }
 

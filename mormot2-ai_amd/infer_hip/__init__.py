@@ -131,6 +131,16 @@ def lib():
             "ihip_model_chunk": (i32, [vp, i64]),
             "ihip_enqueue_stream_read": (i32, [vp, u64, u64, u64]),
             "ihip_model_rotary": (i32, [vp, i64, i64, vp]),
+            "ihip_model_new_context": (i32, [vp, C.POINTER(vp)]),
+            "ihip_context_destroy": (None, [vp]),
+            "ihip_model_context": (vp, [vp]),
+            "ihip_context_forward": (i32, [vp, vp, i64, vp, i32]),
+            "ihip_context_forward_embeds": (i32, [vp, vp, i64, vp, i32, vp, i32]),
+            "ihip_context_reuse": (i32, [vp, vp, i64, C.POINTER(i64)]),
+            "ihip_context_truncate": (i32, [vp, i64]),
+            "ihip_context_length": (i32, [vp, C.POINTER(i64), C.POINTER(i64)]),
+            "ihip_context_greedy": (i32, [vp, vp, i64, i64, vp]),
+            "ihip_context_decode": (i32, [vp, C.c_int32, i64, vp]),
             "ihip_model_timing": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
             "ihip_synth_blocks": (i32, [vp, i32, i64, i64, u64, i32, i32, i32]),
             "ihip_synth_normal": (i32, [vp, i32, i64, i64, u64, C.c_float, i32]),
@@ -412,6 +422,85 @@ class Model:
         a, b = C.c_double(), C.c_double()
         check(lib().ihip_model_timing(self.h, C.byref(a), C.byref(b)), "timing")
         return a.value, b.value
+
+    def new_context(self):
+        """A new, empty context of this model (NewDeviceContext)."""
+        return ModelContext(self)
+
+    def context(self):
+        """The model's own context (the one forward/greedy/decode use)."""
+        return ModelContext(self, own=True)
+
+
+class ModelContext:
+    """One sequence on the device (a TDecoderContext of TDecoderDevice): its
+    KV cache, grown as tokens come; the weights are the model's."""
+
+    def __init__(self, model, own=False):
+        self.model = model
+        self.own = own
+        self.vocab = model.vocab
+        self.hidden = model.spec.struct.hidden
+        if own:
+            self.h = C.c_void_p(lib().ihip_model_context(model.h))
+        else:
+            h = C.c_void_p()
+            check(lib().ihip_model_new_context(model.h, C.byref(h)), "new_context")
+            self.h = h
+
+    def close(self):
+        if self.h and not self.own and self.model.h:
+            lib().ihip_context_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        if getattr(self, "h", None) and getattr(self.model, "h", None):
+            self.close()
+
+    def forward(self, ids, all_logits=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        lg = np.empty((len(ids) if all_logits else 1, self.vocab), np.float32)
+        check(lib().ihip_context_forward(self.h, _p(ids), len(ids), _p(lg), int(all_logits)),
+              "forward")
+        return lg if all_logits else lg[0]
+
+    def forward_embeds(self, embeds, all_logits=False, normed=False, logits=True, head=0):
+        """ForwardEmbeds: rows [count, hidden] in place of token embeddings;
+        returns (logits or None, the last row's final norm or None)."""
+        e = np.ascontiguousarray(embeds, np.float32).reshape(-1, self.hidden)
+        n = e.shape[0]
+        lg = np.empty((n if all_logits else 1, self.vocab), np.float32) if logits else None
+        nv = np.empty(self.hidden, np.float32) if normed else None
+        check(lib().ihip_context_forward_embeds(self.h, _p(e), n, _p(lg), int(all_logits), _p(nv),
+                                                head), "forward_embeds")
+        if lg is not None and not all_logits:
+            lg = lg[0]
+        return lg, nv
+
+    def reuse(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        kept = C.c_int64()
+        check(lib().ihip_context_reuse(self.h, _p(ids), len(ids), C.byref(kept)), "reuse")
+        return kept.value
+
+    def truncate(self, length):
+        check(lib().ihip_context_truncate(self.h, int(length)), "truncate")
+
+    def length(self):
+        n, cap = C.c_int64(), C.c_int64()
+        check(lib().ihip_context_length(self.h, C.byref(n), C.byref(cap)), "length")
+        return n.value, cap.value
+
+    def greedy(self, prompt, max_new):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max_new, np.int32)
+        check(lib().ihip_context_greedy(self.h, _p(p), len(p), max_new, _p(out)), "greedy")
+        return out
+
+    def decode(self, first, steps):
+        out = np.empty(steps, np.int32)
+        check(lib().ihip_context_decode(self.h, int(first), steps, _p(out)), "decode")
+        return out
 
 
 # ---------------------------------------------------------------- GGUF

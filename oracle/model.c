@@ -50,6 +50,13 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
 
 void orc_model_set_f32(orc_model* m, int f32) { m->f32 = f32; }
 
+int orc_model_truncate(orc_model* m, int64_t length)
+{
+  if (length < 0 || length > m->length) return IHIP_E_ARG;
+  m->length = length;
+  return 0;
+}
+
 double orc_model_route_gap(orc_model* m)
 {
   double g = m->route_gap;
@@ -105,18 +112,31 @@ static float half_round(float v)
   return orc_half_to_single(orc_single_to_half(v));
 }
 
+/* ForwardRows (TQwen3Model.Forward / ForwardEmbeds): ids, or embedding rows
+ * [n, hidden] in their place; normed (or NULL): the last row after the final
+ * norm */
+int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds, int64_t n,
+                           float* logits, int all_logits, float* normed);
+
 int orc_model_forward(orc_model* m, const int32_t* ids, int64_t n, float* logits,
                       int all_logits)
+{
+  return orc_model_forward_rows(m, ids, NULL, n, logits, all_logits, NULL);
+}
+
+int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds, int64_t n,
+                           float* logits, int all_logits, float* normed)
 {
   const ihip_model_desc* d = &m->d;
   int64_t h = d->hidden, hd = d->head_dim, qw = (int64_t)d->heads * hd,
           kvw = (int64_t)d->kv_heads * hd, past = m->length, half = hd / 2;
   int64_t f = d->ffn > d->expert_ffn ? d->ffn : d->expert_ffn;
   int err = 0;
-  if (n <= 0 || past + n > m->max_tokens)
+  if (n <= 0 || past + n > m->max_tokens || (!ids && !embeds))
     return IHIP_E_ARG;
-  for (int64_t i = 0; i < n; i++)
-    if (ids[i] < 0 || ids[i] >= d->vocab) return IHIP_E_ARG;
+  if (ids)
+    for (int64_t i = 0; i < n; i++)
+      if (ids[i] < 0 || ids[i] >= d->vocab) return IHIP_E_ARG;
   float* x = (float*)malloc(n * h * 4);
   float* hh = (float*)malloc(n * h * 4);
   float* tmp = (float*)malloc(n * h * 4);
@@ -139,8 +159,11 @@ int orc_model_forward(orc_model* m, const int32_t* ids, int64_t n, float* logits
   orc_rotary(d, past, n, cs);
   const float* cosv = cs;
   const float* sinv = cs + n * half;
-  for (int64_t i = 0; i < n; i++)
-    orc_row_to_f32(d->embed.data, d->embed.dtype, ids[i], h, x + i * h);
+  if (ids)
+    for (int64_t i = 0; i < n; i++)
+      orc_row_to_f32(d->embed.data, d->embed.dtype, ids[i], h, x + i * h);
+  else
+    memcpy(x, embeds, n * h * 4);
   for (int l = 0; l < d->layers && !err; l++) {
     const ihip_layer_desc* L = &m->layer[l];
     /* AttentionBlock */
@@ -217,8 +240,11 @@ int orc_model_forward(orc_model* m, const int32_t* ids, int64_t n, float* logits
   }
   if (!err) {
     m->length = past + n;
-    if (logits) {
+    if (logits || normed) {
       orc_rmsnorm(x, n, h, (const float*)d->final_norm.data, d->rms_eps, hh);
+      if (normed) memcpy(normed, hh + (n - 1) * h, h * 4);
+    }
+    if (logits) {
       ihip_tensor head = d->head.data ? d->head : d->embed;
       if (all_logits)
         err |= lin(m, hh, n, h, head, 0, d->vocab, NULL, logits);

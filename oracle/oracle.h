@@ -105,6 +105,12 @@ void orc_model_destroy(orc_model* m);
 /* f32 != 0: every Linear in the F32 arithmetic (orc_linear_f32) instead of
  * the CPU's quantized one - the oracle of the device's IHIP_MODE_F32 */
 void orc_model_set_f32(orc_model* m, int f32);
+/* ids, or embedding rows [count, hidden] in their place (ForwardEmbeds);
+ * normed (or NULL): the last row after the final norm */
+int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds, int64_t count,
+                           float* logits, int all_logits, float* normed);
+/* back to length tokens (TDecoderContext.Truncate) */
+int orc_model_truncate(orc_model* m, int64_t length);
 /* the smallest k-th vs (k+1)-th router logit gap since the last call (then reset) */
 double orc_model_route_gap(orc_model* m);
 int orc_model_forward(orc_model* m, const int32_t* ids, int64_t count,

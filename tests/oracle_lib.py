@@ -56,6 +56,8 @@ def lib():
         L.orc_model_destroy.restype = None
         L.orc_model_set_f32.argtypes = [vp, C.c_int]
         L.orc_model_set_f32.restype = None
+        L.orc_model_forward_rows.argtypes = [vp, vp, vp, i64, vp, C.c_int, vp]
+        L.orc_model_truncate.argtypes = [vp, i64]
         L.orc_model_route_gap.restype = C.c_double
         L.orc_model_route_gap.argtypes = [vp]
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
@@ -222,6 +224,20 @@ class Model:
         if rc:
             raise RuntimeError(rc)
         return lg if all_logits else lg[0]
+
+    def forward_embeds(self, embeds, hidden, normed=False):
+        """ForwardEmbeds: (last row's logits, its final norm or None)."""
+        e = np.ascontiguousarray(embeds, np.float32).reshape(-1, hidden)
+        lg = np.empty(self.desc.vocab, np.float32)
+        nv = np.empty(hidden, np.float32) if normed else None
+        rc = lib().orc_model_forward_rows(self.h, None, _p(e), e.shape[0], _p(lg), 0, _p(nv))
+        if rc:
+            raise RuntimeError(rc)
+        return lg, nv
+
+    def truncate(self, length):
+        if lib().orc_model_truncate(self.h, int(length)):
+            raise ValueError("truncate beyond the cached tokens")
 
     def route_gap(self):
         """The smallest k-th vs (k+1)-th router logit gap of the rows routed
