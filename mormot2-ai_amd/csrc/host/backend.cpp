@@ -295,6 +295,9 @@ static void pick_lpr(int64_t G, int64_t out, int cus, int& lpr, int& U)
 
 uint64_t q8_row_bytes(int64_t in) { return (uint64_t)in + 4 * (uint64_t)(in / 32); }
 
+// bytes of one row staged by gemv_rows (codes, scales, half sums; 16-aligned)
+static int rows_stride(int in) { return ((in + 12 * (in / 32)) + 15) & ~15; }
+
 int enqueue_quantize(ihip_ctx* c, uint64_t x, int64_t rows, int64_t in, int kind, uint64_t xq)
 {
   struct {
@@ -476,6 +479,19 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       const int64_t wgs = std::max<int64_t>(1, std::min((waves + 3) / 4, hold));
       return launch(c, name, dim3((unsigned)wgs, (unsigned)(k.nseg > 1 ? k.nseg : 1)), dim3(256), &a);
     }
+  }
+  if (batch && q8 && !k.w2 && !k.dtype2 && k.in <= 8192 && !float_fmt(k.dtype)) {
+    // a small batch of quantized rows: the rows staged in LDS once per block,
+    // each weight group loaded and decoded once for all of them (gemv_rows)
+    snprintf(name, sizeof name, "gemv_%s_q8_r8u%d", fmt_name(k.dtype), U);
+    const int64_t rpw_r = 64 / a.lpr, tiles_r = (k.out + rpw_r - 1) / rpw_r;
+    const int TB = U == 1 ? 2 : 1;
+    const size_t shmem = (size_t)8 * (size_t)rows_stride((int)k.in);
+    const unsigned gyr = (unsigned)(k.items ? k.nitems : (k.rows + 7) / 8);
+    const int64_t hold = (int64_t)c->cus * std::max(1, resident_blocks(c, name, 256, shmem));
+    const int64_t per_chunk = (hold + gyr - 1) / gyr;
+    const int64_t wgs_r = std::max<int64_t>(1, std::min((tiles_r + 4 * TB - 1) / (4 * TB), per_chunk));
+    return launch(c, name, dim3((unsigned)wgs_r, gyr), dim3(256), &a, shmem);
   }
   if (k.dtype2) {
     if (!k.nw || k.nseg < 2 || k.nseg1 < 1 || k.nseg1 >= k.nseg || !linear_ok(k.dtype2, k.in))

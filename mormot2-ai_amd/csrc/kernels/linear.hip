@@ -944,6 +944,249 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   }
 }
 
+// -------------------------------------------------- rows of a small batch
+// Q8 mode, quantized weights, up to RB = 8 activation rows per block
+// (blockIdx.y: a chunk of 8 rows, or a grouped-expert work item): the rows'
+// quantized codes, their scales and the sums of each half group staged in
+// LDS once per block; every weight group is loaded once and decoded once
+// into registers, then dotted with each row's group from LDS. The
+// arithmetic per row is the one-row GEMV's (exact integer group or
+// super-block sums, the scales in double, the same reduction order), so a
+// batch row gives the bits of that row alone.
+constexpr int RB = 8;
+
+// bytes of one staged row: codes [in], dx [G] floats, half sums [G] int2
+__host__ __device__ constexpr int rows_stride(int in) { return ((in + 12 * (in / 32)) + 15) & ~15; }
+
+// one row's activation group from the stage
+struct XRow {
+  int w[8];
+  float dx;
+  int sl, sh;
+};
+
+// SUMS: the half sums are read too (the types with an offset or a min)
+template <bool SUMS>
+__device__ __forceinline__ void stage_xrow(const uint8_t* row, int G, int g, XRow& x)
+{
+  const uint4* p = (const uint4*)(row + g * 32);
+  const uint4 u0 = p[0], u1 = p[1];
+  x.w[0] = (int)u0.x; x.w[1] = (int)u0.y; x.w[2] = (int)u0.z; x.w[3] = (int)u0.w;
+  x.w[4] = (int)u1.x; x.w[5] = (int)u1.y; x.w[6] = (int)u1.z; x.w[7] = (int)u1.w;
+  x.dx = ((const float*)(row + 32 * G))[g];
+  if constexpr (SUMS) {
+    const int2 hs = ((const int2*)(row + 36 * G))[g];
+    x.sl = hs.x;
+    x.sh = hs.y;
+  } else {
+    x.sl = x.sh = 0;
+  }
+}
+
+// the 8 code dwords of a group, decoded once for every row
+template <int F>
+__device__ __forceinline__ void decode_codes(const Raw& r, uint32_t (&cw)[8])
+{
+#pragma unroll
+  for (int hi = 0; hi < 2; hi++)
+#pragma unroll
+    for (int d = 0; d < 4; d++) cw[4 * hi + d] = code_bytes<F>(r, d, hi);
+}
+
+template <int F, int U, int TB>
+__device__ __forceinline__ void gemv_rows(const LinArgs& a)
+{
+  extern __shared__ __align__(16) uint8_t xst[];
+  const int lane = threadIdx.x & 63;
+  const int lpr = a.lpr;
+  const int lr = lane & (lpr - 1);
+  const int rsub = lane / lpr;
+  const int rpw = 64 / lpr;
+  const int G = a.in >> 5;
+  const int RS = rows_stride(a.in);
+  constexpr bool SUMS = !(F == DT_Q8_0 || F == DT_MXFP4);
+  const uint8_t* w = a.w;
+  const float* bias = a.bias;
+  int nrows;
+  int64_t xr[RB], yr[RB];
+  if (a.items) {
+    const int4 it = a.items[blockIdx.y];
+    if (it.z <= 0) return;
+    w += (int64_t)it.x * a.stride;
+    if (bias) bias += (int64_t)it.x * a.out;
+    nrows = min(RB, it.z);
+#pragma unroll
+    for (int r = 0; r < RB; r++) {
+      const int sl = r < nrows ? a.perm[it.y + r] : 0;
+      xr[r] = a.x_per_slot ? sl / a.x_per_slot : 0;
+      yr[r] = sl;
+    }
+  } else {
+    const int64_t r0 = (int64_t)blockIdx.y * RB;
+    nrows = min(RB, a.rows - (int)r0);
+#pragma unroll
+    for (int r = 0; r < RB; r++) xr[r] = yr[r] = r0 + r;
+  }
+  // the stage: each thread takes groups of the rows (16-byte loads of the
+  // codes, the half sums formed here once)
+  const int64_t qstride = (int64_t)a.in + 4 * (int64_t)G;
+  for (int t = threadIdx.x; t < nrows * G; t += blockDim.x) {
+    const int r = t / G, g = t - r * G;
+    const uint8_t* src = a.xq + xr[r] * qstride;
+    const uint4 u0 = *(const uint4*)(src + g * 32), u1 = *(const uint4*)(src + g * 32 + 16);
+    const float dx = ((const float*)(src + a.in))[g];
+    int sl = 0, sh = 0;
+    sl = sdot4((int)u0.x, 0x01010101, sl); sl = sdot4((int)u0.y, 0x01010101, sl);
+    sl = sdot4((int)u0.z, 0x01010101, sl); sl = sdot4((int)u0.w, 0x01010101, sl);
+    sh = sdot4((int)u1.x, 0x01010101, sh); sh = sdot4((int)u1.y, 0x01010101, sh);
+    sh = sdot4((int)u1.z, 0x01010101, sh); sh = sdot4((int)u1.w, 0x01010101, sh);
+    uint8_t* dst = xst + r * RS;
+    *(uint4*)(dst + g * 32) = u0;
+    *(uint4*)(dst + g * 32 + 16) = u1;
+    ((float*)(dst + 32 * G))[g] = dx;
+    ((int2*)(dst + 36 * G))[g] = make_int2(sl, sh);
+  }
+  __syncthreads();
+
+  const Regions rg = regions(F, a.out, a.in);
+  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= tiles) return;  // after the stage: every thread took its share
+  Raw cur[TB][U], nxt[TB][U];
+  // the weights of a step: TB tiles, every load issued before the first use
+  auto load = [&](int64_t sb, Raw (&raw)[TB][U]) {
+#pragma unroll
+    for (int i = 0; i < TB; i++) {
+      const int64_t o = min((sb + (int64_t)i * nw) * rpw + rsub, (int64_t)a.out - 1);
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        const int g = min(lr + k * lpr, G - 1);
+        load_group<F, true, F == DT_Q4_K>(w, rg, o, G, g, a.in, raw[i][k]);
+      }
+    }
+  };
+  int64_t tb = wid;
+  load(tb, cur);
+  while (tb < tiles) {
+    const int64_t nb = tb + (int64_t)TB * nw;
+    // the next step's weights in flight while this one is computed
+    if (nb < tiles) load(nb, nxt);
+#pragma unroll
+    for (int i = 0; i < TB; i++) {
+      const int64_t t = tb + (int64_t)i * nw;
+      const int64_t o = t * rpw + rsub;
+      const bool valid = t < tiles && o < a.out;
+      uint32_t cw[U][8];
+      Raw raw[U];
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        raw[k] = cur[i][k];
+        if constexpr (F == DT_Q4_K) expand_header(raw[k]);
+        decode_codes<F>(raw[k], cw[k]);
+      }
+      float bo = 0.f;
+      if (bias && valid) bo = bias[o];
+      // the per-group weight factors of the K-quants, once for all rows
+      int ksc[U], km[U];
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        if constexpr (F == DT_Q4_K) {
+          scale_min_k4((lr + k * lpr) & 7, raw[k].q1.y, raw[k].q1.z, raw[k].q1.w, ksc[k], km[k]);
+        } else {
+          ksc[k] = (int)(int8_t)(raw[k].a & 255u);
+          km[k] = (int)(int8_t)(raw[k].a >> 8);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; r++) {
+        if (r >= nrows) break;
+        const uint8_t* xrow = xst + r * RS;
+        double v;
+        if constexpr (is_k_quant(F)) {
+          // the one-row GEMV's K-quant order: exact sums over the 8 lanes of
+          // a super-block, the double term per lane, the super-block sets last
+          int is[U], ms[U];
+          XRow xg[U];
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            const int g = lr + k * lpr;
+            stage_xrow<SUMS>(xrow, G, min(g, G - 1), xg[k]);
+            int sl = 0, sh = 0;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+              sl = sdot4((int)cw[k][d], xg[k].w[d], sl);
+              sh = sdot4((int)cw[k][4 + d], xg[k].w[4 + d], sh);
+            }
+            if constexpr (F == DT_Q4_K) {
+              is[k] = __mul24(ksc[k], sl + sh);
+              ms[k] = __mul24(km[k], xg[k].sl + xg[k].sh);
+            } else {
+              is[k] = __mul24(ksc[k], sl - 32 * xg[k].sl) + __mul24(km[k], sh - 32 * xg[k].sh);
+              ms[k] = 0;
+            }
+            const bool ok = valid && g < G;
+            is[k] = ok ? is[k] : 0;
+            ms[k] = ok ? ms[k] : 0;
+          }
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            is[k] = wave_sum(is[k], 8);
+            ms[k] = wave_sum(ms[k], 8);
+          }
+          double tot = 0.0;
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            const double tt = superblock_q8k<F>(raw[k], is[k], ms[k], xg[k].dx);
+            tot += (valid && lr + k * lpr < G) ? tt : 0.0;
+          }
+          if (lpr > 8) tot = tot + xpart<8>(tot);
+          if (lpr > 16) tot = tot + xpart<16>(tot);
+          if (lpr > 32) tot = tot + xpart<32>(tot);
+          v = tot;
+        } else {
+          double accd = 0.0;
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            const int g = lr + k * lpr;
+            XRow xg;
+            stage_xrow<SUMS>(xrow, G, min(g, G - 1), xg);
+            int sd = 0;
+#pragma unroll
+            for (int d = 0; d < 8; d++) sd = sdot4((int)cw[k][d], xg.w[d], sd);
+            const double dxd = xg.dx;
+            const int sxq = xg.sl + xg.sh;
+            double tt;
+            if constexpr (F == DT_Q8_0) {
+              tt = (double)sd * ((double)half_to_float(raw[k].a) * dxd);
+            } else if constexpr (F == DT_MXFP4) {
+              tt = (double)sd * (mxfp4_q8_scale(raw[k].a) * dxd);
+            } else if constexpr (F == DT_Q4_0) {
+              tt = (double)(sd - 8 * sxq) * ((double)half_to_float(raw[k].a) * dxd);
+            } else if constexpr (F == DT_Q5_0) {
+              tt = (double)(sd - 16 * sxq) * ((double)half_to_float(raw[k].a) * dxd);
+            } else {  // Q5_1
+              const double t1 = (double)sd * ((double)half_to_float(raw[k].a & 0xffffu) * dxd);
+              tt = t1 + (double)half_to_float(raw[k].a >> 16) * (dxd * (double)sxq);
+            }
+            if (valid && g < G) accd += tt;
+          }
+          v = wave_sum(accd, lpr);
+        }
+        if (lr == 0 && valid) {
+          if (bias) v = (double)bo + v;
+          a.y[yr[r] * a.out + o] = (float)v;
+        }
+      }
+    }
+    tb = nb;
+#pragma unroll
+    for (int i = 0; i < TB; i++)
+#pragma unroll
+      for (int k = 0; k < U; k++) cur[i][k] = nxt[i][k];
+  }
+}
+
 // ------------------------------------------------------------ float rows
 // One activation row against F32 / BF16 / F16 weights in the Q8 arithmetic
 // (TInferCpuBackend.Linear's float branch, backend.cpu.pas:1548-1565: the
@@ -1261,6 +1504,14 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   IHIP_GEMV(PFX##_b8u3, F, M, 3, 8, false, false)    \
   IHIP_GEMV(PFX##_b8u4, F, M, 4, 8, false, false)
 
+#define IHIP_ROWS(NAME, F, U, TB) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv_rows<F, U, TB>(a); }
+#define IHIP_ROWS_U(PFX, F)         \
+  IHIP_ROWS(PFX##_r8u1, F, 1, 2)    \
+  IHIP_ROWS(PFX##_r8u2, F, 2, 1)    \
+  IHIP_ROWS(PFX##_r8u3, F, 3, 1)    \
+  IHIP_ROWS(PFX##_r8u4, F, 4, 1)
+
 #define IHIP_CMB(NAME, F, M, U) \
   extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv_cmb<F, M, U>(a); }
 
@@ -1303,32 +1554,39 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   extern "C" __global__ __launch_bounds__(256) void dequant_##NAME(ihip::DeqArgs a) { ihip::dequant<F>(a); }
 #ifdef IHIP_ONLY_FMT_Q8_0
 IHIP_GEMV_FMT(q8_0, ihip::DT_Q8_0)
+IHIP_ROWS_U(gemv_q8_0_q8, ihip::DT_Q8_0)
 IHIP_DEQ(q8_0, ihip::DT_Q8_0)
 #endif
 #ifdef IHIP_ONLY_FMT_Q4_0
 IHIP_GEMV_FMT(q4_0, ihip::DT_Q4_0)
+IHIP_ROWS_U(gemv_q4_0_q8, ihip::DT_Q4_0)
 IHIP_DEQ(q4_0, ihip::DT_Q4_0)
 #endif
 #ifdef IHIP_ONLY_FMT_MXFP4
 IHIP_GEMV_FMT(mxfp4, ihip::DT_MXFP4)
+IHIP_ROWS_U(gemv_mxfp4_q8, ihip::DT_MXFP4)
 IHIP_DEQ(mxfp4, ihip::DT_MXFP4)
 #endif
 #ifdef IHIP_ONLY_FMT_Q5_0
 IHIP_GEMV_FMT(q5_0, ihip::DT_Q5_0)
+IHIP_ROWS_U(gemv_q5_0_q8, ihip::DT_Q5_0)
 IHIP_DEQ(q5_0, ihip::DT_Q5_0)
 #endif
 #ifdef IHIP_ONLY_FMT_Q5_1
 IHIP_GEMV_FMT(q5_1, ihip::DT_Q5_1)
+IHIP_ROWS_U(gemv_q5_1_q8, ihip::DT_Q5_1)
 IHIP_DEQ(q5_1, ihip::DT_Q5_1)
 #endif
 #ifdef IHIP_ONLY_FMT_Q4_K
 IHIP_GEMV_FMT(q4_k, ihip::DT_Q4_K)
+IHIP_ROWS_U(gemv_q4_k_q8, ihip::DT_Q4_K)
 IHIP_GEMV_MIX_U(gemv_q4_k_q6_k_q8, ihip::DT_Q4_K, ihip::DT_Q6_K, 1)
 IHIP_GEMV_MIX_U(gemv_q4_k_q6_k_f32, ihip::DT_Q4_K, ihip::DT_Q6_K, 0)
 IHIP_DEQ(q4_k, ihip::DT_Q4_K)
 #endif
 #ifdef IHIP_ONLY_FMT_Q6_K
 IHIP_GEMV_FMT(q6_k, ihip::DT_Q6_K)
+IHIP_ROWS_U(gemv_q6_k_q8, ihip::DT_Q6_K)
 IHIP_DEQ(q6_k, ihip::DT_Q6_K)
 #endif
 #ifdef IHIP_ONLY_FMT_F32
