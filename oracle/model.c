@@ -12,7 +12,7 @@ struct orc_model {
   ihip_model_desc d;
   ihip_layer_desc* layer;
   int64_t max_tokens, length;
-  int kv_f16, threads, f32;
+  int kv_f16, threads, f32, fast;
   /* the smallest gap between the k-th and (k+1)-th router logit of any
    * routed row since the last orc_model_route_gap (a near tie there could
    * pick another expert on another arithmetic) */
@@ -49,6 +49,10 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
 }
 
 void orc_model_set_f32(orc_model* m, int f32) { m->f32 = f32; }
+
+void orc_model_set_threads(orc_model* m, int threads) { m->threads = threads > 0 ? threads : 1; }
+
+void orc_model_set_fast(orc_model* m, int fast) { m->fast = fast && orc_fast_available(); }
 
 int orc_model_truncate(orc_model* m, int64_t length)
 {
@@ -95,6 +99,9 @@ void orc_model_destroy(orc_model* m)
 static int lin(orc_model* m, const float* x, int64_t rows, int64_t in, ihip_tensor w,
                uint64_t offset, int64_t out, const float* bias, float* y)
 {
+  if (m->fast)
+    return orc_fast_linear(x, rows, in, (const uint8_t*)w.data + offset, w.dtype, out, bias, y,
+                           m->threads);
   if (m->f32)
     return orc_linear_f32(x, rows, in, (const uint8_t*)w.data + offset, w.dtype, out, bias, y,
                           m->threads);
@@ -183,8 +190,12 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       kc[i] = m->kv_f16 ? half_round(k[i]) : k[i];
       vc[i] = m->kv_f16 ? half_round(v[i]) : v[i];
     }
-    orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads,
-                         attn, L->window, (const float*)L->sinks.data, 0);
+    if (m->fast)
+      orc_fast_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads, attn,
+                         L->window, (const float*)L->sinks.data, m->threads);
+    else
+      orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads,
+                           attn, L->window, (const float*)L->sinks.data, 0);
     err |= lin(m, attn, n, qw, L->o, 0, h, (const float*)L->o_bias.data, tmp);
     add(x, tmp, n * h);
     /* the feed-forward block */

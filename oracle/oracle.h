@@ -105,6 +105,12 @@ void orc_model_destroy(orc_model* m);
 /* f32 != 0: every Linear in the F32 arithmetic (orc_linear_f32) instead of
  * the CPU's quantized one - the oracle of the device's IHIP_MODE_F32 */
 void orc_model_set_f32(orc_model* m, int f32);
+/* fast != 0: TInferCpuFastBackend's default mode (fast.c: AVX2 Linear on
+ * tiles of 16 outputs over the pool, the fast attention) - the timed CPU
+ * baseline; needs orc_fast_available() */
+void orc_model_set_fast(orc_model* m, int fast);
+/* the worker threads of the model's Linear and attention */
+void orc_model_set_threads(orc_model* m, int threads);
 /* ids, or embedding rows [count, hidden] in their place (ForwardEmbeds);
  * normed (or NULL): the last row after the final norm */
 int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds, int64_t count,
@@ -125,6 +131,14 @@ int orc_sampler_create(double temperature, int32_t top_k, double top_p, double m
                        int64_t seed, void** out);
 void orc_sampler_destroy(void* s);
 int64_t orc_sampler_next(void* s, const float* logits, int64_t count);
+
+/* fast.c: TInferCpuFastBackend (backend.cpu.pas:1975-2506) with AVX2 */
+int orc_fast_available(void);
+int orc_fast_linear(const float* x, int64_t rows, int64_t in, const void* w, int dtype,
+                    int64_t out, const float* bias, float* y, int threads);
+void orc_fast_attention(const float* q, int64_t rows, int64_t heads, int64_t head_dim,
+                        const float* keys, const float* values, int64_t past, int64_t kv_heads,
+                        float* y, int64_t window, const float* sinks, int threads);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,15 @@ def lib():
         L.orc_model_set_f32.restype = None
         L.orc_model_forward_rows.argtypes = [vp, vp, vp, i64, vp, C.c_int, vp]
         L.orc_model_truncate.argtypes = [vp, i64]
+        L.orc_model_set_threads.argtypes = [vp, C.c_int]
+        L.orc_model_set_threads.restype = None
+        L.orc_model_set_fast.argtypes = [vp, C.c_int]
+        L.orc_model_set_fast.restype = None
+        L.orc_fast_available.restype = C.c_int
+        L.orc_fast_linear.argtypes = [vp, i64, i64, vp, C.c_int, i64, vp, vp, C.c_int]
+        L.orc_fast_attention.argtypes = [vp, i64, i64, i64, vp, vp, i64, i64, vp, i64, vp,
+                                         C.c_int]
+        L.orc_fast_attention.restype = None
         L.orc_model_route_gap.restype = C.c_double
         L.orc_model_route_gap.argtypes = [vp]
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
@@ -120,6 +129,22 @@ def linear(x, w, dtype, out, bias=None, threads=8, f32=False):
     rc = fn(_p(x), rows, nin, _p(w), dtype, out, _p(b), _p(y), threads)
     if rc:
         raise ValueError(f"oracle linear failed: {rc}")
+    return y
+
+
+def fast_available():
+    return bool(lib().orc_fast_available())
+
+
+def fast_linear(x, w, dtype, out, bias=None, threads=8):
+    """TInferCpuFastBackend.Linear's default mode (AVX2, tiles of 16)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, nin = x.shape
+    y = np.empty((rows, out), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    rc = lib().orc_fast_linear(_p(x), rows, nin, _p(w), dtype, out, _p(b), _p(y), threads)
+    if rc:
+        raise ValueError(f"fast linear failed: {rc}")
     return y
 
 
@@ -197,7 +222,7 @@ def argmax(v):
 class Model:
     """The CPU decoder over a model description (mormot_ai_hip.ihip_model_desc)."""
 
-    def __init__(self, desc, max_tokens, kv_f16=False, threads=8, f32=False):
+    def __init__(self, desc, max_tokens, kv_f16=False, threads=8, f32=False, fast=False):
         self.desc = desc  # keeps the host tensors alive
         h = C.c_void_p()
         rc = lib().orc_model_create(C.addressof(desc.struct), max_tokens, int(kv_f16), threads,
@@ -207,6 +232,8 @@ class Model:
         self.h = h
         if f32:
             lib().orc_model_set_f32(self.h, 1)
+        if fast:
+            lib().orc_model_set_fast(self.h, 1)
 
     def close(self):
         if self.h:
@@ -238,6 +265,9 @@ class Model:
     def truncate(self, length):
         if lib().orc_model_truncate(self.h, int(length)):
             raise ValueError("truncate beyond the cached tokens")
+
+    def set_threads(self, n):
+        lib().orc_model_set_threads(self.h, int(n))
 
     def route_gap(self):
         """The smallest k-th vs (k+1)-th router logit gap of the rows routed
