@@ -1069,7 +1069,12 @@ int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_
          (const int*)pastp, (double*)part, scale, (int32_t)rows, (int32_t)heads, (int32_t)kvh,
          (int32_t)hd, (int32_t)past, (int32_t)window, f16, splits};
   int rc;
-  if ((hd == 64 || hd == 128) && rows > 1) {
+  if ((hd == 64 || hd == 128) && rows > 1 && c->attn_mfma) {
+    // tiles of 16 rows on the f64 matrix cores
+    char name[32];
+    snprintf(name, sizeof name, "attention_mfma_%s_%d", f16 ? "f16" : "f32", (int)hd);
+    rc = launch(c, name, dim3((unsigned)heads, (unsigned)((rows + 15) / 16), (unsigned)splits), dim3(256), &a);
+  } else if ((hd == 64 || hd == 128) && rows > 1) {
     // tiles of 8 rows sharing each range's keys
     char name[32];
     snprintf(name, sizeof name, "attention_rows_%s_%d", f16 ? "f16" : "f32", (int)hd);

@@ -751,6 +751,218 @@ extern "C" __global__ __launch_bounds__(256) void attention_rows_f32_128(AttnArg
   attention_rows_t<false, 128>(a);
 }
 
+// The ranges of ATTM rows at once on the f64 matrix cores (prompt chunks,
+// head_dim HD = 64 or 128): one block per (head, tile of ATTM = 16
+// consecutive rows, range s), the rows' ranges as attention_rows forms them
+// (a tile's keys span at most ATT_CHUNK + 15). Scores Q K^T and the weighted
+// values P V are v_mfma_f64_16x16x4f64 products: q (float), the cached keys
+// and values (half or float) and the weights are exact as doubles, every
+// product is exact and the sums run in double - only their order differs
+// from the CPU's sequential dot (CausalRows, backend.cpu.pas:1305-1354), a
+// difference of the order of 1e-16 relative before the result is rounded
+// to single. Per MFMA, lane l holds A[l % 16][l / 16] and B[l / 16][l % 16];
+// D[l / 16 + 4 v][l % 16] comes back in its register v. The k index of a
+// lane group (l / 16) runs over a contiguous quarter of the dimensions (the
+// scores) or of the tile's keys (the values), so each lane reads its own
+// contiguous part of a row: the sum is over the same terms, permuted.
+constexpr int ATTM = 16;
+constexpr int ATTMK = ATT_CHUNK + ATTM;  // keys of a tile's range, padded to 16
+typedef double dbl4 __attribute__((ext_vector_type(4)));
+
+template <bool F16, int HD>
+__device__ __forceinline__ void attention_mfma_t(const AttnArgs& a)
+{
+  __shared__ double sc[ATTM][ATTMK + 1];  // scores, then weights (row, tile key)
+  __shared__ double stat[ATTM][2];
+  __shared__ int rk[ATTM][2];             // a row's keys [k0, k1) (absolute)
+  const int h = xcd_head(blockIdx.x, a.heads), r0 = blockIdx.y * ATTM, s = blockIdx.z;
+  const int t = threadIdx.x, w = t >> 6, l = t & 63, lq = l >> 4, lc = l & 15;
+  constexpr int d = HD;
+  const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
+  const int g = h / (a.heads / a.kvh);
+  const int past = a.pastp ? *a.pastp : a.past;
+  if (t < ATTM) {
+    const int r = t;
+    const int total = past + r0 + r + 1;
+    const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
+    const int cnt = total - first;
+    const int j0 = min(cnt, s * ATT_CHUNK), j1 = min(cnt, j0 + ATT_CHUNK);
+    int k0 = first + j0, k1 = first + j1;
+    if (r0 + r >= a.rows || k0 >= k1) k0 = k1 = -1;  // no key of this range
+    rk[r][0] = k0;
+    rk[r][1] = k1;
+  }
+  __syncthreads();
+  // the tile's keys [kb, ke): from the first row with keys to the last
+  int kb = 0x7fffffff, ke = -1;
+#pragma unroll
+  for (int r = 0; r < ATTM; r++)
+    if (rk[r][0] >= 0) {
+      kb = min(kb, rk[r][0]);
+      ke = max(ke, rk[r][1]);
+    }
+  const int nblk = ke > kb ? (ke - kb + 15) >> 4 : 0;  // blocks of 16 keys (<= 9)
+  if (nblk > 0) {
+    // ---- scores: wave w takes key blocks w, w + 4, w + 8; lane group lq
+    // the dimensions [lq * d / 4, (lq + 1) * d / 4)
+    constexpr int DQ = d / 4;  // k steps = a lane's dimensions
+    const int qr = min(r0 + lc, a.rows - 1);
+    double qa[DQ];
+    {
+      const float4* qp = (const float4*)(a.q + (int64_t)qr * qw + (int64_t)h * d + lq * DQ);
+#pragma unroll
+      for (int i = 0; i < DQ / 4; i++) {
+        const float4 u = qp[i];
+        qa[4 * i] = u.x;
+        qa[4 * i + 1] = u.y;
+        qa[4 * i + 2] = u.z;
+        qa[4 * i + 3] = u.w;
+      }
+    }
+    for (int kbk = w; kbk < nblk; kbk += 4) {
+      const int key = min(kb + 16 * kbk + lc, ke - 1);
+      const int64_t kr = (int64_t)key * kvw + (int64_t)g * d + lq * DQ;
+      constexpr int NW = F16 ? DQ / 8 : DQ / 4;  // 16-byte words of a lane's part
+      uint4 u[NW];
+      if constexpr (F16) {
+        const uint4* p = (const uint4*)((const uint16_t*)a.kc + kr);
+#pragma unroll
+        for (int i = 0; i < NW; i++) u[i] = p[i];
+      } else {
+        const uint4* p = (const uint4*)((const float*)a.kc + kr);
+#pragma unroll
+        for (int i = 0; i < NW; i++) u[i] = p[i];
+      }
+      dbl4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int i = 0; i < NW; i++) {
+        const uint32_t wv[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if constexpr (F16) {
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[8 * i + 2 * j], (double)half_to_float(wv[j] & 0xffffu), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[8 * i + 2 * j + 1], (double)half_to_float(wv[j] >> 16), acc, 0, 0, 0);
+          } else {
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(qa[4 * i + j], (double)bits_float(wv[j]), acc, 0, 0, 0);
+          }
+        }
+      }
+      // D[row][key]: row lq + 4 v, key column lc of this block
+      const int kk = 16 * kbk + lc, kabs = kb + kk;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int r = lq + 4 * v;
+        const bool in = kabs >= rk[r][0] && kabs < rk[r][1];
+        sc[r][kk] = in ? acc[v] * a.scale : -1.0e308;
+      }
+    }
+  }
+  __syncthreads();
+  const int nk = 16 * nblk;
+  // ---- per row: the range maximum, the weights exp(score - max), their sum
+  // (wave w takes rows 4w .. 4w + 3)
+#pragma unroll
+  for (int rr = 0; rr < 4; rr++) {
+    const int r = 4 * w + rr;
+    double m = -1.0e308;
+    for (int j = l; j < nk; j += 64) m = fmax(m, sc[r][j]);
+    m = wave_max(m);
+    double e = 0;
+    for (int j = l; j < nk; j += 64) {
+      const double x = sc[r][j];
+      const double p = x > -1.0e308 ? exp(x - m) : 0.0;
+      sc[r][j] = p;
+      e += p;
+    }
+    e = wave_sum(e, 64);
+    if (l == 0) {
+      stat[r][0] = m;
+      stat[r][1] = e;
+    }
+  }
+  __syncthreads();
+  // ---- the weighted values: wave w the dimensions [w * d / 4, (w + 1) *
+  // d / 4) as NT tiles of 16 (HD 128: the even and the odd dimensions of the
+  // wave's 32); lane group lq the tile keys [lq * S, (lq + 1) * S)
+  constexpr int NT = d / 64;
+  const int S = nk >> 2;  // k steps (nk is a multiple of 16)
+  dbl4 o[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) o[n] = dbl4{0.0, 0.0, 0.0, 0.0};
+  if (nblk > 0) {
+    const int dim0 = w * (d / 4) + NT * lc;  // this lane's column dimension(s)
+    const int64_t vb = (int64_t)g * d + dim0;
+    constexpr int VU = 12;  // value loads in flight per lane
+    for (int t0 = 0; t0 < S; t0 += VU) {
+      float vv[VU][NT];
+#pragma unroll
+      for (int u = 0; u < VU; u++) {
+        const int key = min(kb + lq * S + min(t0 + u, S - 1), ke - 1);
+        const int64_t e = (int64_t)key * kvw + vb;
+        if constexpr (F16) {
+          if constexpr (NT == 2) {
+            const uint32_t x = *(const uint32_t*)((const uint16_t*)a.vc + e);
+            vv[u][0] = half_to_float(x & 0xffffu);
+            vv[u][1] = half_to_float(x >> 16);
+          } else {
+            vv[u][0] = half_to_float(((const uint16_t*)a.vc)[e]);
+          }
+        } else {
+          if constexpr (NT == 2) {
+            const float2 x = *(const float2*)((const float*)a.vc + e);
+            vv[u][0] = x.x;
+            vv[u][1] = x.y;
+          } else {
+            vv[u][0] = ((const float*)a.vc)[e];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VU; u++) {
+        if (t0 + u < S) {
+          const double p = sc[lc][lq * S + t0 + u];
+#pragma unroll
+          for (int n = 0; n < NT; n++)
+            o[n] = __builtin_amdgcn_mfma_f64_16x16x4f64(p, (double)vv[u][n], o[n], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // ---- the partial results: row lq + 4 v, dimension(s) dim0 + n
+  const int dim0 = w * (d / 4) + NT * lc;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int r = lq + 4 * v;
+    if (r0 + r >= a.rows) continue;
+    double* out = a.part + (((int64_t)h * a.rows + r0 + r) * a.splits + s) * (d + 2);
+#pragma unroll
+    for (int n = 0; n < NT; n++) out[dim0 + n] = o[n][v];
+  }
+  if (t < ATTM && r0 + t < a.rows) {
+    double* out = a.part + (((int64_t)h * a.rows + r0 + t) * a.splits + s) * (d + 2);
+    const bool empty = !(stat[t][1] > 0.0);
+    out[d] = empty ? -1.0e308 : stat[t][0];
+    out[d + 1] = empty ? 0.0 : stat[t][1];
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_mfma_f16_64(AttnArgs a)
+{
+  attention_mfma_t<true, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_mfma_f16_128(AttnArgs a)
+{
+  attention_mfma_t<true, 128>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_mfma_f32_64(AttnArgs a)
+{
+  attention_mfma_t<false, 64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attention_mfma_f32_128(AttnArgs a)
+{
+  attention_mfma_t<false, 128>(a);
+}
+
 extern "C" __global__ __launch_bounds__(256) void attention_part_f16(AttnArgs a)
 {
   attention_part_t<true>(a);

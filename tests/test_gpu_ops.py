@@ -105,6 +105,13 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     (64, 64, 8, 150, 20, 128, True, True),
     (128, 16, 8, 7, 8, 0, False, False),
     (64, 8, 2, 300, 33, 100, False, False),
+    # tiles of 16 prompt rows on the f64 matrix cores: a whole tile, a
+    # partial tile, three ranges from position 0, a window across tiles with
+    # f16 keys and sinks, the largest tile key span (window start moving
+    # inside a tile) with f32 keys
+    (128, 32, 4, 0, 16, 0, True, False), (128, 16, 8, 5, 17, 0, False, False),
+    (128, 32, 4, 0, 300, 0, True, True), (64, 64, 8, 300, 100, 128, True, True),
+    (128, 8, 2, 500, 48, 200, False, False), (64, 8, 8, 40, 70, 0, False, True),
     # other head sizes (the ranges kernel): 24 (12 pairs in a 16-lane slot, the
     # tiny gpt-oss), 32, 96 and 192 (a second pair for half the lanes)
     (24, 4, 2, 10, 6, 5, True, True), (24, 4, 2, 150, 1, 0, True, False),
@@ -132,6 +139,32 @@ def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     got = dy.download(np.float32, q.size).reshape(q.shape)
     ref = O.causal_attention(q, heads, hd, keys, vals, past, kvh, window, sk)
     assert ulp(got, ref) <= 2
+
+
+@pytest.fixture(scope="module")
+def ctx_rows():
+    """A context whose prompt attention runs the VALU tiles of 8 rows
+    (IHIP_ATTN_MFMA=0, read when the context is created)."""
+    import os
+    old = os.environ.get("IHIP_ATTN_MFMA")
+    os.environ["IHIP_ATTN_MFMA"] = "0"
+    try:
+        c = H.Context(0)
+    finally:
+        if old is None:
+            del os.environ["IHIP_ATTN_MFMA"]
+        else:
+            os.environ["IHIP_ATTN_MFMA"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("hd,heads,kvh,past,rows,window,sinks,f16", [
+    (128, 32, 4, 0, 130, 0, False, True), (64, 64, 8, 150, 20, 128, True, True),
+    (128, 16, 8, 7, 8, 0, False, False), (64, 8, 2, 300, 33, 100, False, False)])
+def test_attention_valu_tiles(ctx_rows, hd, heads, kvh, past, rows, window, sinks, f16):
+    """The VALU prompt tiles (kept as the IHIP_ATTN_MFMA=0 path) against the oracle."""
+    test_attention(ctx_rows, hd, heads, kvh, past, rows, window, sinks, f16)
 
 
 @pytest.mark.parametrize("E,k,norm", [(128, 8, True), (32, 4, True), (16, 3, False)])
