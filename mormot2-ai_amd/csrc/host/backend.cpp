@@ -436,14 +436,44 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       const int* perm;
       int32_t x_per_slot, pad2;
       const float* x;
+      double* part;
+      int32_t ksplit, klen;
     } g = {(const uint8_t*)k.w, (const uint8_t*)xq, (const float*)k.bias, (float*)k.y, k.stride,
            (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, (const void*)k.items,
-           (const int*)k.perm, k.x_per_slot, 0, (const float*)k.x};
+           (const int*)k.perm, k.x_per_slot, 0, (const float*)k.x, nullptr, 1, 0};
     if (k.items && k.item_rows > 64) return fail(IHIP_E_ARG, "EnqueueLinear: items of at most 64 slots");
     char gname[32];
     snprintf(gname, sizeof gname, "gemm_%s", fmt_name(k.dtype));
+    const unsigned gx = (unsigned)((k.out + 63) / 64);
     const unsigned gy = (unsigned)(k.items ? k.nitems : (k.rows + 63) / 64);
-    return launch(c, gname, dim3((unsigned)((k.out + 63) / 64), gy), dim3(256), &g);
+    // float weights with too few tiles to fill the chip (a router: 128
+    // outputs): the sum split into ksplit parts of >= 256 values, one block
+    // each, then their double sums added in split order
+    int ksplit = 1;
+    if (float_fmt(k.dtype) && !k.items && !k.no_alloc && !c->capturing && c->gemm_split) {
+      const int64_t tiles = (int64_t)gx * gy;
+      while (ksplit < 16 && tiles * ksplit * 2 <= (int64_t)c->cus * 2 && k.in / (ksplit * 2) >= 256)
+        ksplit *= 2;
+    }
+    if (ksplit > 1) {
+      const int64_t n = k.rows * k.out;
+      int rc = scratch(c, c->scratch_split, c->scratch_split_bytes, (uint64_t)n * ksplit * 8);
+      if (rc) return rc;
+      g.part = (double*)c->scratch_split;
+      g.ksplit = ksplit;
+      g.klen = (int32_t)(((k.in + ksplit - 1) / ksplit + 31) / 32 * 32);
+      if ((rc = launch(c, gname, dim3(gx, gy, (unsigned)ksplit), dim3(256), &g))) return rc;
+      struct {
+        const double* part;
+        const float* bias;
+        float* y;
+        int64_t n;
+        int32_t out, ksplit;
+      } sa = {(const double*)c->scratch_split, (const float*)k.bias, (float*)k.y, n,
+              (int32_t)k.out, ksplit};
+      return launch(c, "gemm_split_sum", dim3((unsigned)((n + 255) / 256)), dim3(256), &sa);
+    }
+    return launch(c, gname, dim3(gx, gy), dim3(256), &g);
   }
   if (k.nw && (batch || k.in > 4096 || xq))
     return fail(IHIP_E_ARG, "EnqueueLinear: the fused rmsnorm takes one float row of at most 4096");

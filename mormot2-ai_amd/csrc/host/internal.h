@@ -60,6 +60,7 @@ struct ihip_ctx {
   int gemm_min_rows = ihip::GEMM_MIN_ROWS;  // the smallest chunk on the GEMM (IHIP_GEMM_MIN_ROWS)
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
+  bool gemm_split = true;  // float-weight GEMMs of few tiles split over the sum (IHIP_GEMM_SPLIT=0: off)
   bool attn_mfma = true;  // prompt attention ranges on the f64 matrix cores (IHIP_ATTN_MFMA=0: VALU tiles of 8 rows)
   hipStream_t stream = nullptr;
   std::vector<ihip::Module> modules;
@@ -73,6 +74,7 @@ struct ihip_ctx {
   uint64_t scratch_y = 0, scratch_y_bytes = 0;
   uint64_t scratch_q = 0, scratch_q_bytes = 0;
   uint64_t scratch_bad = 0;
+  uint64_t scratch_split = 0, scratch_split_bytes = 0;  // split sums of the float-weight GEMM
   uint64_t scratch_argmax = 0;  // [ARGMAX_PARTS] block results of argmax_part
   uint64_t scratch_attn = 0, scratch_attn_bytes = 0;
   // the device address of static_scratch.hip's array on this device
@@ -154,6 +156,9 @@ struct LinearCall {
   // one block writes the picks (by id) to ids and their weights to rw
   uint64_t rl = 0, rw = 0;
   int rexp = 0, rk = 0, rnorm = 0;
+  // the caller cannot allocate (ihip_enqueue_linear_at_static): no path
+  // that grows the context's scratch
+  bool no_alloc = false;
   bool batch_rows() const { return items != 0; }
 };
 // whether one launch can take matrices of types a then b (gemv_<a>_<b>_*)

@@ -46,7 +46,7 @@ extern "C" int ihip_enqueue_linear_at_static(ihip_ctx* c, uint64_t x, int64_t ro
                                 std::to_string(in) + " dtype " + std::to_string(dtype));
   LinearCall k;
   k.x = x; k.rows = rows; k.in = in; k.dtype = dtype; k.w = w; k.out = out; k.y = y;
-  k.bias = bias; k.mode = mode;
+  k.bias = bias; k.mode = mode; k.no_alloc = true;
   const int kind = q8_kind(dtype);
   // one row quantizes its groups in the GEMV's registers; several rows are
   // quantized once into the array, as the context's scratch would hold them

@@ -45,6 +45,10 @@ struct GemmArgs {
   const int* perm;
   int32_t x_per_slot, pad2;
   const float* x;  // float rows [*, in] (float weights)
+  // float weights, ksplit > 1: block z sums the values [z klen, (z + 1) klen)
+  // and writes its double partial sums (no bias) to part [ksplit, rows, out]
+  double* part;
+  int32_t ksplit, klen;
 };
 
 constexpr int GBM = 64, GBN = 64, GKC = 8;  // tile rows, outputs, groups per chunk
@@ -423,11 +427,14 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
   const int lr = t >> 2, lk = 8 * (t & 3);
   const float* xrow = a.x + (int64_t)sxr[lr] * a.in;
   const int64_t wrow = (int64_t)min(col0 + lr, a.out - 1) * a.in;
+  // this block's values of the sum: [kb, ke)
+  const int kb = a.ksplit > 1 ? (int)blockIdx.z * a.klen : 0;
+  const int ke = a.ksplit > 1 ? min(a.in, kb + a.klen) : a.in;
   float xv[8], wv[8];
   auto load = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const int k = min(k0 + lk + u, a.in - 1);
+      const int k = min(k0 + lk + u, ke - 1);
       xv[u] = xrow[k];
       wv[u] = wval<F>(wb, wrow + k);
     }
@@ -444,8 +451,8 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
   for (int i = 0; i < 2; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) acc[i][j] = v4d{0.0, 0.0, 0.0, 0.0};
-  const int nch = (a.in + FKC - 1) / FKC;
-  load(0);
+  const int nch = (ke - kb + FKC - 1) / FKC;
+  load(kb);
   store(0);
   __syncthreads();
   // operand lane mapping of v_mfma_f64_16x16x4_f64 (probed on gfx950): A
@@ -453,12 +460,12 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
   // result register e of lane l = row 4 e + l / 16, column l % 16
   const int ar = l & 15, ak = l >> 4;
   for (int c = 0; c < nch; c++) {
-    const int buf = c & 1, k0 = c * FKC;
+    const int buf = c & 1, k0 = kb + c * FKC;
     if (c + 1 < nch) load(k0 + FKC);
 #pragma unroll
     for (int kk = 0; kk < FKC; kk += 4) {
       // a chunk past the end of the sum: values beyond in read 0 weight
-      const bool kin = k0 + kk + ak < a.in;
+      const bool kin = k0 + kk + ak < ke;
       double av[2], bv[2];
 #pragma unroll
       for (int i = 0; i < 2; i++) av[i] = (double)xs[buf][32 * wm + 16 * i + ar][kk + ak];
@@ -485,6 +492,10 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
         const int rt = 32 * wm + 16 * i + 4 * e + ak;
         if (rt < nrows) {
           double v = acc[i][j][e];
+          if (a.ksplit > 1) {
+            a.part[((int64_t)blockIdx.z * a.rows + syr[rt]) * a.out + o] = v;
+            continue;
+          }
           if (bias) v = b + v;
           a.y[(int64_t)syr[rt] * a.out + o] = (float)v;
         }

@@ -1386,6 +1386,27 @@ extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_128(AttnO
   attention_one_t<false, 128>(a);
 }
 
+// the split sums of the float-weight GEMM (gemm_flt with ksplit > 1): y[r,
+// o] = bias[o] + the ksplit double partial sums of (r, o) in split order,
+// rounded to single
+struct SplitSumArgs {
+  const double* part;  // [ksplit, rows, out]
+  const float* bias;   // [out] or null
+  float* y;            // [rows, out]
+  int64_t n;           // rows * out
+  int32_t out, ksplit;
+};
+
+extern "C" __global__ __launch_bounds__(256) void gemm_split_sum(SplitSumArgs a)
+{
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  double v = a.part[i];
+  for (int z = 1; z < a.ksplit; z++) v = v + a.part[(int64_t)z * a.n + i];
+  if (a.bias) v = (double)a.bias[i % a.out] + v;
+  a.y[i] = (float)v;
+}
+
 struct RouteArgs {
   const float* logits;
   int* ids;
