@@ -464,6 +464,10 @@ if __name__ == "__main__":
     main()
     # every device buffer is freed and the line is printed: leave without
     # waiting on interpreter teardown (the CPU baseline's OpenMP pool and the
-    # HIP runtime's threads), so no process of the run outlives it
+    # HIP runtime's threads), so no process of the run outlives it - except
+    # under rocprofv3, whose results are written by the exit handlers
     sys.stderr.flush()
-    os._exit(0)
+    profiled = any(k.startswith("ROCP") for k in os.environ) or \
+        "rocprof" in os.environ.get("LD_PRELOAD", "")
+    if not profiled:
+        os._exit(0)
