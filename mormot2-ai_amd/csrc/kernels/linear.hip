@@ -28,6 +28,11 @@
 
 namespace ihip {
 
+// threads per block of every kernel here (the host launches 256): blockDim.x
+// itself costs a vector load of the dispatch's hidden arguments, and a wait
+// for it, before the first weight load
+constexpr int NT = 256;
+
 struct LinArgs {
   const uint8_t* w;    // matrix base (plain) or expert 0 (ids)
   const float* x;      // [rows, in] float activations
@@ -716,10 +721,11 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       // blocks of the slots
       if (blockIdx.x == 0 && threadIdx.x < 64) {
         int sid[8];
-        float sw[8];
-        if (a.rexp <= 64) route_wave<1, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-        else if (a.rexp <= 128) route_wave<2, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-        else route_wave<4, true>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+        float sw[8], lg[4];
+        route_logits(a.rl, a.rexp, lg);
+        if (a.rexp <= 64) route_wave<1, true>(lg, a.rexp, a.rk, a.rnorm, sid, sw);
+        else if (a.rexp <= 128) route_wave<2, true>(lg, a.rexp, a.rk, a.rnorm, sid, sw);
+        else route_wave<4, true>(lg, a.rexp, a.rk, a.rnorm, sid, sw);
         int myid = -1;
         float myw = 0.f;
 #pragma unroll
@@ -739,8 +745,8 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     const bool later = routed;
     const int e = later ? 0 : a.ids[slot];
     if (!later && (e < 0 || (a.nexp > 0 && e >= a.nexp))) {
-      for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
-           o += (int64_t)gridDim.x * blockDim.x)
+      for (int64_t o = (int64_t)(blockIdx.x * NT + threadIdx.x); o < a.out;
+           o += (int64_t)gridDim.x * NT)
         a.y[(int64_t)slot * a.out + o] = 0.f;
       return;
     }
@@ -766,18 +772,22 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   }
   const Regions rg = regions(F, out, a.in);
   const int64_t tiles = ((int64_t)out + rpw - 1) / rpw;
-  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
     IHIP_STAMP(0);
-    if ((int64_t)blockIdx.x * (blockDim.x >> 6) >= tiles) return;  // the whole block: no tile
+    if ((int64_t)blockIdx.x * (NT >> 6) >= tiles) return;  // the whole block: no tile
     // T tiles per wave step, their weight loads issued together (and the
     // first ones before the activation row is read), so a wave keeps several
     // 16-byte loads per lane in flight
     constexpr int T = GLU ? (U == 1 ? 2 : 1) : (U == 1 ? 4 : (U == 2 ? 2 : 1));
     // the activation row's global loads first, then the first step's weight
     // loads, so the row is staged while the weights are on their way
+    // a self-routed token: the router logits first (the route needs them
+    // before any weight address is known)
+    float rlg[4];
+    if (GLU && NORM && a.ids && a.rl) route_logits(a.rl, a.rexp, rlg);
     XStage st;
     const bool quantized = !NORM && stage_q8<F, MODE>() && a.xq != nullptr;
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
@@ -790,16 +800,16 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       // weights for the down launch
       int sid[8];
       float sw[8];
-      if (a.rexp <= 64) route_wave<1, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-      else if (a.rexp <= 128) route_wave<2, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
-      else route_wave<4, false>(a.rl, a.rexp, a.rk, a.rnorm, sid, sw);
+      if (a.rexp <= 64) route_wave<1, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
+      else if (a.rexp <= 128) route_wave<2, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
+      else route_wave<4, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
       IHIP_STAMP(7);
       int e = -1;
 #pragma unroll
       for (int s = 0; s < 8; s++) e = s == (int)yrow0 ? sid[s] : e;
       if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
-        for (int64_t o = (int64_t)(blockIdx.x * blockDim.x + threadIdx.x); o < a.out;
-             o += (int64_t)gridDim.x * blockDim.x)
+        for (int64_t o = (int64_t)(blockIdx.x * NT + threadIdx.x); o < a.out;
+             o += (int64_t)gridDim.x * NT)
           a.y[yrow0 * a.out + o] = 0.f;
         return;
       }
@@ -1030,7 +1040,7 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
   // the stage: each thread takes groups of the rows (16-byte loads of the
   // codes, the half sums formed here once)
   const int64_t qstride = (int64_t)a.in + 4 * (int64_t)G;
-  for (int t = threadIdx.x; t < nrows * G; t += blockDim.x) {
+  for (int t = threadIdx.x; t < nrows * G; t += NT) {
     const int r = t / G, g = t - r * G;
     const uint8_t* src = a.xq + xr[r] * qstride;
     const uint4 u0 = *(const uint4*)(src + g * 32), u1 = *(const uint4*)(src + g * 32 + 16);
@@ -1050,8 +1060,8 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
 
   const Regions rg = regions(F, a.out, a.in);
   const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
-  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
   if (wid >= tiles) return;  // after the stage: every thread took its share
   Raw cur[TB][U], nxt[TB][U];
   // the weights of a step: TB tiles, every load issued before the first use
@@ -1241,11 +1251,11 @@ __device__ __forceinline__ void gemv_flt(const LinArgs& a)
   const int NC = a.in / VPC;  // chunks per row: at most 64 NJ
   const int nj = (NC + 63) / 64;
   const int64_t rb = (int64_t)a.in * ES;  // row bytes
-  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
   const int64_t steps = ((int64_t)out + FRW - 1) / FRW;
   __shared__ __align__(16) float xs[XN];
-  if ((int64_t)blockIdx.x * (blockDim.x >> 6) >= steps) return;  // the whole block: no rows
+  if ((int64_t)blockIdx.x * (NT >> 6) >= steps) return;  // the whole block: no rows
   XStage st;
   stage_load<F, 1, NORM>(a.x, nullptr, a.in, a.nw, st);
   // the first step's weights while the row is staged
@@ -1322,6 +1332,11 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
   const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
   const int n = K * a.in;
   float* dxs = (float*)(cmb_xs + n);
+  // the activation rows need no expert id: their loads go first (the first
+  // XN values; more, gpt-oss's 4 x 2880, in further chunks below)
+  const int nc0 = min(XN, n);
+  XStage st0;
+  stage_load<F, MODE, false>(a.x, nullptr, nc0, nullptr, st0);
   // this wave's slots and their experts (a bad id adds nothing)
   const uint8_t* wi[2];
   bool ok[2];
@@ -1346,12 +1361,14 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
         for (int k = 0; k < U; k++)
           load_group<F, true, F == DT_Q4_K>(wi[i], rg, o, G, min(lr + k * lpr, G - 1), a.in, raw[i][k]);
     }
+    // (a launch without them issues no load for them: a uniform branch)
 #pragma unroll
-    for (int i = 0; i < 2; i++) eb[i] = *(a.bias ? a.bias + e[i] * a.out + o : a.x);
-    er = *(a.res ? a.res + o : a.x);
+    for (int i = 0; i < 2; i++) eb[i] = a.bias ? a.bias[e[i] * a.out + o] : 0.f;
+    er = a.res ? a.res[o] : 0.f;
   };
   load(t);
-  for (int c0 = 0; c0 < n; c0 += XN) {
+  stage_store<F, MODE, false>(st0, false, nc0, 0.0, cmb_xs, dxs, a.bad, 1);
+  for (int c0 = XN; c0 < n; c0 += XN) {
     XStage st;
     const int nc = min(XN, n - c0);
     stage_load<F, MODE, false>(a.x + c0, nullptr, nc, nullptr, st);
@@ -1416,7 +1433,7 @@ struct DeqArgs {
 template <int F>
 __device__ __forceinline__ void dequant(const DeqArgs& a)
 {
-  int wrow = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  int wrow = blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
   int lane = threadIdx.x & 63;
   if (wrow >= a.rows) return;
   int64_t o = a.ids ? (int64_t)a.ids[wrow] : a.row0 + wrow;

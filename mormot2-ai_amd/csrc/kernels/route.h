@@ -34,7 +34,7 @@ __device__ __forceinline__ int logit_rank(const float* lg, int E32, int i, float
 }
 
 // a token's route in one wave, without LDS or barriers (every lane of the
-// wave calls it; E <= 64 * NPL, K <= min(E, 8)). Logit i sits in lane
+// wave calls it with its route_logits; E <= 64 * NPL, K <= min(E, 8)). Logit i sits in lane
 // i % 64, register i / 64, as an order-preserving key (-0 as +0; NaN and the
 // padding as 0: never picked). The k-th largest key is found by bisection on
 // its 32 bits (a wave ballot and popcount per bit), the picks are the keys
@@ -43,17 +43,29 @@ __device__ __forceinline__ int logit_rank(const float* lg, int E32, int i, float
 // the softmax over all E logits in double (each lane's logits summed, then
 // the wave tree), the pick's probability rounded to single, renormed by the
 // picked weights summed in pick order (logit descending, id ascending).
+// route_logits(): a lane's logits l, l + 64, l + 128, l + 192 (E <= 256), all
+// loads issued together (an index past E reads the last logit, unused), so a
+// caller issues them with its other first loads and waits for memory once.
+__device__ __forceinline__ void route_logits(const float* logits, int E, float (&f)[4])
+{
+  const int l = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < 4; r++) f[r] = logits[min(l + 64 * r, E - 1)];
+}
+
 template <int NPL, bool W>
-__device__ __forceinline__ void route_wave(const float* logits, int E, int K, int norm, int (&sid)[8],
+__device__ __forceinline__ void route_wave(const float (&fin)[4], int E, int K, int norm, int (&sid)[8],
                                            float (&sw)[8])
 {
   const int l = threadIdx.x & 63;
   float f[NPL];
   uint32_t key[NPL];
 #pragma unroll
+  for (int r = 0; r < NPL; r++) f[r] = fin[r];
+#pragma unroll
   for (int r = 0; r < NPL; r++) {
     const int i = l + 64 * r;
-    f[r] = i < E ? logits[i] : -INFINITY;
+    if (i >= E) f[r] = -INFINITY;
     const uint32_t b = __builtin_bit_cast(uint32_t, f[r]);
     int k = (int)(b ^ ((b >> 31) * 0x7fffffffu));
     if (k == -1) k = 0;
