@@ -273,10 +273,16 @@ bool linear_ok(int t, int64_t in)
 // four tiles of them, else wide rows (more waves for a short matrix)
 static void pick_lpr_order(int64_t G, const int (&order)[4], int& lpr, int& U)
 {
+  // at most this many groups per lane (IHIP_GEMV_UMAX, 1..4: fewer give
+  // wider rows, shorter per-lane work, more waves)
+  static const int umax = [] {
+    const char* v = getenv("IHIP_GEMV_UMAX");
+    return v ? std::min(4, std::max(1, atoi(v))) : 4;
+  }();
   int best = -1;
   for (int l : order) {
     int u = (int)((G + l - 1) / l);
-    if (u > 4) continue;
+    if (u > umax && !(l == 64 && u <= 4)) continue;
     int waste = l * u - (int)G;
     if (best < 0 || waste < best) {
       best = waste;

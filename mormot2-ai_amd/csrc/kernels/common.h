@@ -144,6 +144,20 @@ __device__ __forceinline__ double load_agent(const double* p)
   return __builtin_bit_cast(double, __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT));
 }
+// the kernel's argument block (BYTES of explicit arguments, then the hidden
+// ones with the grid size) read into the scalar cache in one round trip at
+// entry: the compiler loads each field where it is first used, and a field
+// in a line not yet cached then costs a memory round trip of its own, one
+// after another, before the first weight load is issued
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs()
+{
+  const uint32_t* kp = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t acc = 0;
+#pragma unroll
+  for (int o = 0; o < BYTES + 64; o += 64) acc ^= kp[o / 4];
+  __asm__ volatile("; kernargs %0" ::"s"(acc));
+}
 __device__ __forceinline__ void wait_stores() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // the launch's last block to arrive (all of the block's stores complete

@@ -1497,7 +1497,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
 
 // ------------------------------------------------------- exported symbols
 #define IHIP_GEMV(NAME, F, M, U, R, GLU, ...) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv<F, M, U, R, GLU, __VA_ARGS__>(a); }
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::touch_kernargs<sizeof(ihip::LinArgs)>(); ihip::gemv<F, M, U, R, GLU, __VA_ARGS__>(a); }
 
 #define IHIP_GEMV_U(PFX, F, M)                       \
   IHIP_GEMV(PFX##_u1, F, M, 1, 1, false, false)      \
@@ -1522,7 +1522,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   IHIP_GEMV(PFX##_b8u4, F, M, 4, 8, false, false)
 
 #define IHIP_ROWS(NAME, F, U, TB) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv_rows<F, U, TB>(a); }
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::touch_kernargs<sizeof(ihip::LinArgs)>(); ihip::gemv_rows<F, U, TB>(a); }
 #define IHIP_ROWS_U(PFX, F)         \
   IHIP_ROWS(PFX##_r8u1, F, 1, 2)    \
   IHIP_ROWS(PFX##_r8u2, F, 2, 1)    \
@@ -1530,7 +1530,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   IHIP_ROWS(PFX##_r8u4, F, 4, 1)
 
 #define IHIP_CMB(NAME, F, M, U) \
-  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::gemv_cmb<F, M, U>(a); }
+  extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a) { ihip::touch_kernargs<sizeof(ihip::LinArgs)>(); ihip::gemv_cmb<F, M, U>(a); }
 
 #define IHIP_CMB_U(PFX, F, M)      \
   IHIP_CMB(PFX##_cmb_u1, F, M, 1) \
@@ -1542,6 +1542,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
 #define IHIP_GEMV_MIX(NAME, F, F2, M, U)                                              \
   extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a)               \
   {                                                                                    \
+    ihip::touch_kernargs<sizeof(ihip::LinArgs)>();                                     \
     if ((int)blockIdx.y < a.nseg1) ihip::gemv<F, M, U, 1, false, true>(a);             \
     else ihip::gemv<F2, M, U, 1, false, true>(a);                                      \
   }
@@ -1552,6 +1553,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
 #define IHIP_FLT1(NAME, F, NORM, NJ)                                          \
   extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a)       \
   {                                                                             \
+    ihip::touch_kernargs<sizeof(ihip::LinArgs)>();                              \
     ihip::gemv_flt<F, NORM, NJ>(a);                                             \
   }
 // rows of at most 512 (j8) or 1024 (j16) 16-byte chunks

@@ -1371,18 +1371,22 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
 
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_64(AttnOneArgs a)
 {
+  ihip::touch_kernargs<sizeof(AttnOneArgs)>();
   attention_one_t<true, 64>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_128(AttnOneArgs a)
 {
+  ihip::touch_kernargs<sizeof(AttnOneArgs)>();
   attention_one_t<true, 128>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_64(AttnOneArgs a)
 {
+  ihip::touch_kernargs<sizeof(AttnOneArgs)>();
   attention_one_t<false, 64>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_128(AttnOneArgs a)
 {
+  ihip::touch_kernargs<sizeof(AttnOneArgs)>();
   attention_one_t<false, 128>(a);
 }
 
