@@ -516,6 +516,38 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       return launch(c, name, dim3((unsigned)wgs, (unsigned)(k.nseg > 1 ? k.nseg : 1)), dim3(256), &a);
     }
   }
+  // a small batch of quantized rows on the int8 matrix cores: 8 rows (or an
+  // item of at most 8 slots) x 128 outputs per block, the weights read once
+  // per 8 rows (gemm8), when its tiles fill the chip (a block walks the
+  // groups of its tiles in turn: a short matrix is left to gemv_rows below,
+  // whose waves split the rows' groups)
+  const int64_t blocks8 = ((k.out + 127) / 128) * (k.items ? k.nitems : (k.rows + 7) / 8);
+  if (batch && q8 && !k.w2 && !k.dtype2 && !float_fmt(k.dtype) && c->use_gemm8 && gemm_fmt(k.dtype) &&
+      blocks8 >= c->cus) {
+    struct {
+      const uint8_t* w;
+      const uint8_t* xq;
+      const float* bias;
+      float* y;
+      int64_t stride;
+      int32_t out, in, rows, pad;
+      const void* items;
+      const int* perm;
+      int32_t x_per_slot, pad2;
+      const float* x;
+      double* part;
+      int32_t ksplit, klen;
+    } g = {(const uint8_t*)k.w, (const uint8_t*)xq, (const float*)k.bias, (float*)k.y, k.stride,
+           (int32_t)k.out, (int32_t)k.in, (int32_t)k.rows, 0, (const void*)k.items,
+           (const int*)k.perm, k.x_per_slot, 0, (const float*)k.x, nullptr, 1, 0};
+    snprintf(name, sizeof name, "gemm8_%s", fmt_name(k.dtype));
+    const int64_t tiles8 = (k.out + 127) / 128;
+    const unsigned gy8 = (unsigned)(k.items ? k.nitems : (k.rows + 7) / 8);
+    const int64_t hold = (int64_t)c->cus * std::max(1, resident_blocks(c, name, 256));
+    const int64_t per_chunk = (hold + gy8 - 1) / gy8;
+    const int64_t gx8 = std::max<int64_t>(1, std::min(tiles8, per_chunk));
+    return launch(c, name, dim3((unsigned)gx8, gy8), dim3(256), &g);
+  }
   if (batch && q8 && !k.w2 && !k.dtype2 && k.in <= 8192 && !float_fmt(k.dtype)) {
     // a small batch of quantized rows: the rows staged in LDS once per block,
     // each weight group loaded and decoded once for all of them (gemv_rows)

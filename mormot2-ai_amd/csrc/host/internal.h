@@ -60,6 +60,7 @@ struct ihip_ctx {
   int gemm_min_rows = ihip::GEMM_MIN_ROWS;  // the smallest chunk on the GEMM (IHIP_GEMM_MIN_ROWS)
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
+  bool use_gemm8 = true;  // 2..79 quantized rows on the int8 matrix cores, gemm8 (IHIP_GEMM8=0: the VALU gemv_rows)
   bool gemm_split = true;  // float-weight GEMMs of few tiles split over the sum (IHIP_GEMM_SPLIT=0: off)
   bool attn_mfma = true;  // prompt attention ranges on the f64 matrix cores (IHIP_ATTN_MFMA=0: VALU tiles of 8 rows)
   hipStream_t stream = nullptr;

@@ -372,6 +372,248 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
   }
 }
 
+// ------------------------------------------------ a small batch of rows
+// gemm8: the same arithmetic for at most 8 activation rows (blockIdx.y: a
+// chunk of 8 rows, or a grouped-expert item of at most 8 slots), the weights
+// streamed once: a block owns 128 outputs (4 waves of 32) and walks the
+// output tiles of its grid share. Per 32-value group a wave runs the MFMA of
+// the big GEMM with the rows in A lanes 0..7 (lanes 8..31 zero): of its
+// result registers, 0..3 hold the 8 rows x 32 outputs, one (row, output) per
+// lane and register, so the scaling in double wastes no lane. The chunks of
+// GKC groups (128 weight columns, 8 activation rows) are loaded coalesced
+// into registers a chunk ahead, then through LDS to the lanes.
+constexpr int G8N = 128;  // outputs of a block tile
+
+struct Chunk8 {
+  Raw wr[4];    // weight groups: column t / 8 + 32 p, group t % 8
+  v4u32 xc[2];  // activation codes (t < 64): row t / 8, group t % 8
+  float dx;
+};
+
+template <int F>
+__device__ __forceinline__ void chunk8_load(const GemmArgs& a, const uint8_t* wb, const Regions& rg,
+                                            int col0, const int* sxr, int64_t xstride, int G, int gc,
+                                            Chunk8& cr)
+{
+  const int t = threadIdx.x;
+  const int g = min(gc + (t & 7), G - 1);
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const int64_t o = min(col0 + (t >> 3) + 32 * p, a.out - 1);
+    load_group<F, true>(wb, rg, o, G, g, a.in, cr.wr[p]);
+  }
+  if (t < 64) {
+    const uint8_t* xr = a.xq + (int64_t)sxr[t >> 3] * xstride;
+    const v4u32* q = (const v4u32*)(xr + (int64_t)g * 32);
+    cr.xc[0] = q[0];
+    cr.xc[1] = q[1];
+    cr.dx = ((const float*)(xr + a.in))[g];
+  }
+}
+
+template <int F>
+__device__ __forceinline__ void chunk8_store(const Chunk8& cr, uint32_t* sw, uint32_t* sa, float* sdx,
+                                             int* sbs)
+{
+  const int t = threadIdx.x;
+  constexpr int WS = GKC * raw_dwords<F>() + 1;
+#pragma unroll
+  for (int p = 0; p < 4; p++) raw_put<F>(sw + ((t >> 3) + 32 * p) * WS + (t & 7), GKC, cr.wr[p]);
+  if (t < 64) {
+    const int row = t >> 3, j = t & 7;
+    uint32_t* d = sa + row * GSA + j * 8;
+    *(v4u32*)d = cr.xc[0];
+    *(v4u32*)(d + 4) = cr.xc[1];
+    sdx[j * 8 + row] = cr.dx;
+    if constexpr (needs_xsum(F)) {
+      const v4u32 u0 = cr.xc[0], u1 = cr.xc[1];
+      int sm = 0;
+      sm = sdot4((int)u0.x, 0x01010101, sm); sm = sdot4((int)u0.y, 0x01010101, sm);
+      sm = sdot4((int)u0.z, 0x01010101, sm); sm = sdot4((int)u0.w, 0x01010101, sm);
+      sm = sdot4((int)u1.x, 0x01010101, sm); sm = sdot4((int)u1.y, 0x01010101, sm);
+      sm = sdot4((int)u1.z, 0x01010101, sm); sm = sdot4((int)u1.w, 0x01010101, sm);
+      sbs[j * 8 + row] = sm;
+    }
+  }
+}
+
+template <int F>
+__device__ __forceinline__ void gemm8(const GemmArgs& a)
+{
+  constexpr int WS = GKC * raw_dwords<F>() + 1;
+  __shared__ uint32_t sw_[G8N * WS];
+  __shared__ __align__(16) uint32_t sa_[8 * GSA];
+  __shared__ __align__(16) float sdx_[GKC * 8];
+  __shared__ int sbs_[needs_xsum(F) ? GKC * 8 : 1];
+  __shared__ int sxr[8], syr[8];
+  const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5;
+  const int G = a.in >> 5;
+  const int64_t xstride = (int64_t)a.in + 4 * (int64_t)G;
+  const uint8_t* wb = a.w;
+  const float* bias = a.bias;
+  int nrows;
+  if (a.items) {
+    const int4 it = a.items[blockIdx.y];
+    if (it.z <= 0) return;
+    wb += (int64_t)it.x * a.stride;
+    if (bias) bias += (int64_t)it.x * a.out;
+    nrows = min(8, it.z);
+    if (t < 8) {
+      const int sl = a.perm[it.y + min(t, nrows - 1)];
+      sxr[t] = a.x_per_slot ? sl / a.x_per_slot : 0;
+      syr[t] = sl;
+    }
+  } else {
+    const int r0 = blockIdx.y * 8;
+    nrows = min(8, a.rows - r0);
+    if (t < 8) sxr[t] = syr[t] = r0 + min(t, nrows - 1);
+  }
+  __syncthreads();
+  const Regions rg = regions(F, a.out, a.in);
+  const int ntiles = (a.out + G8N - 1) / G8N;
+  const int nch = (G + GKC - 1) / GKC;
+  // this block's (tile, chunk) steps, tile-major: step q is chunk q % nch of
+  // tile blockIdx.x + (q / nch) gridDim.x
+  const int mytiles = ((int)blockIdx.x < ntiles) ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int nsteps = mytiles * nch;
+  if (nsteps == 0) return;
+  const int arow = l & 31;  // A lane: row arow (rows 8.. are zero)
+  const uint32_t* myw = sw_ + (32 * w + (l & 31)) * WS;
+  const uint32_t* mya = sa_ + min(arow, 7) * GSA;
+  auto step_at = [&](int q, int& col0, int& gc) {
+    col0 = ((int)blockIdx.x + (q / nch) * (int)gridDim.x) * G8N;
+    gc = (q % nch) * GKC;
+  };
+  double acc[4];
+  int isum[4], msum[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    acc[i] = 0.0;
+    isum[i] = msum[i] = 0;
+  }
+  Chunk8 cr;
+  int col0, gc;
+  step_at(0, col0, gc);
+  chunk8_load<F>(a, wb, rg, col0, sxr, xstride, G, gc, cr);
+  chunk8_store<F>(cr, sw_, sa_, sdx_, sbs_);
+  if (nsteps > 1) {
+    int c1, g1;
+    step_at(1, c1, g1);
+    chunk8_load<F>(a, wb, rg, c1, sxr, xstride, G, g1, cr);
+  }
+  __syncthreads();
+  for (int q = 0; q < nsteps; q++) {
+    step_at(q, col0, gc);
+#pragma unroll
+    for (int j = 0; j < GKC; j++) {
+      const int g = gc + j;
+      if (g < G) {
+        const Raw r = raw_get<F>(myw + j, GKC);
+        uint2 x0 = *(const uint2*)(mya + j * 8 + 2 * h);
+        uint2 x1 = *(const uint2*)(mya + j * 8 + 4 + 2 * h);
+        if (arow >= 8) x0 = x1 = make_uint2(0u, 0u);
+        const float* sdx = sdx_ + j * 8;
+        const int* sbs = sbs_ + (needs_xsum(F) ? j * 8 : 0);
+        const v4i bv = b_operand<F>(r, h);
+        v16i s;
+        v16i s2 = {};
+        if constexpr (F == DT_Q6_K) {
+          const v16i z = {};
+          s = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+              (long)(((uint64_t)x0.y << 32) | x0.x),
+              (long)(((uint64_t)(uint32_t)bv.y << 32) | (uint32_t)bv.x), z, 0, 0, 0);
+          s2 = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+              (long)(((uint64_t)x1.y << 32) | x1.x),
+              (long)(((uint64_t)(uint32_t)bv.w << 32) | (uint32_t)bv.z), z, 0, 0, 0);
+        } else {
+          const v4i av = {(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+          const v16i z = {};
+          s = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z, 0, 0, 0);
+        }
+        // result register i < 4 of lane l: row 4 h + i, output l % 32
+        if constexpr (F == DT_Q4_K) {
+          int sc, mn;
+          scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, mn);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            isum[i] += __mul24(sc, s[i]);
+            msum[i] += __mul24(mn, sbs[4 * h + i]);
+          }
+          if ((g & 7) == 7) {
+            const double hd = half_to_float(r.q1.x & 0xffffu), hm = half_to_float(r.q1.x >> 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const double dx = sdx[4 * h + i];
+              acc[i] = acc[i] + ((hd * dx) * (double)isum[i] - (hm * dx) * (double)msum[i]);
+              isum[i] = msum[i] = 0;
+            }
+          }
+        } else if constexpr (F == DT_Q6_K) {
+          const int sa = (int)(int8_t)(r.a & 255u), sb = (int)(int8_t)(r.a >> 8);
+#pragma unroll
+          for (int i = 0; i < 4; i++) isum[i] += __mul24(sa, s[i]) + __mul24(sb, s2[i]);
+          if ((g & 7) == 7) {
+            const double d = half_to_float(r.d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const double dx = sdx[4 * h + i];
+              acc[i] = acc[i] + (d * dx) * (double)isum[i];
+              isum[i] = 0;
+            }
+          }
+        } else if constexpr (F == DT_Q5_1) {
+          const double d = half_to_float(r.a & 0xffffu), m = half_to_float(r.a >> 16);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const double dx = sdx[4 * h + i];
+            const double tt = (double)s[i] * (d * dx);
+            acc[i] = acc[i] + (tt + m * (dx * (double)sbs[4 * h + i]));
+          }
+        } else {
+          double dw;
+          if constexpr (F == DT_MXFP4) dw = mxfp4_q8_scale(r.a);
+          else dw = half_to_float(r.a);
+          const float4 d4 = *(const float4*)&sdx[4 * h];
+          const double dxs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[i] = __builtin_fma((double)s[i], dw * dxs[i], acc[i]);
+        }
+      }
+    }
+    __syncthreads();  // the chunk's LDS reads are done
+    if (q + 1 < nsteps) {
+      chunk8_store<F>(cr, sw_, sa_, sdx_, sbs_);
+      if (q + 2 < nsteps) {
+        int c2, g2;
+        step_at(q + 2, c2, g2);
+        chunk8_load<F>(a, wb, rg, c2, sxr, xstride, G, g2, cr);
+      }
+    }
+    // the tile's last chunk: its outputs, then a fresh sum
+    if (q % nch == nch - 1) {
+      const int o = col0 + 32 * w + (l & 31);
+      if (o < a.out) {
+        const double b = bias ? (double)bias[o] : 0.0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int rt = 4 * h + i;
+          if (rt < nrows) {
+            double v = acc[i];
+            if (bias) v = b + v;
+            a.y[(int64_t)syr[rt] * a.out + o] = (float)v;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        acc[i] = 0.0;
+        isum[i] = msum[i] = 0;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------- float weights
 // y[r, o] = bias[o] + sum_i x[r, i] w[o, i] for F32 / BF16 / F16 weights in
 // the Q8 arithmetic of TInferCpuBackend.Linear's float branch
@@ -505,8 +747,13 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
 
 }  // namespace ihip
 
-#define IHIP_GEMM(NAME, F) \
-  extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm<F>(a); }
+#define IHIP_GEMM(NAME, F)                                                                      \
+  extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm<F>(a); } \
+  extern "C" __global__ __launch_bounds__(256) void gemm8_##NAME(ihip::GemmArgs a)                    \
+  {                                                                                                 \
+    ihip::touch_kernargs<sizeof(ihip::GemmArgs)>();                                                 \
+    ihip::gemm8<F>(a);                                                                              \
+  }
 
 #define IHIP_GEMM_FLT(NAME, F) \
   extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm_flt<F>(a); }

@@ -155,6 +155,31 @@ def test_linear_q8_mode_cpu_bits(ctx, dtype):
     assert differ <= max(2, total // 1000), (differ, total)
 
 
+# small batches whose 128-output tiles fill the chip run on the int8 matrix
+# cores (gemm8: 8 rows per block, the weights read once per 8 rows); the
+# last row chunk partial, rows past it absent
+GEMM8_SHAPES = [(8, 256, 40000), (3, 512, 33000), (13, 1024, 32896), (2, 2048, 36000)]
+
+
+@pytest.mark.parametrize("dtype", BLOCK_FMTS)
+def test_gemm8_q8_mode_cpu_bits(ctx, dtype):
+    rng = np.random.default_rng(11)
+    total, differ = 0, 0
+    for rows, cols, out in GEMM8_SHAPES:
+        if not fits(dtype, cols):
+            continue
+        w = weights(dtype, out, cols, rows * 31 + cols + out)
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        b = rng.standard_normal(out).astype(np.float32) if rows != 3 else None
+        y = ctx.linear(x, w, dtype, out, b, mode=H.MODE_Q8)
+        ref = O.linear(x, w, dtype, out, b)
+        u = ulp_diff(y, ref)
+        assert u.max() <= 1, (H.NAMES[dtype], rows, cols, out, int(u.max()))
+        total += u.size
+        differ += int(np.count_nonzero(u))
+    assert differ <= max(2, total // 1000), (differ, total)
+
+
 GEMM_FMTS = [H.Q8_0, H.Q4_0, H.MXFP4, H.Q5_0, H.Q5_1, H.Q4_K, H.Q6_K, H.F32, H.BF16, H.F16]
 GEMM_SHAPES = [(16, 256, 64), (64, 2048, 1024), (200, 768, 136), (130, 2560, 100), (40, 2880, 70)]
 
