@@ -894,7 +894,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
 #pragma unroll
     for (int r = 0; r < R; r++) {
       if (pstart >= 0) {
-        int s = r < nrows ? a.perm[pstart + r] : 0;
+        int s = a.perm[pstart + min(r, nrows - 1)];  // (a row past the item: its last slot, unused)
         xr[r] = a.x_per_slot ? s / a.x_per_slot : 0;
         yr[r] = s;
       } else {
@@ -1027,7 +1027,9 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
     nrows = min(RB, it.z);
 #pragma unroll
     for (int r = 0; r < RB; r++) {
-      const int sl = r < nrows ? a.perm[it.y + r] : 0;
+      // every load issued before the first is used (a row past the item's
+      // reads its last slot, unused)
+      const int sl = a.perm[it.y + min(r, nrows - 1)];
       xr[r] = a.x_per_slot ? sl / a.x_per_slot : 0;
       yr[r] = sl;
     }
@@ -1037,6 +1039,24 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
 #pragma unroll
     for (int r = 0; r < RB; r++) xr[r] = yr[r] = r0 + r;
   }
+  const Regions rg = regions(F, a.out, a.in);
+  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
+  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
+  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
+  Raw cur[TB][U], nxt[TB][U];
+  // the weights of a step: TB tiles, every load issued before the first use
+  auto load = [&](int64_t sb, Raw (&raw)[TB][U]) {
+#pragma unroll
+    for (int i = 0; i < TB; i++) {
+      const int64_t o = min((sb + (int64_t)i * nw) * rpw + rsub, (int64_t)a.out - 1);
+#pragma unroll
+      for (int k = 0; k < U; k++) {
+        const int g = min(lr + k * lpr, G - 1);
+        load_group<F, true, F == DT_Q4_K>(w, rg, o, G, g, a.in, raw[i][k]);
+      }
+    }
+  };
+  int64_t tb = wid;
   // the stage: each thread takes groups of the rows (16-byte loads of the
   // codes, the half sums formed here once)
   const int64_t qstride = (int64_t)a.in + 4 * (int64_t)G;
@@ -1057,26 +1077,7 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
     ((int2*)(dst + 36 * G))[g] = make_int2(sl, sh);
   }
   __syncthreads();
-
-  const Regions rg = regions(F, a.out, a.in);
-  const int64_t tiles = ((int64_t)a.out + rpw - 1) / rpw;
-  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
-  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
   if (wid >= tiles) return;  // after the stage: every thread took its share
-  Raw cur[TB][U], nxt[TB][U];
-  // the weights of a step: TB tiles, every load issued before the first use
-  auto load = [&](int64_t sb, Raw (&raw)[TB][U]) {
-#pragma unroll
-    for (int i = 0; i < TB; i++) {
-      const int64_t o = min((sb + (int64_t)i * nw) * rpw + rsub, (int64_t)a.out - 1);
-#pragma unroll
-      for (int k = 0; k < U; k++) {
-        const int g = min(lr + k * lpr, G - 1);
-        load_group<F, true, F == DT_Q4_K>(w, rg, o, G, g, a.in, raw[i][k]);
-      }
-    }
-  };
-  int64_t tb = wid;
   load(tb, cur);
   while (tb < tiles) {
     const int64_t nb = tb + (int64_t)TB * nw;
