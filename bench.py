@@ -300,6 +300,7 @@ def main():
     ap.add_argument("--sample-steps", type=int, default=32,
                     help="decode steps with device sampling after the greedy ones (0: none)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-f32", action="store_true", help="skip the F32-mode decode leg")
     ap.add_argument("--kv-f32", action="store_true")
     ap.add_argument("--no-graphs", action="store_true",
                     help="direct launches per decode step (the profiler cannot trace graphs)")
@@ -381,6 +382,28 @@ def main():
         log(f"  {k:40s} {v}")
     model.close()
 
+    # the same decode in the reference GPU's own contract (IHIP_MODE_F32: float
+    # activations, each code dequantized exactly, f32 sums per group;
+    # linear.cu:1-6), after the same prompt
+    f32_mode = None
+    if not args.no_f32:
+        mf = H.Model(ctx, spec, mode=H.MODE_F32, kv_f16=not args.kv_f32, max_tokens=max_tokens)
+        t = time.perf_counter()
+        lgf = mf.forward(prompt)
+        f32_prefill = time.perf_counter() - t
+        idf = mf.decode(int(np.argmax(lgf)), 8)
+        ctx.sync()
+        t = time.perf_counter()
+        mf.decode(int(idf[-1]), 64)
+        ctx.sync()
+        ft = (time.perf_counter() - t) / 64
+        mf.close()
+        f32_mode = {"tok_s": round(1.0 / ft, 1), "ms_per_token": round(ft * 1e3, 4), "steps": 64,
+                    "prefill_ms": round(f32_prefill * 1e3, 1),
+                    "arithmetic": "f32 activations x exactly dequantized codes, f32 group sums"}
+        log(f"f32-mode decode 64 steps: {ft * 1e3:.3f} ms/token, {1.0 / ft:.1f} tok/s "
+            f"(prefill {f32_prefill * 1e3:.0f} ms)")
+
     sweep = {}
     if not args.no_sweep:
         for dtype in (H.Q8_0, H.Q4_0, H.Q4_K, H.Q6_K, H.MXFP4):
@@ -439,6 +462,7 @@ def main():
         "prefill_tok_s": round(args.prompt / prefill_s, 1),
         "prefill_first_ms": round(cold_s * 1e3, 2),
         "sampled_decode": sampled,
+        "f32_mode_decode": f32_mode,
         "decode_weight_GBps": round(wbytes * tok_s / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK,
                      "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK, 4),
