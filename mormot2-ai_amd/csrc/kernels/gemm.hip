@@ -192,7 +192,7 @@ __device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, u
     *(v4u32*)d = cr.xc[2 * k];
     *(v4u32*)(d + 4) = cr.xc[2 * k + 1];
     sdx[j * GBM + row] = cr.dx[k];
-    if constexpr (needs_xsum(F)) {
+    if constexpr (needs_xsum(F) && F != DT_Q4_K) {  // (Q4_K: the m_j sums on the matrix cores)
       const v4u32 u0 = cr.xc[2 * k], u1 = cr.xc[2 * k + 1];
       int sm = 0;
       sm = sdot4((int)u0.x, 0x01010101, sm); sm = sdot4((int)u0.y, 0x01010101, sm);
@@ -254,6 +254,10 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
     acc[i] = 0.0;
     isum[i] = msum[i] = 0;
   }
+  // Q4_K: the super-block's minimum sum sum_j m_j bsum_j kept on the matrix
+  // cores: A times the group's m_j broadcast (m < 64), accumulated over the
+  // 8 groups of the super-block, exact int32
+  v16i cm = {};
 
   // chunk c + 1 is in registers (its loads issued during chunk c - 1) while
   // chunk c is computed from LDS; loads past the last group read the last
@@ -280,6 +284,28 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
           const v4i bv = b_operand<F>(r, h);
           v16i s;
           v16i s2 = {};
+          if constexpr (F == DT_Q4_K) {
+            int sc, mn;
+            scale_min_k4(g & 7, r.q1.y, r.q1.z, r.q1.w, sc, mn);
+            const int mb = (int)(((uint32_t)mn * 0x010101u) | ((uint32_t)mn << 24));
+            const v4i bm = {mb, mb, mb, mb};
+            const v4i av = {(int)x0.x, (int)x0.y, (int)x1.x, (int)x1.y};
+            const v16i z = {};
+            s = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z, 0, 0, 0);
+            cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bm, (g & 7) == 0 ? z : cm, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) isum[i] += __mul24(sc, s[i]);  // |sums| < 2^16, sc < 64
+            if ((g & 7) == 7) {  // (Q4_K rows hold whole super-blocks)
+              const double hd = half_to_float(r.q1.x & 0xffffu), hm = half_to_float(r.q1.x >> 16);
+#pragma unroll
+              for (int i = 0; i < 16; i++) {
+                const double dx = sdx[j][rb + 8 * (i >> 2) + (i & 3)];
+                acc[i] = acc[i] + ((hd * dx) * (double)isum[i] - (hm * dx) * (double)cm[i]);
+                isum[i] = 0;
+              }
+            }
+            continue;
+          }
           if constexpr (F == DT_Q6_K) {
             // the two 16-value sub-blocks of the group, each its own sum
             const v16i z = {};
