@@ -190,7 +190,7 @@ def decode_kernels(ctx, model, spec, first, steps, past):
     out = {}
     model.use_graphs(False)
     tok = first
-    for key, prefix in (("dominant", dom_name), ("attention", "attention_one")):
+    for key, prefix in (("dominant", dom_name), ("attention", "attention_")):
         ctx.kernel_timer(prefix, capacity=steps * c["layers"] + 64)
         ids = model.decode(tok, steps)
         n, ms = ctx.kernel_timer_read()
