@@ -177,7 +177,7 @@ constexpr int GSW = GKC * raw_dwords<DT_Q8_0>() + 1;  // LDS dwords per weight c
 constexpr int GSA = GKC * 8 + 2;                     // LDS dwords per activation row
 
 template <int F>
-__device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, uint32_t* sa, float* sdx,
+__device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, uint32_t* sa, double* sdx,
                                             int* sbs)
 {
   const int t = threadIdx.x;
@@ -191,7 +191,7 @@ __device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, u
     uint32_t* d = sa + row * GSA + j * 8;
     *(v4u32*)d = cr.xc[2 * k];
     *(v4u32*)(d + 4) = cr.xc[2 * k + 1];
-    sdx[j * GBM + row] = cr.dx[k];
+    sdx[j * GBM + row] = (double)cr.dx[k];  // widened once here, not per output
     if constexpr (needs_xsum(F) && F != DT_Q4_K) {  // (Q4_K: the m_j sums on the matrix cores)
       const v4u32 u0 = cr.xc[2 * k], u1 = cr.xc[2 * k + 1];
       int sm = 0;
@@ -211,7 +211,7 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
   // the rows' scales and code sums
   __shared__ uint32_t sw_[GBN * GSW];
   __shared__ __align__(16) uint32_t sa_[GBM * GSA];
-  __shared__ __align__(16) float sdx_[GKC * GBM];
+  __shared__ __align__(16) double sdx_[GKC * GBM];
   __shared__ int sbs_[needs_xsum(F) ? GKC * GBM : 1];
   __shared__ int sxr[GBM], syr[GBM];
   const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5;
@@ -277,7 +277,7 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
         const Raw r = raw_get<F>(myw + j, GKC);
         const uint2 x0 = *(const uint2*)(mya + j * 8 + 2 * h);
         const uint2 x1 = *(const uint2*)(mya + j * 8 + 4 + 2 * h);
-        float (*sdx)[GBM] = (float (*)[GBM])sdx_;
+        double (*sdx)[GBM] = (double (*)[GBM])sdx_;
         int (*sbs)[GBM] = (int (*)[GBM])sbs_;
         const int buf = 0;
         (void)buf;
@@ -368,13 +368,13 @@ __device__ __forceinline__ void gemm(const GemmArgs& a)
             // s * dw * dx is exact in double (at most 19 + 11 + 11 significant
             // bits), so one fused multiply-add rounds as the CPU's multiply-then-add
             // the 16 rows' scales: four 16-byte LDS reads, all issued first
-            float4 dq[4];
+            double2 dq[8];
 #pragma unroll
-            for (int q = 0; q < 4; q++) dq[q] = *(const float4*)&sdx[j][rb + 8 * q];
+            for (int q = 0; q < 8; q++) dq[q] = *(const double2*)&sdx[j][rb + 8 * (q >> 1) + 2 * (q & 1)];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-              const float4 d4 = dq[i >> 2];
-              const double dx = (i & 3) == 0 ? d4.x : (i & 3) == 1 ? d4.y : (i & 3) == 2 ? d4.z : d4.w;
+              const double2 d2 = dq[i >> 1];
+              const double dx = (i & 1) ? d2.y : d2.x;
               acc[i] = __builtin_fma((double)s[i], dw * dx, acc[i]);
             }
           }
