@@ -413,6 +413,49 @@ int ihip_context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t 
                         int32_t* out_ids);
 int ihip_context_decode(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out_ids);
 
+/* ---- TNativeLlmClient's device side (src/mormot.ai.llm.native.pas) ----
+ * The tokenizer, chat template and output parser stay the caller's; the
+ * parser's stop is given as token ids. */
+/* NativeDecode (llm.native.pas:2135-2185) on a context: the prompt's cached
+ * start kept (Reuse), the rest computed, then draws of a fresh TInferSampler
+ * (`sampling`, NULL or temperature <= 0: greedy) among the first draw_ids
+ * rows of the logits (<= 0: the vocabulary; the ids a tokenizer has), each
+ * drawn token fed back until one of stop_ids is drawn or max_new tokens are
+ * out. The context is limited to max_positions, or max_context when smaller
+ * and > 0: a longer prompt is refused, max_new is cut to what fits. The last
+ * drawn token is not fed (the context holds n + count - 1 tokens).
+ * out_ids[max_new] receives the tokens, *out_count their number, *reused the
+ * prompt tokens kept from the cache, *stopped whether a stop id ended it
+ * (reused and stopped may be NULL). */
+int ihip_native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                       const ihip_sampling* sampling, int64_t draw_ids, const int32_t* stop_ids,
+                       int64_t nstop, int64_t max_context, int32_t* out_ids, int64_t* out_count,
+                       int64_t* reused, int* stopped);
+/* TNativePromptCache (llm.native.pas:2192-2350): up to `slots` idle contexts
+ * of a model kept between requests, least recently used first */
+typedef struct ihip_prompt_cache ihip_prompt_cache;
+int ihip_prompt_cache_create(ihip_model* m, int64_t slots, ihip_prompt_cache** out);
+/* frees the idle contexts (a context acquired and not released stays the
+ * caller's) */
+void ihip_prompt_cache_destroy(ihip_prompt_cache* pc);
+/* SetSlots: the least recently used beyond the new count are freed */
+int ihip_prompt_cache_set_slots(ihip_prompt_cache* pc, int64_t slots);
+/* Clear: every idle context freed */
+int ihip_prompt_cache_clear(ihip_prompt_cache* pc);
+/* Acquire: the idle context sharing the longest start with the prompt (its
+ * last token excluded, as Reuse computes it again); with none shared and the
+ * cache full, the least recently used; else a new context. The context is
+ * the caller's until released. */
+int ihip_prompt_cache_acquire(ihip_prompt_cache* pc, const int32_t* prompt, int64_t n, ihip_mctx** out);
+/* Release: counts the request (a hit when reused > 0) and keeps the context
+ * as the most recently used (with no slot it is freed; a full cache frees
+ * its least recently used) */
+int ihip_prompt_cache_release(ihip_prompt_cache* pc, ihip_mctx* s, int64_t reused);
+/* the requests, hits and reused tokens counted so far, and the idle contexts
+ * (any pointer may be NULL) */
+int ihip_prompt_cache_stats(ihip_prompt_cache* pc, int64_t* requests, int64_t* hits, int64_t* reused,
+                            int64_t* idle);
+
 /* ======================================================================
  * GGUF v3 files (TGgufFile, src/infer/mormot.ai.infer.loader.gguf.pas:94-170)
  * and the decoder description of a llama.cpp file

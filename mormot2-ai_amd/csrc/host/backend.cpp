@@ -945,16 +945,6 @@ int ihip_enqueue_argmax(ihip_ctx* c, uint64_t v, int64_t n, uint64_t out)
 
 }  // extern "C"
 
-// TInferSampler (sampler.pas:52-435) on the device: the settings, the
-// splitmix64 state and the buffers of sample_probs / _compact / _pick
-struct ihip_sampler {
-  ihip_ctx* c = nullptr;
-  double temperature = 0, top_p = 1, min_p = 0;
-  int32_t top_k = 0;
-  int64_t n_max = 0;
-  std::vector<void*> mem;
-  uint64_t state = 0, p = 0, bsum = 0, bq = 0, bcnt = 0, bmass = 0, cid = 0, ckey = 0, cp = 0;
-};
 
 namespace {
 constexpr int SAMPLE_BUCKETS = 128, SAMPLE_MAX_BLOCKS = 256;

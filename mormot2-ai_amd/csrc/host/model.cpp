@@ -61,6 +61,9 @@ struct ihip_mctx {
   bool graph_ready = false;
   int64_t graph_capacity = 0;
   int graph_sampler = -1;
+  // the rows of the logits a draw considers (0: the vocabulary; NativeDecode
+  // draws among the ids its tokenizer has), and the count the graph holds
+  int64_t draw_ids = 0, graph_draw = -1;
   double prefill_ms = 0, decode_ms = 0;
   bool is_default = false;  // the model's own context (ihip_model_*), freed with it
 };
@@ -607,8 +610,9 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
 static int next_token(ihip_mctx* s)
 {
   ihip_model* m = s->m;
-  return m->sampler ? ihip_enqueue_sample(m->c, m->sampler, s->logits, m->d.vocab, s->next)
-                    : ihip_enqueue_argmax(m->c, s->logits, m->d.vocab, s->next);
+  const int64_t n = s->draw_ids > 0 ? std::min<int64_t>(s->draw_ids, m->d.vocab) : m->d.vocab;
+  return m->sampler ? ihip_enqueue_sample(m->c, m->sampler, s->logits, n, s->next)
+                    : ihip_enqueue_argmax(m->c, s->logits, n, s->next);
 }
 
 // the decode step as a graph: embed(tok) -> layers(pos) -> head -> next id
@@ -659,6 +663,7 @@ static int decode_graph(ihip_mctx* s)
   s->graph_ready = true;
   s->graph_capacity = s->capacity;
   s->graph_sampler = m->sampler_epoch;
+  s->graph_draw = s->draw_ids;
   return 0;
 }
 
@@ -785,7 +790,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   // a graph holds this context's cache and ranges: captured again when the
   // cache grew or the sampler changed since
   if (m->use_graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
-                        s->graph_sampler != m->sampler_epoch) &&
+                        s->graph_sampler != m->sampler_epoch || s->graph_draw != s->draw_ids) &&
       (rc = decode_graph(s)))
     return rc;
   std::vector<float> cs(m->d.head_dim);
@@ -973,6 +978,105 @@ static int context_decode(ihip_mctx* s, int32_t first, int64_t steps, int32_t* o
   return rc;
 }
 
+// ---------------------------------------------------------------------
+// TNativeLlmClient's device side (src/mormot.ai.llm.native.pas): NativeDecode
+// (:2135-2185), one request on a context, and TNativePromptCache
+// (:2192-2350), the contexts kept between requests for their prompts. The
+// tokenizer, chat template and output parser stay the caller's: the parser's
+// stop is a set of token ids here.
+
+// the cached tokens of s that start prompt, at most count of them (a position
+// fed an embedding row matches no id): TDecoderContext.Usable
+static int64_t usable(const ihip_mctx* s, const int32_t* prompt, int64_t count)
+{
+  int64_t n = 0;
+  const int64_t lim = std::min<int64_t>(std::max<int64_t>(count, 0), s->length);
+  while (n < lim && s->ids[n] >= 0 && s->ids[n] == prompt[n]) n++;
+  return n;
+}
+
+// the draws of a request from a fresh TInferSampler: the model's sampler kept
+// when its settings are the request's (its stream restarted at the seed, the
+// decode graphs kept), else replaced (the graphs captured again)
+static int request_sampler(ihip_model* m, const ihip_sampling* smp)
+{
+  const bool greedy = !smp || !(smp->temperature > 0);
+  if (greedy) return m->sampler ? ihip_model_sampling(m, smp) : (smp ? ihip_model_sampling(m, smp) : 0);
+  ihip_sampler* k = m->sampler;
+  if (k && k->temperature == smp->temperature && k->top_k == smp->top_k && k->top_p == smp->top_p &&
+      k->min_p == smp->min_p) {
+    const uint64_t seed = (uint64_t)smp->seed;
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)k->state, (void*)&seed, 8, m->c->stream));
+    IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+    return 0;
+  }
+  return ihip_model_sampling(m, smp);
+}
+
+static int native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                         const ihip_sampling* smp, int64_t draw_ids, const int32_t* stop,
+                         int64_t nstop, int64_t max_context, int32_t* out_ids, int64_t* out_count,
+                         int64_t* reused, int* stopped)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  int64_t limit = d.max_positions > 0 ? d.max_positions : INT64_MAX;
+  if (max_context > 0 && max_context < limit) limit = max_context;
+  if (n < 1) return fail(IHIP_E_ARG, "NativeDecode: empty prompt");
+  if (n > limit)
+    return fail(IHIP_E_ARG, "NativeDecode: a prompt of " + std::to_string(n) +
+                                " tokens exceeds the context of " + std::to_string(limit));
+  if (max_new <= 0) return fail(IHIP_E_ARG, "NativeDecode: " + std::to_string(max_new) + " new tokens");
+  for (int64_t i = 0; i < n; i++)
+    if (prompt[i] < 0 || prompt[i] >= d.vocab) return fail(IHIP_E_ARG, "NativeDecode: token id outside the vocabulary");
+  // token k is fed at position n + k - 1 only when another one follows
+  if (max_new > limit - n + 1) max_new = limit - n + 1;
+  int rc = request_sampler(m, smp);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> g(m->c->lock);
+  s->draw_ids = draw_ids > 0 && draw_ids < d.vocab ? draw_ids : 0;
+  // the cached start of the prompt stays, the rest is computed
+  const int64_t kept = usable(s, prompt, n - 1);
+  s->length = kept;
+  if ((rc = prepare(s, n + max_new))) return rc;
+  for (int64_t done = kept; done < n && !rc;) {
+    const int64_t k = chunk_rows(s, s->length, n - done);
+    rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr);
+    done += k;
+  }
+  if (!rc) rc = next_token(s);
+  if (rc) return rc;
+  int32_t id = 0;
+  IHIP_CHECK(hipMemcpyDtoHAsync(&id, (hipDeviceptr_t)s->next, 4, m->c->stream));
+  IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+  int64_t count = 0;
+  bool stop_hit = false;
+  for (;;) {
+    out_ids[count++] = id;
+    for (int64_t i = 0; i < nstop && !stop_hit; i++) stop_hit = stop[i] == id;
+    if (stop_hit || count == max_new) break;
+    int32_t next = 0;
+    if ((rc = decode_steps(s, id, 1, &next))) return rc;
+    id = next;
+  }
+  *out_count = count;
+  if (reused) *reused = kept;
+  if (stopped) *stopped = stop_hit ? 1 : 0;
+  return 0;
+}
+
+}  // namespace ihip
+
+// the contexts kept between requests, least recently used first
+struct ihip_prompt_cache {
+  ihip_model* m = nullptr;
+  int64_t slots = 0;
+  std::mutex mu;
+  std::vector<ihip_mctx*> idle;
+  int64_t requests = 0, hits = 0, reused = 0;
+};
+
+namespace ihip {
 }  // namespace ihip
 
 using namespace ihip;
@@ -1216,6 +1320,135 @@ int ihip_model_sampling(ihip_model* m, const ihip_sampling* s)
   ihip_sampler_destroy(m->sampler);
   m->sampler = k;
   m->sampler_epoch++;  // every context's decode graph is captured again with it
+  return 0;
+}
+
+int ihip_native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
+                       const ihip_sampling* sampling, int64_t draw_ids, const int32_t* stop_ids,
+                       int64_t nstop, int64_t max_context, int32_t* out_ids, int64_t* out_count,
+                       int64_t* reused, int* stopped)
+{
+  if (!s || (!prompt && n > 0) || !out_ids || !out_count || nstop < 0 || (nstop > 0 && !stop_ids))
+    return fail(IHIP_E_ARG, "ihip_native_decode");
+  *out_count = 0;
+  return native_decode(s, prompt, n, max_new, sampling, draw_ids, stop_ids, nstop, max_context,
+                       out_ids, out_count, reused, stopped);
+}
+
+int ihip_prompt_cache_create(ihip_model* m, int64_t slots, ihip_prompt_cache** out)
+{
+  if (!m || !out || slots < 0) return fail(IHIP_E_ARG, "ihip_prompt_cache_create");
+  auto* pc = new ihip_prompt_cache;
+  pc->m = m;
+  pc->slots = slots;
+  *out = pc;
+  return 0;
+}
+
+static void free_contexts(std::vector<ihip_mctx*>& drop)
+{
+  for (ihip_mctx* x : drop) ihip_context_destroy(x);
+  drop.clear();
+}
+
+void ihip_prompt_cache_destroy(ihip_prompt_cache* pc)
+{
+  if (!pc) return;
+  free_contexts(pc->idle);
+  delete pc;
+}
+
+int ihip_prompt_cache_set_slots(ihip_prompt_cache* pc, int64_t slots)
+{
+  if (!pc || slots < 0) return fail(IHIP_E_ARG, "ihip_prompt_cache_set_slots");
+  std::vector<ihip_mctx*> drop;
+  {
+    std::lock_guard<std::mutex> g(pc->mu);
+    pc->slots = slots;
+    const int64_t n = (int64_t)pc->idle.size() - slots;
+    if (n > 0) {  // the least recently used go
+      drop.assign(pc->idle.begin(), pc->idle.begin() + n);
+      pc->idle.erase(pc->idle.begin(), pc->idle.begin() + n);
+    }
+  }
+  free_contexts(drop);
+  return 0;
+}
+
+int ihip_prompt_cache_clear(ihip_prompt_cache* pc)
+{
+  if (!pc) return fail(IHIP_E_ARG, "ihip_prompt_cache_clear");
+  std::vector<ihip_mctx*> drop;
+  {
+    std::lock_guard<std::mutex> g(pc->mu);
+    drop.swap(pc->idle);
+  }
+  free_contexts(drop);
+  return 0;
+}
+
+int ihip_prompt_cache_acquire(ihip_prompt_cache* pc, const int32_t* prompt, int64_t n, ihip_mctx** out)
+{
+  if (!pc || !out || (n > 0 && !prompt)) return fail(IHIP_E_ARG, "ihip_prompt_cache_acquire");
+  *out = nullptr;
+  {
+    std::lock_guard<std::mutex> g(pc->mu);
+    int64_t best = -1, longest = 0;
+    for (size_t i = 0; i < pc->idle.size(); i++) {
+      // as Reuse keeps them: the last token is always computed again
+      const int64_t common = usable(pc->idle[i], prompt, n - 1);
+      if (common > longest) {
+        longest = common;
+        best = (int64_t)i;
+      }
+    }
+    // no shared token: the buffers of the least recently used, once full
+    if (best < 0 && !pc->idle.empty() && (int64_t)pc->idle.size() >= pc->slots) best = 0;
+    if (best >= 0) {
+      *out = pc->idle[best];
+      pc->idle.erase(pc->idle.begin() + best);
+      return 0;
+    }
+  }
+  return ihip_model_new_context(pc->m, out);
+}
+
+int ihip_prompt_cache_release(ihip_prompt_cache* pc, ihip_mctx* s, int64_t reused)
+{
+  if (!pc) return fail(IHIP_E_ARG, "ihip_prompt_cache_release");
+  if (!s) return 0;
+  if (s->m != pc->m) return fail(IHIP_E_ARG, "ihip_prompt_cache_release: a context of another model");
+  ihip_mctx* drop = nullptr;
+  {
+    std::lock_guard<std::mutex> g(pc->mu);
+    pc->requests++;
+    if (reused > 0) {
+      pc->hits++;
+      pc->reused += reused;
+    }
+    if (pc->slots == 0) {
+      drop = s;
+    } else {
+      if ((int64_t)pc->idle.size() >= pc->slots) {
+        drop = pc->idle.front();
+        pc->idle.erase(pc->idle.begin());
+      }
+      pc->idle.push_back(s);
+    }
+  }
+  if (drop) ihip_context_destroy(drop);
+  return 0;
+}
+
+int ihip_prompt_cache_stats(ihip_prompt_cache* pc, int64_t* requests, int64_t* hits, int64_t* reused,
+                            int64_t* idle)
+{
+  if (!pc) return fail(IHIP_E_ARG, "ihip_prompt_cache_stats");
+  std::lock_guard<std::mutex> g(pc->mu);
+  if (requests) *requests = pc->requests;
+  if (hits) *hits = pc->hits;
+  if (reused) *reused = pc->reused;
+  if (idle) *idle = (int64_t)pc->idle.size();
   return 0;
 }
 

@@ -141,6 +141,16 @@ def lib():
             "ihip_context_length": (i32, [vp, C.POINTER(i64), C.POINTER(i64)]),
             "ihip_context_greedy": (i32, [vp, vp, i64, i64, vp]),
             "ihip_context_decode": (i32, [vp, C.c_int32, i64, vp]),
+            "ihip_native_decode": (i32, [vp, vp, i64, i64, C.POINTER(Sampling), i64, vp, i64, i64,
+                                         vp, C.POINTER(i64), C.POINTER(i64), C.POINTER(C.c_int)]),
+            "ihip_prompt_cache_create": (i32, [vp, i64, C.POINTER(vp)]),
+            "ihip_prompt_cache_destroy": (None, [vp]),
+            "ihip_prompt_cache_set_slots": (i32, [vp, i64]),
+            "ihip_prompt_cache_clear": (i32, [vp]),
+            "ihip_prompt_cache_acquire": (i32, [vp, vp, i64, C.POINTER(vp)]),
+            "ihip_prompt_cache_release": (i32, [vp, vp, i64]),
+            "ihip_prompt_cache_stats": (i32, [vp, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64),
+                                              C.POINTER(i64)]),
             "ihip_model_timing": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
             "ihip_synth_blocks": (i32, [vp, i32, i64, i64, u64, i32, i32, i32]),
             "ihip_synth_normal": (i32, [vp, i32, i64, i64, u64, C.c_float, i32]),
@@ -501,6 +511,85 @@ class ModelContext:
         out = np.empty(steps, np.int32)
         check(lib().ihip_context_decode(self.h, int(first), steps, _p(out)), "decode")
         return out
+
+    def native_decode(self, prompt, max_new, sampling_kw=None, stop=(), max_context=0,
+                      draw_ids=0):
+        """NativeDecode (llm.native.pas:2135-2185) on this context: returns
+        (tokens, prompt tokens reused from the cache, stopped by a stop id).
+        sampling_kw: the TInferSampling settings (None: greedy)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        st = np.ascontiguousarray(list(stop), np.int32)
+        out = np.empty(max(int(max_new), 1), np.int32)
+        n, reused, stopped = C.c_int64(), C.c_int64(), C.c_int()
+        smp = sampling(**sampling_kw) if sampling_kw else None
+        check(lib().ihip_native_decode(self.h, _p(p), len(p), int(max_new),
+                                       C.byref(smp) if smp is not None else None, int(draw_ids),
+                                       _p(st) if len(st) else None, len(st), int(max_context),
+                                       _p(out), C.byref(n), C.byref(reused), C.byref(stopped)),
+              "native_decode")
+        return out[:n.value].copy(), reused.value, bool(stopped.value)
+
+
+class PromptCache:
+    """TNativePromptCache (llm.native.pas:2192-2350): idle contexts of a model
+    kept between requests; acquire() hands out the one sharing the longest
+    start with a prompt, release() takes it back."""
+
+    def __init__(self, model, slots=1):
+        self.model = model
+        h = C.c_void_p()
+        check(lib().ihip_prompt_cache_create(model.h, int(slots), C.byref(h)), "prompt_cache")
+        self.h = h
+
+    def close(self):
+        if self.h and self.model.h:
+            lib().ihip_prompt_cache_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        if getattr(self, "h", None) and getattr(self.model, "h", None):
+            self.close()
+
+    def set_slots(self, slots):
+        check(lib().ihip_prompt_cache_set_slots(self.h, int(slots)), "set_slots")
+
+    def clear(self):
+        check(lib().ihip_prompt_cache_clear(self.h), "clear")
+
+    def acquire(self, prompt):
+        """A context for the prompt, the caller's until released."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        h = C.c_void_p()
+        check(lib().ihip_prompt_cache_acquire(self.h, _p(p), len(p), C.byref(h)), "acquire")
+        ctx = ModelContext.__new__(ModelContext)
+        ctx.model, ctx.own, ctx.vocab = self.model, False, self.model.vocab
+        ctx.hidden = self.model.spec.struct.hidden
+        ctx.h = h
+        return ctx
+
+    def release(self, ctx, reused):
+        check(lib().ihip_prompt_cache_release(self.h, ctx.h, int(reused)), "release")
+        ctx.h = None  # the cache's again
+
+    def stats(self):
+        r, hi, ru, idle = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int64()
+        check(lib().ihip_prompt_cache_stats(self.h, C.byref(r), C.byref(hi), C.byref(ru),
+                                            C.byref(idle)), "stats")
+        return {"requests": r.value, "hits": hi.value, "reused": ru.value, "idle": idle.value}
+
+
+def native_generate(cache, prompt, max_new, sampling_kw=None, stop=(), max_context=0, draw_ids=0):
+    """TNativeLlmClient.Generate's device part (llm.native.pas:2447-2481): a
+    context from the prompt cache, NativeDecode on it, the context back to
+    the cache (freed instead when the request fails)."""
+    ctx = cache.acquire(prompt)
+    try:
+        out = ctx.native_decode(prompt, max_new, sampling_kw, stop, max_context, draw_ids)
+    except Exception:
+        ctx.close()
+        raise
+    cache.release(ctx, out[1])
+    return out
 
 
 # ---------------------------------------------------------------- GGUF
