@@ -313,7 +313,25 @@ typedef struct {
   ihip_tensor exp_gate_bias, exp_up_bias, exp_down_bias; /* [E, fi], [E, fi], [E, h] */
   int32_t window;          /* sliding window, 0 = full attention */
   int32_t moe;             /* 1: the FFN is a mixture of experts */
+  /* Qwen3.5 (model.qwen35.pas:426-543, decoder.pas:2625-2855) */
+  int32_t mixer;           /* IHIP_MIXER_ATTENTION or IHIP_MIXER_DELTANET */
+  int32_t output_gate;     /* 1: q is [2 * heads * head_dim, h]: per head its
+                              query rows, then its gate rows (Spec.OutputGate) */
+  /* the Gated DeltaNet (mixer IHIP_MIXER_DELTANET): cd = 2 * key heads *
+   * key dim + value heads * value dim channels, vd = value heads * value dim */
+  ihip_tensor lin_qkv;     /* [cd, h]: the q, k and v channels */
+  ihip_tensor lin_z;       /* [vd, h]: the output gate */
+  ihip_tensor lin_b, lin_a; /* [value heads, h]: beta and the decay input */
+  ihip_tensor lin_out;     /* [h, vd] */
+  ihip_tensor lin_conv;    /* [cd, conv] F32: the depthwise causal convolution */
+  ihip_tensor lin_dt_bias; /* [value heads] F32 */
+  ihip_tensor lin_neg_a;   /* [value heads] F32: -exp(A_log) */
+  ihip_tensor lin_norm;    /* [value dim] F32: the gated RMSNorm's weight */
 } ihip_layer_desc;
+
+/* ihip_layer_desc.mixer (TDecoderMixer, decoder.pas:95-105) */
+#define IHIP_MIXER_ATTENTION 0
+#define IHIP_MIXER_DELTANET 1
 
 /* the settings of TDecoderConfig (decoder.pas:158-225) that this path reads */
 typedef struct {
@@ -330,6 +348,14 @@ typedef struct {
   double rope_attention;
   ihip_tensor embed, final_norm, head; /* head.data NULL: tied to embed */
   const ihip_layer_desc* layer;        /* [layers] */
+  /* the rotating values of every head, from its start (RopeDims,
+   * decoder.pas:216; 0: the whole head) */
+  int32_t rope_dims;
+  /* the DeltaNet shapes (decoder.pas:217-224), 0 without such a layer */
+  int32_t lin_key_heads, lin_value_heads, lin_key_dim, lin_value_dim, lin_conv;
+  /* LinTiled: value head h reads key head h mod key heads (llama.cpp's
+   * order), else key head h / (value heads / key heads) */
+  int32_t lin_tiled;
 } ihip_model_desc;
 
 /* the model on the device: every weight uploaded (UploadWeights,

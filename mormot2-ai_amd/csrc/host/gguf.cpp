@@ -18,6 +18,8 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <cstdlib>
+#include <strings.h>
 #include <initializer_list>
 #include <cmath>
 #include <cstring>
@@ -407,7 +409,8 @@ namespace {
 struct DescBuilder {
   ihip_gguf* g;
   std::string arch;
-  int used = 0;  // tensors understood
+  int used = 0;    // tensors understood
+  int trunk = -1;  // the tensors of the model (-1: every tensor of the file)
 
   [[noreturn]] void refuse(const std::string& m) const { g->refuse(m); }
   // a count of the metadata, bounded (GgufCount, model.qwen3.pas:405-413)
@@ -676,6 +679,131 @@ struct DescBuilder {
     }
   }
 
+  // TQwen35Model.LoadGgufConfig / LoadWeights (model.qwen35.pas:371-452,
+  // :534-640): the Gated DeltaNet layers and the gated attention of qwen35
+  void qwen35(ihip_model_desc& d)
+  {
+    // weights folded with a Hadamard transform want it on the activations too
+    for (const Value& v : g->values)
+      if (v.key.size() >= 6 && strncasecmp(v.key.c_str(), "prism.", 6) == 0)
+        refuse(v.key + " (weights of a transformed basis) not supported");
+    if (has("rope.scaling.type") && g->str(arch + ".rope.scaling.type") != "none")
+      refuse("rope scaling \"" + g->str(arch + ".rope.scaling.type") + "\" not supported");
+    if (has("attention.sliding_window")) refuse("sliding window attention not supported");
+    const Tensor* emb = g->tensor("token_embd.weight");
+    if (!emb) refuse("no tensor token_embd.weight in " + g->name);
+    if (emb->ndim != 2 || emb->shape[0] > (1 << 22))
+      refuse(fmt("token_embd.weight is shaped [%lld...] of %d dimensions", (long long)emb->shape[0], emb->ndim));
+    d.vocab = (int32_t)emb->shape[0];
+    d.hidden = count("embedding_length");
+    // the multi-token prediction layers follow the model: not computed
+    const int32_t blocks = count("block_count");
+    const int64_t mtp = has("nextn_predict_layers") ? g->integer(arch + ".nextn_predict_layers") : 0;
+    if (mtp < 0 || mtp >= blocks) refuse(fmt("%lld prediction layers of %d blocks", (long long)mtp, blocks));
+    d.layers = blocks - (int32_t)mtp;
+    d.heads = count("attention.head_count");
+    d.kv_heads = count("attention.head_count_kv");
+    d.head_dim = count("attention.key_length");
+    if (has("attention.value_length") && count("attention.value_length") != d.head_dim)
+      refuse("key and value heads of different sizes");
+    d.ffn = count("feed_forward_length");
+    d.max_positions = count("context_length");
+    d.rms_eps = (float)g->real(arch + ".attention.layer_norm_rms_epsilon");
+    d.rope_theta = g->real(arch + ".rope.freq_base");
+    d.swiglu_alpha = 1.0f;
+    d.swiglu_limit = 0.0f;
+    d.rope_dims = count("rope.dimension_count");
+    if ((d.rope_dims & 1) || d.rope_dims > d.head_dim)
+      refuse(fmt("%d rotating values of a head of %d", d.rope_dims, d.head_dim));
+    d.lin_conv = count("ssm.conv_kernel");
+    d.lin_key_dim = count("ssm.state_size");
+    d.lin_key_heads = count("ssm.group_count");
+    d.lin_value_heads = count("ssm.time_step_rank");
+    const int32_t inner = count("ssm.inner_size");
+    if (inner % d.lin_value_heads)
+      refuse(fmt("an inner size of %d for %d value heads", inner, d.lin_value_heads));
+    d.lin_value_dim = inner / d.lin_value_heads;
+    // llama.cpp's converter tiles the value heads when they outnumber the key heads
+    d.lin_tiled = d.lin_value_heads != d.lin_key_heads;
+    // the kind of every layer: recurrent_layers, else every interval-th is full
+    const Value* rl = g->find(arch + ".attention.recurrent_layers");
+    if (rl && (rl->vtype != ARR || rl->etype != BOOLV || rl->count != blocks))
+      refuse(fmt("attention.recurrent_layers is no array of %d booleans", blocks));
+    int32_t interval = 4;
+    if (!rl && has("full_attention_interval")) interval = count("full_attention_interval");
+    check_config(d);
+    bool lin = false;
+    std::vector<int> rec((size_t)d.layers);
+    for (int i = 0; i < d.layers; i++) {
+      rec[i] = rl ? rl->data[i] != 0 : (i + 1) % interval != 0;
+      lin = lin || rec[i];
+    }
+    if (!lin) {
+      d.lin_key_heads = d.lin_value_heads = d.lin_key_dim = d.lin_value_dim = d.lin_conv = 0;
+      d.lin_tiled = 0;
+    } else if (d.lin_key_heads > 1024 || d.lin_value_heads > 1024 || d.lin_value_heads % d.lin_key_heads ||
+               d.lin_key_dim > 1024 || d.lin_value_dim > 1024 || d.lin_conv > 64) {
+      refuse(fmt("DeltaNet heads of %d x %d (keys) and %d x %d (values) with a convolution of %d",
+                 d.lin_key_heads, d.lin_key_dim, d.lin_value_heads, d.lin_value_dim, d.lin_conv));
+    }
+    const int64_t h = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd, kvw = (int64_t)d.kv_heads * hd;
+    const int64_t vh = d.lin_value_heads, vd = vh * d.lin_value_dim,
+                  cd = 2 * (int64_t)d.lin_key_heads * d.lin_key_dim + vd, kw = d.lin_conv;
+    d.embed = embedding(d);
+    d.final_norm = weight("output_norm.weight", {h});
+    // llama.cpp ties the head to the embedding by leaving output.weight out
+    d.head = g->tensor("output.weight") ? matrix("output.weight", d.vocab, h) : ihip_tensor{};
+    g->layers.assign((size_t)d.layers, ihip_layer_desc{});
+    for (int i = 0; i < d.layers; i++) {
+      ihip_layer_desc& L = g->layers[i];
+      const std::string b = "blk." + std::to_string(i) + ".";
+      L.input_norm = weight(b + "attn_norm.weight", {h});
+      L.post_norm = weight(b + "post_attention_norm.weight", {h});
+      L.gate = matrix(b + "ffn_gate.weight", d.ffn, h);
+      L.up = matrix(b + "ffn_up.weight", d.ffn, h);
+      L.down = matrix(b + "ffn_down.weight", h, d.ffn);
+      if (rec[i]) {
+        L.mixer = IHIP_MIXER_DELTANET;
+        L.lin_qkv = matrix(b + "attn_qkv.weight", cd, h);
+        L.lin_z = matrix(b + "attn_gate.weight", vd, h);
+        L.lin_b = matrix(b + "ssm_beta.weight", vh, h);
+        L.lin_a = matrix(b + "ssm_alpha.weight", vh, h);
+        L.lin_out = matrix(b + "ssm_out.weight", h, vd);
+        L.lin_conv = weight(b + "ssm_conv1d.weight", {cd, kw});
+        L.lin_dt_bias = weight(b + "ssm_dt.bias", {vh});
+        // ssm_a holds -exp(A_log): negative and finite, by its bits (a file
+        // holding A_log itself would let the state grow instead of decay)
+        L.lin_neg_a = weight(b + "ssm_a", {vh});
+        for (int64_t j = 0; j < vh; j++) {
+          uint32_t bits;
+          memcpy(&bits, (const float*)L.lin_neg_a.data + j, 4);
+          if (!(bits & 0x80000000u) || (bits & 0x7f800000u) == 0x7f800000u)
+            refuse(fmt("blk.%d.ssm_a[%lld] is no -exp(A_log)", i, (long long)j));
+        }
+        L.lin_norm = weight(b + "ssm_norm.weight", {d.lin_value_dim});
+      } else {
+        // per head the query rows, then the gate rows
+        L.output_gate = 1;
+        L.q = matrix(b + "attn_q.weight", 2 * qw, h);
+        L.k = matrix(b + "attn_k.weight", kvw, h);
+        L.v = matrix(b + "attn_v.weight", kvw, h);
+        L.o = matrix(b + "attn_output.weight", h, qw);
+        L.q_norm = weight(b + "attn_q_norm.weight", {hd});
+        L.k_norm = weight(b + "attn_k_norm.weight", {hd});
+      }
+    }
+    // the tensors of the layers after the model are not the model's
+    trunk = 0;
+    for (const Tensor& t : g->tensors) {
+      int64_t n = -1;
+      if (t.name.compare(0, 4, "blk.") == 0) {
+        size_t dot = t.name.find('.', 4);
+        if (dot != std::string::npos && dot > 4) n = atoll(t.name.substr(4, dot - 4).c_str());
+      }
+      if (n < d.layers) trunk++;
+    }
+  }
+
   // the token embedding: read per token, so its block scales are checked here
   ihip_tensor embedding(const ihip_model_desc& d)
   {
@@ -696,12 +824,15 @@ struct DescBuilder {
       qwen3(d, true);
     } else if (arch == "gpt-oss") {
       gptoss(d);
+    } else if (arch == "qwen35") {
+      qwen35(d);
     } else {
-      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, gpt-oss)");
+      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, gpt-oss, qwen35)");
     }
     // an unknown tensor means a model this path does not understand
-    if (used != (int)g->tensors.size())
-      refuse(fmt("%zu tensors in the file, %d understood", g->tensors.size(), used));
+    const int64_t expect = trunk >= 0 ? trunk : (int64_t)g->tensors.size();
+    if (used != expect)
+      refuse(fmt("%lld tensors of the model in the file, %d understood", (long long)expect, used));
     d.layer = g->layers.data();
     g->have_desc = true;
   }

@@ -357,10 +357,15 @@ _LAYER_TENSORS = ["input_norm", "q", "k", "v", "o", "q_bias", "k_bias", "v_bias"
                   "q_norm", "k_norm", "sinks", "post_norm", "gate", "up", "down", "router",
                   "router_bias", "exp_gate", "exp_up", "exp_down", "exp_gate_bias",
                   "exp_up_bias", "exp_down_bias"]
+_LIN_TENSORS = ["lin_qkv", "lin_z", "lin_b", "lin_a", "lin_out", "lin_conv", "lin_dt_bias",
+                "lin_neg_a", "lin_norm"]
+MIXER_ATTENTION, MIXER_DELTANET = 0, 1
 
 
 class LayerDesc(C.Structure):
-    _fields_ = [(n, Tensor) for n in _LAYER_TENSORS] + [("window", C.c_int32), ("moe", C.c_int32)]
+    _fields_ = [(n, Tensor) for n in _LAYER_TENSORS] + [
+        ("window", C.c_int32), ("moe", C.c_int32), ("mixer", C.c_int32),
+        ("output_gate", C.c_int32)] + [(n, Tensor) for n in _LIN_TENSORS]
 
 
 class ModelDesc(C.Structure):
@@ -372,7 +377,9 @@ class ModelDesc(C.Structure):
          ("rope_beta_fast", C.c_double), ("rope_beta_slow", C.c_double),
          ("rope_original", C.c_int32), ("rope_truncate", C.c_int32),
          ("rope_attention", C.c_double), ("embed", Tensor), ("final_norm", Tensor),
-         ("head", Tensor), ("layer", C.POINTER(LayerDesc))]
+         ("head", Tensor), ("layer", C.POINTER(LayerDesc))] + \
+        [(n, C.c_int32) for n in ("rope_dims", "lin_key_heads", "lin_value_heads",
+                                  "lin_key_dim", "lin_value_dim", "lin_conv", "lin_tiled")]
 
 
 class Model:

@@ -1,8 +1,9 @@
 /* model.c - TEST INFRASTRUCTURE ONLY (see oracle.h).
  * The CPU decoder: TDecoderModel.ForwardPart (decoder.pas:3245-3369) with
- * AttentionBlock (:2625-2702), DenseBlock/DenseFfn (:2866-2899), MoeBlock
- * (:3037-3053) and Experts (:3092-3150) over TInferCpuBackend, and Greedy
- * (:3390-3426). */
+ * AttentionBlock (:2625-2702, the output gate and partial rotary of Qwen3.5
+ * included), DeltaNetBlock (:2704-2753), DenseBlock/DenseFfn (:2866-2899),
+ * MoeBlock (:3037-3053) and Experts (:3092-3150) over TInferCpuBackend, and
+ * Greedy (:3390-3426). */
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -19,6 +20,11 @@ struct orc_model {
   double route_gap;
   float** keys;
   float** values;
+  /* per DeltaNet layer: the last conv - 1 inputs of every channel and the
+   * state S [value heads, value dim, key dim] (TDecoderContext.fConv/fState) */
+  float** conv;
+  float** state;
+  int recurrent;
 };
 
 static uint64_t row_bytes(int t, int64_t cols)
@@ -40,7 +46,18 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
   int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   m->keys = (float**)calloc(d->layers, sizeof(float*));
   m->values = (float**)calloc(d->layers, sizeof(float*));
+  m->conv = (float**)calloc(d->layers, sizeof(float*));
+  m->state = (float**)calloc(d->layers, sizeof(float*));
+  const int64_t cd = 2 * (int64_t)d->lin_key_heads * d->lin_key_dim +
+                     (int64_t)d->lin_value_heads * d->lin_value_dim;
   for (int l = 0; l < d->layers; l++) {
+    if (d->layer[l].mixer == IHIP_MIXER_DELTANET) {
+      m->recurrent = 1;
+      m->conv[l] = (float*)calloc(cd * (d->lin_conv > 1 ? d->lin_conv - 1 : 1), sizeof(float));
+      m->state[l] = (float*)calloc((int64_t)d->lin_value_heads * d->lin_value_dim * d->lin_key_dim,
+                                   sizeof(float));
+      continue;
+    }
     m->keys[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
     m->values[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
   }
@@ -57,6 +74,10 @@ void orc_model_set_fast(orc_model* m, int fast) { m->fast = fast && orc_fast_ava
 int orc_model_truncate(orc_model* m, int64_t length)
 {
   if (length < 0 || length > m->length) return IHIP_E_ARG;
+  /* a recurrent state holds the whole sequence: back to 0 only
+   * (TDecoderContext.Restorable, decoder.pas:1180-1197, without restore
+   * points) */
+  if (m->recurrent && length != 0 && length != m->length) return IHIP_E_ARG;
   m->length = length;
   return 0;
 }
@@ -89,9 +110,13 @@ void orc_model_destroy(orc_model* m)
   for (int l = 0; l < m->d.layers; l++) {
     free(m->keys[l]);
     free(m->values[l]);
+    free(m->conv[l]);
+    free(m->state[l]);
   }
   free(m->keys);
   free(m->values);
+  free(m->conv);
+  free(m->state);
   free(m->layer);
   free(m);
 }
@@ -136,7 +161,12 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
 {
   const ihip_model_desc* d = &m->d;
   int64_t h = d->hidden, hd = d->head_dim, qw = (int64_t)d->heads * hd,
-          kvw = (int64_t)d->kv_heads * hd, past = m->length, half = hd / 2;
+          kvw = (int64_t)d->kv_heads * hd, past = m->length;
+  const int64_t rot = d->rope_dims > 0 ? d->rope_dims : hd, half = rot / 2;
+  const int64_t kh = d->lin_key_heads, vh = d->lin_value_heads, dk = d->lin_key_dim,
+                dv = d->lin_value_dim, vd = vh * dv, cd = 2 * kh * dk + vd;
+  /* LinGroup (decoder.pas:2457-2463) */
+  const int64_t group = (d->lin_tiled || kh <= 0) ? 1 : vh / kh;
   int64_t f = d->ffn > d->expert_ffn ? d->ffn : d->expert_ffn;
   int err = 0;
   if (n <= 0 || past + n > m->max_tokens || (!ids && !embeds))
@@ -162,6 +192,13 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
   float* eout = (float*)malloc(n * h * 4);
   int64_t* rowi = (int64_t*)malloc(n * sizeof(int64_t));
   float* roww = (float*)malloc(n * 4);
+  float* qg = (float*)malloc(n * 2 * qw * 4);
+  float* gq = (float*)malloc(n * qw * 4);
+  float* qkv = (float*)malloc(n * (cd > 0 ? cd : 1) * 4);
+  float* z = (float*)malloc(n * (vd > 0 ? vd : 1) * 4);
+  float* beta = (float*)malloc(n * (vh > 0 ? vh : 1) * 4);
+  float* decay = (float*)malloc(n * (vh > 0 ? vh : 1) * 4);
+  float* core = (float*)malloc(n * (vd > 0 ? vd : 1) * 4);
 
   orc_rotary(d, past, n, cs);
   const float* cosv = cs;
@@ -173,17 +210,48 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
     memcpy(x, embeds, n * h * 4);
   for (int l = 0; l < d->layers && !err; l++) {
     const ihip_layer_desc* L = &m->layer[l];
+    if (L->mixer == IHIP_MIXER_DELTANET) {
+      /* DeltaNetBlock: pre-norm, the four projections, DeltaPrep, the
+       * recurrence, the gated RMSNorm per value head, the output projection */
+      orc_rmsnorm(x, n, h, (const float*)L->input_norm.data, d->rms_eps, hh);
+      err |= lin(m, hh, n, h, L->lin_qkv, 0, cd, NULL, qkv);
+      err |= lin(m, hh, n, h, L->lin_z, 0, vd, NULL, z);
+      err |= lin(m, hh, n, h, L->lin_b, 0, vh, NULL, beta);
+      err |= lin(m, hh, n, h, L->lin_a, 0, vh, NULL, decay);
+      if (past == 0) {
+        memset(m->conv[l], 0, cd * (d->lin_conv > 1 ? d->lin_conv - 1 : 1) * 4);
+        memset(m->state[l], 0, vh * dv * dk * 4);
+      }
+      orc_delta_prep(qkv, beta, decay, z, n, m->conv[l], (const float*)L->lin_conv.data,
+                     (const float*)L->lin_dt_bias.data, (const float*)L->lin_neg_a.data, kh, vh,
+                     dk, dv, d->lin_conv);
+      orc_delta_rule(qkv, n, cd, kh, vh, dk, dv, group, beta, decay, m->state[l], core);
+      orc_rmsnorm(core, n * vh, dv, (const float*)L->lin_norm.data, d->rms_eps, core);
+      for (int64_t i = 0; i < n * vd; i++) core[i] = core[i] * z[i];
+      err |= lin(m, core, n, vd, L->lin_out, 0, h, NULL, tmp);
+      add(x, tmp, n * h);
+      goto ffn;
+    }
     /* AttentionBlock */
     orc_rmsnorm(x, n, h, (const float*)L->input_norm.data, d->rms_eps, hh);
-    err |= lin(m, hh, n, h, L->q, 0, qw, (const float*)L->q_bias.data, q);
+    if (L->output_gate) {
+      /* per head the query, then its gate */
+      err |= lin(m, hh, n, h, L->q, 0, 2 * qw, NULL, qg);
+      for (int64_t r = 0; r < n * d->heads; r++) {
+        memcpy(q + r * hd, qg + r * 2 * hd, hd * 4);
+        memcpy(gq + r * hd, qg + r * 2 * hd + hd, hd * 4);
+      }
+    } else {
+      err |= lin(m, hh, n, h, L->q, 0, qw, (const float*)L->q_bias.data, q);
+    }
     err |= lin(m, hh, n, h, L->k, 0, kvw, (const float*)L->k_bias.data, k);
     err |= lin(m, hh, n, h, L->v, 0, kvw, (const float*)L->v_bias.data, v);
     if (L->q_norm.data) {
       orc_rmsnorm(q, n * d->heads, hd, (const float*)L->q_norm.data, d->rms_eps, q);
       orc_rmsnorm(k, n * d->kv_heads, hd, (const float*)L->k_norm.data, d->rms_eps, k);
     }
-    orc_rope(q, n, d->heads, hd, cosv, sinv, hd);
-    orc_rope(k, n, d->kv_heads, hd, cosv, sinv, hd);
+    orc_rope(q, n, d->heads, hd, cosv, sinv, rot);
+    orc_rope(k, n, d->kv_heads, hd, cosv, sinv, rot);
     float* kc = m->keys[l] + past * kvw;
     float* vc = m->values[l] + past * kvw;
     for (int64_t i = 0; i < n * kvw; i++) {
@@ -196,8 +264,10 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
     else
       orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads,
                            attn, L->window, (const float*)L->sinks.data, 0);
+    if (L->output_gate) orc_gate_sigmoid(attn, gq, n * qw);
     err |= lin(m, attn, n, qw, L->o, 0, h, (const float*)L->o_bias.data, tmp);
     add(x, tmp, n * h);
+  ffn:
     /* the feed-forward block */
     orc_rmsnorm(x, n, h, (const float*)L->post_norm.data, d->rms_eps, hh);
     if (!L->moe) {
@@ -266,6 +336,7 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
   free(x); free(hh); free(tmp); free(q); free(k); free(v); free(attn);
   free(gate); free(up); free(cs); free(route); free(chosen); free(cw);
   free(gather); free(eout); free(rowi); free(roww);
+  free(qg); free(gq); free(qkv); free(z); free(beta); free(decay); free(core);
   return err ? IHIP_E_ARG : 0;
 }
 

@@ -163,7 +163,7 @@ int64_t orc_argmax(const float* v, int64_t n)
  * decoder.pas:1759-1829 YarnFrequencies */
 static void inv_freq(const ihip_model_desc* dsc, float* f, float* ropescale)
 {
-  int64_t d = dsc->head_dim, half = d / 2;
+  int64_t d = dsc->rope_dims > 0 ? dsc->rope_dims : dsc->head_dim, half = d / 2;
   double lt = log(dsc->rope_theta);
   for (int64_t i = 0; i < half; i++) {
     float e = (float)((double)(2 * i) / (double)d);
@@ -209,10 +209,11 @@ static void inv_freq(const ihip_model_desc* dsc, float* f, float* ropescale)
     *ropescale = (float)(0.1 * log((double)fct) + 1.0);
 }
 
-/* decoder.pas:2539-2561 TDecoderModel.Rotary */
+/* decoder.pas:2539-2561 TDecoderModel.Rotary: [rows, rot / 2] cos, then sin,
+ * rot the rotating values of a head (RopeDims) */
 int orc_rotary(const ihip_model_desc* dsc, int64_t first, int64_t rows, float* cs)
 {
-  int64_t half = dsc->head_dim / 2;
+  int64_t half = (dsc->rope_dims > 0 ? dsc->rope_dims : dsc->head_dim) / 2;
   float* f = (float*)malloc(half * sizeof(float));
   float rs;
   inv_freq(dsc, f, &rs);

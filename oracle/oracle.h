@@ -27,6 +27,8 @@
  *   orc_route                                    - brute-force numpy softmax/top-k
  *   orc_argmax                                   - numpy argmax + NaN/tie cases
  *   orc_rotary                                   - numpy float32 step replay
+ *   orc_delta_prep, orc_delta_rule, orc_gate_sigmoid - transformers' float32
+ *       intermediate states and logits of tiny-qwen35 (tests/test_qwen35.py)
  *   orc_model_*                                  - composed of the above;
  *       checked against a numpy float64 forward of a tiny model
  */
@@ -90,6 +92,22 @@ void orc_route(const float* logits, int64_t experts, int64_t k, int norm_topk,
                int32_t* chosen, float* weights);
 /* sampler.pas:123-160 InferArgMax */
 int64_t orc_argmax(const float* v, int64_t n);
+
+/* deltanet.c: GateBySigmoid (decoder.pas:2594-2610): a[i] *= sigmoid(gate[i]) */
+void orc_gate_sigmoid(float* a, const float* gate, int64_t n);
+/* deltanet.c: TDecoderModel.DeltaPrep (decoder.pas:2755-2855) over every item
+ * in order: qkv [rows, 2 kh dk + vh dv] convolved (conv [channels, kw - 1],
+ * oldest first, moved on) and silu'd, q/k heads L2-normed (q times dk^-0.5);
+ * beta = sigmoid, decay = exp(neg_a * softplus(decay + dt_bias)), z = silu(z) */
+void orc_delta_prep(float* qkv, float* beta, float* decay, float* z, int64_t rows,
+                    float* conv, const float* conv_w, const float* dt_bias, const float* neg_a,
+                    int64_t kh, int64_t vh, int64_t dk, int64_t dv, int64_t kw);
+/* deltanet.c: TInferCpuBackend.DeltaRule (backend.cpu.pas:1890-1972, double):
+ * state [vh, dv, dk], y [rows, vh * dv]; value head h reads key head
+ * (h / group) % kh */
+void orc_delta_rule(const float* qkv, int64_t rows, int64_t stride, int64_t kh, int64_t vh,
+                    int64_t dk, int64_t dv, int64_t group, const float* beta, const float* decay,
+                    float* state, float* y);
 
 /* decoder.pas:1735-1750 + 1759-1829: the inverse frequencies (and YaRN) of a
  * model; decoder.pas:2539-2561 Rotary: [rows, half] cos, then sin */

@@ -9,9 +9,14 @@ converter and ggml's reference quantizers, and by transformers in float32):
   tiny-gpt-oss/gguf/*.gguf: the model files of TTestInferQwen3
   (tests/test.infer.qwen3.pas:1485-1566, :5600-5660) and the device tests
   (tests/test.infer.cuda.pas:1560-1640, :1950-2010);
+- tiny-qwen35/gguf/{bf16,q8_0,text-bf16,text-q8_0,bad-*}.gguf: the qwen35
+  files of TTestInferQwen35 (tests/test.infer.qwen35.pas) and the device
+  tests of the DeltaNet (tests/test.infer.cuda.pas);
 - the case ids, logits, greedy tokens and margins of tiny-qwen3,
-  tiny-qwen3/untied, tiny-qwen3moe and tiny-gpt-oss/mxfp4 (tensors.bin,
-  described by manifest.json), gathered into expected.npz.
+  tiny-qwen3/untied, tiny-qwen3moe, tiny-gpt-oss/mxfp4, tiny-qwen35 and
+  tiny-qwen35/text (with the one-token-at-a-time logits and the first layer's
+  mixer output of the last two) (tensors.bin, described by manifest.json),
+  gathered into expected.npz.
 
 Every file is checked against the sha256 its manifest records before it is
 copied. The damaged files go to gguf/bad/ (CPU tests only). Run from the
@@ -52,7 +57,7 @@ def cases(folder):
     for t in m["tensors"]:
         name = t["name"]
         if not name.startswith("case") or name.split(".", 1)[1] not in (
-                "ids", "logits", "greedy", "greedy_margin"):
+                "ids", "logits", "greedy", "greedy_margin", "logits_steps", "layer00_attn"):
             continue
         dt = {"f32": np.float32, "i32": np.int32}[t["dtype"]]
         a = np.frombuffer(blob[t["offset"]:t["offset"] + t["bytes"]], dt).reshape(t["shape"])
@@ -66,7 +71,7 @@ def main(ref):
     # the reader fixture
     copy_dir(os.path.join(root, "tiny-gguf"), ["model.gguf"], OUT, {})
     sets = [("tiny-qwen3-gguf", "qwen3"), (os.path.join("tiny-qwen3moe", "gguf"), "qwen3moe"),
-            (os.path.join("tiny-gpt-oss", "gguf"), "gpt-oss")]
+            (os.path.join("tiny-gpt-oss", "gguf"), "gpt-oss"), (os.path.join("tiny-qwen35", "gguf"), "qwen35")]
     for folder, tag in sets:
         src = os.path.join(root, folder)
         files = json.load(open(os.path.join(src, "manifest.json"))).get("files", {})
@@ -77,7 +82,8 @@ def main(ref):
         copy_dir(src, bad, os.path.join(OUT, "bad", tag), files)
     expected = {}
     for folder, tag in [("tiny-qwen3", "qwen3"), (os.path.join("tiny-qwen3", "untied"), "qwen3-untied"),
-                        ("tiny-qwen3moe", "qwen3moe"), (os.path.join("tiny-gpt-oss", "mxfp4"), "gpt-oss")]:
+                        ("tiny-qwen3moe", "qwen3moe"), (os.path.join("tiny-gpt-oss", "mxfp4"), "gpt-oss"),
+                        ("tiny-qwen35", "qwen35"), (os.path.join("tiny-qwen35", "text"), "qwen35-text")]:
         for k, v in cases(os.path.join(root, folder)).items():
             expected[f"{tag}/{k}"] = v
     np.savez_compressed(os.path.join(OUT, "expected.npz"), **expected)

@@ -51,6 +51,12 @@ def lib():
         L.orc_argmax.restype = i64
         L.orc_argmax.argtypes = [vp, i64]
         L.orc_rotary.argtypes = [vp, i64, i64, vp]
+        L.orc_gate_sigmoid.argtypes = [vp, vp, i64]
+        L.orc_gate_sigmoid.restype = None
+        L.orc_delta_prep.argtypes = [vp, vp, vp, vp, i64, vp, vp, vp, vp, i64, i64, i64, i64, i64]
+        L.orc_delta_prep.restype = None
+        L.orc_delta_rule.argtypes = [vp, i64, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp]
+        L.orc_delta_rule.restype = None
         L.orc_model_create.argtypes = [vp, i64, C.c_int, C.c_int, C.POINTER(vp)]
         L.orc_model_destroy.argtypes = [vp]
         L.orc_model_destroy.restype = None
@@ -187,6 +193,35 @@ def route(logits, k, norm_topk=True):
     w = np.empty(k, np.float32)
     lib().orc_route(_p(lg), lg.size, k, int(norm_topk), _p(ids), _p(w))
     return ids, w
+
+
+def gate_sigmoid(a, gate):
+    """GateBySigmoid: a * sigmoid(gate)."""
+    a = np.array(a, np.float32)
+    g = np.ascontiguousarray(gate, np.float32)
+    lib().orc_gate_sigmoid(_p(a), _p(g), a.size)
+    return a
+
+
+def delta_prep(qkv, beta, decay, z, conv, conv_w, dt_bias, neg_a, kh, vh, dk, dv, kw):
+    """DeltaPrep over rows: returns (qkv, beta, decay, z, conv) after it."""
+    out = [np.array(v, np.float32) for v in (qkv, beta, decay, z, conv)]
+    w = [np.ascontiguousarray(v, np.float32) for v in (conv_w, dt_bias, neg_a)]
+    lib().orc_delta_prep(_p(out[0]), _p(out[1]), _p(out[2]), _p(out[3]), out[0].shape[0],
+                         _p(out[4]), _p(w[0]), _p(w[1]), _p(w[2]), kh, vh, dk, dv, kw)
+    return out
+
+
+def delta_rule(qkv, kh, vh, dk, dv, group, beta, decay, state):
+    """DeltaRule (double branch): returns (y [rows, vh * dv], state after)."""
+    q = np.ascontiguousarray(qkv, np.float32)
+    st = np.array(state, np.float32)
+    y = np.zeros((q.shape[0], vh * dv), np.float32)
+    b = np.ascontiguousarray(beta, np.float32)
+    g = np.ascontiguousarray(decay, np.float32)
+    lib().orc_delta_rule(_p(q), q.shape[0], q.shape[1], kh, vh, dk, dv, group, _p(b), _p(g),
+                         _p(st), _p(y))
+    return y, st
 
 
 class Sampler:
