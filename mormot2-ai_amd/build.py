@@ -22,7 +22,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 LINEAR_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf16", "f16"]
 # gemm.hip (the MFMA prefill GEMM) once per quantized weight type
 GEMM_FMTS = ["q8_0", "q4_0", "mxfp4", "q5_0", "q5_1", "q4_k", "q6_k", "f32", "bf16", "f16"]
-KERNELS = ([("ops", "ops", [])] +
+KERNELS = ([("ops", "ops", []), ("deltanet", "deltanet", [])] +
            [("linear_" + f, "linear", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in LINEAR_FMTS] +
            [("gemm_" + f, "gemm", ["-DIHIP_ONLY_FMT_" + f.upper()]) for f in GEMM_FMTS])
 HOST = ["runtime", "backend", "model", "synth", "gguf"]

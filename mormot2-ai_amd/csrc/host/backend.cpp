@@ -873,7 +873,7 @@ int ihip_enqueue_qkrope(ihip_ctx* c, uint64_t q, uint64_t k, uint64_t v, uint64_
     void* vc;
     const int* pastp;
     double eps;
-    int32_t rows, heads, kvh, hd, past, f16;
+    int32_t rows, heads, kvh, hd, past, f16, rot, pad;
   } a = {(float*)q, (const float*)k, (const float*)v, (const float*)qn, (const float*)kn,
          (const float*)cs, (void*)kc, (void*)vc, nullptr, eps, (int32_t)rows, (int32_t)heads,
          (int32_t)kvh, (int32_t)hd, (int32_t)past, kv_f16};

@@ -2,7 +2,9 @@
 // (src/infer/mormot.ai.infer.model.qwen3.cuda.pas:150-1761) for HIP: the
 // whole decoder on the device behind TDecoderDevice (decoder.pas:907-928).
 // Qwen3 dense, Qwen3-MoE and gpt-oss shapes: per-head q/k norms, biases,
-// sinks, sliding windows, clamped SwiGLU, experts chosen on the device.
+// sinks, sliding windows, clamped SwiGLU, experts chosen on the device;
+// Qwen3.5: Gated DeltaNet layers with their states per context, the output
+// gate of the attention and a partial rotary share.
 //
 // A prompt runs in chunks of up to CHUNK rows (CHUNK_MAX of
 // model.qwen3.cuda.pas:308 is 256; here 1024 by default, so that a prompt
@@ -29,6 +31,10 @@ struct DevLayer {
   int qd = 0, kd = 0, vd = 0, od = 0, gd = 0, ud = 0, dd = 0, rd = 0, egd = 0, eud = 0, edd = 0;
   int64_t eg_stride = 0, ed_stride = 0;
   int window = 0, moe = 0;
+  // Qwen3.5: the mixer and the output gate; a DeltaNet layer's weights
+  int mixer = IHIP_MIXER_ATTENTION, output_gate = 0;
+  uint64_t lqkv = 0, lz = 0, lb = 0, la = 0, lout = 0, lconv = 0, ldt = 0, lnega = 0, lnorm = 0;
+  int lqkvd = 0, lzd = 0, lbd = 0, lad = 0, loutd = 0;
 };
 
 }  // namespace ihip
@@ -48,6 +54,11 @@ struct ihip_mctx {
   uint64_t xq0 = 0, xqk = 0, xqf = 0;  // quantized h (Q8_0, Q8_K) and FFN input
   uint64_t perm = 0, items = 0;         // the experts of a prompt chunk (moe_plan)
   uint64_t attn_part = 0, attn_part_bytes = 0;  // flash-decoding partials
+  // Qwen3.5: per DeltaNet layer its convolution inputs and state S (zero when
+  // a sequence starts); the chunk's DeltaNet channels, gates, beta, decay and
+  // the rule's output; a gated attention's query+gate rows and its gates
+  std::vector<uint64_t> conv, state;
+  uint64_t qkv = 0, z = 0, beta = 0, decay = 0, core = 0, qg = 0, gq = 0;
   // zeroed counters of the decode attention's heads (the last range block of
   // a head merges the head)
   uint64_t done = 0;
@@ -77,6 +88,8 @@ struct ihip_model {
   uint64_t embed = 0, final_norm = 0, head = 0;
   int embed_dt = 0, head_dt = 0;
   bool any_moe = false;
+  bool recurrent = false;  // a DeltaNet layer: the context carries states
+  bool gated = false;      // an attention layer with an output gate
   // the host ranges of the uploaded weights: forgotten when the model goes,
   // as a model does in its destructor (backend.pas:151-158) - new host
   // tensors at a reused address must not meet the stale device copy
@@ -94,9 +107,12 @@ namespace ihip {
 
 // decoder.pas:1735-1741 and 1759-1829: inverse frequencies, every step
 // rounded to single as the reference's float32 tensors; YaRN when factor > 0
+// the rotating values of a head (RopeDims): the whole head unless given
+static int64_t rope_dims(const ihip_model_desc& d) { return d.rope_dims > 0 ? d.rope_dims : d.head_dim; }
+
 static void inv_freq(const ihip_model_desc& d, std::vector<float>& f, float& scale)
 {
-  const int64_t dim = d.head_dim, half = dim / 2;
+  const int64_t dim = rope_dims(d), half = dim / 2;
   const double lt = std::log(d.rope_theta);
   f.assign(half, 0.f);
   for (int64_t i = 0; i < half; i++) {
@@ -138,13 +154,14 @@ static void inv_freq(const ihip_model_desc& d, std::vector<float>& f, float& sca
 }
 
 // TDecoderModel.Rotary (decoder.pas:2539-2561): the angle in single, cos and
-// sin rounded to single, then times the YaRN scale in single
+// sin rounded to single, then times the YaRN scale in single; [rows, rot / 2]
+// cos, then sin
 static void rotary(const ihip_model_desc& d, int64_t first, int64_t rows, float* cs)
 {
   std::vector<float> f;
   float rs;
   inv_freq(d, f, rs);
-  const int64_t half = d.head_dim / 2;
+  const int64_t half = rope_dims(d) / 2;
   float* sn = cs + rows * half;
   for (int64_t r = 0; r < rows; r++)
     for (int64_t i = 0; i < half; i++) {
@@ -250,11 +267,11 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
     void* vc;
     const int* pastp;
     double eps;
-    int32_t rows, heads, kvh, hd, past, f16;
+    int32_t rows, heads, kvh, hd, past, f16, rot, pad;
   } ra = {(float*)s->q, (const float*)s->k, (const float*)s->v, (const float*)L.qn,
           (const float*)L.kn, (const float*)s->cs, (void*)s->kc[l], (void*)s->vc[l],
           graph ? (const int*)s->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads,
-          d.kv_heads, d.head_dim, (int32_t)past, m->kv_f16};
+          d.kv_heads, d.head_dim, (int32_t)past, m->kv_f16, (int32_t)rope_dims(d), 0};
   int rc = launch(m->c, "qkrope", dim3((unsigned)(d.heads + d.kv_heads), (unsigned)n), dim3(64), &ra);
   if (rc) return rc;
   int64_t maxkeys = graph ? s->capacity : past + n;
@@ -271,7 +288,7 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
 static bool one_row_fused(const ihip_model* m)
 {
   const ihip_model_desc& d = m->d;
-  if (d.hidden > 4096) return false;
+  if (d.hidden > 4096 || m->recurrent || m->gated || rope_dims(d) != d.head_dim) return false;
   if (d.experts > 0) {
     const int64_t K = d.experts_used;
     if (K < 1 || K > 8 || K * d.expert_ffn * 4 > 65536) return false;
@@ -419,6 +436,98 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
   return 0;
 }
 
+// the launch arguments of deltanet.hip
+struct DnConvArgs {
+  float* qkv;
+  const float* w;
+  float* conv;
+  int32_t rows, channels, kw, pad;
+};
+struct DnPrepArgs {
+  float* qkv;
+  float* beta;
+  float* decay;
+  float* z;
+  const float* dt_bias;
+  const float* neg_a;
+  int32_t kh, vh, dk, dv, channels, pad;
+};
+struct DnRuleArgs {
+  const float* qkv;
+  const float* beta;
+  const float* decay;
+  float* state;
+  float* y;
+  int32_t rows, stride, kh, vh, dk, dv, group, pad;
+};
+struct DnNormArgs {
+  float* x;
+  const float* w;
+  const float* z;
+  double eps;
+  int32_t rows, cols;
+};
+struct GateArgs {
+  const float* qg;
+  float* q;
+  float* g;
+  int64_t n;
+  int32_t hd, pad;
+};
+
+// DeltaNetBlock (decoder.pas:2704-2753) of layer l over n rows, h holding
+// their input norm: the four projections, the convolution and DeltaPrep, the
+// delta rule on the layer's state, the gated RMSNorm, the output projection
+// into tmp
+static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  const DevLayer& L = m->L[l];
+  const int64_t H = d.hidden, kh = d.lin_key_heads, vh = d.lin_value_heads, dk = d.lin_key_dim,
+                dv = d.lin_value_dim, vd = vh * dv, cd = 2 * kh * dk + vd;
+  int rc;
+  if ((rc = lin(s, s->h, qh, n, H, L.lqkvd, L.lqkv, cd, 0, s->qkv)) ||
+      (rc = lin(s, s->h, qh, n, H, L.lzd, L.lz, vd, 0, s->z)) ||
+      (rc = lin(s, s->h, qh, n, H, L.lbd, L.lb, vh, 0, s->beta)) ||
+      (rc = lin(s, s->h, qh, n, H, L.lad, L.la, vh, 0, s->decay)))
+    return rc;
+  DnConvArgs ca = {(float*)s->qkv, (const float*)L.lconv, (float*)s->conv[l], (int32_t)n, (int32_t)cd,
+                   d.lin_conv, 0};
+  if ((rc = launch(m->c, "dn_conv", dim3((unsigned)((cd + 255) / 256)), dim3(256), &ca))) return rc;
+  DnPrepArgs pa = {(float*)s->qkv, (float*)s->beta, (float*)s->decay, (float*)s->z, (const float*)L.ldt,
+                   (const float*)L.lnega, (int32_t)kh, (int32_t)vh, (int32_t)dk, (int32_t)dv, (int32_t)cd, 0};
+  if ((rc = launch(m->c, "dn_prep", dim3((unsigned)(2 * kh + vh), (unsigned)n), dim3(64), &pa))) return rc;
+  // LinGroup (decoder.pas:2457-2463)
+  const int32_t group = d.lin_tiled ? 1 : (int32_t)(vh / kh);
+  DnRuleArgs ra = {(const float*)s->qkv, (const float*)s->beta, (const float*)s->decay, (float*)s->state[l],
+                   (float*)s->core, (int32_t)n, (int32_t)cd, (int32_t)kh, (int32_t)vh, (int32_t)dk,
+                   (int32_t)dv, group, 0};
+  if ((rc = launch(m->c, "dn_rule", dim3((unsigned)vh, (unsigned)((dv + 3) / 4)), dim3(256), &ra))) return rc;
+  DnNormArgs na = {(float*)s->core, (const float*)L.lnorm, (const float*)s->z, (double)d.rms_eps,
+                   (int32_t)(n * vh), (int32_t)dv};
+  if ((rc = launch(m->c, "dn_gatenorm", dim3((unsigned)((n * vh + 3) / 4)), dim3(256), &na))) return rc;
+  QCache qc{s->xq0, s->xqk};
+  return lin(s, s->core, n == 1 ? nullptr : &qc, n, vd, L.loutd, L.lout, H, 0, s->tmp);
+}
+
+// a new sequence: the convolution sees zeros before it, the states are 0
+// (DeltaNetBlock, decoder.pas:2723-2729); outside any capture
+static int reset_states(ihip_mctx* s)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  const int64_t cd = 2 * (int64_t)d.lin_key_heads * d.lin_key_dim + (int64_t)d.lin_value_heads * d.lin_value_dim;
+  for (int l = 0; l < d.layers; l++) {
+    if (!s->conv[l]) continue;
+    IHIP_CHECK(hipMemsetAsync((void*)s->conv[l], 0, (size_t)cd * std::max(d.lin_conv - 1, 1) * 4,
+                              m->c->stream));
+    IHIP_CHECK(hipMemsetAsync((void*)s->state[l], 0,
+                              (size_t)d.lin_value_heads * d.lin_value_dim * d.lin_key_dim * 4, m->c->stream));
+  }
+  return 0;
+}
+
 // the layers of one chunk of n rows at positions past.., x holding the
 // embeddings; leaves h = the final norm of x. graph: the position is read
 // from s->pos (decode step under capture)
@@ -438,13 +547,31 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
     const DevLayer& L = m->L[l];
     QCache qh{s->xq0, s->xqk};
     QCache* qhp = one ? nullptr : &qh;
-    // attention block (decoder.pas:2625-2702)
-    if ((rc = lin(s, s->h, qhp, n, H, L.qd, L.q, qw, L.qb, s->q))) return rc;
-    if ((rc = lin(s, s->h, qhp, n, H, L.kd, L.k, kvw, L.kb, s->k))) return rc;
-    if ((rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
-    if ((rc = rope_attn(s, l, n, past, graph))) return rc;
-    QCache qa{s->xq0, s->xqk};
-    if ((rc = lin(s, s->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, s->tmp))) return rc;
+    if (L.mixer == IHIP_MIXER_DELTANET) {
+      if ((rc = deltanet_block(s, l, n, qhp))) return rc;
+    } else {
+      // attention block (decoder.pas:2625-2702)
+      if (L.output_gate) {
+        // per head the query, then its gate: apart into q and gq
+        if ((rc = lin(s, s->h, qhp, n, H, L.qd, L.q, 2 * qw, 0, s->qg))) return rc;
+        GateArgs ga = {(const float*)s->qg, (float*)s->q, (float*)s->gq, n * qw, (int32_t)hd, 0};
+        if ((rc = launch(m->c, "split_gate", dim3((unsigned)((n * qw + 255) / 256)), dim3(256), &ga)))
+          return rc;
+      } else if ((rc = lin(s, s->h, qhp, n, H, L.qd, L.q, qw, L.qb, s->q))) {
+        return rc;
+      }
+      if ((rc = lin(s, s->h, qhp, n, H, L.kd, L.k, kvw, L.kb, s->k))) return rc;
+      if ((rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
+      if ((rc = rope_attn(s, l, n, past, graph))) return rc;
+      if (L.output_gate) {
+        // GateBySigmoid (decoder.pas:2594-2610) before the output projection
+        GateArgs ga = {nullptr, (float*)s->attn, (float*)s->gq, n * qw, (int32_t)hd, 0};
+        if ((rc = launch(m->c, "gate_sigmoid", dim3((unsigned)((n * qw + 255) / 256)), dim3(256), &ga)))
+          return rc;
+      }
+      QCache qa{s->xq0, s->xqk};
+      if ((rc = lin(s, s->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, s->tmp))) return rc;
+    }
     // residual, then the pre-FFN norm
     if ((rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, L.post_norm, s->h, n, H, d.rms_eps)))
       return rc;
@@ -575,7 +702,8 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
   std::vector<float> cs((size_t)n * d.head_dim);
   rotary(d, s->length, n, cs.data());
   IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
-  int rc = 0;
+  int rc = s->length == 0 && m->recurrent ? reset_states(s) : 0;
+  if (rc) return rc;
   if (ids) {
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, (void*)ids, n * 4, c->stream));
     rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, d.vocab, d.hidden, s->tok, n, s->x);
@@ -727,6 +855,7 @@ static int prepare(ihip_mctx* s, int64_t tokens)
     std::vector<uint64_t> nk(d.layers, 0), nv(d.layers, 0);
     int rc = 0;
     for (int l = 0; l < d.layers && !rc; l++) {
+      if (m->L[l].mixer == IHIP_MIXER_DELTANET) continue;  // a state, no rows
       void* a = nullptr;
       void* b = nullptr;
       hipError_t e = hipMalloc(&a, (uint64_t)cap * kvw * es);
@@ -797,6 +926,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   int32_t tok = first;
   for (int64_t i = 0; i < steps; i++) {
     int32_t pos = (int32_t)s->length;
+    if (pos == 0 && m->recurrent && (rc = reset_states(s))) return rc;
     rotary(m->d, pos, 1, cs.data());
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, &tok, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->pos, &pos, 4, c->stream));
@@ -846,7 +976,9 @@ static int context_new(ihip_model* m, int64_t capacity, ihip_mctx** out)
   int64_t EK = m->any_moe ? (int64_t)d.experts_used * d.expert_ffn : 0;
   int64_t wide = std::max<int64_t>({F, EK, qw, H, (int64_t)d.experts});
   const int64_t K1 = std::max(d.experts_used, 1), E1 = std::max(d.experts, 1);
-  const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn});
+  const int64_t lvd = (int64_t)d.lin_value_heads * d.lin_value_dim,
+                lcd = 2 * (int64_t)d.lin_key_heads * d.lin_key_dim + lvd;
+  const uint64_t qin = std::max<int64_t>({H, qw, F, (int64_t)d.expert_ffn, lvd});
   const uint64_t qrow = qin + 4 * (qin / 32);
   int rc = 0;
   auto bad = [&](int r) {
@@ -868,6 +1000,22 @@ static int context_new(ihip_model* m, int64_t capacity, ihip_mctx** out)
       (rc = dalloc_ctx(s, (N * K1 / 8 + 1 + E1) * 16, s->items)) ||
       (rc = dalloc_ctx(s, N * qrow, s->xq0)) || (rc = dalloc_ctx(s, N * qrow, s->xqk)) ||
       (rc = dalloc_ctx(s, N * K1 * qrow, s->xqf)) || (rc = dalloc_ctx(s, 256 * 128, s->done)))
+    return bad(rc);
+  s->conv.assign(d.layers, 0);
+  s->state.assign(d.layers, 0);
+  if (m->recurrent) {
+    const int64_t lvh = std::max(d.lin_value_heads, 1);
+    if ((rc = dalloc_ctx(s, N * lcd * 4, s->qkv)) || (rc = dalloc_ctx(s, N * lvd * 4, s->z)) ||
+        (rc = dalloc_ctx(s, N * lvh * 4, s->beta)) || (rc = dalloc_ctx(s, N * lvh * 4, s->decay)) ||
+        (rc = dalloc_ctx(s, N * lvd * 4, s->core)))
+      return bad(rc);
+    for (int l = 0; l < d.layers; l++)
+      if (m->L[l].mixer == IHIP_MIXER_DELTANET &&
+          ((rc = dalloc_ctx(s, lcd * std::max(d.lin_conv - 1, 1) * 4, s->conv[l])) ||
+           (rc = dalloc_ctx(s, lvd * d.lin_key_dim * 4, s->state[l]))))
+        return bad(rc);
+  }
+  if (m->gated && ((rc = dalloc_ctx(s, N * 2 * qw * 4, s->qg)) || (rc = dalloc_ctx(s, N * qw * 4, s->gq))))
     return bad(rc);
   // the attention counters start at zero (a fill kernel would do under
   // capture; this runs once, outside any capture)
@@ -992,6 +1140,10 @@ static int64_t usable(const ihip_mctx* s, const int32_t* prompt, int64_t count)
   int64_t n = 0;
   const int64_t lim = std::min<int64_t>(std::max<int64_t>(count, 0), s->length);
   while (n < lim && s->ids[n] >= 0 && s->ids[n] == prompt[n]) n++;
+  // a recurrent state holds the whole sequence: all of it or nothing
+  // (TDecoderContext.Usable / Restorable, decoder.pas:1180-1230, without
+  // restore points)
+  if (s->m->recurrent && n != s->length) n = 0;
   return n;
 }
 
@@ -1127,9 +1279,34 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
     DevLayer& L = m->L[l];
     L.window = s.window;
     L.moe = s.moe;
+    L.mixer = s.mixer;
+    L.output_gate = s.output_gate != 0;
     any_moe |= s.moe != 0;
+    if (s.mixer != IHIP_MIXER_ATTENTION && s.mixer != IHIP_MIXER_DELTANET)
+      return bad(fail(IHIP_E_ARG, "model: layer " + std::to_string(l) + " has an unknown mixer"));
+    if (s.mixer == IHIP_MIXER_DELTANET) {
+      // Qwen3.5's Gated DeltaNet (model.qwen35.pas:552-590)
+      const int64_t vh = d.lin_value_heads, vd = vh * d.lin_value_dim,
+                    cd = 2 * (int64_t)d.lin_key_heads * d.lin_key_dim + vd;
+      m->recurrent = true;
+      if ((rc = upf(m, s.input_norm, H, L.input_norm)) || (rc = upf(m, s.post_norm, H, L.post_norm)) ||
+          (rc = upw(m, s.lin_qkv, cd, H, 1, L.lqkv, L.lqkvd)) || (rc = upw(m, s.lin_z, vd, H, 1, L.lz, L.lzd)) ||
+          (rc = upw(m, s.lin_b, vh, H, 1, L.lb, L.lbd)) || (rc = upw(m, s.lin_a, vh, H, 1, L.la, L.lad)) ||
+          (rc = upw(m, s.lin_out, H, vd, 1, L.lout, L.loutd)) ||
+          (rc = upf(m, s.lin_conv, cd * d.lin_conv, L.lconv)) || (rc = upf(m, s.lin_dt_bias, vh, L.ldt)) ||
+          (rc = upf(m, s.lin_neg_a, vh, L.lnega)) || (rc = upf(m, s.lin_norm, d.lin_value_dim, L.lnorm)) ||
+          (rc = upw(m, s.gate, d.ffn, H, 1, L.gate, L.gd)) || (rc = upw(m, s.up, d.ffn, H, 1, L.up, L.ud)) ||
+          (rc = upw(m, s.down, H, d.ffn, 1, L.down, L.dd)))
+        return bad(rc);
+      if (!L.lqkv || !L.lz || !L.lb || !L.la || !L.lout || !L.lconv || !L.ldt || !L.lnega || !L.lnorm ||
+          s.moe)
+        return bad(fail(IHIP_E_ARG, "model: DeltaNet layer " + std::to_string(l) + " lacks a tensor"));
+      continue;
+    }
+    m->gated |= L.output_gate != 0;
     if ((rc = upf(m, s.input_norm, H, L.input_norm)) || (rc = upf(m, s.post_norm, H, L.post_norm)) ||
-        (rc = upw(m, s.q, qw, H, 1, L.q, L.qd)) || (rc = upw(m, s.k, kvw, H, 1, L.k, L.kd)) ||
+        (rc = upw(m, s.q, L.output_gate ? 2 * qw : qw, H, 1, L.q, L.qd)) ||
+        (rc = upw(m, s.k, kvw, H, 1, L.k, L.kd)) ||
         (rc = upw(m, s.v, kvw, H, 1, L.v, L.vd)) || (rc = upw(m, s.o, H, qw, 1, L.o, L.od)) ||
         (rc = upf(m, s.q_bias, qw, L.qb)) || (rc = upf(m, s.k_bias, kvw, L.kb)) ||
         (rc = upf(m, s.v_bias, kvw, L.vb)) || (rc = upf(m, s.o_bias, H, L.ob)) ||
@@ -1156,6 +1333,16 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
     }
   }
   if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
+  const int64_t rot = rope_dims(d);
+  if (rot < 2 || rot > hd || (rot & 1)) return bad(fail(IHIP_E_ARG, "model: an odd or oversized rotary share"));
+  // the DeltaNet kernels keep a state column in a wave's registers (keys of
+  // up to 256) and the convolution inputs in a thread's (up to 8)
+  if (m->recurrent &&
+      (d.lin_key_heads < 1 || d.lin_value_heads < d.lin_key_heads || d.lin_value_heads % d.lin_key_heads ||
+       d.lin_key_dim < 1 || d.lin_key_dim > 256 || d.lin_value_dim < 1 || d.lin_value_dim > 1024 ||
+       d.lin_conv < 1 || d.lin_conv > 8))
+    return bad(fail(IHIP_E_UNSUPPORTED, "model: DeltaNet shapes beyond the device kernels (keys <= 256, "
+                                        "convolution <= 8)"));
   // moe_plan counts the slots per expert in LDS (4096 experts); a chunk's
   // work items stay within one grid dimension
   if (any_moe && (d.experts > 4096 || CHUNK * d.experts_used > 65535))
@@ -1256,6 +1443,11 @@ int ihip_context_truncate(ihip_mctx* s, int64_t length)
   if (!s || length < 0 || length > s->length)
     return fail(IHIP_E_ARG, "ihip_context_truncate(" + std::to_string(length) + ") of " +
                                 std::to_string(s ? s->length : 0) + " tokens");
+  // a DeltaNet state holds the whole sequence: no way back but to 0
+  // (TDecoderContext.Truncate / Restorable, decoder.pas:996-1010, :1190-1197)
+  if (s->m->recurrent && length != 0 && length != s->length)
+    return fail(IHIP_E_ARG, "ihip_context_truncate(" + std::to_string(length) +
+                                "): a recurrent state cannot go back there");
   s->length = length;  // the cache keeps every row: any length is restorable
   return 0;
 }
@@ -1265,8 +1457,7 @@ int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t*
   if (!s || (!ids && count > 0) || !kept) return fail(IHIP_E_ARG, "ihip_context_reuse");
   // the common prefix, at most count - 1 tokens (the last one is computed
   // again for its logits); a position fed an embedding row matches no id
-  int64_t n = 0, lim = std::min<int64_t>(count > 0 ? count - 1 : 0, s->length);
-  while (n < lim && s->ids[n] >= 0 && s->ids[n] == ids[n]) n++;
+  const int64_t n = usable(s, ids, count > 0 ? count - 1 : 0);
   s->length = n;
   *kept = n;
   return 0;

@@ -288,17 +288,20 @@ struct RopeArgs {
   const int* pastp;  // device position of row 0 (graph replay), or null: past
   double eps;
   int32_t rows, heads, kvh, hd, past, f16;
+  int32_t rot;       // the rotating values of a head from its start (0: all)
+  int32_t pad;
 };
 
 // per (head: the q heads, then the kv heads; row): the Q/K head RMSNorm of
-// decoder.pas:2668-2673, rotate_half RoPE in double (backend.cpu.pas:
-// 1862-1888), K and V stored into the cache at past + row (decoder.pas:
+// decoder.pas:2668-2673, rotate_half RoPE in double over the first rot
+// values (backend.cpu.pas:1862-1888; cs holds [rows, rot / 2] cos, then
+// sin), K and V stored into the cache at past + row (decoder.pas:
 // 2688-2691); one wave per head
 extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
 {
   __shared__ float nv[512];
   int hh = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-  int d = a.hd, half = d >> 1;
+  int d = a.hd, half = (a.rot > 0 ? a.rot : d) >> 1;
   const int past = a.pastp ? *a.pastp : a.past;
   bool isq = hh < a.heads;
   int h = isq ? hh : hh - a.heads;
@@ -339,6 +342,13 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
       ((float*)a.kc)[dst + i] = o0;
       ((float*)a.kc)[dst + i + half] = o1;
     }
+  }
+  // the values beyond the rotating part: normed, not rotated
+  for (int c = 2 * half + t; c < d; c += 64) {
+    float o = nv[c];
+    if (isq) a.q[src + c] = o;
+    else if (a.f16) ((uint16_t*)a.kc)[dst + c] = float_to_half(o);
+    else ((float*)a.kc)[dst + c] = o;
   }
   if (!isq)
     for (int c = t; c < d; c += 64) {

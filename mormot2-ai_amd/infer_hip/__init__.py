@@ -466,7 +466,8 @@ class ModelContext:
             self.h = h
 
     def close(self):
-        if self.h and not self.own and self.model.h:
+        # a context of a model whose device context is gone is gone with it
+        if self.h and not self.own and self.model.h and getattr(self.model.ctx, "h", None):
             lib().ihip_context_destroy(self.h)
         self.h = None
 
@@ -549,7 +550,7 @@ class PromptCache:
         self.h = h
 
     def close(self):
-        if self.h and self.model.h:
+        if self.h and self.model.h and getattr(self.model.ctx, "h", None):
             lib().ihip_prompt_cache_destroy(self.h)
         self.h = None
 
