@@ -327,7 +327,29 @@ typedef struct {
   ihip_tensor lin_dt_bias; /* [value heads] F32 */
   ihip_tensor lin_neg_a;   /* [value heads] F32: -exp(A_log) */
   ihip_tensor lin_norm;    /* [value dim] F32: the gated RMSNorm's weight */
+  /* Gemma 4 (model.gemma4.pas:509-860, decoder.pas:2625-3091, :3245-3369) */
+  int32_t head_dim, kv_heads; /* this layer's heads (0: the model's) */
+  int32_t k_is_v;          /* 1: no v: the values are the raw keys (KIsV) */
+  int32_t rope_set;        /* 0: the first rotary set, 1: the second (Rope2) */
+  int32_t exp_gate_up;     /* 1: exp_gate is [E, 2 fi, h], per expert its gate
+                              rows then its up rows; exp_up unused */
+  int32_t reserved1;
+  ihip_tensor attn_out_norm; /* [h] F32: the attention output normed before
+                                the residual (SandwichNorm), or NULL */
+  ihip_tensor ffn_out_norm;  /* [h] F32: the feed-forward output normed
+                                before the residual, or NULL */
+  /* moe == IHIP_FFN_DENSE_MOE (dfDenseMoe): the dense block's output norm,
+   * the experts' input and output norms, the router input's norm weight
+   * (an RMSNorm of the residual times it) and the expert scales */
+  ihip_tensor dense_out_norm, moe_in_norm, moe_out_norm, router_norm;
+  ihip_tensor expert_scale;  /* [E] F32: each route weight times its expert's */
+  ihip_tensor scalar;        /* [1] F32: the layer's output state times it, or NULL */
 } ihip_layer_desc;
+
+/* ihip_layer_desc.moe (TDecoderFfn, decoder.pas:107-115) */
+#define IHIP_FFN_DENSE 0
+#define IHIP_FFN_MOE 1
+#define IHIP_FFN_DENSE_MOE 2
 
 /* ihip_layer_desc.mixer (TDecoderMixer, decoder.pas:95-105) */
 #define IHIP_MIXER_ATTENTION 0
@@ -356,7 +378,23 @@ typedef struct {
   /* LinTiled: value head h reads key head h mod key heads (llama.cpp's
    * order), else key head h / (value heads / key heads) */
   int32_t lin_tiled;
+  /* Gemma 4 */
+  int32_t activation;      /* IHIP_ACT_SILU (SwiGLU) or IHIP_ACT_GELU_TANH (GeGLU) */
+  int32_t value_norm;      /* 1: every V head RMS-normed without weight */
+  float embed_scale;       /* > 0: the embeddings of ids times it (single) */
+  float reserved2;
+  double attention_scale;  /* > 0: the score factor, else 1 / sqrt(head dim) */
+  double logit_softcap;    /* > 0: logits := tanh(logits / c) * c */
+  /* the second rotary set (Rope2Theta, decoder.pas:1742-1752): its theta, and
+   * the rotating pairs from the start of its heads (the others keep
+   * frequency 0) */
+  double rope2_theta;
+  int32_t rope2_pairs, reserved3;
 } ihip_model_desc;
+
+/* ihip_model_desc.activation (TDecoderActivation) */
+#define IHIP_ACT_SILU 0
+#define IHIP_ACT_GELU_TANH 1
 
 /* the model on the device: every weight uploaded (UploadWeights,
  * model.qwen3.cuda.pas:602-828); mode: the Linear arithmetic; kv_f16: a

@@ -520,11 +520,13 @@ struct DescBuilder {
   }
   // the experts of a layer as one [E, rows, cols] block tensor
   // (TDecoderModel.GgufExperts, decoder.pas:2175-2202)
-  ihip_tensor experts(const std::string& name, int64_t e, int64_t rows, int64_t cols)
+  // (floats: BF16/F16/F32 in place when `floats`, widened exactly on the device)
+  ihip_tensor experts(const std::string& name, int64_t e, int64_t rows, int64_t cols, bool floats = false)
   {
     const Tensor& t = checked(name, {e, rows, cols}, true);
-    if (!block_type(t.dtype)) refuse(name + " is " + dtype_name(t.dtype) + ", not supported for experts here");
-    check_scales(t, name);
+    if (!block_type(t.dtype) && !floats)
+      refuse(name + " is " + dtype_name(t.dtype) + ", not supported for experts here");
+    if (block_type(t.dtype)) check_scales(t, name);
     used++;
     return ihip_tensor{t.data, t.dtype, 0};
   }
@@ -804,6 +806,153 @@ struct DescBuilder {
     }
   }
 
+  // a number of the metadata for layer i: an array of one per layer, or one
+  // for all (GgufPerLayer, model.gemma4.pas:477-507)
+  int32_t per_layer(const std::string& key, int i, int layers) const
+  {
+    const Value* v = g->find(arch + "." + key);
+    if (!v || v->vtype != ARR) return count(key);
+    if (v->count != layers) refuse(fmt("%s has %lld values for %d layers", key.c_str(), (long long)v->count, layers));
+    int64_t x;
+    if (v->etype == I32) { int32_t t; memcpy(&t, v->data + 4 * i, 4); x = t; }
+    else if (v->etype == U32) { uint32_t t; memcpy(&t, v->data + 4 * i, 4); x = t; }
+    else refuse(key + " is an array of " + TYPE_NAME[v->etype] + ", expected integers");
+    if (x <= 0 || x > (int64_t(1) << 30)) refuse(fmt("%s[%d] = %lld out of range", key.c_str(), i, (long long)x));
+    return (int32_t)x;
+  }
+  // a positive integer of the metadata, or 0 when it is missing
+  int64_t int_or0(const std::string& key) const { return has(key) ? g->integer(arch + "." + key) : 0; }
+
+  // TGemma4Model.LoadGgufConfig / LoadWeights (model.gemma4.pas:509-679,
+  // :727-860): sliding and full layers of their own heads, two rotary sets,
+  // K=V, sandwich norms, GeGLU, the dense block beside the experts
+  void gemma4(ihip_model_desc& d)
+  {
+    // what this family does not compute: per-layer embeddings, shared KV
+    // layers, prediction layers, a scaled RoPE, a width per layer, an untied head
+    if (int_or0("embedding_length_per_layer_input") != 0) refuse("per-layer embeddings not supported");
+    if (int_or0("attention.shared_kv_layers") != 0) refuse("shared KV layers not supported");
+    if (int_or0("nextn_predict_layers") != 0) refuse("prediction layers not supported");
+    if (has("rope.scaling.type") && g->str(arch + ".rope.scaling.type") != "none")
+      refuse("rope scaling \"" + g->str(arch + ".rope.scaling.type") + "\" not supported");
+    if (const Value* v = g->find(arch + ".feed_forward_length"))
+      if (v->vtype == ARR) refuse("a feed-forward width per layer (the double-wide MLP) not supported");
+    if (g->tensor("output.weight")) refuse("an untied head not supported");
+    const Tensor* emb = g->tensor("token_embd.weight");
+    if (!emb) refuse("no tensor token_embd.weight in " + g->name);
+    if (emb->ndim != 2 || emb->shape[0] > (1 << 22))
+      refuse(fmt("token_embd.weight is shaped [%lld...] of %d dimensions", (long long)emb->shape[0], emb->ndim));
+    d.vocab = (int32_t)emb->shape[0];
+    d.hidden = count("embedding_length");
+    d.layers = count("block_count");
+    if (d.layers > 1024) refuse(fmt("%d layers", d.layers));
+    d.heads = count("attention.head_count");
+    d.ffn = count("feed_forward_length");
+    d.max_positions = count("context_length");
+    d.rms_eps = (float)g->real(arch + ".attention.layer_norm_rms_epsilon");
+    // the sliding heads (key_length_swa) and the full ones (key_length)
+    d.head_dim = count("attention.key_length_swa");
+    const int32_t full = count("attention.key_length");
+    if (count("attention.value_length_swa") != d.head_dim || count("attention.value_length") != full)
+      refuse("key and value heads of different sizes");
+    if (count("rope.dimension_count_swa") != d.head_dim || count("rope.dimension_count") != full)
+      refuse(fmt("rotating %d and %d values of heads of %d and %d", count("rope.dimension_count_swa"),
+                 count("rope.dimension_count"), d.head_dim, full));
+    d.rope_theta = g->real(arch + ".rope.freq_base_swa");
+    d.rope2_theta = g->real(arch + ".rope.freq_base");
+    // rope_freqs: 1 for the rotating pairs of the full head, 1e30 after them
+    const Tensor* fr = g->tensor("rope_freqs.weight");
+    if (!fr || fr->dtype != DT_F32 || fr->ndim != 1 || fr->shape[0] != full / 2)
+      refuse(fmt("rope_freqs.weight is not F32 [%d]", full / 2));
+    const float* f = (const float*)fr->data;
+    int r = 0;
+    while (r < full / 2 && f[r] == 1.0f) r++;
+    for (int i = r; i < full / 2; i++)
+      if (!(f[i] >= 1e30f))
+        refuse(fmt("rope_freqs.weight[%d] = %g is neither 1 before the others nor 1e30 after them", i, f[i]));
+    if (r == 0) refuse("rope_freqs.weight rotates no pair");
+    used++;
+    d.rope2_pairs = r;
+    d.activation = IHIP_ACT_GELU_TANH;
+    d.attention_scale = 1.0;
+    d.value_norm = 1;
+    d.swiglu_alpha = 1.0f;
+    if (has("final_logit_softcapping")) d.logit_softcap = g->real(arch + ".final_logit_softcapping");
+    d.embed_scale = (float)std::sqrt((double)d.hidden);
+    if (int_or0("expert_count") != 0) {
+      d.experts = count("expert_count");
+      d.experts_used = count("expert_used_count");
+      d.expert_ffn = count("expert_feed_forward_length");
+      d.norm_topk = 1;
+    }
+    // the kind of every layer: sliding_window_pattern (true: sliding)
+    const Value* pat = g->find(arch + ".attention.sliding_window_pattern");
+    if (!pat || pat->vtype != ARR || pat->etype != BOOLV || pat->count != d.layers)
+      refuse(fmt("attention.sliding_window_pattern is no array of %d booleans", d.layers));
+    const int32_t window = count("attention.sliding_window");
+    g->layers.assign((size_t)d.layers, ihip_layer_desc{});
+    for (int i = 0; i < d.layers; i++) {
+      ihip_layer_desc& L = g->layers[i];
+      L.kv_heads = per_layer("attention.head_count_kv", i, d.layers);
+      if (pat->data[i]) {
+        L.window = window;
+        if (!d.kv_heads) d.kv_heads = L.kv_heads;
+      } else {
+        L.head_dim = full;
+        L.rope_set = 1;
+        // attention_k_eq_v: no attn_v, the values are the keys
+        L.k_is_v = g->tensor("blk." + std::to_string(i) + ".attn_v.weight") == nullptr;
+      }
+      if (L.kv_heads > d.heads || d.heads % L.kv_heads)
+        refuse(fmt("layer %d has %d KV heads for %d heads", i, L.kv_heads, d.heads));
+    }
+    if (!d.kv_heads) refuse("no sliding layer");
+    check_config(d);
+    if (full > 1024 || full & 1 || (int64_t)d.heads * full > (1 << 16)) refuse(fmt("full heads of %d", full));
+    const int64_t h = d.hidden, E = d.experts, fi = d.expert_ffn;
+    d.embed = embedding(d);
+    d.final_norm = weight("output_norm.weight", {h});
+    // the router input: an RMSNorm without weight times scale and hidden^-0.5,
+    // folded into one norm weight (float32 products, as the reference)
+    const float root = (float)(1 / std::sqrt(1.0 * (double)h));
+    for (int i = 0; i < d.layers; i++) {
+      ihip_layer_desc& L = g->layers[i];
+      const std::string b = "blk." + std::to_string(i) + ".";
+      const int64_t hd = L.head_dim ? L.head_dim : d.head_dim, qw = (int64_t)d.heads * hd,
+                    kvw = (int64_t)L.kv_heads * hd;
+      L.q = matrix(b + "attn_q.weight", qw, h);
+      L.k = matrix(b + "attn_k.weight", kvw, h);
+      if (!L.k_is_v) L.v = matrix(b + "attn_v.weight", kvw, h);
+      L.o = matrix(b + "attn_output.weight", h, qw);
+      L.q_norm = weight(b + "attn_q_norm.weight", {hd});
+      L.k_norm = weight(b + "attn_k_norm.weight", {hd});
+      L.input_norm = weight(b + "attn_norm.weight", {h});
+      L.attn_out_norm = weight(b + "post_attention_norm.weight", {h});
+      L.post_norm = weight(b + "ffn_norm.weight", {h});
+      L.ffn_out_norm = weight(b + "post_ffw_norm.weight", {h});
+      L.scalar = weight(b + "layer_output_scale.weight", {1});
+      L.gate = matrix(b + "ffn_gate.weight", d.ffn, h);
+      L.up = matrix(b + "ffn_up.weight", d.ffn, h);
+      L.down = matrix(b + "ffn_down.weight", h, d.ffn);
+      if (E > 0) {
+        L.moe = IHIP_FFN_DENSE_MOE;
+        L.dense_out_norm = weight(b + "post_ffw_norm_1.weight", {h});
+        L.moe_in_norm = weight(b + "pre_ffw_norm_2.weight", {h});
+        L.moe_out_norm = weight(b + "post_ffw_norm_2.weight", {h});
+        L.router = matrix(b + "ffn_gate_inp.weight", E, h);
+        const ihip_tensor sc = weight(b + "ffn_gate_inp.scale", {h});
+        auto folded = std::make_unique<std::vector<float>>((size_t)h);
+        for (int64_t j = 0; j < h; j++) (*folded)[j] = ((const float*)sc.data)[j] * root;
+        L.router_norm = ihip_tensor{folded->data(), DT_F32, 0};
+        g->widened.push_back(std::move(folded));
+        L.expert_scale = weight(b + "ffn_down_exps.scale", {E});
+        L.exp_gate = experts(b + "ffn_gate_up_exps.weight", E, 2 * fi, h, true);
+        L.exp_gate_up = 1;
+        L.exp_down = experts(b + "ffn_down_exps.weight", E, h, fi, true);
+      }
+    }
+  }
+
   // the token embedding: read per token, so its block scales are checked here
   ihip_tensor embedding(const ihip_model_desc& d)
   {
@@ -826,8 +975,10 @@ struct DescBuilder {
       gptoss(d);
     } else if (arch == "qwen35") {
       qwen35(d);
+    } else if (arch == "gemma4") {
+      gemma4(d);
     } else {
-      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, gpt-oss, qwen35)");
+      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, gpt-oss, qwen35, gemma4)");
     }
     // an unknown tensor means a model this path does not understand
     const int64_t expect = trunk >= 0 ? trunk : (int64_t)g->tensors.size();

@@ -360,12 +360,18 @@ _LAYER_TENSORS = ["input_norm", "q", "k", "v", "o", "q_bias", "k_bias", "v_bias"
 _LIN_TENSORS = ["lin_qkv", "lin_z", "lin_b", "lin_a", "lin_out", "lin_conv", "lin_dt_bias",
                 "lin_neg_a", "lin_norm"]
 MIXER_ATTENTION, MIXER_DELTANET = 0, 1
+FFN_DENSE, FFN_MOE, FFN_DENSE_MOE = 0, 1, 2
+ACT_SILU, ACT_GELU_TANH = 0, 1
+_GEMMA_TENSORS = ["attn_out_norm", "ffn_out_norm", "dense_out_norm", "moe_in_norm", "moe_out_norm",
+                  "router_norm", "expert_scale", "scalar"]
 
 
 class LayerDesc(C.Structure):
     _fields_ = [(n, Tensor) for n in _LAYER_TENSORS] + [
         ("window", C.c_int32), ("moe", C.c_int32), ("mixer", C.c_int32),
-        ("output_gate", C.c_int32)] + [(n, Tensor) for n in _LIN_TENSORS]
+        ("output_gate", C.c_int32)] + [(n, Tensor) for n in _LIN_TENSORS] + [
+        (n, C.c_int32) for n in ("head_dim", "kv_heads", "k_is_v", "rope_set", "exp_gate_up",
+                                 "reserved1")] + [(n, Tensor) for n in _GEMMA_TENSORS]
 
 
 class ModelDesc(C.Structure):
@@ -379,7 +385,11 @@ class ModelDesc(C.Structure):
          ("rope_attention", C.c_double), ("embed", Tensor), ("final_norm", Tensor),
          ("head", Tensor), ("layer", C.POINTER(LayerDesc))] + \
         [(n, C.c_int32) for n in ("rope_dims", "lin_key_heads", "lin_value_heads",
-                                  "lin_key_dim", "lin_value_dim", "lin_conv", "lin_tiled")]
+                                  "lin_key_dim", "lin_value_dim", "lin_conv", "lin_tiled",
+                                  "activation", "value_norm")] + \
+        [("embed_scale", C.c_float), ("reserved2", C.c_float), ("attention_scale", C.c_double),
+         ("logit_softcap", C.c_double), ("rope2_theta", C.c_double), ("rope2_pairs", C.c_int32),
+         ("reserved3", C.c_int32)]
 
 
 class Model:

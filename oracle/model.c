@@ -43,7 +43,6 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
   m->kv_f16 = kv_f16;
   m->threads = threads > 0 ? threads : 1;
   m->route_gap = INFINITY;
-  int64_t kvw = (int64_t)d->kv_heads * d->head_dim;
   m->keys = (float**)calloc(d->layers, sizeof(float*));
   m->values = (float**)calloc(d->layers, sizeof(float*));
   m->conv = (float**)calloc(d->layers, sizeof(float*));
@@ -58,8 +57,11 @@ int orc_model_create(const ihip_model_desc* d, int64_t max_tokens, int kv_f16, i
                                    sizeof(float));
       continue;
     }
-    m->keys[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
-    m->values[l] = (float*)calloc(max_tokens * kvw, sizeof(float));
+    const ihip_layer_desc* L = &d->layer[l];
+    const int64_t lkvw = (int64_t)(L->kv_heads > 0 ? L->kv_heads : d->kv_heads) *
+                         (L->head_dim > 0 ? L->head_dim : d->head_dim);
+    m->keys[l] = (float*)calloc(max_tokens * lkvw, sizeof(float));
+    m->values[l] = (float*)calloc(max_tokens * lkvw, sizeof(float));
   }
   *out = m;
   return 0;
@@ -139,6 +141,15 @@ static void add(float* x, const float* t, int64_t n)
   for (int64_t i = 0; i < n; i++) x[i] = x[i] + t[i];
 }
 
+/* TDecoderModel.Activate (decoder.pas:2857-2863): SwiGLU or GeGLU */
+static void activate(const ihip_model_desc* d, float* gate, const float* up, int64_t n)
+{
+  if (d->activation == IHIP_ACT_GELU_TANH)
+    orc_geglu(gate, up, n);
+  else
+    orc_swiglu(gate, up, n, d->swiglu_alpha, d->swiglu_limit);
+}
+
 static float half_round(float v)
 {
   return orc_half_to_single(orc_single_to_half(v));
@@ -160,9 +171,21 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
                            float* logits, int all_logits, float* normed)
 {
   const ihip_model_desc* d = &m->d;
-  int64_t h = d->hidden, hd = d->head_dim, qw = (int64_t)d->heads * hd,
-          kvw = (int64_t)d->kv_heads * hd, past = m->length;
-  const int64_t rot = d->rope_dims > 0 ? d->rope_dims : hd, half = rot / 2;
+  const int64_t h = d->hidden, past = m->length;
+  const int64_t rot = d->rope_dims > 0 ? d->rope_dims : d->head_dim, half = rot / 2;
+  /* the widest heads of any layer (Gemma 4: per layer), and the heads of the
+   * second rotary set */
+  int64_t qw = (int64_t)d->heads * d->head_dim, kvw = (int64_t)d->kv_heads * d->head_dim,
+          hdmax = d->head_dim, hd2 = 0;
+  for (int l = 0; l < d->layers; l++) {
+    const ihip_layer_desc* L = &m->layer[l];
+    const int64_t lhd = L->head_dim > 0 ? L->head_dim : d->head_dim;
+    const int64_t lkvh = L->kv_heads > 0 ? L->kv_heads : d->kv_heads;
+    if (d->heads * lhd > qw) qw = d->heads * lhd;
+    if (lkvh * lhd > kvw) kvw = lkvh * lhd;
+    if (lhd > hdmax) hdmax = lhd;
+    if (L->rope_set) hd2 = lhd;
+  }
   const int64_t kh = d->lin_key_heads, vh = d->lin_value_heads, dk = d->lin_key_dim,
                 dv = d->lin_value_dim, vd = vh * dv, cd = 2 * kh * dk + vd;
   /* LinGroup (decoder.pas:2457-2463) */
@@ -183,7 +206,11 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
   float* attn = (float*)malloc(n * qw * 4);
   float* gate = (float*)malloc(n * (f > 0 ? f : 1) * 4);
   float* up = (float*)malloc(n * (f > 0 ? f : 1) * 4);
-  float* cs = (float*)malloc(n * hd * 4);
+  float* cs = (float*)malloc(n * hdmax * 4);
+  float* cs2 = (float*)malloc(n * (hd2 > 0 ? hd2 : 1) * 4);
+  float* ones = (float*)malloc(hdmax * 4);
+  float* dense = (float*)malloc(n * h * 4);
+  for (int64_t i = 0; i < hdmax; i++) ones[i] = 1.0f;
   int64_t E = d->experts > 0 ? d->experts : 1, K = d->experts_used > 0 ? d->experts_used : 1;
   float* route = (float*)malloc(n * E * 4);
   int32_t* chosen = (int32_t*)malloc(n * K * 4);
@@ -201,13 +228,16 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
   float* core = (float*)malloc(n * (vd > 0 ? vd : 1) * 4);
 
   orc_rotary(d, past, n, cs);
-  const float* cosv = cs;
-  const float* sinv = cs + n * half;
-  if (ids)
+  if (hd2 > 0) orc_rotary2(d, hd2, past, n, cs2);
+  if (ids) {
     for (int64_t i = 0; i < n; i++)
       orc_row_to_f32(d->embed.data, d->embed.dtype, ids[i], h, x + i * h);
-  else
+    /* Gemma scales the embeddings of ids (ForwardPart, decoder.pas:3305-3309) */
+    if (d->embed_scale > 0)
+      for (int64_t i = 0; i < n * h; i++) x[i] = x[i] * d->embed_scale;
+  } else {
     memcpy(x, embeds, n * h * 4);
+  }
   for (int l = 0; l < d->layers && !err; l++) {
     const ihip_layer_desc* L = &m->layer[l];
     if (L->mixer == IHIP_MIXER_DELTANET) {
@@ -232,7 +262,10 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       add(x, tmp, n * h);
       goto ffn;
     }
-    /* AttentionBlock */
+    /* AttentionBlock, with this layer's heads */
+    const int64_t hd = L->head_dim > 0 ? L->head_dim : d->head_dim;
+    const int64_t kvh = L->kv_heads > 0 ? L->kv_heads : d->kv_heads;
+    const int64_t qw = (int64_t)d->heads * hd, kvw = kvh * hd;
     orc_rmsnorm(x, n, h, (const float*)L->input_norm.data, d->rms_eps, hh);
     if (L->output_gate) {
       /* per head the query, then its gate */
@@ -245,13 +278,23 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       err |= lin(m, hh, n, h, L->q, 0, qw, (const float*)L->q_bias.data, q);
     }
     err |= lin(m, hh, n, h, L->k, 0, kvw, (const float*)L->k_bias.data, k);
-    err |= lin(m, hh, n, h, L->v, 0, kvw, (const float*)L->v_bias.data, v);
+    if (L->k_is_v)
+      memcpy(v, k, n * kvw * 4);  /* the values are the raw keys */
+    else
+      err |= lin(m, hh, n, h, L->v, 0, kvw, (const float*)L->v_bias.data, v);
     if (L->q_norm.data) {
       orc_rmsnorm(q, n * d->heads, hd, (const float*)L->q_norm.data, d->rms_eps, q);
-      orc_rmsnorm(k, n * d->kv_heads, hd, (const float*)L->k_norm.data, d->rms_eps, k);
+      orc_rmsnorm(k, n * kvh, hd, (const float*)L->k_norm.data, d->rms_eps, k);
     }
-    orc_rope(q, n, d->heads, hd, cosv, sinv, rot);
-    orc_rope(k, n, d->kv_heads, hd, cosv, sinv, rot);
+    if (d->value_norm) orc_rmsnorm(v, n * kvh, hd, ones, d->rms_eps, v);
+    if (L->rope_set) {
+      /* the second set: every pair of the head, frequency 0 beyond its share */
+      orc_rope(q, n, d->heads, hd, cs2, cs2 + n * (hd / 2), 0);
+      orc_rope(k, n, kvh, hd, cs2, cs2 + n * (hd / 2), 0);
+    } else {
+      orc_rope(q, n, d->heads, hd, cs, cs + n * half, rot);
+      orc_rope(k, n, kvh, hd, cs, cs + n * half, rot);
+    }
     float* kc = m->keys[l] + past * kvw;
     float* vc = m->values[l] + past * kvw;
     for (int64_t i = 0; i < n * kvw; i++) {
@@ -259,35 +302,61 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       vc[i] = m->kv_f16 ? half_round(v[i]) : v[i];
     }
     if (m->fast)
-      orc_fast_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads, attn,
+      orc_fast_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, kvh, attn,
                          L->window, (const float*)L->sinks.data, m->threads);
     else
-      orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, d->kv_heads,
-                           attn, L->window, (const float*)L->sinks.data, 0);
+      orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, kvh,
+                           attn, L->window, (const float*)L->sinks.data, d->attention_scale);
     if (L->output_gate) orc_gate_sigmoid(attn, gq, n * qw);
     err |= lin(m, attn, n, qw, L->o, 0, h, (const float*)L->o_bias.data, tmp);
+    /* Gemma: the attention output normed before the residual */
+    if (L->attn_out_norm.data)
+      orc_rmsnorm(tmp, n, h, (const float*)L->attn_out_norm.data, d->rms_eps, tmp);
     add(x, tmp, n * h);
   ffn:
-    /* the feed-forward block */
+    /* the feed-forward block: DenseBlock, MoeBlock or DenseMoeBlock
+     * (decoder.pas:2880-2899, :3037-3091), then Gemma's layer scalar */
     orc_rmsnorm(x, n, h, (const float*)L->post_norm.data, d->rms_eps, hh);
-    if (!L->moe) {
+    if (L->moe != IHIP_FFN_MOE) {
       err |= lin(m, hh, n, h, L->gate, 0, d->ffn, NULL, gate);
       err |= lin(m, hh, n, h, L->up, 0, d->ffn, NULL, up);
-      orc_swiglu(gate, up, n * d->ffn, d->swiglu_alpha, d->swiglu_limit);
+      activate(d, gate, up, n * d->ffn);
       err |= lin(m, gate, n, d->ffn, L->down, 0, h, NULL, tmp);
-    } else {
-      int64_t fi = d->expert_ffn;
-      err |= lin(m, hh, n, h, L->router, 0, E, (const float*)L->router_bias.data, route);
+    }
+    if (L->moe != IHIP_FFN_DENSE) {
+      float* dst = tmp;
+      if (L->moe == IHIP_FFN_DENSE_MOE) {
+        /* the dense output normed; the router on the residual's own norm, the
+         * experts on another, their sum normed */
+        orc_rmsnorm(tmp, n, h, (const float*)L->dense_out_norm.data, d->rms_eps, tmp);
+        orc_rmsnorm(x, n, h, (const float*)L->router_norm.data, d->rms_eps, hh);
+        err |= lin(m, hh, n, h, L->router, 0, E, NULL, route);
+        orc_rmsnorm(x, n, h, (const float*)L->moe_in_norm.data, d->rms_eps, hh);
+        dst = dense;
+      } else {
+        err |= lin(m, hh, n, h, L->router, 0, E, (const float*)L->router_bias.data, route);
+      }
+      /* Experts (decoder.pas:3092-3150): the route of every row, then
+       * expert by expert in id order over its gathered rows */
+      const int64_t fi = d->expert_ffn;
+      const float* escale = (const float*)L->expert_scale.data;
       for (int64_t r = 0; r < n; r++) {
         orc_route(route + r * E, E, K, d->norm_topk, chosen + r * K, cw + r * K);
         if (K < E) {
           double g = route_gap(route + r * E, E, chosen + r * K, K);
           if (g < m->route_gap) m->route_gap = g;
         }
+        if (escale)
+          for (int64_t j = 0; j < K; j++) cw[r * K + j] = cw[r * K + j] * escale[chosen[r * K + j]];
       }
-      memset(tmp, 0, n * h * 4);
-      uint64_t gb = row_bytes(L->exp_gate.dtype, h) * fi;
-      uint64_t db = row_bytes(L->exp_down.dtype, fi) * h;
+      memset(dst, 0, n * h * 4);
+      /* gate and up of an expert: two tensors, or one [E, 2 fi, h] with the
+       * gate rows first */
+      const uint64_t rb = row_bytes(L->exp_gate.dtype, h);
+      const uint64_t gstride = rb * fi * (L->exp_gate_up ? 2 : 1);
+      const ihip_tensor ut = L->exp_gate_up ? L->exp_gate : L->exp_up;
+      const uint64_t uoff = L->exp_gate_up ? rb * fi : 0;
+      const uint64_t db = row_bytes(L->exp_down.dtype, fi) * h;
       for (int64_t e = 0; e < E; e++) {
         int64_t cnt = 0;
         for (int64_t r = 0; r < n; r++)
@@ -302,22 +371,34 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
         const float* bg = L->exp_gate_bias.data ? (const float*)L->exp_gate_bias.data + e * fi : NULL;
         const float* bu = L->exp_up_bias.data ? (const float*)L->exp_up_bias.data + e * fi : NULL;
         const float* bd = L->exp_down_bias.data ? (const float*)L->exp_down_bias.data + e * h : NULL;
-        err |= lin(m, gather, cnt, h, L->exp_gate, e * gb, fi, bg, gate);
-        err |= lin(m, gather, cnt, h, L->exp_up, e * gb, fi, bu, up);
-        orc_swiglu(gate, up, cnt * fi, d->swiglu_alpha, d->swiglu_limit);
+        err |= lin(m, gather, cnt, h, L->exp_gate, e * gstride, fi, bg, gate);
+        err |= lin(m, gather, cnt, h, ut, e * gstride + uoff, fi, bu, up);
+        activate(d, gate, up, cnt * fi);
         err |= lin(m, gate, cnt, fi, L->exp_down, e * db, h, bd, eout);
         for (int64_t c = 0; c < cnt; c++) {
           float w = roww[c];
-          float* dst = tmp + rowi[c] * h;
+          float* o = dst + rowi[c] * h;
           const float* src = eout + c * h;
           for (int64_t i = 0; i < h; i++) {
             float p = w * src[i];
-            dst[i] = dst[i] + p;
+            o[i] = o[i] + p;
           }
         }
       }
+      if (L->moe == IHIP_FFN_DENSE_MOE) {
+        orc_rmsnorm(dense, n, h, (const float*)L->moe_out_norm.data, d->rms_eps, dense);
+        add(tmp, dense, n * h);
+      }
     }
+    /* Gemma: the feed-forward output normed before the residual */
+    if (L->ffn_out_norm.data)
+      orc_rmsnorm(tmp, n, h, (const float*)L->ffn_out_norm.data, d->rms_eps, tmp);
     add(x, tmp, n * h);
+    /* Gemma: the whole state times the layer's scalar */
+    if (L->scalar.data) {
+      const float sc = *(const float*)L->scalar.data;
+      for (int64_t i = 0; i < n * h; i++) x[i] = x[i] * sc;
+    }
   }
   if (!err) {
     m->length = past + n;
@@ -331,12 +412,15 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
         err |= lin(m, hh, n, h, head, 0, d->vocab, NULL, logits);
       else
         err |= lin(m, hh + (n - 1) * h, 1, h, head, 0, d->vocab, NULL, logits);
+      if (d->logit_softcap > 0)
+        orc_softcap(logits, (all_logits ? n : 1) * d->vocab, d->logit_softcap);
     }
   }
   free(x); free(hh); free(tmp); free(q); free(k); free(v); free(attn);
   free(gate); free(up); free(cs); free(route); free(chosen); free(cw);
   free(gather); free(eout); free(rowi); free(roww);
   free(qg); free(gq); free(qkv); free(z); free(beta); free(decay); free(core);
+  free(cs2); free(ones); free(dense);
   return err ? IHIP_E_ARG : 0;
 }
 

@@ -232,3 +232,58 @@ int orc_rotary(const ihip_model_desc* dsc, int64_t first, int64_t rows, float* c
   free(f);
   return 0;
 }
+
+/* decoder.pas:1742-1752 and :2524-2537 TDecoderModel.Rotary2: the second
+ * rotary set over heads of hd2 values: 1 / theta2 ^ (2i / hd2), each step
+ * rounded to single, for the first rope2_pairs pairs, 0 for the others (cos
+ * 1, sin 0); [rows, hd2 / 2] cos, then sin */
+int orc_rotary2(const ihip_model_desc* dsc, int64_t hd2, int64_t first, int64_t rows, float* cs)
+{
+  int64_t half = hd2 / 2;
+  float* f = (float*)calloc(half > 0 ? half : 1, sizeof(float));
+  double lt = log(dsc->rope2_theta);
+  for (int64_t i = 0; i < half && i < dsc->rope2_pairs; i++) {
+    float e = (float)((double)(2 * i) / (double)hd2);
+    float p = (float)exp(lt * (double)e);
+    f[i] = 1.0f / p;
+  }
+  float* sn = cs + rows * half;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t i = 0; i < half; i++) {
+      float angle = f[i] * (float)(first + r);
+      cs[r * half + i] = (float)cos((double)angle);
+      sn[r * half + i] = (float)sin((double)angle);
+    }
+  free(f);
+  return 0;
+}
+
+/* backend.cpu.pas:1836-1860 GeluTanhGlu: gelu_tanh(g) in double rounded to
+ * single, then the product */
+void orc_geglu(float* gate, const float* up, int64_t n)
+{
+  const double k = 0.7978845608028654;
+  for (int64_t i = 0; i < n; i++) {
+    double g = gate[i];
+    double t = k * (g + 0.044715 * g * g * g);
+    if (t > 20) t = 1;
+    else if (t < -20) t = -1;
+    else t = 1 - 2 / (exp(2 * t) + 1);
+    float b = (float)(0.5 * g * (1 + t));
+    gate[i] = b * up[i];
+  }
+}
+
+/* decoder.pas:1293-1312 InferSoftcap: tanh(x / cap) * cap, each step single */
+void orc_softcap(float* x, int64_t n, double cap)
+{
+  for (int64_t i = 0; i < n; i++) {
+    float a = (float)(x[i] / cap);
+    double d = a;
+    float t;
+    if (d > 20) t = 1;
+    else if (d < -20) t = -1;
+    else t = (float)(1 - 2 / (exp(2 * d) + 1));
+    x[i] = (float)(t * cap);
+  }
+}

@@ -29,6 +29,8 @@
  *   orc_rotary                                   - numpy float32 step replay
  *   orc_delta_prep, orc_delta_rule, orc_gate_sigmoid - transformers' float32
  *       intermediate states and logits of tiny-qwen35 (tests/test_qwen35.py)
+ *   orc_rotary2, orc_geglu, orc_softcap           - transformers' float32 logits
+ *       of tiny-gemma4 and closed forms (tests/test_gemma4.py)
  *   orc_model_*                                  - composed of the above;
  *       checked against a numpy float64 forward of a tiny model
  */
@@ -93,6 +95,12 @@ void orc_route(const float* logits, int64_t experts, int64_t k, int norm_topk,
 /* sampler.pas:123-160 InferArgMax */
 int64_t orc_argmax(const float* v, int64_t n);
 
+/* decoder.pas:2524-2537 Rotary2: the second rotary set over heads of hd2 */
+int orc_rotary2(const ihip_model_desc* d, int64_t hd2, int64_t first, int64_t rows, float* cs);
+/* backend.cpu.pas:1836-1860 GeluTanhGlu: gate := gelu_tanh(gate) * up */
+void orc_geglu(float* gate, const float* up, int64_t n);
+/* decoder.pas:1293-1312 InferSoftcap */
+void orc_softcap(float* x, int64_t n, double cap);
 /* deltanet.c: GateBySigmoid (decoder.pas:2594-2610): a[i] *= sigmoid(gate[i]) */
 void orc_gate_sigmoid(float* a, const float* gate, int64_t n);
 /* deltanet.c: TDecoderModel.DeltaPrep (decoder.pas:2755-2855) over every item

@@ -12,10 +12,13 @@ converter and ggml's reference quantizers, and by transformers in float32):
 - tiny-qwen35/gguf/{bf16,q8_0,text-bf16,text-q8_0,bad-*}.gguf: the qwen35
   files of TTestInferQwen35 (tests/test.infer.qwen35.pas) and the device
   tests of the DeltaNet (tests/test.infer.cuda.pas);
+- tiny-gemma4/gguf/{bf16,q8_0,dense-bf16,dense-q8_0,rope44,bad-*}.gguf: the
+  gemma4 files of TTestInferGemma4 (tests/test.infer.gemma4.pas);
 - the case ids, logits, greedy tokens and margins of tiny-qwen3,
   tiny-qwen3/untied, tiny-qwen3moe, tiny-gpt-oss/mxfp4, tiny-qwen35 and
   tiny-qwen35/text (with the one-token-at-a-time logits and the first layer's
-  mixer output of the last two) (tensors.bin, described by manifest.json),
+  mixer output of the last two), tiny-gemma4 and tiny-gemma4/dense
+  (tensors.bin, described by manifest.json),
   gathered into expected.npz.
 
 Every file is checked against the sha256 its manifest records before it is
@@ -71,19 +74,22 @@ def main(ref):
     # the reader fixture
     copy_dir(os.path.join(root, "tiny-gguf"), ["model.gguf"], OUT, {})
     sets = [("tiny-qwen3-gguf", "qwen3"), (os.path.join("tiny-qwen3moe", "gguf"), "qwen3moe"),
-            (os.path.join("tiny-gpt-oss", "gguf"), "gpt-oss"), (os.path.join("tiny-qwen35", "gguf"), "qwen35")]
+            (os.path.join("tiny-gpt-oss", "gguf"), "gpt-oss"), (os.path.join("tiny-qwen35", "gguf"), "qwen35"),
+            (os.path.join("tiny-gemma4", "gguf"), "gemma4")]
     for folder, tag in sets:
         src = os.path.join(root, folder)
         files = json.load(open(os.path.join(src, "manifest.json"))).get("files", {})
         good = [n for n in sorted(os.listdir(src)) if n.endswith(".gguf") and not n.startswith(
-            ("bad-", "tok-"))]
-        bad = [n for n in sorted(os.listdir(src)) if n.startswith("bad-") and n.endswith(".gguf")]
+            ("bad-", "tok-", "tokenizer"))]
+        bad = [n for n in sorted(os.listdir(src)) if n.startswith("bad-") and n.endswith(".gguf")
+               and not n.startswith("bad-tokenizer")]
         copy_dir(src, good, os.path.join(OUT, tag), files)
         copy_dir(src, bad, os.path.join(OUT, "bad", tag), files)
     expected = {}
     for folder, tag in [("tiny-qwen3", "qwen3"), (os.path.join("tiny-qwen3", "untied"), "qwen3-untied"),
                         ("tiny-qwen3moe", "qwen3moe"), (os.path.join("tiny-gpt-oss", "mxfp4"), "gpt-oss"),
-                        ("tiny-qwen35", "qwen35"), (os.path.join("tiny-qwen35", "text"), "qwen35-text")]:
+                        ("tiny-qwen35", "qwen35"), (os.path.join("tiny-qwen35", "text"), "qwen35-text"),
+                        ("tiny-gemma4", "gemma4"), (os.path.join("tiny-gemma4", "dense"), "gemma4-dense")]:
         for k, v in cases(os.path.join(root, folder)).items():
             expected[f"{tag}/{k}"] = v
     np.savez_compressed(os.path.join(OUT, "expected.npz"), **expected)

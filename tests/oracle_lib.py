@@ -51,6 +51,11 @@ def lib():
         L.orc_argmax.restype = i64
         L.orc_argmax.argtypes = [vp, i64]
         L.orc_rotary.argtypes = [vp, i64, i64, vp]
+        L.orc_rotary2.argtypes = [vp, i64, i64, i64, vp]
+        L.orc_geglu.argtypes = [vp, vp, i64]
+        L.orc_geglu.restype = None
+        L.orc_softcap.argtypes = [vp, i64, C.c_double]
+        L.orc_softcap.restype = None
         L.orc_gate_sigmoid.argtypes = [vp, vp, i64]
         L.orc_gate_sigmoid.restype = None
         L.orc_delta_prep.argtypes = [vp, vp, vp, vp, i64, vp, vp, vp, vp, i64, i64, i64, i64, i64]
@@ -193,6 +198,28 @@ def route(logits, k, norm_topk=True):
     w = np.empty(k, np.float32)
     lib().orc_route(_p(lg), lg.size, k, int(norm_topk), _p(ids), _p(w))
     return ids, w
+
+
+def geglu(g, u):
+    """GeluTanhGlu: gelu_tanh(g) * u."""
+    g = np.array(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    lib().orc_geglu(_p(g), _p(u), g.size)
+    return g
+
+
+def softcap(x, cap):
+    x = np.array(x, np.float32)
+    lib().orc_softcap(_p(x), x.size, float(cap))
+    return x
+
+
+def rotary2(desc, hd2, first, rows):
+    """Rotary2: ([rows, hd2 / 2] cos, sin) of the second set."""
+    cs = np.empty(rows * hd2, np.float32)
+    lib().orc_rotary2(C.addressof(desc.struct), hd2, first, rows, _p(cs))
+    half = hd2 // 2
+    return cs[:rows * half].reshape(rows, half), cs[rows * half:].reshape(rows, half)
 
 
 def gate_sigmoid(a, gate):
