@@ -601,11 +601,43 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
 }
 
-static WeightEntry* find_weight(ihip_ctx* c, const void* host, int t, uint64_t bytes)
+static WeightEntry* find_weight(ihip_ctx* c, const void* host, int t, uint64_t bytes, int64_t stride_rows = 0)
 {
   for (auto& w : c->weights)
-    if (w.host == host && w.dtype == t && w.bytes == bytes) return &w;
+    if (w.host == host && w.dtype == t && w.bytes == bytes && w.stride_rows == stride_rows) return &w;
   return nullptr;
+}
+
+int weight_rows(ihip_ctx* c, const void* host, int t, int64_t out, int64_t in, int64_t count,
+                int64_t stride_rows, uint64_t* dev)
+{
+  if (!c || !host || !dev || out < 1 || in < 1 || count < 1 || stride_rows < out || !block_values(t) ||
+      in % block_values(t))
+    return fail(IHIP_E_ARG, "weight_rows: bad shape or type");
+  const uint64_t rb = row_bytes(t, in), bytes = rb * (uint64_t)out * (uint64_t)count;
+  if (WeightEntry* w = find_weight(c, host, t, bytes, stride_rows)) {
+    *dev = w->dev;
+    return 0;
+  }
+  if (c->capturing) return fail(IHIP_E_CAPTURE, "weight_rows: upload while capturing");
+  std::vector<uint8_t> rows(bytes), staged(bytes);
+  for (int64_t e = 0; e < count; e++)
+    memcpy(rows.data() + (uint64_t)e * out * rb, (const uint8_t*)host + (uint64_t)e * stride_rows * rb,
+           (size_t)(out * rb));
+  void* p = nullptr;
+  IHIP_CHECK(hipSetDevice(c->device));
+  IHIP_CHECK(hipMalloc(&p, (bytes + 255) & ~(uint64_t)255));
+  repack(rows.data(), staged.data(), t, out, in, count);
+  hipError_t e = hipMemcpyHtoD((hipDeviceptr_t)p, staged.data(), bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "weight_rows upload");
+  }
+  WeightEntry w{host, t, bytes, (uint64_t)p};
+  w.stride_rows = stride_rows;
+  c->weights.push_back(w);
+  *dev = (uint64_t)p;
+  return 0;
 }
 
 }  // namespace ihip
@@ -884,10 +916,10 @@ int ihip_enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, ui
                            int64_t rows, int64_t heads, int64_t kvh, int64_t hd, int64_t past,
                            int64_t window, uint64_t sinks, double scale, int kv_f16)
 {
-  if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 8 || hd > 256 || past < 0 ||
+  if (!c || rows < 1 || heads < 1 || kvh < 1 || heads % kvh || hd < 2 || hd > 512 || past < 0 ||
       window < 0)
     return fail(IHIP_E_ARG, "ihip_enqueue_attention");
-  if (hd % 8) return fail(IHIP_E_ARG, "attention: head size not a multiple of 8");
+  if (hd & 1) return fail(IHIP_E_ARG, "attention: an odd head size");
   int64_t maxkeys = past + rows;
   if (window > 0 && maxkeys > window) maxkeys = window;
   const int splits = attention_splits(maxkeys);
@@ -908,6 +940,7 @@ int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k,
     int* ids;
     float* w;
     int32_t experts, k, norm, rows;
+    const float* scale;
   } a = {(const float*)logits, (int*)ids, (float*)w, (int32_t)experts, (int32_t)k, norm_topk, 1};
   return launch(c, "route", dim3(1), dim3(256), &a);
 }
@@ -1138,8 +1171,9 @@ int enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_
     snprintf(name, sizeof name, "attention_rows_%s_%d", f16 ? "f16" : "f32", (int)hd);
     rc = launch(c, name, dim3((unsigned)heads, (unsigned)((rows + 7) / 8), (unsigned)splits), dim3(256), &a);
   } else {
-    rc = launch(c, f16 ? "attention_part_f16" : "attention_part_f32",
-                dim3((unsigned)heads, (unsigned)rows, (unsigned)splits), dim3(256), &a);
+    const char* name = hd > 256 ? (f16 ? "attention_part_f16_512" : "attention_part_f32_512")
+                                : (f16 ? "attention_part_f16" : "attention_part_f32");
+    rc = launch(c, name, dim3((unsigned)heads, (unsigned)rows, (unsigned)splits), dim3(256), &a);
   }
   if (rc) return rc;
   return launch(c, "attention_merge", dim3((unsigned)heads, (unsigned)rows), dim3(128), &a);

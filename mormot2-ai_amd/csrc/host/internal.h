@@ -37,6 +37,7 @@ struct WeightEntry {
   int dtype;
   uint64_t bytes;
   uint64_t dev;
+  int64_t stride_rows = 0;  // weight_rows: the rows from one matrix to the next
 };
 
 struct Kernel {
@@ -116,6 +117,12 @@ hipFunction_t kernel(ihip_ctx* c, const char* name);
 // the blocks of `block` threads of kernel `name` that one CU runs at once
 int resident_blocks(ihip_ctx* c, const char* name, int block, size_t shmem = 0);
 int launch(ihip_ctx* c, const char* name, dim3 grid, dim3 block, void* args, size_t shmem = 0);
+// count matrices of out rows each, matrix e starting stride_rows rows after
+// matrix e - 1 in the host tensor (the gate rows, or the up rows, of experts
+// stored [E, 2 * out, in]): uploaded contiguous like ihip_weight's, cached by
+// host address and stride
+int weight_rows(ihip_ctx* c, const void* host, int t, int64_t out, int64_t in, int64_t count,
+                int64_t stride_rows, uint64_t* dev);
 // grows a scratch buffer to at least bytes (never while capturing)
 int scratch(ihip_ctx* c, uint64_t& buf, uint64_t& cap, uint64_t bytes);
 

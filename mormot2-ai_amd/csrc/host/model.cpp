@@ -4,7 +4,11 @@
 // Qwen3 dense, Qwen3-MoE and gpt-oss shapes: per-head q/k norms, biases,
 // sinks, sliding windows, clamped SwiGLU, experts chosen on the device;
 // Qwen3.5: Gated DeltaNet layers with their states per context, the output
-// gate of the attention and a partial rotary share.
+// gate of the attention and a partial rotary share. Gemma 4: heads of their
+// own shape per layer, K=V, the value norm, a second rotary set, the norms
+// around both blocks, GeGLU, the dense block beside the experts (expert
+// scales, experts stored gate-and-up in one tensor), the layer scalar, the
+// embedding scale and the logit softcap.
 //
 // A prompt runs in chunks of up to CHUNK rows (CHUNK_MAX of
 // model.qwen3.cuda.pas:308 is 256; here 1024 by default, so that a prompt
@@ -35,6 +39,13 @@ struct DevLayer {
   int mixer = IHIP_MIXER_ATTENTION, output_gate = 0;
   uint64_t lqkv = 0, lz = 0, lb = 0, la = 0, lout = 0, lconv = 0, ldt = 0, lnega = 0, lnorm = 0;
   int lqkvd = 0, lzd = 0, lbd = 0, lad = 0, loutd = 0;
+  // Gemma 4: this layer's heads, K=V, the rotary set; the norms around the
+  // blocks, those of the dense block beside the experts, the expert scales
+  // and the layer scalar (0: none)
+  int64_t hd = 0, kvh = 0;
+  int k_is_v = 0, rope_set = 0;
+  uint64_t attn_out_norm = 0, ffn_out_norm = 0, dense_out_norm = 0, moe_in_norm = 0, moe_out_norm = 0;
+  uint64_t router_norm = 0, expert_scale = 0, scalar = 0;
 };
 
 }  // namespace ihip
@@ -59,6 +70,8 @@ struct ihip_mctx {
   // the rule's output; a gated attention's query+gate rows and its gates
   std::vector<uint64_t> conv, state;
   uint64_t qkv = 0, z = 0, beta = 0, decay = 0, core = 0, qg = 0, gq = 0;
+  // Gemma 4: the second rotary set's cos/sin, the experts' sum of a row
+  uint64_t cs2 = 0, moe = 0;
   // zeroed counters of the decode attention's heads (the last range block of
   // a head merges the head)
   uint64_t done = 0;
@@ -90,6 +103,9 @@ struct ihip_model {
   bool any_moe = false;
   bool recurrent = false;  // a DeltaNet layer: the context carries states
   bool gated = false;      // an attention layer with an output gate
+  bool gemma = false;      // Gemma 4's settings: no fused one-row path
+  // the widest heads of any layer, and the heads of the second rotary set
+  int64_t max_qw = 0, max_kvw = 0, max_hd = 0, hd2 = 0;
   // the host ranges of the uploaded weights: forgotten when the model goes,
   // as a model does in its destructor (backend.pas:151-158) - new host
   // tensors at a reused address must not meet the stale device copy
@@ -176,6 +192,29 @@ static void rotary(const ihip_model_desc& d, int64_t first, int64_t rows, float*
     }
 }
 
+// TDecoderModel.Rotary2 (decoder.pas:1742-1752, :2524-2537): the second
+// set over heads of hd2, 1 / theta2 ^ (2i / hd2) (each step rounded to
+// single) for the first rope2_pairs pairs, frequency 0 for the others; no
+// YaRN scale
+static void rotary2(const ihip_model_desc& d, int64_t hd2, int64_t first, int64_t rows, float* cs)
+{
+  const int64_t half = hd2 / 2;
+  const double lt = std::log(d.rope2_theta);
+  std::vector<float> f(half, 0.f);
+  for (int64_t i = 0; i < half && i < d.rope2_pairs; i++) {
+    float e = (float)((double)(2 * i) / (double)hd2);
+    float p = (float)std::exp(lt * (double)e);
+    f[i] = 1.0f / p;
+  }
+  float* sn = cs + rows * half;
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t i = 0; i < half; i++) {
+      float angle = f[i] * (float)(first + r);
+      cs[r * half + i] = (float)std::cos((double)angle);
+      sn[r * half + i] = (float)std::sin((double)angle);
+    }
+}
+
 static int upw(ihip_model* m, const ihip_tensor& t, int64_t out, int64_t in, int64_t count,
                uint64_t& dev, int& dt)
 {
@@ -256,6 +295,7 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
   ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
   const DevLayer& L = m->L[l];
+  const int64_t hd = L.hd, kvh = L.kvh;
   struct {
     float* q;
     const float* k;
@@ -267,19 +307,24 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
     void* vc;
     const int* pastp;
     double eps;
-    int32_t rows, heads, kvh, hd, past, f16, rot, pad;
-  } ra = {(float*)s->q, (const float*)s->k, (const float*)s->v, (const float*)L.qn,
-          (const float*)L.kn, (const float*)s->cs, (void*)s->kc[l], (void*)s->vc[l],
-          graph ? (const int*)s->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads,
-          d.kv_heads, d.head_dim, (int32_t)past, m->kv_f16, (int32_t)rope_dims(d), 0};
-  int rc = launch(m->c, "qkrope", dim3((unsigned)(d.heads + d.kv_heads), (unsigned)n), dim3(64), &ra);
+    int32_t rows, heads, kvh, hd, past, f16, rot, vnorm;
+  } ra = {(float*)s->q, (const float*)s->k,
+          // K=V: the values are the raw keys (normed by ValueNorm, not rotated)
+          (const float*)(L.k_is_v ? s->k : s->v), (const float*)L.qn, (const float*)L.kn,
+          (const float*)(L.rope_set ? s->cs2 : s->cs), (void*)s->kc[l], (void*)s->vc[l],
+          graph ? (const int*)s->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads, (int32_t)kvh,
+          (int32_t)hd, (int32_t)past, m->kv_f16,
+          // the second set: every pair of the head (those beyond its share
+          // have frequency 0)
+          (int32_t)(L.rope_set ? 0 : rope_dims(d)), d.value_norm};
+  int rc = launch(m->c, "qkrope", dim3((unsigned)(d.heads + kvh), (unsigned)n), dim3(64), &ra);
   if (rc) return rc;
   int64_t maxkeys = graph ? s->capacity : past + n;
   if (L.window > 0 && maxkeys > L.window) maxkeys = L.window;
   // a graph replays one grid for every position: splits for the longest
-  return enqueue_attention(m->c, s->q, s->kc[l], s->vc[l], s->attn, s->attn_part, n, d.heads, d.kv_heads,
-                           d.head_dim, past, graph ? s->pos : 0, L.window, L.sinks,
-                           1.0 / std::sqrt((double)d.head_dim), m->kv_f16,
+  return enqueue_attention(m->c, s->q, s->kc[l], s->vc[l], s->attn, s->attn_part, n, d.heads, kvh, hd, past,
+                           graph ? s->pos : 0, L.window, L.sinks,
+                           d.attention_scale > 0 ? d.attention_scale : 1.0 / std::sqrt((double)hd), m->kv_f16,
                            attention_splits(maxkeys));
 }
 
@@ -288,7 +333,7 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
 static bool one_row_fused(const ihip_model* m)
 {
   const ihip_model_desc& d = m->d;
-  if (d.hidden > 4096 || m->recurrent || m->gated || rope_dims(d) != d.head_dim) return false;
+  if (d.hidden > 4096 || m->recurrent || m->gated || m->gemma || rope_dims(d) != d.head_dim) return false;
   if (d.experts > 0) {
     const int64_t K = d.experts_used;
     if (K < 1 || K > 8 || K * d.expert_ffn * 4 > 65536) return false;
@@ -414,6 +459,7 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
         int* ids;
         float* w;
         int32_t experts, k, norm, rows;
+        const float* scale;
       } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, 1};
       if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
@@ -473,6 +519,18 @@ struct GateArgs {
   float* g;
   int64_t n;
   int32_t hd, pad;
+};
+// the launch arguments of ops.hip's element-wise kernels (EltArgs) and softcap
+struct EltArgs2 {
+  float* x;
+  const float* t;
+  int64_t n;
+  float alpha, limit;
+};
+struct SoftcapArgs {
+  float* x;
+  int64_t n;
+  double cap;
 };
 
 // DeltaNetBlock (decoder.pas:2704-2753) of layer l over n rows, h holding
@@ -535,16 +593,27 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
 {
   ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
-  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
-                kvw = (int64_t)d.kv_heads * hd;
+  const int64_t H = d.hidden;
   // one row (decode): every GEMV quantizes its activation row in registers;
   // a chunk: the rows are quantized once per activation buffer
   const bool one = n == 1;
   if (one && one_row_fused(m)) return layers_one(s, past, graph);
-  int rc = ihip_enqueue_rmsnorm(m->c, s->x, m->L[0].input_norm, s->h, n, H, d.rms_eps);
+  // the gate/up activation fused into a one-row GEMV: SwiGLU only
+  const bool glu_fused = one && d.activation == IHIP_ACT_SILU;
+  // TDecoderModel.Activate (decoder.pas:2857-2863): SwiGLU or GeGLU in place
+  auto activate = [&](uint64_t gate, uint64_t up, int64_t count) {
+    if (d.activation == IHIP_ACT_GELU_TANH) {
+      EltArgs2 ea = {(float*)gate, (const float*)up, count, 0.f, 0.f};
+      return launch(m->c, "geglu", dim3((unsigned)((count + 255) / 256)), dim3(256), &ea);
+    }
+    return ihip_enqueue_swiglu(m->c, gate, up, count, d.swiglu_alpha, d.swiglu_limit);
+  };
+  auto norm = [&](uint64_t x, uint64_t w, uint64_t y) { return ihip_enqueue_rmsnorm(m->c, x, w, y, n, H, d.rms_eps); };
+  int rc = norm(s->x, m->L[0].input_norm, s->h);
   if (rc) return rc;
   for (int l = 0; l < d.layers; l++) {
     const DevLayer& L = m->L[l];
+    const int64_t hd = L.hd, qw = (int64_t)d.heads * hd, kvw = L.kvh * hd;
     QCache qh{s->xq0, s->xqk};
     QCache* qhp = one ? nullptr : &qh;
     if (L.mixer == IHIP_MIXER_DELTANET) {
@@ -561,7 +630,7 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         return rc;
       }
       if ((rc = lin(s, s->h, qhp, n, H, L.kd, L.k, kvw, L.kb, s->k))) return rc;
-      if ((rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
+      if (!L.k_is_v && (rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
       if ((rc = rope_attn(s, l, n, past, graph))) return rc;
       if (L.output_gate) {
         // GateBySigmoid (decoder.pas:2594-2610) before the output projection
@@ -571,6 +640,8 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
       }
       QCache qa{s->xq0, s->xqk};
       if ((rc = lin(s, s->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, s->tmp))) return rc;
+      // Gemma: the attention output normed before the residual
+      if (L.attn_out_norm && (rc = norm(s->tmp, L.attn_out_norm, s->tmp))) return rc;
     }
     // residual, then the pre-FFN norm
     if ((rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, L.post_norm, s->h, n, H, d.rms_eps)))
@@ -578,10 +649,10 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
     QCache qf{s->xq0, s->xqk};
     QCache* qfp = one ? nullptr : &qf;
     bool moe_out = false;  // the FFN output is the expert rows (added by the next norm)
-    if (!L.moe) {
+    if (L.moe != IHIP_FFN_MOE) {
       // DenseFfn (decoder.pas:2866-2878)
       const int64_t F = d.ffn;
-      if (one) {
+      if (glu_fused) {
         // gate, up and SwiGLU in one pass
         LinearCall k;
         k.x = s->h; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
@@ -592,26 +663,40 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
       } else {
         if ((rc = lin(s, s->h, qfp, n, H, L.gd, L.gate, F, 0, s->gate))) return rc;
         if ((rc = lin(s, s->h, qfp, n, H, L.ud, L.up, F, 0, s->up))) return rc;
-        if ((rc = ihip_enqueue_swiglu(m->c, s->gate, s->up, n * F, d.swiglu_alpha,
-                                      d.swiglu_limit)))
-          return rc;
+        if ((rc = activate(s->gate, s->up, n * F))) return rc;
       }
       QCache qg{s->xqf, s->xqf};
       if ((rc = lin(s, s->gate, one ? nullptr : &qg, n, F, L.dd, L.down, H, 0, s->tmp))) return rc;
-    } else {
+    }
+    if (L.moe != IHIP_FFN_DENSE) {
       // MoeBlock (decoder.pas:3037-3053) with the experts chosen on the
-      // device (model.qwen3.cuda.pas:1152-1205)
+      // device (model.qwen3.cuda.pas:1152-1205); DenseMoeBlock (:3057-3091):
+      // the dense output normed, the router on the residual's own norm, the
+      // experts on another, their sum normed
+      const bool beside = L.moe == IHIP_FFN_DENSE_MOE;
       const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
-      if ((rc = lin(s, s->h, qfp, n, H, L.rd, L.router, E, L.router_b, s->route))) return rc;
+      QCache qr{s->xq0, s->xqk};
+      QCache* qx = qfp;
+      if (beside) {
+        if ((rc = norm(s->tmp, L.dense_out_norm, s->tmp)) || (rc = norm(s->x, L.router_norm, s->h))) return rc;
+        qx = one ? nullptr : &qr;
+      }
+      if ((rc = lin(s, s->h, qx, n, H, L.rd, L.router, E, L.router_b, s->route))) return rc;
       struct {
         const float* logits;
         int* ids;
         float* w;
         int32_t experts, k, norm, rows;
+        const float* scale;
       } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
-              d.norm_topk, (int32_t)n};
+              d.norm_topk, (int32_t)n, (const float*)L.expert_scale};
       if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
-      if (one) {
+      QCache qe{s->xq0, s->xqk};
+      if (beside) {
+        if ((rc = norm(s->x, L.moe_in_norm, s->h))) return rc;
+        qf = qe;
+      }
+      if (glu_fused) {
         // the token's K experts: gate, up and SwiGLU in one pass per slot,
         // then down per slot; the weighted sum goes into the next norm
         LinearCall k;
@@ -654,21 +739,44 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         if ((rc = lin_ids(s, s->h, xqu, n, H, L.eud, L.eu, L.eg_stride, FI, s->ids_dev, n * K, (int)K,
                           L.eub, s->up, qu)))
           return rc;
-        if ((rc = ihip_enqueue_swiglu(m->c, s->gate, s->up, n * K * FI, d.swiglu_alpha,
-                                      d.swiglu_limit)))
-          return rc;
+        if ((rc = activate(s->gate, s->up, n * K * FI))) return rc;
         if ((rc = lin_ids(s, s->gate, s->xqf, n * K, FI, L.edd, L.ed, L.ed_stride, H, s->ids_dev,
                           n * K, 1, L.edb, s->eout, false)))
           return rc;
       }
-      moe_out = true;
+      if (beside) {
+        // the experts' sum in slot (= id) order, normed, added to the dense
+        // output, normed again (below, as the FFN output norm)
+        struct {
+          const float* d;
+          const float* w;
+          float* y;
+          int32_t k, n, rows, pad;
+        } ca = {(const float*)s->eout, (const float*)s->rw, (float*)s->moe, (int32_t)K, (int32_t)H, (int32_t)n, 0};
+        if ((rc = launch(m->c, "moecombine", dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), &ca)) ||
+            (rc = norm(s->moe, L.moe_out_norm, s->moe)) || (rc = ihip_enqueue_add(m->c, s->tmp, s->moe, n * H)))
+          return rc;
+      } else {
+        moe_out = true;
+      }
     }
-    // residual, then the next layer's input norm (or the final norm)
+    // Gemma: the feed-forward output normed before the residual
+    if (L.ffn_out_norm && (rc = norm(s->tmp, L.ffn_out_norm, s->tmp))) return rc;
+    // residual, then the next layer's input norm (or the final norm); Gemma
+    // scales the whole state by the layer's scalar between the two
     uint64_t nw = l + 1 < d.layers ? m->L[l + 1].input_norm : m->final_norm;
-    if (moe_out)
+    if (L.scalar) {
+      if (moe_out) return fail(IHIP_E_ARG, "model: a layer scalar after experts alone");
+      EltArgs2 sa = {(float*)s->x, (const float*)L.scalar, n * H, 0.f, 0.f};
+      if ((rc = ihip_enqueue_add(m->c, s->x, s->tmp, n * H)) ||
+          (rc = launch(m->c, "mul_scalar", dim3((unsigned)((n * H + 255) / 256)), dim3(256), &sa)))
+        return rc;
+      rc = norm(s->x, nw, s->h);
+    } else if (moe_out) {
       rc = enqueue_addnorm_moe(m->c, s->x, s->eout, s->rw, d.experts_used, nw, s->h, n, H, d.rms_eps);
-    else
+    } else {
       rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, nw, s->h, n, H, d.rms_eps);
+    }
     if (rc) return rc;
   }
   return 0;
@@ -691,6 +799,26 @@ static int head(ihip_mctx* s, int64_t n, bool all, uint64_t y)
              m->head, d.vocab, 0, y);
 }
 
+// Gemma: the embeddings of ids times the embedding scale (ForwardPart,
+// decoder.pas:3305-3309)
+static int embed_scale(ihip_mctx* s, int64_t n)
+{
+  ihip_model* m = s->m;
+  if (!(m->d.embed_scale > 0)) return 0;
+  EltArgs2 a = {(float*)s->x, nullptr, n * m->d.hidden, m->d.embed_scale, 0.f};
+  return launch(m->c, "mul_scalar", dim3((unsigned)((n * m->d.hidden + 255) / 256)), dim3(256), &a);
+}
+
+// Gemma: the logits soft-capped (InferSoftcap, decoder.pas:3360-3368), before
+// any pick
+static int softcap(ihip_mctx* s, int64_t rows, uint64_t logits)
+{
+  ihip_model* m = s->m;
+  if (!(m->d.logit_softcap > 0)) return 0;
+  SoftcapArgs a = {(float*)logits, rows * m->d.vocab, m->d.logit_softcap};
+  return launch(m->c, "softcap", dim3((unsigned)((a.n + 255) / 256)), dim3(256), &a);
+}
+
 // one chunk: ids (or embedding rows) and cos/sin uploaded, embeddings,
 // layers, head; normed (host, or null): the last row after the final norm
 static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t n,
@@ -699,14 +827,19 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
   ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
   ihip_ctx* c = m->c;
-  std::vector<float> cs((size_t)n * d.head_dim);
+  std::vector<float> cs((size_t)n * d.head_dim), cs2((size_t)n * std::max<int64_t>(m->hd2, 1));
   rotary(d, s->length, n, cs.data());
   IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
+  if (m->hd2) {
+    rotary2(d, m->hd2, s->length, n, cs2.data());
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs2, cs2.data(), cs2.size() * 4, c->stream));
+  }
   int rc = s->length == 0 && m->recurrent ? reset_states(s) : 0;
   if (rc) return rc;
   if (ids) {
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, (void*)ids, n * 4, c->stream));
     rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, d.vocab, d.hidden, s->tok, n, s->x);
+    if (!rc) rc = embed_scale(s, n);
   } else {
     // ForwardEmbeds: the caller's rows in place of the token embeddings
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->x, (void*)embeds, (size_t)n * d.hidden * 4,
@@ -725,6 +858,7 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
       IHIP_CHECK(hipMemcpyDtoHAsync(normed, (hipDeviceptr_t)src, (size_t)d.hidden * 4, c->stream));
   }
   if (!rc && want_logits) rc = head(s, n, all, logits_dev);
+  if (!rc && want_logits) rc = softcap(s, all ? n : 1, logits_dev);
   // the host vectors must outlive the copies
   IHIP_CHECK(hipStreamSynchronize(c->stream));
   if (!rc) {
@@ -749,8 +883,10 @@ static int decode_body(ihip_mctx* s)
   ihip_model* m = s->m;
   ihip_ctx* c = m->c;
   int rc = ihip_enqueue_embed(c, m->embed, m->embed_dt, m->d.vocab, m->d.hidden, s->tok, 1, s->x);
+  if (!rc) rc = embed_scale(s, 1);
   if (!rc) rc = layers(s, 1, 0, true);
   if (!rc) rc = head(s, 1, false, s->logits);
+  if (!rc) rc = softcap(s, 1, s->logits);
   if (!rc) rc = next_token(s);
   return rc;
 }
@@ -822,7 +958,7 @@ static const uint64_t ATTN_PART_MAX = 1ull << 30;
 
 static uint64_t part_bytes(const ihip_model* m, int64_t rows, int64_t keys)
 {
-  return (uint64_t)m->d.heads * rows * attention_splits(keys) * (m->d.head_dim + 2) * 8;
+  return (uint64_t)m->d.heads * rows * attention_splits(keys) * (m->max_hd + 2) * 8;
 }
 
 // rows of the next chunk after `past` cached tokens, at most `want`
@@ -851,11 +987,12 @@ static int prepare(ihip_mctx* s, int64_t tokens)
     if (cap < tokens + tokens / 4) cap = tokens + tokens / 4;
     if (cap < 64) cap = 64;
     if (cap > maxpos) cap = maxpos;
-    const uint64_t es = m->kv_f16 ? 2 : 4, kvw = (uint64_t)d.kv_heads * d.head_dim;
+    const uint64_t es = m->kv_f16 ? 2 : 4;
     std::vector<uint64_t> nk(d.layers, 0), nv(d.layers, 0);
     int rc = 0;
     for (int l = 0; l < d.layers && !rc; l++) {
       if (m->L[l].mixer == IHIP_MIXER_DELTANET) continue;  // a state, no rows
+      const uint64_t kvw = (uint64_t)(m->L[l].kvh * m->L[l].hd);
       void* a = nullptr;
       void* b = nullptr;
       hipError_t e = hipMalloc(&a, (uint64_t)cap * kvw * es);
@@ -922,11 +1059,15 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
                         s->graph_sampler != m->sampler_epoch || s->graph_draw != s->draw_ids) &&
       (rc = decode_graph(s)))
     return rc;
-  std::vector<float> cs(m->d.head_dim);
+  std::vector<float> cs(m->d.head_dim), cs2(std::max<int64_t>(m->hd2, 1));
   int32_t tok = first;
   for (int64_t i = 0; i < steps; i++) {
     int32_t pos = (int32_t)s->length;
     if (pos == 0 && m->recurrent && (rc = reset_states(s))) return rc;
+    if (m->hd2) {
+      rotary2(m->d, m->hd2, pos, 1, cs2.data());
+      IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs2, cs2.data(), cs2.size() * 4, c->stream));
+    }
     rotary(m->d, pos, 1, cs.data());
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, &tok, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->pos, &pos, 4, c->stream));
@@ -969,8 +1110,7 @@ static int context_new(ihip_model* m, int64_t capacity, ihip_mctx** out)
   ihip_mctx* s = new ihip_mctx();
   s->m = m;
   const ihip_model_desc& d = m->d;
-  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
-                kvw = (int64_t)d.kv_heads * hd;
+  const int64_t H = d.hidden, hd = m->max_hd, qw = m->max_qw, kvw = m->max_kvw;
   const int64_t N = CHUNK;
   int64_t F = std::max<int64_t>(d.ffn, 1);
   int64_t EK = m->any_moe ? (int64_t)d.experts_used * d.expert_ffn : 0;
@@ -1017,6 +1157,8 @@ static int context_new(ihip_model* m, int64_t capacity, ihip_mctx** out)
   }
   if (m->gated && ((rc = dalloc_ctx(s, N * 2 * qw * 4, s->qg)) || (rc = dalloc_ctx(s, N * qw * 4, s->gq))))
     return bad(rc);
+  if (m->hd2 > 0 && (rc = dalloc_ctx(s, N * m->hd2 * 4, s->cs2))) return bad(rc);
+  if (m->gemma && (rc = dalloc_ctx(s, N * H * 4, s->moe))) return bad(rc);
   // the attention counters start at zero (a fill kernel would do under
   // capture; this runs once, outside any capture)
   {
@@ -1256,13 +1398,17 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
   m->mode = mode;
   m->kv_f16 = kv_f16;
   const ihip_model_desc& d = m->d;
-  const int64_t H = d.hidden, hd = d.head_dim, qw = (int64_t)d.heads * hd,
-                kvw = (int64_t)d.kv_heads * hd;
+  const int64_t H = d.hidden;
   int rc = 0;
   auto bad = [&](int r) {
     ihip_model_destroy(m);
     return r;
   };
+  m->gemma = d.activation != IHIP_ACT_SILU || d.value_norm || d.embed_scale > 0 || d.logit_softcap > 0 ||
+             d.attention_scale > 0;
+  m->max_hd = d.head_dim;
+  m->max_qw = (int64_t)d.heads * d.head_dim;
+  m->max_kvw = (int64_t)d.kv_heads * d.head_dim;
   // UploadWeights (model.qwen3.cuda.pas:602-828)
   if ((rc = upw(m, d.embed, d.vocab, H, 1, m->embed, m->embed_dt))) return bad(rc);
   if (d.head.data) {
@@ -1277,6 +1423,33 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
   for (int l = 0; l < d.layers; l++) {
     const ihip_layer_desc& s = m->layer_desc[l];
     DevLayer& L = m->L[l];
+    // this layer's heads (Gemma 4: its own per layer)
+    const int64_t hd = s.head_dim > 0 ? s.head_dim : d.head_dim;
+    const int64_t kvh = s.kv_heads > 0 ? s.kv_heads : d.kv_heads;
+    const int64_t qw = (int64_t)d.heads * hd, kvw = kvh * hd;
+    L.hd = hd;
+    L.kvh = kvh;
+    L.k_is_v = s.k_is_v != 0;
+    L.rope_set = s.rope_set != 0;
+    if (kvh < 1 || d.heads % kvh || (hd & 1) || hd < 2 || hd > 512)
+      return bad(fail(IHIP_E_ARG, "model: layer " + std::to_string(l) + " has heads of " + std::to_string(hd) +
+                                      " with " + std::to_string(kvh) + " KV heads (even, up to 512)"));
+    if (s.head_dim > 0 || s.kv_heads > 0 || s.k_is_v || s.rope_set || s.attn_out_norm.data || s.ffn_out_norm.data ||
+        s.scalar.data || s.moe == IHIP_FFN_DENSE_MOE || s.exp_gate_up)
+      m->gemma = true;
+    if (s.mixer != IHIP_MIXER_DELTANET) {
+      m->max_hd = std::max(m->max_hd, hd);
+      m->max_qw = std::max(m->max_qw, qw);
+      m->max_kvw = std::max(m->max_kvw, kvw);
+      if (L.rope_set) {
+        if (m->hd2 && m->hd2 != hd)
+          return bad(fail(IHIP_E_ARG, "model: layers of the second rotary set with heads of two sizes"));
+        m->hd2 = hd;
+      }
+    }
+    if ((rc = upf(m, s.attn_out_norm, H, L.attn_out_norm)) || (rc = upf(m, s.ffn_out_norm, H, L.ffn_out_norm)) ||
+        (rc = upf(m, s.scalar, 1, L.scalar)))
+      return bad(rc);
     L.window = s.window;
     L.moe = s.moe;
     L.mixer = s.mixer;
@@ -1313,16 +1486,31 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
         (rc = upf(m, s.q_norm, hd, L.qn)) || (rc = upf(m, s.k_norm, hd, L.kn)) ||
         (rc = upf(m, s.sinks, d.heads, L.sinks)))
       return bad(rc);
-    if (!s.moe) {
+    if (s.moe != IHIP_FFN_MOE) {
       if ((rc = upw(m, s.gate, d.ffn, H, 1, L.gate, L.gd)) || (rc = upw(m, s.up, d.ffn, H, 1, L.up, L.ud)) ||
           (rc = upw(m, s.down, H, d.ffn, 1, L.down, L.dd)))
         return bad(rc);
-    } else {
+    }
+    if (s.moe != IHIP_FFN_DENSE) {
       const int64_t E = d.experts, FI = d.expert_ffn;
+      if (s.exp_gate_up) {
+        // [E, 2 FI, H], per expert its gate rows then its up rows: uploaded
+        // as two matrices of FI rows per expert
+        if (!s.exp_gate.data) return bad(fail(IHIP_E_ARG, "experts: no gate_up tensor"));
+        const uint64_t rb = row_bytes(s.exp_gate.dtype, H);
+        m->uploaded.emplace_back((const uint8_t*)s.exp_gate.data, rb * 2 * FI * E);
+        L.egd = L.eud = s.exp_gate.dtype;
+        if ((rc = weight_rows(c, s.exp_gate.data, L.egd, FI, H, E, 2 * FI, &L.eg)) ||
+            (rc = weight_rows(c, (const uint8_t*)s.exp_gate.data + rb * FI, L.eud, FI, H, E, 2 * FI, &L.eu)))
+          return bad(rc);
+      } else if ((rc = upw(m, s.exp_gate, FI, H, E, L.eg, L.egd)) || (rc = upw(m, s.exp_up, FI, H, E, L.eu, L.eud))) {
+        return bad(rc);
+      }
       if ((rc = upw(m, s.router, E, H, 1, L.router, L.rd)) || (rc = upf(m, s.router_bias, E, L.router_b)) ||
-          (rc = upw(m, s.exp_gate, FI, H, E, L.eg, L.egd)) ||
-          (rc = upw(m, s.exp_up, FI, H, E, L.eu, L.eud)) ||
           (rc = upw(m, s.exp_down, H, FI, E, L.ed, L.edd)) ||
+          (rc = upf(m, s.dense_out_norm, H, L.dense_out_norm)) || (rc = upf(m, s.moe_in_norm, H, L.moe_in_norm)) ||
+          (rc = upf(m, s.moe_out_norm, H, L.moe_out_norm)) || (rc = upf(m, s.router_norm, H, L.router_norm)) ||
+          (rc = upf(m, s.expert_scale, E, L.expert_scale)) ||
           (rc = upf(m, s.exp_gate_bias, E * FI, L.egb)) ||
           (rc = upf(m, s.exp_up_bias, E * FI, L.eub)) ||
           (rc = upf(m, s.exp_down_bias, E * H, L.edb)))
@@ -1332,9 +1520,12 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       L.ed_stride = (int64_t)row_bytes(L.edd, FI) * H;
     }
   }
-  if (hd % 8 || hd > 256) return bad(fail(IHIP_E_ARG, "model: head size not a multiple of 8 up to 256"));
+  const int64_t hd = d.head_dim;
+  if ((hd & 1) || hd > 512) return bad(fail(IHIP_E_ARG, "model: an odd head size or one beyond 512"));
   const int64_t rot = rope_dims(d);
   if (rot < 2 || rot > hd || (rot & 1)) return bad(fail(IHIP_E_ARG, "model: an odd or oversized rotary share"));
+  if (m->hd2 && (d.rope2_pairs < 1 || d.rope2_pairs > m->hd2 / 2 || !(d.rope2_theta > 1)))
+    return bad(fail(IHIP_E_ARG, "model: the second rotary set's pairs or theta"));
   // the DeltaNet kernels keep a state column in a wave's registers (keys of
   // up to 256) and the convolution inputs in a thread's (up to 8)
   if (m->recurrent &&

@@ -275,6 +275,52 @@ extern "C" __global__ __launch_bounds__(256) void swiglu(EltArgs a)
   }
 }
 
+// TInferCpuBackend.GeluTanhGlu (backend.cpu.pas:1836-1860): x = gate, t = up;
+// gelu_tanh(g) in double (tanh as 1 - 2 / (exp(2t) + 1), +-1 beyond 20)
+// rounded to single, then the product
+extern "C" __global__ __launch_bounds__(256) void geglu(EltArgs a)
+{
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.n) return;
+  const double g = a.x[i];
+  double t = 0.7978845608028654 * (g + 0.044715 * g * g * g);
+  if (t > 20) t = 1;
+  else if (t < -20) t = -1;
+  else t = 1 - 2 / (exp(2 * t) + 1);
+  const float b = (float)(0.5 * g * (1 + t));
+  a.x[i] = b * a.t[i];
+}
+
+// x := x * t[0] (Gemma's layer scalar, decoder.pas:3330-3336), or x * alpha
+// with t null (the embedding scale, :3305-3309)
+extern "C" __global__ __launch_bounds__(256) void mul_scalar(EltArgs a)
+{
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.n) return;
+  const float s = a.t ? a.t[0] : a.alpha;
+  a.x[i] = a.x[i] * s;
+}
+
+struct SoftcapArgs {
+  float* x;
+  int64_t n;
+  double cap;
+};
+
+// InferSoftcap (decoder.pas:1293-1312): tanh(x / c) * c, each step single
+extern "C" __global__ __launch_bounds__(256) void softcap(SoftcapArgs a)
+{
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.n) return;
+  const float v = (float)(a.x[i] / a.cap);
+  const double d = v;
+  float t;
+  if (d > 20) t = 1;
+  else if (d < -20) t = -1;
+  else t = (float)(1 - 2 / (exp(2 * d) + 1));
+  a.x[i] = (float)(t * a.cap);
+}
+
 // ------------------------------------------------------------------ qkrope
 struct RopeArgs {
   float* q;
@@ -289,7 +335,7 @@ struct RopeArgs {
   double eps;
   int32_t rows, heads, kvh, hd, past, f16;
   int32_t rot;       // the rotating values of a head from its start (0: all)
-  int32_t pad;
+  int32_t vnorm;     // 1: every V head RMS-normed without weight (ValueNorm)
 };
 
 // per (head: the q heads, then the kv heads; row): the Q/K head RMSNorm of
@@ -350,12 +396,26 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
     else if (a.f16) ((uint16_t*)a.kc)[dst + c] = float_to_half(o);
     else ((float*)a.kc)[dst + c] = o;
   }
-  if (!isq)
+  if (!isq) {
+    // ValueNorm (decoder.pas:2674-2676): the RMSNorm of RmsNorm with unit
+    // weights, so the normed value itself
+    double inv = 1.0;
+    if (a.vnorm) {
+      double sv = 0;
+      for (int c = t; c < d; c += 64) {
+        double x = a.v[src + c];
+        sv = sv + x * x;
+      }
+      sv = wave_sum(sv, 64);
+      inv = 1.0 / sqrt(sv / (double)d + a.eps);
+    }
     for (int c = t; c < d; c += 64) {
       float vv = a.v[src + c];
+      if (a.vnorm) vv = 1.0f * (float)((double)vv * inv);
       if (a.f16) ((uint16_t*)a.vc)[dst + c] = float_to_half(vv);
       else ((float*)a.vc)[dst + c] = vv;
     }
+  }
 }
 
 // --------------------------------------------------------------- attention
@@ -396,13 +456,15 @@ __device__ __forceinline__ int xcd_head(unsigned x, int heads)
 // key row at once, and each lane of the value pass holds a dimension pair of
 // all its keys, so a block waits for memory once per pass.
 #define ATT_CHUNK 128
-template <bool F16>
+// NP: dimension pairs per lane in the value pass, 2 for heads up to 256, 4
+// for heads up to 512 (Gemma 4's full layers)
+template <bool F16, int NP = 2>
 __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
 {
-  __shared__ double qd[256];
+  __shared__ double qd[128 * NP];
   __shared__ double sc[ATT_CHUNK];
   __shared__ double red[8];
-  __shared__ double accs[4][256];
+  __shared__ double accs[4][128 * NP];
   const int h = xcd_head(blockIdx.x, a.heads), r = blockIdx.y, s = blockIdx.z, t = threadIdx.x;
   const int d = a.hd;
   const int64_t kvw = (int64_t)a.kvh * d, qw = (int64_t)a.heads * d;
@@ -429,7 +491,12 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   if (t < n) {
     const int64_t kb = base + (int64_t)t * kvw;
     double acc = 0;
-    if constexpr (F16) {
+    if (F16 && (d & 7)) {
+      // a head that is no multiple of 8 (rows not 16-byte aligned): one by one
+      for (int i = 0; i < d; i++) acc = acc + qd[i] * (double)half_to_float(((const uint16_t*)a.kc)[kb + i]);
+    } else if (!F16 && (d & 3)) {
+      for (int i = 0; i < d; i++) acc = acc + qd[i] * (double)((const float*)a.kc)[kb + i];
+    } else if constexpr (F16) {
       const uint4* p = (const uint4*)((const uint16_t*)a.kc + kb);
       for (int k0 = 0; k0 < d / 8; k0 += 16) {
         uint4 u[16];
@@ -483,28 +550,31 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   __syncthreads();
   if ((t & 63) == 0) red[4 + (t >> 6)] = e;
   // the weighted values: a key takes a slot of lps lanes (hd / 2 rounded up
-  // to a power of two, at most 64), each lane a dimension pair (two for
-  // hd > 128); lanes past the key's pairs hold zeros. The 4 waves and the
-  // key slots of a wave split the range.
+  // to a power of two, at most 64), each lane a dimension pair (up to NP of
+  // them for hd > 128); lanes past the key's pairs hold zeros. The 4 waves
+  // and the key slots of a wave split the range.
   const int lpk = d >> 1;                                      // dimension pairs of a key
   const int lps = lpk >= 64 ? 64 : 1 << (32 - __clz(lpk - 1));  // lanes per key slot
   const int kpw = 64 / lps;                                    // keys side by side in a wave
   const int w = t >> 6, l = t & 63;
   const int lane_key = l / lps, pair = l % lps;
   const int step = 4 * kpw;
-  double a0[2] = {0, 0}, a1[2] = {0, 0};  // two dimension pairs (hd 256)
-  // the lane's pairs inside the key (pair, pair + 64)
-  const bool live0 = pair < lpk, live1 = pair + 64 < lpk;
-  const int npair = live1 ? 2 : (live0 ? 1 : 0);
-  constexpr int VB = F16 ? 32 : 16;  // value loads in flight per lane
+  double a0[NP], a1[NP];  // the lane's dimension pairs pair, pair + 64, ..
+#pragma unroll
+  for (int c = 0; c < NP; c++) a0[c] = a1[c] = 0;
+  int npair = 0;
+#pragma unroll
+  for (int c = 0; c < NP; c++)
+    if (pair + 64 * c < lpk) npair = c + 1;
+  constexpr int VB = (F16 ? 32 : 16) * 2 / NP;  // value loads in flight per lane
   for (int jb = w * kpw + lane_key; jb < n; jb += VB * step) {
     if constexpr (F16) {
-      uint32_t v[VB][2];
+      uint32_t v[VB][NP];
 #pragma unroll
       for (int u = 0; u < VB; u++) {
         int j = jb + u * step;
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int c = 0; c < NP; c++)
           v[u][c] = (j < n && c < npair)
                         ? ((const uint32_t*)((const uint16_t*)a.vc + base + (int64_t)j * kvw))[pair + 64 * c]
                         : 0u;
@@ -515,7 +585,7 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
         if (j < n) {
           double p = sc[j];
 #pragma unroll
-          for (int c = 0; c < 2; c++)
+          for (int c = 0; c < NP; c++)
             if (c < npair) {
               a0[c] = a0[c] + p * (double)half_to_float(v[u][c] & 0xffffu);
               a1[c] = a1[c] + p * (double)half_to_float(v[u][c] >> 16);
@@ -523,12 +593,12 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
         }
       }
     } else {
-      float2 v[VB][2];
+      float2 v[VB][NP];
 #pragma unroll
       for (int u = 0; u < VB; u++) {
         int j = jb + u * step;
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int c = 0; c < NP; c++)
           v[u][c] = (j < n && c < npair)
                         ? ((const float2*)((const float*)a.vc + base + (int64_t)j * kvw))[pair + 64 * c]
                         : make_float2(0.f, 0.f);
@@ -539,7 +609,7 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
         if (j < n) {
           double p = sc[j];
 #pragma unroll
-          for (int c = 0; c < 2; c++)
+          for (int c = 0; c < NP; c++)
             if (c < npair) {
               a0[c] = a0[c] + p * (double)v[u][c].x;
               a1[c] = a1[c] + p * (double)v[u][c].y;
@@ -551,13 +621,13 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   // the key slots of a wave, then the waves
   for (int o = lps; o < 64; o <<= 1)
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
+    for (int c = 0; c < NP; c++) {
       a0[c] += __shfl_xor(a0[c], o);
       a1[c] += __shfl_xor(a1[c], o);
     }
   if (lane_key == 0)
 #pragma unroll
-    for (int c = 0; c < 2; c++)
+    for (int c = 0; c < NP; c++)
       if (c < npair) {
         accs[w][2 * (pair + 64 * c)] = a0[c];
         accs[w][2 * (pair + 64 * c) + 1] = a1[c];
@@ -981,6 +1051,17 @@ extern "C" __global__ __launch_bounds__(256) void attention_part_f16(AttnArgs a)
 extern "C" __global__ __launch_bounds__(256) void attention_part_f32(AttnArgs a)
 {
   attention_part_t<false>(a);
+}
+
+// heads of 257..512 values (Gemma 4's full layers)
+extern "C" __global__ __launch_bounds__(256) void attention_part_f16_512(AttnArgs a)
+{
+  attention_part_t<true, 4>(a);
+}
+
+extern "C" __global__ __launch_bounds__(256) void attention_part_f32_512(AttnArgs a)
+{
+  attention_part_t<false, 4>(a);
 }
 
 // y = sum_s exp(m_s - M) acc_s / (sum_s exp(m_s - M) l_s + exp(sink - M)),
@@ -1426,6 +1507,7 @@ struct RouteArgs {
   int* ids;
   float* w;
   int32_t experts, k, norm, rows;
+  const float* scale;  // [experts]: each weight times its expert's (Gemma 4), or null
 };
 
 // one block of 256 per row (route_block of route.h)
@@ -1436,8 +1518,10 @@ extern "C" __global__ __launch_bounds__(256) void route(RouteArgs a)
   const int row = blockIdx.x;
   route_block<4096>(a.logits + (int64_t)row * a.experts, a.experts, a.k, a.norm, sid, sw);
   if ((int)threadIdx.x < a.k) {
+    float w = sw[threadIdx.x];
+    if (a.scale) w = w * a.scale[sid[threadIdx.x]];
     a.ids[(int64_t)row * a.k + threadIdx.x] = sid[threadIdx.x];
-    a.w[(int64_t)row * a.k + threadIdx.x] = sw[threadIdx.x];
+    a.w[(int64_t)row * a.k + threadIdx.x] = w;
   }
 }
 

@@ -116,7 +116,12 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     # tiny gpt-oss), 32, 96 and 192 (a second pair for half the lanes)
     (24, 4, 2, 10, 6, 5, True, True), (24, 4, 2, 150, 1, 0, True, False),
     (32, 4, 2, 200, 3, 0, False, True), (96, 8, 4, 130, 2, 0, False, False),
-    (192, 4, 1, 60, 2, 0, True, True)])
+    (192, 4, 1, 60, 2, 0, True, True),
+    # heads of 44 (no multiple of 8: keys read one value at a time), 320 and
+    # 512 (Gemma 4's full layers: up to four pairs per lane)
+    (44, 4, 1, 30, 3, 0, False, True), (44, 4, 2, 70, 2, 0, False, False),
+    (320, 4, 2, 150, 2, 0, False, True), (512, 8, 1, 260, 3, 0, False, False),
+    (512, 4, 2, 40, 1, 0, True, True)])
 def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     rng = np.random.default_rng(past + rows)
     T = past + rows
