@@ -215,12 +215,14 @@ def decode_kernels(ctx, model, spec, first, steps, past):
                         for k, (n, ms) in sorted(rep.items(), key=lambda kv: -kv[1][1])}
     model.use_graphs(True)
     d = out["dominant"]
+    # (a model whose FFN runs otherwise, as Gemma 4's GeGLU, launches no such
+    # kernel: 0, and the per-token breakdown says what ran)
     d.update({"kernel": dom_name, "what": what, "bytes_per_launch": nb, "weight_bytes": wb,
-              "GBps": nb / (d["avg_us"] * 1e-6) / 1e9})
+              "GBps": nb / (d["avg_us"] * 1e-6) / 1e9 if d["launches"] else 0.0})
     a = out["attention"]
     qw = c["heads"] * hd
     abytes = int(a["keys_avg"] * kvw * 2 * 2 + qw * 4 * 2 + kvw * 4 * 2)
-    if not c.get("window"):
+    if not c.get("window") and not c.get("family") and a["launches"]:
         a.update({"bytes_per_launch": abytes, "GBps": abytes / (a["avg_us"] * 1e-6) / 1e9})
     return out, tok, past
 

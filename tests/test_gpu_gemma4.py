@@ -144,3 +144,19 @@ def test_gemma4_native_decode_sampled(ctx):
     assert reused == len(p1) + len(t1) - 1
     cache.close()
     m.close()
+
+
+def test_gemma4_real_widths(ctx):
+    # Gemma-4-26B-A4B's widths (sliding heads of 256, full heads of 512 with
+    # K=V, 128 experts of 704 beside a dense GeGLU of 2112) over 6 layers and
+    # a small vocabulary, a window of 1024: the device's greedy tokens are the
+    # CPU decoder's
+    from infer_hip import models
+    s = models.Spec(models.tiny("gemma4-26b-a4b-q8_0", layers=6, vocab=4096), seed=3)
+    prompt = np.random.default_rng(5).integers(0, 4096, 90).astype(np.int32)
+    dev = H.Model(ctx, s, max_tokens=160)
+    got = dev.greedy(prompt, 32)
+    ref, margins = O.Model(s, 160, threads=16).greedy(prompt, 32)
+    print("min margin", float(margins.min()), flush=True)
+    assert np.array_equal(got, ref)
+    dev.close()

@@ -6,7 +6,9 @@ full layer count, expert count, vocabulary and widths of each model config:
 - configs[4], gpt-oss-20b (MXFP4 experts, bf16 attention, windows, sinks,
   YaRN);
 - configs[2], Qwen3-0.6B Q4_K_M after its own 512-token prompt;
-- configs[0], Qwen3-0.6B Q8_0 after a 96-token prompt.
+- configs[0], Qwen3-0.6B Q8_0 after a 96-token prompt;
+- Qwen3.5-0.8B and Gemma-4-26B-A4B in Q8_0 (no BASELINE config names them),
+  after 96-token prompts.
 
 Every prompt here is at least 80 rows, so the prefill runs on the MFMA GEMM
 (the MoE prompts on its grouped-expert items), not on the 8-row GEMVs. The
@@ -64,6 +66,11 @@ FULL = [
     ("gpt-oss-20b-mxfp4", 96),
     ("qwen3-0.6b-q4_k_m", 512),
     ("qwen3-0.6b-q8_0", 96),
+    # beyond the BASELINE configurations: Qwen3.5-0.8B (Gated DeltaNet, heads
+    # of 256) and Gemma-4-26B-A4B (heads of 256 and 512, 128 experts beside
+    # the dense block)
+    ("qwen35-0.8b-q8_0", 96),
+    ("gemma4-26b-a4b-q8_0", 96),
 ]
 
 

@@ -147,3 +147,18 @@ def test_qwen35_native_decode(ctx):
     assert np.array_equal(t2, want2)
     cache.close()
     m.close()
+
+
+def test_qwen35_real_widths(ctx):
+    # Qwen3.5-0.8B's widths (16 key and value heads of 128: a state column of
+    # 128 per wave, attention heads of 256) over 8 layers and a small
+    # vocabulary: the device's greedy tokens are the CPU decoder's
+    from infer_hip import models
+    s = models.Spec(models.tiny("qwen35-0.8b-q8_0", layers=8, vocab=4096), seed=3)
+    prompt = np.random.default_rng(5).integers(0, 4096, 90).astype(np.int32)
+    dev = H.Model(ctx, s, max_tokens=160)
+    got = dev.greedy(prompt, 32)
+    ref, margins = O.Model(s, 160, threads=16).greedy(prompt, 32)
+    print("min margin", float(margins.min()), flush=True)
+    assert np.array_equal(got, ref)
+    dev.close()
