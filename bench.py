@@ -204,7 +204,8 @@ def decode_kernels(ctx, model, spec, first, steps, past):
             # the window layers read fewer keys; configs without windows read all
             out[key]["keys_avg"] = keys
     # every kernel of `steps` steps: the per-token breakdown
-    ctx.kernel_timer("*", capacity=steps * (8 * c["layers"] + 16))
+    # (the unfused layers of Qwen3.5 and Gemma 4 launch up to ~24 kernels each)
+    ctx.kernel_timer("*", capacity=min(60000, steps * (24 * c["layers"] + 32)))
     ids = model.decode(tok, steps)
     rep = ctx.kernel_timer_report()
     ctx.kernel_timer(None)
