@@ -468,10 +468,22 @@ int ihip_context_forward_embeds(ihip_mctx* s, const float* embeds, int64_t count
  * id), drop the rest; *kept = the tokens kept */
 int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t* kept);
 /* TDecoderContext.Truncate (decoder.pas:996-1016): keep the first length
- * tokens (the device keeps every row, so any length is restorable) */
+ * tokens (the device keeps every row, so any length is restorable, but for
+ * a model with DeltaNet layers: 0, the cached length, or a restore point) */
 int ihip_context_truncate(ihip_mctx* s, int64_t length);
 /* cached tokens and the cache's capacity (either pointer may be NULL) */
 int ihip_context_length(ihip_mctx* s, int64_t* length, int64_t* capacity);
+/* TDecoderContext.CheckpointId / MaxCheckpoints (decoder.pas:466-620,
+ * :1019-1081): a context of a model with DeltaNet layers keeps its states
+ * before every `id` token of an aligned forward (each part starting at the
+ * sequence start or at an `id` token), the last `max` of them (4 by default,
+ * DECODER_CHECKPOINTS); Reuse then takes the last one before the end of the
+ * common start, Truncate goes back to any of them. id -1: none. Another id
+ * drops the restore points. */
+int ihip_context_set_checkpoints(ihip_mctx* s, int32_t id, int64_t max);
+/* the lengths of the restore points held, the oldest first (at most cap of
+ * them written); count: how many there are */
+int ihip_context_checkpoints(ihip_mctx* s, int64_t* lengths, int64_t cap, int64_t* count);
 /* ihip_model_greedy and ihip_model_decode on a context */
 int ihip_context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
                         int32_t* out_ids);

@@ -72,6 +72,16 @@ struct ihip_mctx {
   uint64_t qkv = 0, z = 0, beta = 0, decay = 0, core = 0, qg = 0, gq = 0;
   // Gemma 4: the second rotary set's cos/sin, the experts' sum of a row
   uint64_t cs2 = 0, moe = 0;
+  // the restore points of the DeltaNet states (TDecoderContext.CheckpointId,
+  // MaxCheckpoints, decoder.pas:466-620, :1049-1230): the states before the
+  // CheckpointId tokens of aligned parts, the oldest first; each in a slot of
+  // per-layer copies of conv and state
+  int32_t ckpt_id = -1;
+  int64_t ckpt_max = 4;     // DECODER_CHECKPOINTS (decoder.pas:305)
+  bool aligned = true;      // the cached rows were split as a fresh pass splits them
+  bool state_ok = true;     // false while (or after a failure of) a forward
+  std::vector<std::pair<int64_t, int>> ckpts;  // (length, slot)
+  std::vector<std::vector<uint64_t>> slot_conv, slot_state;
   // zeroed counters of the decode attention's heads (the last range block of
   // a head merges the head)
   uint64_t done = 0;
@@ -799,6 +809,123 @@ static int head(ihip_mctx* s, int64_t n, bool all, uint64_t y)
              m->head, d.vocab, 0, y);
 }
 
+// ---- restore points of a recurrent state (TDecoderContext,
+// decoder.pas:996-1230)
+
+static int dalloc_ctx(ihip_mctx* s, uint64_t bytes, uint64_t& p);
+
+static bool ckpt_on(const ihip_mctx* s) { return s->m->recurrent && s->ckpt_id >= 0 && s->ckpt_max > 0; }
+
+static int64_t find_ckpt(const ihip_mctx* s, int64_t length)
+{
+  for (size_t i = 0; i < s->ckpts.size(); i++)
+    if (s->ckpts[i].first == length) return (int64_t)i;
+  return -1;
+}
+
+// SaveStates / LoadStates: every DeltaNet layer's conv and state to or from
+// a slot (device copies on the stream)
+static int copy_states(ihip_mctx* s, int slot, bool save)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  const int64_t vd = (int64_t)d.lin_value_heads * d.lin_value_dim, cd = 2 * (int64_t)d.lin_key_heads * d.lin_key_dim + vd;
+  const uint64_t cb = (uint64_t)cd * std::max(d.lin_conv - 1, 1) * 4, sb = (uint64_t)vd * d.lin_key_dim * 4;
+  if (save && slot >= (int)s->slot_conv.size()) {
+    s->slot_conv.resize(slot + 1, std::vector<uint64_t>(d.layers, 0));
+    s->slot_state.resize(slot + 1, std::vector<uint64_t>(d.layers, 0));
+  }
+  for (int l = 0; l < d.layers; l++) {
+    if (!s->conv[l]) continue;
+    uint64_t& pc = s->slot_conv[slot][l];
+    uint64_t& ps = s->slot_state[slot][l];
+    int rc;
+    if (!pc && ((rc = dalloc_ctx(s, cb, pc)) || (rc = dalloc_ctx(s, sb, ps)))) return rc;
+    const uint64_t dc = save ? pc : s->conv[l], sc = save ? s->conv[l] : pc;
+    const uint64_t ds = save ? ps : s->state[l], ss = save ? s->state[l] : ps;
+    IHIP_CHECK(hipMemcpyDtoDAsync((hipDeviceptr_t)dc, (hipDeviceptr_t)sc, cb, m->c->stream));
+    IHIP_CHECK(hipMemcpyDtoDAsync((hipDeviceptr_t)ds, (hipDeviceptr_t)ss, sb, m->c->stream));
+  }
+  return 0;
+}
+
+// SaveCheckpoint (decoder.pas:1049-1081): the states of the cached rows, when
+// they are whole, aligned and new; the oldest goes when the count is full
+static int save_checkpoint(ihip_mctx* s)
+{
+  if (s->ckpt_max <= 0 || s->length == 0 || !s->state_ok || !s->aligned || find_ckpt(s, s->length) >= 0)
+    return 0;
+  int slot = -1;
+  if ((int64_t)s->ckpts.size() >= s->ckpt_max) {
+    slot = s->ckpts.front().second;
+    s->ckpts.erase(s->ckpts.begin());
+  } else {
+    // the lowest slot no restore point uses
+    for (int k = 0; slot < 0; k++) {
+      bool used = false;
+      for (auto& c : s->ckpts) used = used || c.second == k;
+      if (!used) slot = k;
+    }
+  }
+  int rc = copy_states(s, slot, true);
+  if (rc) return rc;
+  s->ckpts.emplace_back(s->length, slot);
+  return 0;
+}
+
+// a forward part starting at token id (-1: an embedding row), the first of
+// its call or the start of a chunk: CheckPart (decoder.pas:1083-1102) and the
+// restore point before a CheckpointId token (ForwardRows, :3230-3237)
+static int part_start(ihip_mctx* s, int32_t id, bool first)
+{
+  if (!s->m->recurrent) return 0;
+  if (s->length > 0 && !s->state_ok)
+    return fail(IHIP_E_ARG, "forward: the recurrent state is undone by an earlier failure - reset it, or "
+                            "truncate it to a restore point");
+  if (ckpt_on(s) && s->length > 0 && id == s->ckpt_id) {
+    int rc = save_checkpoint(s);
+    if (rc) return rc;
+  } else if (first && s->length > 0 && s->ckpt_id >= 0) {
+    s->aligned = false;
+  }
+  s->state_ok = false;
+  return 0;
+}
+
+// Restorable (decoder.pas:1180-1211): the device cache keeps every row, so
+// only a recurrent state limits the lengths a context can go back to
+static bool restorable(const ihip_mctx* s, int64_t length)
+{
+  if (length < 0 || length > s->length) return false;
+  if (length == 0) return true;
+  if (s->m->recurrent && (length != s->length || !s->state_ok) && find_ckpt(s, length) < 0) return false;
+  return true;
+}
+
+// Truncate (decoder.pas:996-1017)
+static int truncate_to(ihip_mctx* s, int64_t length)
+{
+  if (!restorable(s, length))
+    return fail(IHIP_E_ARG, "truncate(" + std::to_string(length) + ") of " + std::to_string(s->length) +
+                                " tokens: a recurrent state cannot go back there");
+  if (length == 0) {
+    s->length = 0;
+    s->ckpts.clear();
+    s->aligned = true;
+    s->state_ok = true;
+    return 0;
+  }
+  if (s->m->recurrent && (length != s->length || !s->state_ok)) {
+    int rc = copy_states(s, s->ckpts[find_ckpt(s, length)].second, false);
+    if (rc) return rc;
+    s->state_ok = true;
+    s->aligned = true;
+  }
+  s->length = length;
+  while (!s->ckpts.empty() && s->ckpts.back().first > length) s->ckpts.pop_back();
+  return 0;
+}
+
 // Gemma: the embeddings of ids times the embedding scale (ForwardPart,
 // decoder.pas:3305-3309)
 static int embed_scale(ihip_mctx* s, int64_t n)
@@ -822,11 +949,13 @@ static int softcap(ihip_mctx* s, int64_t rows, uint64_t logits)
 // one chunk: ids (or embedding rows) and cos/sin uploaded, embeddings,
 // layers, head; normed (host, or null): the last row after the final norm
 static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t n,
-                 bool want_logits, bool all, uint64_t logits_dev, float* normed)
+                 bool want_logits, bool all, uint64_t logits_dev, float* normed, bool first = false)
 {
   ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
   ihip_ctx* c = m->c;
+  int rc0 = part_start(s, ids ? ids[0] : -1, first);
+  if (rc0) return rc0;
   std::vector<float> cs((size_t)n * d.head_dim), cs2((size_t)n * std::max<int64_t>(m->hd2, 1));
   rotary(d, s->length, n, cs.data());
   IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
@@ -864,6 +993,7 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
   if (!rc) {
     for (int64_t i = 0; i < n; i++) s->ids[s->length + i] = ids ? ids[i] : -1;
     s->length += n;
+    s->state_ok = true;
   }
   return rc;
 }
@@ -962,10 +1092,15 @@ static uint64_t part_bytes(const ihip_model* m, int64_t rows, int64_t keys)
 }
 
 // rows of the next chunk after `past` cached tokens, at most `want`
-static int64_t chunk_rows(const ihip_mctx* s, int64_t past, int64_t want)
+static int64_t chunk_rows(const ihip_mctx* s, int64_t past, int64_t want, const int32_t* ids = nullptr)
 {
   int64_t n = std::min(want, s->m->chunk_rows);
   while (n > 1 && part_bytes(s->m, n, past + n) > ATTN_PART_MAX) n = (n + 1) / 2;
+  // a recurrent context with restore points: a part ends before every
+  // CheckpointId token (ForwardRows, decoder.pas:3191-3243)
+  if (ids && s->m->recurrent && s->ckpt_id >= 0 && s->ckpt_max > 0)
+    for (int64_t i = 1; i < n; i++)
+      if (ids[i] == s->ckpt_id) return i;
   return n;
 }
 
@@ -1064,6 +1199,8 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   for (int64_t i = 0; i < steps; i++) {
     int32_t pos = (int32_t)s->length;
     if (pos == 0 && m->recurrent && (rc = reset_states(s))) return rc;
+    // each step is a forward of one token: its own part
+    if ((rc = part_start(s, tok, true))) return rc;
     if (m->hd2) {
       rotary2(m->d, m->hd2, pos, 1, cs2.data());
       IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs2, cs2.data(), cs2.size() * 4, c->stream));
@@ -1081,6 +1218,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
     IHIP_CHECK(hipStreamSynchronize(c->stream));
     s->ids[s->length] = tok;
     s->length++;
+    s->state_ok = true;
     tok = out_ids[i];
   }
   return 0;
@@ -1189,7 +1327,7 @@ static int context_forward(ihip_mctx* s, const int32_t* ids, const float* embeds
   int rc = prepare(s, s->length + count);
   if (rc) return rc;
   for (int64_t done = 0; done < count;) {
-    const int64_t n = chunk_rows(s, s->length, count - done);
+    const int64_t n = chunk_rows(s, s->length, count - done, ids ? ids + done : nullptr);
     const bool last = done + n == count;
     const bool want = logits && (all_logits || last);
     uint64_t ldev = s->logits;
@@ -1206,7 +1344,7 @@ static int context_forward(ihip_mctx* s, const int32_t* ids, const float* embeds
       ldev = s->logits_all;
     }
     rc = chunk(s, ids ? ids + done : nullptr, embeds ? embeds + done * d.hidden : nullptr, n, want,
-               all_logits != 0, ldev, last ? normed : nullptr);
+               all_logits != 0, ldev, last ? normed : nullptr, done == 0);
     if (rc) return rc;
     if (want) {
       float* dst = all_logits ? logits + done * d.vocab : logits;
@@ -1234,8 +1372,8 @@ static int context_greedy(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_
     std::lock_guard<std::mutex> g(c->lock);
     if ((rc = prepare(s, s->length + n + max_new))) return rc;
     for (int64_t done = 0; done < n && !rc;) {
-      const int64_t k = chunk_rows(s, s->length, n - done);
-      rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr);
+      const int64_t k = chunk_rows(s, s->length, n - done, prompt + done);
+      rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr, done == 0);
       done += k;
     }
     if (!rc) rc = next_token(s);
@@ -1282,10 +1420,15 @@ static int64_t usable(const ihip_mctx* s, const int32_t* prompt, int64_t count)
   int64_t n = 0;
   const int64_t lim = std::min<int64_t>(std::max<int64_t>(count, 0), s->length);
   while (n < lim && s->ids[n] >= 0 && s->ids[n] == prompt[n]) n++;
-  // a recurrent state holds the whole sequence: all of it or nothing
-  // (TDecoderContext.Usable / Restorable, decoder.pas:1180-1230, without
-  // restore points)
-  if (s->m->recurrent && n != s->length) n = 0;
+  // a recurrent state holds the whole sequence: all of it, else the last
+  // restore point before the end of the common start whose token is the
+  // prompt's CheckpointId token there too (TDecoderContext.Usable,
+  // decoder.pas:1213-1230)
+  if (!s->m->recurrent || n == 0 || (n == s->length && s->state_ok)) return n;
+  const int64_t prefix = n;
+  n = 0;
+  for (auto& c : s->ckpts)
+    if (c.first < prefix && s->ids[c.first] == s->ckpt_id && c.first > n && restorable(s, c.first)) n = c.first;
   return n;
 }
 
@@ -1331,11 +1474,11 @@ static int native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t
   s->draw_ids = draw_ids > 0 && draw_ids < d.vocab ? draw_ids : 0;
   // the cached start of the prompt stays, the rest is computed
   const int64_t kept = usable(s, prompt, n - 1);
-  s->length = kept;
+  if ((rc = truncate_to(s, kept))) return rc;
   if ((rc = prepare(s, n + max_new))) return rc;
   for (int64_t done = kept; done < n && !rc;) {
-    const int64_t k = chunk_rows(s, s->length, n - done);
-    rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr);
+    const int64_t k = chunk_rows(s, s->length, n - done, prompt + done);
+    rc = chunk(s, prompt + done, nullptr, k, done + k == n, false, s->logits, nullptr, done == kept);
     done += k;
   }
   if (!rc) rc = next_token(s);
@@ -1567,7 +1710,33 @@ void ihip_model_destroy(ihip_model* m)
 int ihip_model_reset(ihip_model* m)
 {
   if (!m) return fail(IHIP_E_ARG, "ihip_model_reset");
-  m->def->length = 0;
+  std::lock_guard<std::mutex> g(m->c->lock);
+  return truncate_to(m->def, 0);
+}
+
+int ihip_context_set_checkpoints(ihip_mctx* s, int32_t id, int64_t max)
+{
+  if (!s || max < 0) return fail(IHIP_E_ARG, "ihip_context_set_checkpoints");
+  std::lock_guard<std::mutex> g(s->m->c->lock);
+  // SetCheckpointId / SetMaxCheckpoints (decoder.pas:1019-1047): another id
+  // drops the restore points (the rows cached were split by the old one);
+  // a smaller count drops the oldest
+  if (id != s->ckpt_id) {
+    s->ckpt_id = id;
+    s->ckpts.clear();
+    s->aligned = s->length == 0;
+  }
+  s->ckpt_max = max;
+  while ((int64_t)s->ckpts.size() > max) s->ckpts.erase(s->ckpts.begin());
+  return 0;
+}
+
+int ihip_context_checkpoints(ihip_mctx* s, int64_t* lengths, int64_t cap, int64_t* count)
+{
+  if (!s || !count || (cap > 0 && !lengths)) return fail(IHIP_E_ARG, "ihip_context_checkpoints");
+  std::lock_guard<std::mutex> g(s->m->c->lock);
+  *count = (int64_t)s->ckpts.size();
+  for (int64_t i = 0; i < *count && i < cap; i++) lengths[i] = s->ckpts[i].first;
   return 0;
 }
 
@@ -1634,13 +1803,10 @@ int ihip_context_truncate(ihip_mctx* s, int64_t length)
   if (!s || length < 0 || length > s->length)
     return fail(IHIP_E_ARG, "ihip_context_truncate(" + std::to_string(length) + ") of " +
                                 std::to_string(s ? s->length : 0) + " tokens");
-  // a DeltaNet state holds the whole sequence: no way back but to 0
-  // (TDecoderContext.Truncate / Restorable, decoder.pas:996-1010, :1190-1197)
-  if (s->m->recurrent && length != 0 && length != s->length)
-    return fail(IHIP_E_ARG, "ihip_context_truncate(" + std::to_string(length) +
-                                "): a recurrent state cannot go back there");
-  s->length = length;  // the cache keeps every row: any length is restorable
-  return 0;
+  // the cache keeps every row: any length but where a DeltaNet state cannot
+  // go back (to 0 or a restore point only)
+  std::lock_guard<std::mutex> g(s->m->c->lock);
+  return truncate_to(s, length);
 }
 
 int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t* kept)
@@ -1648,8 +1814,10 @@ int ihip_context_reuse(ihip_mctx* s, const int32_t* ids, int64_t count, int64_t*
   if (!s || (!ids && count > 0) || !kept) return fail(IHIP_E_ARG, "ihip_context_reuse");
   // the common prefix, at most count - 1 tokens (the last one is computed
   // again for its logits); a position fed an embedding row matches no id
+  std::lock_guard<std::mutex> g(s->m->c->lock);
   const int64_t n = usable(s, ids, count > 0 ? count - 1 : 0);
-  s->length = n;
+  int rc = truncate_to(s, n);
+  if (rc) return rc;
   *kept = n;
   return 0;
 }

@@ -139,6 +139,8 @@ def lib():
             "ihip_context_reuse": (i32, [vp, vp, i64, C.POINTER(i64)]),
             "ihip_context_truncate": (i32, [vp, i64]),
             "ihip_context_length": (i32, [vp, C.POINTER(i64), C.POINTER(i64)]),
+            "ihip_context_set_checkpoints": (i32, [vp, i32, i64]),
+            "ihip_context_checkpoints": (i32, [vp, vp, i64, C.POINTER(i64)]),
             "ihip_context_greedy": (i32, [vp, vp, i64, i64, vp]),
             "ihip_context_decode": (i32, [vp, C.c_int32, i64, vp]),
             "ihip_native_decode": (i32, [vp, vp, i64, i64, C.POINTER(Sampling), i64, vp, i64, i64,
@@ -518,6 +520,19 @@ class ModelContext:
         n, cap = C.c_int64(), C.c_int64()
         check(lib().ihip_context_length(self.h, C.byref(n), C.byref(cap)), "length")
         return n.value, cap.value
+
+    def set_checkpoints(self, token_id, max_count=4):
+        """CheckpointId / MaxCheckpoints: restore points of the recurrent
+        state before every token_id of an aligned forward (-1: none)."""
+        check(lib().ihip_context_set_checkpoints(self.h, int(token_id), int(max_count)),
+              "set_checkpoints")
+
+    def checkpoints(self):
+        """The lengths of the restore points held, the oldest first."""
+        out = np.zeros(64, np.int64)
+        n = C.c_int64()
+        check(lib().ihip_context_checkpoints(self.h, _p(out), len(out), C.byref(n)), "checkpoints")
+        return out[:min(n.value, len(out))].tolist()
 
     def greedy(self, prompt, max_new):
         p = np.ascontiguousarray(prompt, np.int32)

@@ -162,3 +162,55 @@ def test_qwen35_real_widths(ctx):
     print("min margin", float(margins.min()), flush=True)
     assert np.array_equal(got, ref)
     dev.close()
+
+
+def test_qwen35_restore_points(ctx):
+    # CheckpointId = T (a turn start): one forward of three turns keeps the
+    # states before the second and third T; a branched conversation (the
+    # third turn edited) resumes from the restore point before it and gives
+    # the logits of a fresh pass; Truncate goes back to a restore point only;
+    # decoded tokens (parts a fresh pass would not make) add none
+    s = spec("text-q8_0")
+    T = 7
+    a = np.array([T, 11, 12, 13, 14, 15, T, 21, 22, 23, 24, T, 31, 32, 33], np.int32)
+    m = H.Model(ctx, s, max_tokens=96)
+    c = m.new_context()
+    c.set_checkpoints(T, 4)
+    c.forward(a)
+    assert c.checkpoints() == [6, 11]
+    b = np.concatenate([a[:12], [41, 42, 43]]).astype(np.int32)
+    assert c.reuse(b) == 11
+    assert c.checkpoints() == [6, 11]
+    got = c.forward(b[11:])
+    fresh = m.new_context()
+    want = fresh.forward(b)
+    assert rel(got, want) < 1e-6
+    assert rel(want, O.Model(s, 96).forward(b)) < 1e-5
+    # another turn from the cached branch, then back to the first restore point
+    c.forward(np.array([T, 51, 52], np.int32))
+    assert c.checkpoints() == [6, 11, 15]
+    with pytest.raises(H.HipError):
+        c.truncate(9)
+    c.truncate(6)
+    assert c.checkpoints() == [6]
+    assert rel(c.forward(a[6:]), fresh_logits(m, a)) < 1e-6
+    # decoded tokens: a part of one token not starting at T, unaligned
+    c.decode(int(np.argmax(c.forward(np.array([T, 61], np.int32)))), 3)
+    n = c.length()[0]
+    c.forward(np.array([T, 71], np.int32))
+    assert n not in c.checkpoints()
+    # at most max_count kept, the oldest dropped
+    c.set_checkpoints(T, 4)
+    c.truncate(0)
+    c.forward(np.array([T, 1, T, 2, T, 3, T, 4, T, 5, T, 6], np.int32))
+    assert c.checkpoints() == [4, 6, 8, 10]
+    c.close()
+    fresh.close()
+    m.close()
+
+
+def fresh_logits(m, ids):
+    f = m.new_context()
+    out = f.forward(ids)
+    f.close()
+    return out
