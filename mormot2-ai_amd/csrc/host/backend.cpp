@@ -430,7 +430,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   const bool gemm_q8 = (q8 || float_fmt(k.dtype)) && gemm_runs(c, k.dtype, mode);
   if (k.items && k.item_rows > 8 && !gemm_q8)
     return fail(IHIP_E_ARG, "EnqueueLinear: items of more than 8 slots need the GEMM");
-  if (batch && gemm_q8 && (k.items ? k.item_rows > 8 : k.rows >= c->gemm_min_rows)) {
+  const int min_rows = float_fmt(k.dtype) ? c->gemm_min_rows_float : c->gemm_min_rows;
+  if (batch && gemm_q8 && (k.items ? k.item_rows > 8 : k.rows >= min_rows)) {
     struct {
       const uint8_t* w;
       const uint8_t* xq;

@@ -19,6 +19,10 @@ namespace ihip {
 // below 80 rows the GEMVs are faster (a 32-token prompt of Qwen3-0.6B
 // prefills 1.6x faster on them, a 128-token one 7% slower)
 constexpr int GEMM_MIN_ROWS = 80;
+// F32/BF16/F16 weights on the f64 GEMM from 16 rows: gpt-oss-20b's BF16
+// attention matrices take 19.3 ms for a 32-token prefill there against 25.0
+// on the 8-row GEMVs, 20.1 against 36.4 for 64 tokens
+constexpr int GEMM_MIN_ROWS_FLOAT = 16;
 // the GEMM's smallest chunk (one 16-row tile)
 constexpr int GEMM_TILE_ROWS = 16;
 
@@ -70,6 +74,9 @@ struct ihip_ctx {
   int cus = 256;
   bool use_gemm = true;        // Q8 chunks of >= GEMM_MIN_ROWS rows on the MFMA GEMM (IHIP_GEMM=0: off)
   int gemm_min_rows = ihip::GEMM_MIN_ROWS;  // the smallest chunk on the GEMM (IHIP_GEMM_MIN_ROWS)
+  // the smallest chunk of F32/BF16/F16 weights on the f64 GEMM
+  // (IHIP_GEMM_MIN_ROWS_FLOAT)
+  int gemm_min_rows_float = ihip::GEMM_MIN_ROWS_FLOAT;
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
   bool use_gemm8 = true;  // 2..79 quantized rows on the int8 matrix cores, gemm8 (IHIP_GEMM8=0: the VALU gemv_rows)

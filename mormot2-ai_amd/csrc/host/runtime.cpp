@@ -170,6 +170,8 @@ int ihip_create(int device, ihip_ctx** out)
   if (const char* v = getenv("IHIP_GEMV_BLOCKS_PER_CU")) c->gemv_blocks_per_cu = std::max(1, atoi(v));
   if (const char* v = getenv("IHIP_GEMM")) c->use_gemm = atoi(v) != 0;
   if (const char* v = getenv("IHIP_GEMM_MIN_ROWS")) c->gemm_min_rows = std::max(GEMM_TILE_ROWS, atoi(v));
+  if (const char* v = getenv("IHIP_GEMM_MIN_ROWS_FLOAT"))
+    c->gemm_min_rows_float = std::max(GEMM_TILE_ROWS, atoi(v));
   if (const char* v = getenv("IHIP_GEMV_HOLD")) c->gemv_hold = std::max(1, atoi(v));
   if (const char* v = getenv("IHIP_ATTN_MFMA")) c->attn_mfma = atoi(v) != 0;
   if (const char* v = getenv("IHIP_GEMM8")) c->use_gemm8 = atoi(v) != 0;
