@@ -508,13 +508,16 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     if (chunks <= 1024) {
       snprintf(name, sizeof name, "gemv_%s_q8_%srows_j%d", fmt_name(k.dtype), k.nw ? "norm_" : "",
                chunks <= 512 ? 8 : 16);
-      int64_t rows_max = k.out;
-      if (k.nseg > 1)
-        for (int i = 0; i < k.nseg; i++) rows_max = std::max<int64_t>(rows_max, k.oseg[i]);
-      const int64_t waves = rows_max;  // one row per wave step
+      // the rows of every matrix in one index space, a row per wave step:
+      // one round of resident blocks, each staging the activation row once
+      int64_t rows = k.out;
+      if (k.nseg > 1) {
+        rows = 0;
+        for (int i = 0; i < k.nseg; i++) rows += k.oseg[i];
+      }
       const int64_t hold = (int64_t)c->cus * resident_blocks(c, name, 256) * c->gemv_hold;
-      const int64_t wgs = std::max<int64_t>(1, std::min((waves + 3) / 4, hold));
-      return launch(c, name, dim3((unsigned)wgs, (unsigned)(k.nseg > 1 ? k.nseg : 1)), dim3(256), &a);
+      const int64_t wgs = std::max<int64_t>(1, std::min((rows + 3) / 4, hold));
+      return launch(c, name, dim3((unsigned)wgs), dim3(256), &a);
     }
   }
   // a small batch of quantized rows on the int8 matrix cores: 8 rows (or an

@@ -1201,114 +1201,107 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
 // ------------------------------------------------------------ float rows
 // One activation row against F32 / BF16 / F16 weights in the Q8 arithmetic
 // (TInferCpuBackend.Linear's float branch, backend.cpu.pas:1548-1565: the
-// exact float products summed in double). A wave takes FRW rows per step;
-// its 64 lanes read each row as consecutive 16-byte chunks (one contiguous
-// kilobyte per load instruction, every load of the step issued before the
-// first use); the activation row is staged in LDS once per block (normed
-// with NORM) and read per chunk. Rows of up to 3 matrices (nseg) as the
-// one-row GEMV.
-constexpr int FRW = 1;  // rows per wave step
-
+// exact float products summed in double). A wave takes one row per step;
+// its 64 lanes read the row as consecutive 16-byte chunks (one contiguous
+// kilobyte per load instruction), the next row's chunks in flight while this
+// row is summed; the activation row is staged in LDS once per block (normed
+// with NORM) and read per chunk. The rows of up to 3 matrices (nseg) are one
+// index space, so the launch is one round of blocks whatever their shapes.
 template <int F>
 constexpr int f_bytes() { return F == DT_F32 ? 4 : 2; }
-
-// the 16-byte chunks lane + 64 j of rows sp * RW .. (a row past the matrix
-// reads its last row; chunks past the row its last chunk: values unused)
-template <int RW, int NJ>
-__device__ __forceinline__ void flt_load(const uint8_t* w, int64_t rb, int64_t sp, int out, int lane,
-                                         int nj, int NC, uint4 (&wv)[RW][NJ])
-{
-#pragma unroll
-  for (int r = 0; r < RW; r++) {
-    const int64_t o = min(sp * RW + r, (int64_t)out - 1);
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      if (j < nj) {  // the same for the whole launch
-        const int c = min(lane + 64 * j, NC - 1);
-        wv[r][j] = ld<uint4, true>(w + o * rb, (uint32_t)c * 16u);
-      }
-    }
-  }
-}
 
 template <int F, bool NORM, int NJ>
 __device__ __forceinline__ void gemv_flt(const LinArgs& a)
 {
   constexpr int ES = f_bytes<F>(), VPC = 16 / ES;  // values per 16-byte chunk
   const int lane = threadIdx.x & 63;
-  const uint8_t* w = a.w;
-  const float* bias = a.bias;
-  int out = a.out;
-  float* yp = a.y;
-  if (a.nseg > 1) {
-    // (selected, not indexed: an index into the argument block would move it
-    // to scratch memory)
-    const int sg = blockIdx.y;
-    w = sg == 0 ? a.wseg[0] : (sg == 1 ? a.wseg[1] : a.wseg[2]);
-    bias = sg == 0 ? a.bseg[0] : (sg == 1 ? a.bseg[1] : a.bseg[2]);
-    out = sg == 0 ? a.oseg[0] : (sg == 1 ? a.oseg[1] : a.oseg[2]);
-    yp = sg == 0 ? a.yseg[0] : (sg == 1 ? a.yseg[1] : a.yseg[2]);
-  }
+  // the rows of the (up to 3) matrices as one index space: o0 rows of the
+  // first, then o1 of the second, then o2 of the third; a wave takes every
+  // nw-th of them (no block idles on a short matrix beside a long one)
+  const int nseg = a.nseg > 1 ? a.nseg : 1;
+  const int o0 = nseg > 1 ? a.oseg[0] : a.out, o1 = nseg > 1 ? a.oseg[1] : 0, o2 = nseg > 2 ? a.oseg[2] : 0;
+  const int64_t total = (int64_t)o0 + o1 + o2;
   const int NC = a.in / VPC;  // chunks per row: at most 64 NJ
   const int nj = (NC + 63) / 64;
   const int64_t rb = (int64_t)a.in * ES;  // row bytes
   const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
   const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
-  const int64_t steps = ((int64_t)out + FRW - 1) / FRW;
   __shared__ __align__(16) float xs[XN];
-  if ((int64_t)blockIdx.x * (NT >> 6) >= steps) return;  // the whole block: no rows
+  if ((int64_t)blockIdx.x * (NT >> 6) >= total) return;  // the whole block: no rows
+  // (selected, not indexed: an index into the argument block would move it
+  // to scratch memory)
+  auto wrow = [&](int64_t g, int& sg, int& o) -> const uint8_t* {
+    sg = g < o0 ? 0 : (g < (int64_t)o0 + o1 ? 1 : 2);
+    o = (int)(g - (sg == 0 ? 0 : (sg == 1 ? o0 : (int64_t)o0 + o1)));
+    const uint8_t* w = nseg > 1 ? (sg == 0 ? a.wseg[0] : (sg == 1 ? a.wseg[1] : a.wseg[2])) : a.w;
+    return w + (int64_t)o * rb;
+  };
+  auto load = [&](int64_t g, uint4 (&wv)[NJ]) {
+    int sg, o;
+    const uint8_t* wr = wrow(min(g, total - 1), sg, o);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+      if (j < nj) {  // the same for the whole launch
+        const int c = min(lane + 64 * j, NC - 1);
+        wv[j] = ld<uint4, true>(wr, (uint32_t)c * 16u);
+      }
+  };
   XStage st;
   stage_load<F, 1, NORM>(a.x, nullptr, a.in, a.nw, st);
-  // the first step's weights while the row is staged
-  uint4 wv[FRW][NJ];
-  int64_t sp = wid;
-  flt_load<FRW, NJ>(w, rb, sp, out, lane, nj, NC, wv);
+  // the first row's weights while the activation row is staged
+  uint4 wv[NJ], wn[NJ];
+  int64_t g = wid;
+  load(g, wv);
   stage_store<F, 1, NORM>(st, false, a.in, a.eps, (uint8_t*)xs, nullptr, a.bad, 1);
   __syncthreads();
-  while (sp < steps) {
+  while (g < total) {
+    // the next row's weights in flight during this row's sums
+    const int64_t gn = g + nw;
+    if (gn < total) load(gn, wn);
+    double p[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int r = 0; r < FRW; r++) {
-      double p[4] = {0, 0, 0, 0};
+    for (int j = 0; j < NJ; j++) {
+      const int c = lane + 64 * j;
+      if (j < nj && c < NC) {
+        const uint32_t q[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        float v[8];
 #pragma unroll
-      for (int j = 0; j < NJ; j++) {
-        const int c = lane + 64 * j;
-        if (j < nj && c < NC) {
-          const uint32_t q[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
-          float v[8];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            if constexpr (F == DT_F32) {
-              v[i] = bits_float(q[i]);
-            } else if constexpr (F == DT_BF16) {
-              v[2 * i] = bits_float(q[i] << 16);
-              v[2 * i + 1] = bits_float(q[i] & 0xffff0000u);
-            } else {
-              v[2 * i] = half_to_float(q[i] & 0xffffu);
-              v[2 * i + 1] = half_to_float(q[i] >> 16);
-            }
-          }
-          const float4* xp = (const float4*)(xs + c * VPC);
-#pragma unroll
-          for (int h = 0; h < VPC / 4; h++) {
-            const float4 xv = xp[h];
-            p[0] = __builtin_fma((double)v[4 * h], (double)xv.x, p[0]);
-            p[1] = __builtin_fma((double)v[4 * h + 1], (double)xv.y, p[1]);
-            p[2] = __builtin_fma((double)v[4 * h + 2], (double)xv.z, p[2]);
-            p[3] = __builtin_fma((double)v[4 * h + 3], (double)xv.w, p[3]);
+        for (int i = 0; i < 4; i++) {
+          if constexpr (F == DT_F32) {
+            v[i] = bits_float(q[i]);
+          } else if constexpr (F == DT_BF16) {
+            v[2 * i] = bits_float(q[i] << 16);
+            v[2 * i + 1] = bits_float(q[i] & 0xffff0000u);
+          } else {
+            v[2 * i] = half_to_float(q[i] & 0xffffu);
+            v[2 * i + 1] = half_to_float(q[i] >> 16);
           }
         }
-      }
-      double v = wave_sum((p[0] + p[1]) + (p[2] + p[3]), 64);
-      const int64_t o = sp * FRW + r;
-      if (lane == 0 && o < out) {
-        if (bias) v = (double)bias[o] + v;
-        float rr = (float)v;
-        if (a.res) rr = a.res[o] + rr;
-        yp[o] = rr;
+        const float4* xp = (const float4*)(xs + c * VPC);
+#pragma unroll
+        for (int h = 0; h < VPC / 4; h++) {
+          const float4 xv = xp[h];
+          p[0] = __builtin_fma((double)v[4 * h], (double)xv.x, p[0]);
+          p[1] = __builtin_fma((double)v[4 * h + 1], (double)xv.y, p[1]);
+          p[2] = __builtin_fma((double)v[4 * h + 2], (double)xv.z, p[2]);
+          p[3] = __builtin_fma((double)v[4 * h + 3], (double)xv.w, p[3]);
+        }
       }
     }
-    sp += nw;
-    if (sp < steps) flt_load<FRW, NJ>(w, rb, sp, out, lane, nj, NC, wv);
+    double v = wave_sum((p[0] + p[1]) + (p[2] + p[3]), 64);
+    if (lane == 0) {
+      int sg, o;
+      (void)wrow(g, sg, o);
+      const float* bias = nseg > 1 ? (sg == 0 ? a.bseg[0] : (sg == 1 ? a.bseg[1] : a.bseg[2])) : a.bias;
+      float* yp = nseg > 1 ? (sg == 0 ? a.yseg[0] : (sg == 1 ? a.yseg[1] : a.yseg[2])) : a.y;
+      if (bias) v = (double)bias[o] + v;
+      float rr = (float)v;
+      if (a.res) rr = a.res[o] + rr;
+      yp[o] = rr;
+    }
+    g = gn;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) wv[j] = wn[j];
   }
 }
 
