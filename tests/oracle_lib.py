@@ -284,8 +284,12 @@ def argmax(v):
 class Model:
     """The CPU decoder over a model description (mormot_ai_hip.ihip_model_desc)."""
 
-    def __init__(self, desc, max_tokens, kv_f16=False, threads=8, f32=False, fast=False):
+    def __init__(self, desc, max_tokens, kv_f16=False, threads=None, f32=False, fast=False):
         self.desc = desc  # keeps the host tensors alive
+        if threads is None:
+            # a tiny model's Linear is too short for a thread pool (and the
+            # test workers already share the cores)
+            threads = 1 if desc.struct.hidden <= 512 else 8
         h = C.c_void_p()
         rc = lib().orc_model_create(C.addressof(desc.struct), max_tokens, int(kv_f16), threads,
                                     C.byref(h))
