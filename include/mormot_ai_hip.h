@@ -243,9 +243,11 @@ int ihip_enqueue_attention(ihip_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc,
                            int64_t window, uint64_t sinks, double scale,
                            int kv_f16);
 /* the router of TDecoderModel.Route (decoder.pas:2901-2949) for one row of
- * logits, on the device: ids and weights sorted by id (route, ops.cu:664-720) */
+ * logits, on the device: ids and weights sorted by id (route, ops.cu:664-720);
+ * scale (or 0): [experts] F32, each weight times its expert's after the
+ * renorm (Gemma 4's per_expert_scale) */
 int ihip_enqueue_route(ihip_ctx* ctx, uint64_t logits, int64_t experts,
-                       int64_t k, int norm_topk, uint64_t ids, uint64_t w);
+                       int64_t k, int norm_topk, uint64_t ids, uint64_t w, uint64_t scale);
 /* y = sum over slots in id order of w[s] * d[s] (moecombine, ops.cu:724-734) */
 int ihip_enqueue_moecombine(ihip_ctx* ctx, uint64_t d, uint64_t w, uint64_t y,
                             int64_t k, int64_t n);

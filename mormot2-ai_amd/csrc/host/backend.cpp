@@ -935,7 +935,7 @@ int ihip_enqueue_attention(ihip_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, ui
 }
 
 int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k, int norm_topk,
-                       uint64_t ids, uint64_t w)
+                       uint64_t ids, uint64_t w, uint64_t scale)
 {
   if (!c || experts < 1 || experts > 4096 || k < 1 || k > 64 || k > experts)
     return fail(IHIP_E_ARG, "ihip_enqueue_route");
@@ -945,7 +945,8 @@ int ihip_enqueue_route(ihip_ctx* c, uint64_t logits, int64_t experts, int64_t k,
     float* w;
     int32_t experts, k, norm, rows;
     const float* scale;
-  } a = {(const float*)logits, (int*)ids, (float*)w, (int32_t)experts, (int32_t)k, norm_topk, 1};
+  } a = {(const float*)logits, (int*)ids, (float*)w, (int32_t)experts, (int32_t)k, norm_topk, 1,
+         (const float*)scale};
   return launch(c, "route", dim3(1), dim3(256), &a);
 }
 

@@ -117,7 +117,7 @@ def lib():
                                           i64, i64, i64, C.c_double, i32]),
             "ihip_enqueue_attention": (i32, [vp, u64, u64, u64, u64, i64, i64, i64, i64, i64, i64,
                                              u64, C.c_double, i32]),
-            "ihip_enqueue_route": (i32, [vp, u64, i64, i64, i32, u64, u64]),
+            "ihip_enqueue_route": (i32, [vp, u64, i64, i64, i32, u64, u64, u64]),
             "ihip_enqueue_moecombine": (i32, [vp, u64, u64, u64, i64, i64]),
             "ihip_enqueue_embed": (i32, [vp, u64, i32, i64, i64, u64, i64, u64]),
             "ihip_enqueue_argmax": (i32, [vp, u64, i64, u64]),

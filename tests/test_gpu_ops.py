@@ -172,17 +172,24 @@ def test_attention_valu_tiles(ctx_rows, hd, heads, kvh, past, rows, window, sink
     test_attention(ctx_rows, hd, heads, kvh, past, rows, window, sinks, f16)
 
 
-@pytest.mark.parametrize("E,k,norm", [(128, 8, True), (32, 4, True), (16, 3, False)])
-def test_route(ctx, E, k, norm):
+@pytest.mark.parametrize("E,k,norm,scaled", [(128, 8, True, False), (32, 4, True, False),
+                                             (16, 3, False, False), (128, 8, True, True)])
+def test_route(ctx, E, k, norm, scaled):
     rng = np.random.default_rng(E)
+    sc = rng.uniform(0.5, 1.5, E).astype(np.float32) if scaled else None
+    ds = ctx.array(sc) if scaled else None
     for trial in range(5):
         lg = rng.standard_normal(E).astype(np.float32)
         if trial == 1:
             lg[3] = lg[7] = lg.max() + 1  # a tie: the lower id first
         dl = ctx.array(lg)
         di, dw = ctx.alloc(4 * k), ctx.alloc(4 * k)
-        H.check(H.lib().ihip_enqueue_route(ctx.h, dl.ptr, E, k, int(norm), di.ptr, dw.ptr))
+        H.check(H.lib().ihip_enqueue_route(ctx.h, dl.ptr, E, k, int(norm), di.ptr, dw.ptr,
+                                           ds.ptr if scaled else 0))
         ids, w = O.route(lg, k, norm)
+        if scaled:
+            # Route's expert scale (decoder.pas:2939-2941): after the renorm
+            w = (w * sc[ids]).astype(np.float32)
         order = np.argsort(ids, kind="stable")
         assert np.array_equal(di.download(np.int32, k), ids[order])
         assert np.array_equal(dw.download(np.float32, k), w[order])
