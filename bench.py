@@ -86,9 +86,10 @@ def stream_peak(ctx):
     return nbytes / (ms * 1e-3) / 1e9
 
 
-def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20):
+def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20, hot=False):
     """GB/s of one (type, shape, batch, mode): distinct copies of the matrix
-    cycled inside a graph, so the weights stream from HBM."""
+    cycled inside a graph, so the weights stream from HBM; hot: the same copy
+    every time (a matrix under 256 MB then reads from the MALL/L2)."""
     import infer_hip as H
     L = H.lib()
     wbytes = out * H.row_bytes(dtype, cols)
@@ -112,8 +113,9 @@ def gemv_case(ctx, dtype, out, cols, rows, mode, min_bytes=512 << 20):
 
     def enq():
         for i in range(ncopies):
-            H.check(L.ihip_enqueue_linear_at(ctx.h, xin, rows, cols, dtype, big.ptr + i * stride,
-                                             out, dy.ptr, 0, m), "gemv")
+            H.check(L.ihip_enqueue_linear_at(ctx.h, xin, rows, cols, dtype,
+                                             big.ptr + (0 if hot else i) * stride, out, dy.ptr, 0, m),
+                    "gemv")
 
     reps = 3
     ms = time_graph(ctx, enq, reps) / ncopies
@@ -407,7 +409,7 @@ def main():
         log(f"f32-mode decode 64 steps: {ft * 1e3:.3f} ms/token, {1.0 / ft:.1f} tok/s "
             f"(prefill {f32_prefill * 1e3:.0f} ms)")
 
-    sweep = {}
+    sweep, mall_hot = {}, {}
     if not args.no_sweep:
         for dtype in (H.Q8_0, H.Q4_0, H.Q4_K, H.Q6_K, H.MXFP4):
             for out, cols in SWEEP_SHAPES:
@@ -427,6 +429,11 @@ def main():
                         sweep[key] = {"GBps": round(gbps, 1), "us": round(us, 2),
                                       "frac": round(gbps / HBM_PEAK, 3)}
                     log(key, sweep[key])
+                    if rows == 1 and mode == H.MODE_Q8:
+                        # the same launch with the matrix cache-resident
+                        # (labelled apart: not an HBM figure)
+                        hg, hus = gemv_case(ctx, dtype, out, cols, rows, mode, hot=True)
+                        mall_hot[key] = {"GBps": round(hg, 1), "us": round(hus, 2)}
 
     cpu = None
     if not args.no_cpu:
@@ -480,6 +487,9 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "gemv_head_151936x1024_b1_GBps": big,
         "gemv": sweep,
+        # batch-1 GEMVs replaying one copy of the matrix: cache-resident
+        # (MALL/L2) for matrices under 256 MB, not HBM bandwidth
+        "gemv_mall_hot": mall_hot,
         "cpu_baseline": cpu,
         "device": dev_name,
     }
