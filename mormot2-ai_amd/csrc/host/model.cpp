@@ -20,6 +20,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <memory>
 
 #include "internal.h"
 
@@ -39,6 +40,8 @@ struct DevLayer {
   int mixer = IHIP_MIXER_ATTENTION, output_gate = 0;
   uint64_t lqkv = 0, lz = 0, lb = 0, la = 0, lout = 0, lconv = 0, ldt = 0, lnega = 0, lnorm = 0;
   int lqkvd = 0, lzd = 0, lbd = 0, lad = 0, loutd = 0;
+  uint64_t lba = 0;  // beta's rows, then alpha's, as one matrix (types alike), for the one-row path
+  int lbad = 0;
   // Gemma 4: this layer's heads, K=V, the rotary set; the norms around the
   // blocks, those of the dense block beside the experts, the expert scales
   // and the layer scalar (0: none)
@@ -120,6 +123,9 @@ struct ihip_model {
   // as a model does in its destructor (backend.pas:151-158) - new host
   // tensors at a reused address must not meet the stale device copy
   std::vector<std::pair<const uint8_t*, uint64_t>> uploaded;
+  // host copies the model made for an upload (a DeltaNet's beta and alpha
+  // rows as one matrix): kept while their device copies are cached
+  std::vector<std::unique_ptr<std::vector<uint8_t>>> host_owned;
   ihip_sampler* sampler = nullptr;  // null: the argmax
   int sampler_epoch = 0;            // bumped by ihip_model_sampling (graphs captured again)
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
@@ -338,12 +344,76 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
                            attention_splits(maxkeys));
 }
 
+// the launch arguments of deltanet.hip
+struct DnConvArgs {
+  float* qkv;
+  const float* w;
+  float* conv;
+  int32_t rows, channels, kw, pad;
+};
+struct DnPrepArgs {
+  float* qkv;
+  float* beta;
+  float* decay;
+  float* z;
+  const float* dt_bias;
+  const float* neg_a;
+  int32_t kh, vh, dk, dv, channels, pad;
+};
+struct DnConvPrepArgs {
+  float* qkv;
+  const float* w;
+  float* conv;
+  float* beta;
+  float* decay;
+  float* z;
+  const float* dt_bias;
+  const float* neg_a;
+  int32_t kh, vh, dk, dv, channels, kw;
+};
+struct DnRuleArgs {
+  const float* qkv;
+  const float* beta;
+  const float* decay;
+  float* state;
+  float* y;
+  int32_t rows, stride, kh, vh, dk, dv, group, pad;
+};
+struct DnNormArgs {
+  float* x;
+  const float* w;
+  const float* z;
+  double eps;
+  int32_t rows, cols;
+};
+struct GateArgs {
+  const float* qg;
+  float* q;
+  float* g;
+  int64_t n;
+  int32_t hd, pad;
+};
+// the launch arguments of ops.hip's element-wise kernels (EltArgs) and softcap
+struct EltArgs2 {
+  float* x;
+  const float* t;
+  int64_t n;
+  float alpha, limit;
+};
+struct SoftcapArgs {
+  float* x;
+  int64_t n;
+  double cap;
+};
+
+static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh, bool fused = false);
+
 // whether one row runs through layers_one: the norms fused into the GEMVs
 // (hidden <= 4096), a token's experts combined in one launch (<= 8 slots)
 static bool one_row_fused(const ihip_model* m)
 {
   const ihip_model_desc& d = m->d;
-  if (d.hidden > 4096 || m->recurrent || m->gated || m->gemma || rope_dims(d) != d.head_dim) return false;
+  if (d.hidden > 4096 || m->gemma) return false;
   if (d.experts > 0) {
     const int64_t K = d.experts_used;
     if (K < 1 || K > 8 || K * d.expert_ffn * 4 > 65536) return false;
@@ -372,13 +442,20 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
   };
   for (int l = 0; l < d.layers; l++) {
     const DevLayer& L = m->L[l];
+    if (L.mixer == IHIP_MIXER_DELTANET) {
+      // the DeltaNet's projections normed in their staging, the output
+      // projection adding the residual
+      if ((rc = deltanet_block(s, l, 1, nullptr, true))) return rc;
+      goto ffn;
+    }
     // attention block (decoder.pas:2625-2702)
     {
-      // q, k and v: the matrices of one weight type in one launch
+      // q, k and v: the matrices of one weight type in one launch (a gated
+      // attention's q rows: per head its query, then its gate, into qg)
       const int dts[3] = {L.qd, L.kd, L.vd};
       const uint64_t ws[3] = {L.q, L.k, L.v}, bs[3] = {L.qb, L.kb, L.vb},
-                     ys[3] = {s->q, s->k, s->v};
-      const int64_t os[3] = {qw, kvw, kvw};
+                     ys[3] = {L.output_gate ? s->qg : s->q, s->k, s->v};
+      const int64_t os[3] = {L.output_gate ? 2 * qw : qw, kvw, kvw};
       bool done[3] = {false, false, false};
       // two types with a kernel for the pair (Q4_K_M: q, k Q4_K and v Q6_K)
       int t2 = 0;
@@ -418,8 +495,12 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
         rc = enqueue_linear(m->c, k);
       }
       if (rc) return rc;
+      if (L.output_gate) {
+        GateArgs ga = {(const float*)s->qg, (float*)s->q, (float*)s->gq, qw, (int32_t)hd, 0};
+        if ((rc = launch(m->c, "split_gate", dim3((unsigned)((qw + 255) / 256)), dim3(256), &ga))) return rc;
+      }
     }
-    if (hd == 64 || hd == 128) {
+    if ((hd == 64 || hd == 128) && rope_dims(d) == hd) {
       // head norms, RoPE, cache store and the ranges in one launch, then the merge
       AttnOne o;
       o.q = s->q; o.k = s->k; o.v = s->v; o.qn = L.qn; o.kn = L.kn; o.cs = s->cs;
@@ -435,12 +516,18 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
     } else if ((rc = rope_attn(s, l, 1, past, graph))) {
       return rc;
     }
+    if (L.output_gate) {
+      // GateBySigmoid (decoder.pas:2594-2610) before the output projection
+      GateArgs ga = {nullptr, (float*)s->attn, (float*)s->gq, qw, (int32_t)hd, 0};
+      if ((rc = launch(m->c, "gate_sigmoid", dim3((unsigned)((qw + 255) / 256)), dim3(256), &ga))) return rc;
+    }
     {
       LinearCall k;
       k.x = s->attn; k.rows = 1; k.in = qw; k.dtype = L.od; k.w = L.o; k.out = H; k.bias = L.ob;
       k.y = s->x; k.res = s->x; k.mode = m->mode;
       if ((rc = enqueue_linear(m->c, k))) return rc;
     }
+  ffn:
     if (!L.moe) {
       // DenseFfn (decoder.pas:2866-2878): gate, up and SwiGLU in one pass
       const int64_t F = d.ffn;
@@ -492,62 +579,12 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
   return 0;
 }
 
-// the launch arguments of deltanet.hip
-struct DnConvArgs {
-  float* qkv;
-  const float* w;
-  float* conv;
-  int32_t rows, channels, kw, pad;
-};
-struct DnPrepArgs {
-  float* qkv;
-  float* beta;
-  float* decay;
-  float* z;
-  const float* dt_bias;
-  const float* neg_a;
-  int32_t kh, vh, dk, dv, channels, pad;
-};
-struct DnRuleArgs {
-  const float* qkv;
-  const float* beta;
-  const float* decay;
-  float* state;
-  float* y;
-  int32_t rows, stride, kh, vh, dk, dv, group, pad;
-};
-struct DnNormArgs {
-  float* x;
-  const float* w;
-  const float* z;
-  double eps;
-  int32_t rows, cols;
-};
-struct GateArgs {
-  const float* qg;
-  float* q;
-  float* g;
-  int64_t n;
-  int32_t hd, pad;
-};
-// the launch arguments of ops.hip's element-wise kernels (EltArgs) and softcap
-struct EltArgs2 {
-  float* x;
-  const float* t;
-  int64_t n;
-  float alpha, limit;
-};
-struct SoftcapArgs {
-  float* x;
-  int64_t n;
-  double cap;
-};
 
 // DeltaNetBlock (decoder.pas:2704-2753) of layer l over n rows, h holding
 // their input norm: the four projections, the convolution and DeltaPrep, the
 // delta rule on the layer's state, the gated RMSNorm, the output projection
 // into tmp
-static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh)
+static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh, bool fused)
 {
   ihip_model* m = s->m;
   const ihip_model_desc& d = m->d;
@@ -555,26 +592,72 @@ static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh)
   const int64_t H = d.hidden, kh = d.lin_key_heads, vh = d.lin_value_heads, dk = d.lin_key_dim,
                 dv = d.lin_value_dim, vd = vh * dv, cd = 2 * kh * dk + vd;
   int rc;
-  if ((rc = lin(s, s->h, qh, n, H, L.lqkvd, L.lqkv, cd, 0, s->qkv)) ||
-      (rc = lin(s, s->h, qh, n, H, L.lzd, L.lz, vd, 0, s->z)) ||
-      (rc = lin(s, s->h, qh, n, H, L.lbd, L.lb, vh, 0, s->beta)) ||
-      (rc = lin(s, s->h, qh, n, H, L.lad, L.la, vh, 0, s->decay)))
+  uint64_t decay = s->decay;
+  if (fused) {
+    // one row, x the residual: every projection norms it in its staging; the
+    // q/k/v channels, z and beta|alpha (one matrix when their types match,
+    // decay then after beta) in one launch of one weight type
+    LinearCall k;
+    k.x = s->x; k.rows = 1; k.in = H; k.mode = m->mode; k.nw = L.input_norm; k.eps = d.rms_eps;
+    auto seg = [&](uint64_t w, int64_t out, uint64_t y) {
+      k.wseg[k.nseg] = w; k.oseg[k.nseg] = out; k.yseg[k.nseg] = y; k.bseg[k.nseg] = 0; k.nseg++;
+    };
+    if (L.lba && L.lqkvd == L.lzd && L.lzd == L.lbad) {
+      k.dtype = L.lqkvd;
+      seg(L.lqkv, cd, s->qkv);
+      seg(L.lz, vd, s->z);
+      seg(L.lba, 2 * vh, s->beta);
+      k.w = k.wseg[0]; k.y = k.yseg[0]; k.out = k.oseg[0];
+      if ((rc = enqueue_linear(m->c, k))) return rc;
+      decay = s->beta + (uint64_t)vh * 4;
+    } else {
+      const int dts[4] = {L.lqkvd, L.lzd, L.lbd, L.lad};
+      const uint64_t ws[4] = {L.lqkv, L.lz, L.lb, L.la}, ys[4] = {s->qkv, s->z, s->beta, s->decay};
+      const int64_t os[4] = {cd, vd, vh, vh};
+      for (int i = 0; i < 4; i++) {
+        LinearCall one;
+        one.x = s->x; one.rows = 1; one.in = H; one.dtype = dts[i]; one.w = ws[i]; one.out = os[i];
+        one.y = ys[i]; one.mode = m->mode; one.nw = L.input_norm; one.eps = d.rms_eps;
+        if ((rc = enqueue_linear(m->c, one))) return rc;
+      }
+    }
+  } else if ((rc = lin(s, s->h, qh, n, H, L.lqkvd, L.lqkv, cd, 0, s->qkv)) ||
+             (rc = lin(s, s->h, qh, n, H, L.lzd, L.lz, vd, 0, s->z)) ||
+             (rc = lin(s, s->h, qh, n, H, L.lbd, L.lb, vh, 0, s->beta)) ||
+             (rc = lin(s, s->h, qh, n, H, L.lad, L.la, vh, 0, s->decay))) {
     return rc;
-  DnConvArgs ca = {(float*)s->qkv, (const float*)L.lconv, (float*)s->conv[l], (int32_t)n, (int32_t)cd,
-                   d.lin_conv, 0};
-  if ((rc = launch(m->c, "dn_conv", dim3((unsigned)((cd + 255) / 256)), dim3(256), &ca))) return rc;
-  DnPrepArgs pa = {(float*)s->qkv, (float*)s->beta, (float*)s->decay, (float*)s->z, (const float*)L.ldt,
-                   (const float*)L.lnega, (int32_t)kh, (int32_t)vh, (int32_t)dk, (int32_t)dv, (int32_t)cd, 0};
-  if ((rc = launch(m->c, "dn_prep", dim3((unsigned)(2 * kh + vh), (unsigned)n), dim3(64), &pa))) return rc;
+  }
+  if (n == 1 && dv <= 256) {
+    // one row: the convolution and DeltaPrep of each item in one launch (a
+    // wave holds an item's channels, up to 256)
+    DnConvPrepArgs cp = {(float*)s->qkv, (const float*)L.lconv, (float*)s->conv[l], (float*)s->beta, (float*)decay,
+                         (float*)s->z, (const float*)L.ldt, (const float*)L.lnega, (int32_t)kh, (int32_t)vh,
+                         (int32_t)dk, (int32_t)dv, (int32_t)cd, d.lin_conv};
+    if ((rc = launch(m->c, "dn_convprep1", dim3((unsigned)(2 * kh + vh)), dim3(64), &cp))) return rc;
+  } else {
+    DnConvArgs ca = {(float*)s->qkv, (const float*)L.lconv, (float*)s->conv[l], (int32_t)n, (int32_t)cd,
+                     d.lin_conv, 0};
+    if ((rc = launch(m->c, "dn_conv", dim3((unsigned)((cd + 255) / 256)), dim3(256), &ca))) return rc;
+    DnPrepArgs pa = {(float*)s->qkv, (float*)s->beta, (float*)decay, (float*)s->z, (const float*)L.ldt,
+                     (const float*)L.lnega, (int32_t)kh, (int32_t)vh, (int32_t)dk, (int32_t)dv, (int32_t)cd, 0};
+    if ((rc = launch(m->c, "dn_prep", dim3((unsigned)(2 * kh + vh), (unsigned)n), dim3(64), &pa))) return rc;
+  }
   // LinGroup (decoder.pas:2457-2463)
   const int32_t group = d.lin_tiled ? 1 : (int32_t)(vh / kh);
-  DnRuleArgs ra = {(const float*)s->qkv, (const float*)s->beta, (const float*)s->decay, (float*)s->state[l],
+  DnRuleArgs ra = {(const float*)s->qkv, (const float*)s->beta, (const float*)decay, (float*)s->state[l],
                    (float*)s->core, (int32_t)n, (int32_t)cd, (int32_t)kh, (int32_t)vh, (int32_t)dk,
                    (int32_t)dv, group, 0};
   if ((rc = launch(m->c, "dn_rule", dim3((unsigned)vh, (unsigned)((dv + 3) / 4)), dim3(256), &ra))) return rc;
   DnNormArgs na = {(float*)s->core, (const float*)L.lnorm, (const float*)s->z, (double)d.rms_eps,
                    (int32_t)(n * vh), (int32_t)dv};
   if ((rc = launch(m->c, "dn_gatenorm", dim3((unsigned)((n * vh + 3) / 4)), dim3(256), &na))) return rc;
+  if (fused) {
+    // the output projection adds the residual
+    LinearCall k;
+    k.x = s->core; k.rows = 1; k.in = vd; k.dtype = L.loutd; k.w = L.lout; k.out = H;
+    k.y = s->x; k.res = s->x; k.mode = m->mode;
+    return enqueue_linear(m->c, k);
+  }
   QCache qc{s->xq0, s->xqk};
   return lin(s, s->core, n == 1 ? nullptr : &qc, n, vd, L.loutd, L.lout, H, 0, s->tmp);
 }
@@ -1617,6 +1700,17 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
       if (!L.lqkv || !L.lz || !L.lb || !L.la || !L.lout || !L.lconv || !L.ldt || !L.lnega || !L.lnorm ||
           s.moe)
         return bad(fail(IHIP_E_ARG, "model: DeltaNet layer " + std::to_string(l) + " lacks a tensor"));
+      if (s.lin_b.dtype == s.lin_a.dtype) {
+        // beta's rows then alpha's as one matrix: the one-row path reads both
+        // in the launch of the other projections
+        const uint64_t rb = row_bytes(s.lin_b.dtype, H) * vh;
+        auto buf = std::make_unique<std::vector<uint8_t>>(2 * rb);
+        memcpy(buf->data(), s.lin_b.data, rb);
+        memcpy(buf->data() + rb, s.lin_a.data, rb);
+        const ihip_tensor t{buf->data(), s.lin_b.dtype, 0};
+        m->host_owned.push_back(std::move(buf));
+        if ((rc = upw(m, t, 2 * vh, H, 1, L.lba, L.lbad))) return bad(rc);
+      }
       continue;
     }
     m->gated |= L.output_gate != 0;

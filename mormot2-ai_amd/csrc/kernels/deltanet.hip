@@ -137,6 +137,100 @@ extern "C" __global__ __launch_bounds__(64) void dn_prep(DnPrepArgs a)
   for (int j = lane; j < a.dv; j += 64) zz[j] = dn_silu(zz[j]);
 }
 
+struct DnConvPrepArgs {
+  float* qkv;          // [channels]: one row, convolved, silu'd and prepared in place
+  const float* w;      // [channels, kw]
+  float* conv;         // [channels, kw - 1], moved on
+  float* beta;         // [vh]
+  float* decay;        // [vh]
+  float* z;            // [vh * dv]
+  const float* dt_bias;
+  const float* neg_a;
+  int32_t kh, vh, dk, dv, channels, kw;
+};
+
+// one row: the convolution of an item's channels and the item's DeltaPrep in
+// one launch (dn_conv then dn_prep's arithmetic), one wave per item - a q or
+// k head (its dk channels convolved, then L2-normed), or a value head (its dv
+// channels convolved; beta, decay, silu(z))
+extern "C" __global__ __launch_bounds__(64) void dn_convprep1(DnConvPrepArgs a)
+{
+  const int item = blockIdx.x, lane = threadIdx.x;
+  const int i = item - 2 * a.kh;
+  const int first = i < 0 ? item * a.dk : 2 * a.kh * a.dk + i * a.dv;
+  const int cnt = i < 0 ? a.dk : a.dv;
+  const int k1 = a.kw - 1;
+  constexpr int NC = DN_MAXK / 64;  // channels per lane (items of up to 256)
+  float y[NC];
+#pragma unroll
+  for (int u = 0; u < NC; u++) {
+    y[u] = 0.f;
+    const int cc = lane + 64 * u;
+    if (cc >= cnt) continue;
+    const int64_t c = first + cc;
+    float st[DN_MAXKW], w[DN_MAXKW];
+#pragma unroll
+    for (int j = 0; j < DN_MAXKW; j++) {
+      st[j] = j < k1 ? a.conv[c * k1 + j] : 0.f;
+      w[j] = j < a.kw ? a.w[c * a.kw + j] : 0.f;
+    }
+    float wl = w[0];
+#pragma unroll
+    for (int j = 1; j < DN_MAXKW; j++)
+      if (j == k1) wl = w[j];
+    const float x = a.qkv[c];
+    double acc = (double)wl * (double)x;
+#pragma unroll
+    for (int j = 0; j < DN_MAXKW; j++)
+      if (j < k1) acc = __builtin_fma((double)w[j], (double)st[j], acc);
+#pragma unroll
+    for (int j = 0; j + 1 < DN_MAXKW; j++)
+      if (j + 1 < k1) a.conv[c * k1 + j] = st[j + 1];
+    if (k1 > 0) a.conv[c * k1 + k1 - 1] = x;
+    y[u] = dn_silu((float)acc);
+  }
+  if (i < 0) {
+    double acc = 0;
+#pragma unroll
+    for (int u = 0; u < NC; u++) {
+      const double e = y[u];
+      acc = __builtin_fma(e, e, acc);
+    }
+    acc = wave_sum(acc, 64);
+    const float f = (float)(1.0 / sqrt(acc + 1e-6));
+    const float scale = (float)(1.0 / sqrt((double)a.dk));
+#pragma unroll
+    for (int u = 0; u < NC; u++) {
+      const int cc = lane + 64 * u;
+      if (cc >= cnt) continue;
+      float v = y[u] * f;
+      if (item < a.kh) v = v * scale;
+      a.qkv[first + cc] = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < NC; u++) {
+    const int cc = lane + 64 * u;
+    if (cc < cnt) a.qkv[first + cc] = y[u];
+  }
+  if (lane == 0) {
+    a.beta[i] = dn_sigmoid(a.beta[i]);
+    const float x = a.decay[i] + a.dt_bias[i];
+    float sp;
+    if (x > 20) {
+      sp = x;
+    } else {
+      const double e = exp((double)x);
+      sp = e < 1e-6 ? (float)(e - e * e / 2) : (float)log(1.0 + e);
+    }
+    sp = a.neg_a[i] * sp;
+    a.decay[i] = (float)exp((double)sp);
+  }
+  float* zz = a.z + (int64_t)i * a.dv;
+  for (int j = lane; j < a.dv; j += 64) zz[j] = dn_silu(zz[j]);
+}
+
 struct DnRuleArgs {
   const float* qkv;    // [rows, stride]: [q heads | k heads | v heads]
   const float* beta;   // [rows, vh]
