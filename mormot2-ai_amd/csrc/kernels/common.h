@@ -224,6 +224,81 @@ __device__ __forceinline__ T xpart(T v)
   }
 }
 
+// xswap<K>(v): the value of lane ^ K for every K (K 4 and 8 as two
+// bank-masked row shifts: banks that read upward, then banks that read
+// downward), for reductions whose lanes of a block hold different values
+template <int K>
+__device__ __forceinline__ uint32_t xswap_u(uint32_t v)
+{
+  if constexpr (K == 4) {
+    const uint32_t t = __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xF, 0x5, false);
+    return __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);
+  } else if constexpr (K == 8) {
+    const uint32_t t = __builtin_amdgcn_update_dpp(0u, v, 0x108, 0xF, 0x3, false);
+    return __builtin_amdgcn_update_dpp(t, v, 0x118, 0xF, 0xC, false);
+  } else {
+    return xpart_u<K>(v);
+  }
+}
+
+template <int K, typename T>
+__device__ __forceinline__ T xswap(T v)
+{
+  if constexpr (sizeof(T) == 8) {
+    uint64_t b = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = xswap_u<K>((uint32_t)b), hi = xswap_u<K>((uint32_t)(b >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, xswap_u<K>(__builtin_bit_cast(uint32_t, v)));
+  }
+}
+
+// the sums of 8 values (one per row) over aligned blocks of `width` lanes,
+// transposed: at each of the levels 1, 2 and 4 a lane keeps half of its
+// values and adds its partner's half, so after them it holds one row, row
+// 4*bit0 + 2*bit1 + bit2 of its lane (with fewer levels, rows base + i for
+// i < 8 >> levels); the tree per row is wave_sum's, level by level, own +
+// partner, so every row's sum has wave_sum's bits. Returns the count of
+// values left (8, 4, 2 or 1), in v[0..count).
+template <typename T>
+__device__ __forceinline__ int rows_sum8(T (&v)[8], int width, int& base)
+{
+  const int lane = threadIdx.x;
+  int n = 8;
+  base = 0;
+  if (width > 1) {
+    const bool b = lane & 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const T s = b ? v[i] : v[i + 4], k = b ? v[i + 4] : v[i];
+      v[i] = k + xswap<1>(s);
+    }
+    n = 4;
+    base += b ? 4 : 0;
+  }
+  if (width > 2) {
+    const bool b = lane & 2;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const T s = b ? v[i] : v[i + 2], k = b ? v[i + 2] : v[i];
+      v[i] = k + xswap<2>(s);
+    }
+    n = 2;
+    base += b ? 2 : 0;
+  }
+  if (width > 4) {
+    const bool b = lane & 4;
+    const T s = b ? v[0] : v[1], k = b ? v[1] : v[0];
+    v[0] = k + xswap<4>(s);
+    n = 1;
+    base += b ? 1 : 0;
+  }
+  if (width > 8) v[0] = v[0] + xswap<8>(v[0]);
+  if (width > 16) v[0] = v[0] + xswap<16>(v[0]);
+  if (width > 32) v[0] = v[0] + xswap<32>(v[0]);
+  return n;
+}
+
 // the sum over aligned blocks of `width` lanes (1..64, a power of two), in
 // every lane of the block: own + partner at each level, so the result is the
 // one of the lane ^ K butterfly bit for bit

@@ -1109,6 +1109,102 @@ __device__ __forceinline__ void gemv_rows(const LinArgs& a)
           km[k] = (int)(int8_t)(raw[k].a >> 8);
         }
       }
+      if (nrows > 1) {
+        // every row's partial sums at once, reduced transposed: the lane
+        // ends with one row (rows_sum8), lanes 0..7 of the segment store
+        double vr[RB];
+        int n, base;
+        if constexpr (is_k_quant(F)) {
+          double tot = 0.0;
+#pragma unroll
+          for (int k = 0; k < U; k++) {
+            const int g = lr + k * lpr;
+            const int gc = min(g, G - 1);
+            int isr[RB], msr[RB];
+#pragma unroll
+            for (int r = 0; r < RB; r++) {
+              isr[r] = msr[r] = 0;
+              if (r < nrows) {
+                XRow xg;
+                stage_xrow<SUMS>(xst + r * RS, G, gc, xg);
+                int sl = 0, sh = 0;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                  sl = sdot4((int)cw[k][d], xg.w[d], sl);
+                  sh = sdot4((int)cw[k][4 + d], xg.w[4 + d], sh);
+                }
+                if constexpr (F == DT_Q4_K) {
+                  isr[r] = __mul24(ksc[k], sl + sh);
+                  msr[r] = __mul24(km[k], xg.sl + xg.sh);
+                } else {
+                  isr[r] = __mul24(ksc[k], sl - 32 * xg.sl) + __mul24(km[k], sh - 32 * xg.sh);
+                }
+              }
+            }
+            // exact integer sums over the 8 lanes of a super-block
+            int rb;
+            rows_sum8(isr, 8, rb);
+            if constexpr (F == DT_Q4_K) rows_sum8(msr, 8, rb);
+            const float dx = ((const float*)(xst + rb * RS + 32 * G))[gc];
+            const double tt = superblock_q8k<F>(raw[k], isr[0], F == DT_Q4_K ? msr[0] : 0, dx);
+            tot += (valid && g < G) ? tt : 0.0;
+            base = rb;
+          }
+          if (lpr > 8) tot = tot + xswap<8>(tot);
+          if (lpr > 16) tot = tot + xswap<16>(tot);
+          if (lpr > 32) tot = tot + xswap<32>(tot);
+          vr[0] = tot;
+          n = 1;
+        } else {
+#pragma unroll
+          for (int r = 0; r < RB; r++) {
+            double accd = 0.0;
+            if (r < nrows) {
+#pragma unroll
+              for (int k = 0; k < U; k++) {
+                const int g = lr + k * lpr;
+                XRow xg;
+                stage_xrow<SUMS>(xst + r * RS, G, min(g, G - 1), xg);
+                int sd = 0;
+#pragma unroll
+                for (int d = 0; d < 8; d++) sd = sdot4((int)cw[k][d], xg.w[d], sd);
+                const double dxd = xg.dx;
+                const int sxq = xg.sl + xg.sh;
+                double tt;
+                if constexpr (F == DT_Q8_0) {
+                  tt = (double)sd * ((double)half_to_float(raw[k].a) * dxd);
+                } else if constexpr (F == DT_MXFP4) {
+                  tt = (double)sd * (mxfp4_q8_scale(raw[k].a) * dxd);
+                } else if constexpr (F == DT_Q4_0) {
+                  tt = (double)(sd - 8 * sxq) * ((double)half_to_float(raw[k].a) * dxd);
+                } else if constexpr (F == DT_Q5_0) {
+                  tt = (double)(sd - 16 * sxq) * ((double)half_to_float(raw[k].a) * dxd);
+                } else {  // Q5_1
+                  const double t1 = (double)sd * ((double)half_to_float(raw[k].a & 0xffffu) * dxd);
+                  tt = t1 + (double)half_to_float(raw[k].a >> 16) * (dxd * (double)sxq);
+                }
+                if (valid && g < G) accd += tt;
+              }
+            }
+            vr[r] = accd;
+          }
+          n = rows_sum8(vr, lpr, base);
+        }
+        if (lr < 8 && valid) {
+#pragma unroll
+          for (int i = 0; i < RB; i++) {
+            if (i >= n) break;
+            const int row = base + i;
+            int64_t yo = yr[0];
+#pragma unroll
+            for (int r = 1; r < RB; r++) yo = row == r ? yr[r] : yo;
+            double v = vr[i];
+            if (bias) v = (double)bo + v;
+            if (row < nrows) a.y[yo * a.out + o] = (float)v;
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int r = 0; r < RB; r++) {
         if (r >= nrows) break;

@@ -155,6 +155,27 @@ def test_linear_q8_mode_cpu_bits(ctx, dtype):
     assert differ <= max(2, total // 1000), (differ, total)
 
 
+# batches of 2..15 rows on the batch GEMV (rows staged in LDS, the 8 rows'
+# sums reduced transposed across the lanes of an output): every row has the
+# bits of that row run alone, ragged last chunks included, at input widths
+# whose lanes per output run from 2 to 64
+@pytest.mark.parametrize("dtype", BLOCK_FMTS)
+def test_batch_rows_bits_of_one_row(ctx, dtype):
+    rng = np.random.default_rng(21)
+    for cols in (64, 256, 1024, 3072):
+        if not fits(dtype, cols):
+            continue
+        for rows, out in ((2, 300), (3, 1024), (5, 97), (8, 640), (11, 300), (15, 130)):
+            w = weights(dtype, out, cols, rows * 7 + cols + out)
+            x = rng.standard_normal((rows, cols)).astype(np.float32)
+            b = rng.standard_normal(out).astype(np.float32) if rows % 2 else None
+            y = ctx.linear(x, w, dtype, out, b, mode=H.MODE_Q8)
+            for r in range(rows):
+                one = ctx.linear(x[r:r + 1], w, dtype, out, b, mode=H.MODE_Q8)
+                assert np.array_equal(y[r].view(np.uint32), one[0].view(np.uint32)), \
+                    (H.NAMES[dtype], rows, cols, out, r)
+
+
 # small batches whose 128-output tiles fill the chip run on the int8 matrix
 # cores (gemm8: 8 rows per block, the weights read once per 8 rows); the
 # last row chunk partial, rows past it absent
