@@ -1088,6 +1088,8 @@ __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d,
   double pv[MU];
 #pragma unroll
   for (int u = 0; u < MU; u++) pv[u] = rd(min(u, splits - 1) * (d + 2) + ic);
+  // wave 0: the maxima, the weights and the denominator (a wave sum of the
+  // weighted range sums), one barrier before the weighted values
   if (t < 64) {
     double M = -1.0e308;
     for (int s = t; s < splits; s += 64) {
@@ -1098,18 +1100,16 @@ __device__ __forceinline__ void merge_ranges(const double* b, int splits, int d,
     }
     M = wave_max(M);
     if (sink && (double)*sink > M) M = *sink;
+    double den = 0;
     for (int s = t; s < splits; s += 64) {
       const double ms = wts[s];
-      wts[s] = ms > -1.0e308 ? exp(ms - M) : 0.0;
+      const double e = ms > -1.0e308 ? exp(ms - M) : 0.0;
+      wts[s] = e;
+      den = __builtin_fma(e, lsum[s], den);
     }
-    if (t == 0) dsh[0] = M;
-  }
-  __syncthreads();
-  if (t == 0) {
-    double den = 0;
-    for (int s = 0; s < splits; s++) den = den + wts[s] * lsum[s];
-    if (sink) den = den + exp((double)*sink - dsh[0]);
-    dsh[1] = 1.0 / den;
+    den = wave_sum(den, 64);
+    if (sink) den = den + exp((double)*sink - M);
+    if (t == 0) dsh[1] = 1.0 / den;
   }
   __syncthreads();
   const double inv = dsh[1];
@@ -1414,11 +1414,11 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     x0 = j == jnew ? vn0 : (j < n ? x0 : 0.f);
     x1 = j == jnew ? vn1 : (j < n ? x1 : 0.f);
     if (u & 1) {
-      a0o = a0o + p * (double)x0;
-      a1o = a1o + p * (double)x1;
+      a0o = __builtin_fma(p, (double)x0, a0o);
+      a1o = __builtin_fma(p, (double)x1, a1o);
     } else {
-      a0e = a0e + p * (double)x0;
-      a1e = a1e + p * (double)x1;
+      a0e = __builtin_fma(p, (double)x0, a0e);
+      a1e = __builtin_fma(p, (double)x1, a1e);
     }
   }
   double a0 = a0e + a0o, a1 = a1e + a1o;
