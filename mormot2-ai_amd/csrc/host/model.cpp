@@ -406,6 +406,29 @@ struct SoftcapArgs {
   double cap;
 };
 
+// ops.hip's row_tail: a block output's norms, the experts beside it, the
+// residual, the layer scalar and the next input norm in one launch
+struct TailArgs {
+  float* x;
+  const float* t;
+  const float *dn_w, *ed, *ew, *moe_w, *out_w, *scalar, *nw;
+  float* h;
+  double eps;
+  int32_t rows, cols, k, pad;
+};
+
+static int row_tail(ihip_model* m, uint64_t x, uint64_t t, uint64_t dn_w, uint64_t ed, uint64_t ew,
+                    int64_t k, uint64_t moe_w, uint64_t out_w, uint64_t scalar, uint64_t nw,
+                    uint64_t h, int64_t n)
+{
+  const int64_t H = m->d.hidden;
+  if (H > 4096 || (ed && (k < 1 || k > 16))) return fail(IHIP_E_UNSUPPORTED, "row_tail: hidden <= 4096, k <= 16");
+  TailArgs a = {(float*)x, (const float*)t, (const float*)dn_w, (const float*)ed, (const float*)ew,
+                (const float*)moe_w, (const float*)out_w, (const float*)scalar, (const float*)nw,
+                (float*)h, m->d.rms_eps, (int32_t)n, (int32_t)H, (int32_t)k, 0};
+  return launch(m->c, "row_tail", dim3((unsigned)n), dim3(1024), &a);
+}
+
 static int deltanet_block(ihip_mctx* s, int l, int64_t n, QCache* qh, bool fused = false);
 
 // whether one row runs through layers_one: the norms fused into the GEMVs
@@ -691,8 +714,10 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
   // a chunk: the rows are quantized once per activation buffer
   const bool one = n == 1;
   if (one && one_row_fused(m)) return layers_one(s, past, graph);
-  // the gate/up activation fused into a one-row GEMV: SwiGLU only
-  const bool glu_fused = one && d.activation == IHIP_ACT_SILU;
+  // the gate/up activation fused into a one-row GEMV: SwiGLU, or GeGLU
+  // (the kernels' limit < 0)
+  const bool glu_fused = one && (d.activation == IHIP_ACT_SILU || d.activation == IHIP_ACT_GELU_TANH);
+  const float glu_limit = d.activation == IHIP_ACT_GELU_TANH ? -1.0f : d.swiglu_limit;
   // TDecoderModel.Activate (decoder.pas:2857-2863): SwiGLU or GeGLU in place
   auto activate = [&](uint64_t gate, uint64_t up, int64_t count) {
     if (d.activation == IHIP_ACT_GELU_TANH) {
@@ -719,11 +744,24 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         GateArgs ga = {(const float*)s->qg, (float*)s->q, (float*)s->gq, n * qw, (int32_t)hd, 0};
         if ((rc = launch(m->c, "split_gate", dim3((unsigned)((n * qw + 255) / 256)), dim3(256), &ga)))
           return rc;
+      } else if (one && L.qd == L.kd && (L.k_is_v || L.vd == L.qd)) {
+        // one row: q, k and v (k alone when V is K) as the matrices of one launch
+        LinearCall k;
+        k.x = s->h; k.rows = 1; k.in = H; k.dtype = L.qd; k.mode = m->mode;
+        k.nseg = L.k_is_v ? 2 : 3;
+        k.wseg[0] = L.q; k.wseg[1] = L.k; k.wseg[2] = L.v;
+        k.bseg[0] = L.qb; k.bseg[1] = L.kb; k.bseg[2] = L.vb;
+        k.yseg[0] = s->q; k.yseg[1] = s->k; k.yseg[2] = s->v;
+        k.oseg[0] = qw; k.oseg[1] = kvw; k.oseg[2] = kvw;
+        k.w = L.q; k.out = qw; k.y = s->q; k.bias = L.qb;
+        if ((rc = enqueue_linear(m->c, k))) return rc;
+        goto attend;
       } else if ((rc = lin(s, s->h, qhp, n, H, L.qd, L.q, qw, L.qb, s->q))) {
         return rc;
       }
       if ((rc = lin(s, s->h, qhp, n, H, L.kd, L.k, kvw, L.kb, s->k))) return rc;
       if (!L.k_is_v && (rc = lin(s, s->h, qhp, n, H, L.vd, L.v, kvw, L.vb, s->v))) return rc;
+    attend:
       if ((rc = rope_attn(s, l, n, past, graph))) return rc;
       if (L.output_gate) {
         // GateBySigmoid (decoder.pas:2594-2610) before the output projection
@@ -733,12 +771,16 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
       }
       QCache qa{s->xq0, s->xqk};
       if ((rc = lin(s, s->attn, one ? nullptr : &qa, n, qw, L.od, L.o, H, L.ob, s->tmp))) return rc;
-      // Gemma: the attention output normed before the residual
-      if (L.attn_out_norm && (rc = norm(s->tmp, L.attn_out_norm, s->tmp))) return rc;
     }
-    // residual, then the pre-FFN norm
-    if ((rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, L.post_norm, s->h, n, H, d.rms_eps)))
+    // residual, then the pre-FFN norm; Gemma norms the attention output
+    // before the residual
+    if (L.attn_out_norm && L.mixer != IHIP_MIXER_DELTANET && H <= 4096)
+      rc = row_tail(m, s->x, s->tmp, 0, 0, 0, 0, 0, L.attn_out_norm, 0, L.post_norm, s->h, n);
+    else if (L.attn_out_norm && L.mixer != IHIP_MIXER_DELTANET && (rc = norm(s->tmp, L.attn_out_norm, s->tmp)))
       return rc;
+    else
+      rc = ihip_enqueue_addnorm(m->c, s->x, s->tmp, L.post_norm, s->h, n, H, d.rms_eps);
+    if (rc) return rc;
     QCache qf{s->xq0, s->xqk};
     QCache* qfp = one ? nullptr : &qf;
     bool moe_out = false;  // the FFN output is the expert rows (added by the next norm)
@@ -750,7 +792,7 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         LinearCall k;
         k.x = s->h; k.rows = 1; k.in = H; k.dtype = L.gd; k.w = L.gate; k.out = F;
         k.y = s->gate; k.mode = m->mode; k.w2 = L.up; k.alpha = d.swiglu_alpha;
-        k.limit = d.swiglu_limit;
+        k.limit = glu_limit;
         if (L.gd != L.ud) return fail(IHIP_E_ARG, "model: gate and up of one type");
         if ((rc = enqueue_linear(m->c, k))) return rc;
       } else {
@@ -770,11 +812,26 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
       const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
       QCache qr{s->xq0, s->xqk};
       QCache* qx = qfp;
+      // the tail: the dense output's norm waits for row_tail below when it
+      // fits (nothing reads it before)
+      const bool tailed = beside && H <= 4096 && K <= 16;
+      // one row beside the dense block: the router and the experts norm the
+      // residual in their staging (router_norm, moe_in_norm)
+      const bool staged = beside && glu_fused;
       if (beside) {
-        if ((rc = norm(s->tmp, L.dense_out_norm, s->tmp)) || (rc = norm(s->x, L.router_norm, s->h))) return rc;
+        if ((!tailed && (rc = norm(s->tmp, L.dense_out_norm, s->tmp))) ||
+            (!staged && (rc = norm(s->x, L.router_norm, s->h))))
+          return rc;
         qx = one ? nullptr : &qr;
       }
-      if ((rc = lin(s, s->h, qx, n, H, L.rd, L.router, E, L.router_b, s->route))) return rc;
+      if (staged) {
+        LinearCall k;
+        k.x = s->x; k.rows = 1; k.in = H; k.dtype = L.rd; k.w = L.router; k.out = E; k.bias = L.router_b;
+        k.y = s->route; k.mode = m->mode; k.nw = L.router_norm; k.eps = d.rms_eps;
+        if ((rc = enqueue_linear(m->c, k))) return rc;
+      } else if ((rc = lin(s, s->h, qx, n, H, L.rd, L.router, E, L.router_b, s->route))) {
+        return rc;
+      }
       struct {
         const float* logits;
         int* ids;
@@ -785,7 +842,7 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
               d.norm_topk, (int32_t)n, (const float*)L.expert_scale};
       if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
       QCache qe{s->xq0, s->xqk};
-      if (beside) {
+      if (beside && !staged) {
         if ((rc = norm(s->x, L.moe_in_norm, s->h))) return rc;
         qf = qe;
       }
@@ -793,15 +850,24 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         // the token's K experts: gate, up and SwiGLU in one pass per slot,
         // then down per slot; the weighted sum goes into the next norm
         LinearCall k;
-        k.x = s->h; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
+        k.x = staged ? s->x : s->h; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
         k.y = s->gate; k.mode = m->mode; k.ids = s->ids_dev; k.stride = L.eg_stride; k.x_per_slot = 0;
         k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
-        k.limit = d.swiglu_limit;
+        k.limit = glu_limit;
+        if (staged) {
+          k.nw = L.moe_in_norm;
+          k.eps = d.rms_eps;
+        }
         if ((rc = enqueue_linear(m->c, k))) return rc;
         LinearCall dn;
         dn.x = s->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
         dn.y = s->eout; dn.mode = m->mode; dn.ids = s->ids_dev; dn.stride = L.ed_stride;
         dn.x_per_slot = 1; dn.nexp = (int)E; dn.bias = L.edb;
+        if (tailed && K <= 8 && K * FI * 4 <= 65536) {
+          // the slots' weighted sum in slot order in the same launch
+          // (moecombine's arithmetic), into the experts' row of the tail
+          dn.y = s->moe; dn.cw = s->rw;
+        }
         if ((rc = enqueue_linear(m->c, dn))) return rc;
       } else {
         struct {
@@ -837,7 +903,9 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
                           n * K, 1, L.edb, s->eout, false)))
           return rc;
       }
-      if (beside) {
+      if (tailed) {
+        // the experts' sum, its norm and the dense output's: row_tail below
+      } else if (beside) {
         // the experts' sum in slot (= id) order, normed, added to the dense
         // output, normed again (below, as the FFN output norm)
         struct {
@@ -853,11 +921,23 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         moe_out = true;
       }
     }
-    // Gemma: the feed-forward output normed before the residual
-    if (L.ffn_out_norm && (rc = norm(s->tmp, L.ffn_out_norm, s->tmp))) return rc;
     // residual, then the next layer's input norm (or the final norm); Gemma
-    // scales the whole state by the layer's scalar between the two
+    // norms the feed-forward output before the residual and scales the whole
+    // state by the layer's scalar between the two
     uint64_t nw = l + 1 < d.layers ? m->L[l + 1].input_norm : m->final_norm;
+    const bool beside = L.moe == IHIP_FFN_DENSE_MOE;
+    if (!moe_out && H <= 4096 && d.experts_used <= 16 && (beside || L.ffn_out_norm || L.scalar)) {
+      // one row: the expert rows were combined by their down launch
+      const bool combined = beside && glu_fused && d.experts_used <= 8 &&
+                            d.experts_used * d.expert_ffn * 4 <= 65536;
+      rc = row_tail(m, s->x, s->tmp, beside ? L.dense_out_norm : 0,
+                    beside ? (combined ? s->moe : s->eout) : 0, beside && !combined ? s->rw : 0,
+                    combined ? 1 : d.experts_used, beside ? L.moe_out_norm : 0, L.ffn_out_norm,
+                    L.scalar, nw, s->h, n);
+      if (rc) return rc;
+      continue;
+    }
+    if (L.ffn_out_norm && (rc = norm(s->tmp, L.ffn_out_norm, s->tmp))) return rc;
     if (L.scalar) {
       if (moe_out) return fail(IHIP_E_ARG, "model: a layer scalar after experts alone");
       EltArgs2 sa = {(float*)s->x, (const float*)L.scalar, n * H, 0.f, 0.f};

@@ -116,6 +116,26 @@ __device__ __forceinline__ float swiglu_value(float g, float u, float alpha, flo
   return b * u;
 }
 
+// TInferCpuBackend.GeluTanhGlu (backend.cpu.pas:1836-1860) of one value
+// pair: gelu_tanh(g) in double (tanh as 1 - 2 / (exp(2t) + 1), +-1 beyond
+// 20) rounded to single, then the product
+__device__ __forceinline__ float geglu_value(float gf, float u)
+{
+  const double g = gf;
+  double t = 0.7978845608028654 * (g + 0.044715 * g * g * g);
+  if (t > 20) t = 1;
+  else if (t < -20) t = -1;
+  else t = 1 - 2 / (exp(2 * t) + 1);
+  const float b = (float)(0.5 * g * (1 + t));
+  return b * u;
+}
+
+// the fused gate/up activation: GeGLU when limit < 0, else SwiGLU
+__device__ __forceinline__ float glu_value(float g, float u, float alpha, float limit)
+{
+  return limit < 0 ? geglu_value(g, u) : swiglu_value(g, u, alpha, limit);
+}
+
 // ------------------------------------------- results handed between blocks
 // A block that hands results to the launch's last block (which counts the
 // others in with an atomic counter) writes them with agent-scope stores and

@@ -50,7 +50,8 @@ struct LinArgs {
   const int4* items;
   const int* perm;
   // fused SwiGLU: w2 the up projection (same layout, stride and experts as
-  // w), bias2 its bias; y = swiglu(x W^T + bias, x W2^T + bias2)
+  // w), bias2 its bias; y = swiglu(x W^T + bias, x W2^T + bias2), GeGLU
+  // when limit < 0
   const uint8_t* w2;
   const float* bias2;
   float alpha, limit;
@@ -870,7 +871,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
           float r = (float)v;
           if constexpr (GLU) {
             if (bias2) v2 = (double)eb2[i] + v2;
-            r = swiglu_value(r, (float)v2, a.alpha, a.limit);
+            r = glu_value(r, (float)v2, a.alpha, a.limit);
           }
           if (a.res) r = er[i] + r;
           yp[yrow0 * out + o] = r;

@@ -238,6 +238,129 @@ extern "C" __global__ __launch_bounds__(1024) void rmsnorm(NormArgs a)
   }
 }
 
+// ------------------------------------------------ a block's output tail
+// The row-wise steps between a block's output t and the next GEMV, in one
+// launch (one block of 1024 per row, 4 columns a thread, cols <= 4096), each
+// with the arithmetic of its own kernel (rmsnorm's sum order, so the bits of
+// the separate launches):
+//   t := norm(t) * dn_w                          (Gemma's dense output norm)
+//   t := t + norm(sum_j ew_j * ed_j) * moe_w     (the experts beside it:
+//                                                 moecombine, norm, add;
+//                                                 ew null: weights 1, the
+//                                                 rows summed already)
+//   t := norm(t) * out_w                         (the block's output norm)
+//   x := (x + t) * scalar[0]                     (residual, layer scalar)
+//   h := norm(x) * nw                            (the next input norm)
+// each step skipped when its operand is null (decoder.pas:2697-2702,
+// 3057-3091, 3320-3336).
+struct TailArgs {
+  float* x;
+  const float* t;
+  const float* dn_w;
+  const float* ed;
+  const float* ew;
+  const float* moe_w;
+  const float* out_w;
+  const float* scalar;
+  const float* nw;
+  float* h;
+  double eps;
+  int32_t rows, cols, k, pad;
+};
+
+// rmsnorm's arithmetic over a row held 4 columns a thread (v[i] = column
+// t + 1024 i, 0 past the row): v := w * (float)(v * inv)
+__device__ __forceinline__ void tail_norm(float (&v)[NORM_NV], const float (&w)[NORM_NV], int cols,
+                                          double eps, double* sh)
+{
+  const int t = threadIdx.x;
+  double s = 0;
+#pragma unroll
+  for (int i = 0; i < NORM_NV; i++)
+    if (t + 1024 * i < cols) {
+      const double d = v[i];
+      s = s + d * d;
+    }
+  s = wave_sum(s, 64);
+  __syncthreads();  // the previous norm's readers are done with sh
+  if ((t & 63) == 0) sh[t >> 6] = s;
+  __syncthreads();
+  s = 0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
+  const double inv = 1.0 / sqrt(s / (double)cols + eps);
+#pragma unroll
+  for (int i = 0; i < NORM_NV; i++) v[i] = w[i] * (float)((double)v[i] * inv);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void row_tail(TailArgs a)
+{
+  __shared__ double sh[16];
+  const int64_t base = (int64_t)blockIdx.x * a.cols;
+  const int t = threadIdx.x;
+  float tv[NORM_NV], xv[NORM_NV], wd[NORM_NV], wm[NORM_NV], wo[NORM_NV], wn[NORM_NV];
+  float md[16][NORM_NV], mw[16];
+  // every load first: the rows, the expert rows and their weights, the norms
+#pragma unroll
+  for (int i = 0; i < NORM_NV; i++) {
+    const int c = t + 1024 * i;
+    const bool in = c < a.cols;
+    const int cc = in ? c : 0;
+    tv[i] = in ? a.t[base + cc] : 0.f;
+    xv[i] = in ? a.x[base + cc] : 0.f;
+    wd[i] = a.dn_w ? a.dn_w[cc] : 0.f;
+    wm[i] = a.moe_w ? a.moe_w[cc] : 0.f;
+    wo[i] = a.out_w ? a.out_w[cc] : 0.f;
+    wn[i] = a.nw[cc];
+  }
+  if (a.ed) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int64_t sl = (int64_t)blockIdx.x * a.k + min(j, a.k - 1);
+      mw[j] = j < a.k ? (a.ew ? a.ew[sl] : 1.f) : 0.f;
+#pragma unroll
+      for (int i = 0; i < NORM_NV; i++) {
+        const int c = t + 1024 * i;
+        md[j][i] = (j < a.k && c < a.cols) ? a.ed[sl * a.cols + c] : 0.f;
+      }
+    }
+  }
+  if (a.dn_w) tail_norm(tv, wd, a.cols, a.eps, sh);
+  if (a.ed) {
+    // moecombine: the weighted expert rows in slot order, from 0
+    float mv[NORM_NV];
+#pragma unroll
+    for (int i = 0; i < NORM_NV; i++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        if (j < a.k) {
+          const float p = mw[j] * md[j][i];
+          acc = acc + p;
+        }
+      mv[i] = acc;
+    }
+    tail_norm(mv, wm, a.cols, a.eps, sh);
+#pragma unroll
+    for (int i = 0; i < NORM_NV; i++) tv[i] = tv[i] + mv[i];
+  }
+  if (a.out_w) tail_norm(tv, wo, a.cols, a.eps, sh);
+  const float sc = a.scalar ? a.scalar[0] : 1.f;
+#pragma unroll
+  for (int i = 0; i < NORM_NV; i++) {
+    float x = xv[i] + tv[i];
+    if (a.scalar) x = x * sc;
+    xv[i] = x;
+    const int c = t + 1024 * i;
+    if (c < a.cols) a.x[base + c] = x;
+  }
+  tail_norm(xv, wn, a.cols, a.eps, sh);
+#pragma unroll
+  for (int i = 0; i < NORM_NV; i++) {
+    const int c = t + 1024 * i;
+    if (c < a.cols) a.h[base + c] = xv[i];
+  }
+}
+
 struct EltArgs {
   float* x;
   const float* t;
@@ -275,20 +398,13 @@ extern "C" __global__ __launch_bounds__(256) void swiglu(EltArgs a)
   }
 }
 
-// TInferCpuBackend.GeluTanhGlu (backend.cpu.pas:1836-1860): x = gate, t = up;
-// gelu_tanh(g) in double (tanh as 1 - 2 / (exp(2t) + 1), +-1 beyond 20)
-// rounded to single, then the product
+// TInferCpuBackend.GeluTanhGlu (backend.cpu.pas:1836-1860): x = gate, t = up
+// (geglu_value)
 extern "C" __global__ __launch_bounds__(256) void geglu(EltArgs a)
 {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= a.n) return;
-  const double g = a.x[i];
-  double t = 0.7978845608028654 * (g + 0.044715 * g * g * g);
-  if (t > 20) t = 1;
-  else if (t < -20) t = -1;
-  else t = 1 - 2 / (exp(2 * t) + 1);
-  const float b = (float)(0.5 * g * (1 + t));
-  a.x[i] = b * a.t[i];
+  a.x[i] = geglu_value(a.x[i], a.t[i]);
 }
 
 // x := x * t[0] (Gemma's layer scalar, decoder.pas:3330-3336), or x * alpha
