@@ -461,6 +461,9 @@ struct RopeArgs {
 // 2688-2691); one wave per head
 extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
 {
+  // every operand loaded first (heads up to 512: 8 values and 4 rotary
+  // pairs a thread), then the arithmetic: one memory round trip
+  constexpr int NV = 8, NR = 4;
   __shared__ float nv[512];
   int hh = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
   int d = a.hd, half = (a.rot > 0 ? a.rot : d) >> 1;
@@ -470,28 +473,51 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
   int64_t src = isq ? ((int64_t)r * a.heads + h) * d : ((int64_t)r * a.kvh + h) * d;
   const float* in = isq ? a.q + src : a.k + src;
   const float* nw = isq ? a.qn : a.kn;
-  if (nw) {
-    double s = 0;
-    for (int c = t; c < d; c += 64) {
-      double x = in[c];
-      s = s + x * x;
-    }
-    s = wave_sum(s, 64);
-    double inv = 1.0 / sqrt(s / (double)d + a.eps);
-    for (int c = t; c < d; c += 64) {
-      float n = (float)((double)in[c] * inv);
-      nv[c] = nw[c] * n;
-    }
-  } else {
-    for (int c = t; c < d; c += 64) nv[c] = in[c];
-  }
-  __syncthreads();
   const float* cr = a.cs + (int64_t)r * half;
   const float* sr = a.cs + (int64_t)a.rows * half + (int64_t)r * half;
+  float xin[NV], wv[NV], vin[NV], cv[NR], sv[NR];
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int cc = min(t + 64 * i, d - 1);
+    xin[i] = in[cc];
+    wv[i] = nw ? nw[cc] : 1.f;
+    vin[i] = isq ? 0.f : a.v[src + cc];
+  }
+#pragma unroll
+  for (int j = 0; j < NR; j++) {
+    const int ii = min(t + 64 * j, max(half - 1, 0));
+    cv[j] = cr[ii];
+    sv[j] = sr[ii];
+  }
+  if (nw) {
+    double s = 0;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      if (t + 64 * i < d) {
+        double x = xin[i];
+        s = s + x * x;
+      }
+    s = wave_sum(s, 64);
+    double inv = 1.0 / sqrt(s / (double)d + a.eps);
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      if (t + 64 * i < d) {
+        float n = (float)((double)xin[i] * inv);
+        nv[t + 64 * i] = wv[i] * n;
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      if (t + 64 * i < d) nv[t + 64 * i] = xin[i];
+  }
+  __syncthreads();
   int64_t kvw = (int64_t)a.kvh * d;
   int64_t dst = ((int64_t)past + r) * kvw + (int64_t)h * d;
-  for (int i = t; i < half; i += 64) {
-    double x0 = nv[i], x1 = nv[i + half], c = cr[i], s = sr[i];
+#pragma unroll
+  for (int j = 0; j < NR; j++) {
+    const int i = t + 64 * j;
+    if (i >= half) break;
+    double x0 = nv[i], x1 = nv[i + half], c = cv[j], s = sv[j];
     float o0 = (float)(x0 * c - x1 * s);
     float o1 = (float)(x1 * c + x0 * s);
     if (isq) {
@@ -517,16 +543,21 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
     // weights, so the normed value itself
     double inv = 1.0;
     if (a.vnorm) {
-      double sv = 0;
-      for (int c = t; c < d; c += 64) {
-        double x = a.v[src + c];
-        sv = sv + x * x;
-      }
-      sv = wave_sum(sv, 64);
-      inv = 1.0 / sqrt(sv / (double)d + a.eps);
+      double sv2 = 0;
+#pragma unroll
+      for (int i = 0; i < NV; i++)
+        if (t + 64 * i < d) {
+          double x = vin[i];
+          sv2 = sv2 + x * x;
+        }
+      sv2 = wave_sum(sv2, 64);
+      inv = 1.0 / sqrt(sv2 / (double)d + a.eps);
     }
-    for (int c = t; c < d; c += 64) {
-      float vv = a.v[src + c];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c = t + 64 * i;
+      if (c >= d) break;
+      float vv = vin[i];
       if (a.vnorm) vv = 1.0f * (float)((double)vv * inv);
       if (a.f16) ((uint16_t*)a.vc)[dst + c] = float_to_half(vv);
       else ((float*)a.vc)[dst + c] = vv;
