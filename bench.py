@@ -169,7 +169,10 @@ def decode_kernels(ctx, model, spec, first, steps, past):
     per-launch averages and the algorithmic bytes per launch."""
     import infer_hip as H
     c = spec.cfg
-    moe = c.get("moe", False)
+    # experts alone (MoE) or beside a dense FFN (Gemma 4): the experts'
+    # self-routed gate/up launch
+    moe = c.get("moe", False) or c.get("experts", 0) > 0
+    act = "GeGLU" if c.get("family") == "gemma4" else "SwiGLU"
     Hd, hd = c["hidden"], c["head_dim"]
     L0 = spec.layers[0]
     if moe:
@@ -181,12 +184,12 @@ def decode_kernels(ctx, model, spec, first, steps, past):
         nb = wb + 2 * Hd * 4 + E * 4 + K * FI * 4 + K * 8
         if L0.exp_gate_bias.data:
             nb += 2 * K * FI * 4
-        what = f"gate+up+SwiGLU of {K} routed experts ({FI}x{Hd}, {H.NAMES[gt]}), route in-launch"
+        what = f"gate+up+{act} of {K} routed experts ({FI}x{Hd}, {H.NAMES[gt]}), route in-launch"
     else:
         FI, gt = c["ffn"], L0.gate.dtype
         wb = 2 * FI * H.row_bytes(gt, Hd)
         nb = wb + 2 * Hd * 4 + FI * 4
-        what = f"FFN gate+up+SwiGLU ({FI}x{Hd}, {H.NAMES[gt]})"
+        what = f"FFN gate+up+{act} ({FI}x{Hd}, {H.NAMES[gt]})"
     dom_name = f"gemv_{H.NAMES[gt].lower()}_q8_norm_glu"
     kvw = c["kv_heads"] * hd
     out = {}
@@ -218,8 +221,8 @@ def decode_kernels(ctx, model, spec, first, steps, past):
                         for k, (n, ms) in sorted(rep.items(), key=lambda kv: -kv[1][1])}
     model.use_graphs(True)
     d = out["dominant"]
-    # (a model whose FFN runs otherwise, as Gemma 4's GeGLU, launches no such
-    # kernel: 0, and the per-token breakdown says what ran)
+    # (a model whose FFN runs otherwise launches no such kernel: 0, and the
+    # per-token breakdown says what ran)
     d.update({"kernel": dom_name, "what": what, "bytes_per_launch": nb, "weight_bytes": wb,
               "GBps": nb / (d["avg_us"] * 1e-6) / 1e9 if d["launches"] else 0.0})
     a = out["attention"]

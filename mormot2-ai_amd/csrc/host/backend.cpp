@@ -408,6 +408,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     const float* rl;
     float* rw;
     int32_t rexp, rk, rnorm, rpad;
+    const float* rscale;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
@@ -419,7 +420,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          {(float*)k.yseg[0], (float*)k.yseg[1], (float*)k.yseg[2]},
          {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]},
          k.dtype2 ? k.nseg1 : k.nseg, (const float*)k.rl, (float*)k.rw, (int32_t)k.rexp,
-         (int32_t)k.rk, (int32_t)k.rnorm, 0};
+         (int32_t)k.rk, (int32_t)k.rnorm, 0, (const float*)k.rscale};
   if (k.rl && (!k.ids || !k.rw || !k.w2 || !k.nw || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
                k.rk > std::min<int64_t>(k.rexp, 8) || k.rk != k.rows))
     return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts, gate/up with a norm");

@@ -182,6 +182,8 @@ struct LinearCall {
   // one block writes the picks (by id) to ids and their weights to rw
   uint64_t rl = 0, rw = 0;
   int rexp = 0, rk = 0, rnorm = 0;
+  // [rexp] per-expert weight scales (Gemma 4), or 0
+  uint64_t rscale = 0;
   // the caller cannot allocate (ihip_enqueue_linear_at_static): no path
   // that grows the context's scratch
   bool no_alloc = false;

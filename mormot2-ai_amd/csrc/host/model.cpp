@@ -840,7 +840,10 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         const float* scale;
       } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, (int32_t)n, (const float*)L.expert_scale};
-      if ((rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
+      // one row beside the dense block: the route formed in the experts'
+      // gate/up launch (route_wave, the expert scales applied as route does)
+      const bool self_route = staged && E <= 256 && K <= E && K <= 8;
+      if (!self_route && (rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
       QCache qe{s->xq0, s->xqk};
       if (beside && !staged) {
         if ((rc = norm(s->x, L.moe_in_norm, s->h))) return rc;
@@ -857,6 +860,10 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
         if (staged) {
           k.nw = L.moe_in_norm;
           k.eps = d.rms_eps;
+        }
+        if (self_route) {
+          k.rl = s->route; k.rw = s->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
+          k.rscale = L.expert_scale;
         }
         if ((rc = enqueue_linear(m->c, k))) return rc;
         LinearCall dn;

@@ -81,6 +81,8 @@ struct LinArgs {
   const float* rl;
   float* rw;
   int32_t rexp, rk, rnorm, rpad;
+  // each written weight times its expert's scale (Gemma 4), or null
+  const float* rscale;
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
@@ -735,6 +737,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
           myw = (int)threadIdx.x == s2 ? sw[s2] : myw;
         }
         if ((int)threadIdx.x < a.rk) {
+          if (a.rscale) myw = myw * a.rscale[myid];
           ((int*)a.ids)[threadIdx.x] = myid;
           a.rw[threadIdx.x] = myw;
         }
