@@ -635,7 +635,45 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
   __syncthreads();
   double m = -1.0e308;
   const int64_t base = (int64_t)(first + j0) * kvw + (int64_t)g * d;
-  if (t < n) {
+  // f16 keys whose halves are whole 16-byte words: two threads a key, each half of the
+  // dimensions in four interleaved fused multiply-add chains (q and k are
+  // float values, so each product is exact in double and the fused add
+  // rounds as the CPU's add; only the order of the double sum differs);
+  // otherwise a thread a key in the CPU's order
+  const bool paired = F16 && !(d & 15);
+  if (paired) {
+    const int kk = t >> 1, hh = t & 1;
+    const int nw16 = d / 16;  // 16-byte words of half a key row
+    double c4[4] = {0, 0, 0, 0};
+    if (kk < n) {
+      const uint4* p = (const uint4*)((const uint16_t*)a.kc + base + (int64_t)kk * kvw) + hh * nw16;
+      for (int k0 = 0; k0 < nw16; k0 += 16) {
+        uint4 u[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          if (k0 + k < nw16) u[k] = p[k0 + k];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+          if (k0 + k < nw16) {
+            const uint32_t wv[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const int i = hh * (d / 2) + 8 * (k0 + k) + 2 * j;
+              c4[(2 * j) & 3] = __builtin_fma(qd[i], (double)half_to_float(wv[j] & 0xffffu), c4[(2 * j) & 3]);
+              c4[(2 * j + 1) & 3] =
+                  __builtin_fma(qd[i + 1], (double)half_to_float(wv[j] >> 16), c4[(2 * j + 1) & 3]);
+            }
+          }
+      }
+    }
+    const double part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+    double acc = part + xpart<1>(part);  // the other half of the key
+    acc = acc * a.scale;
+    if (kk < n) {
+      if (hh == 0) sc[kk] = acc;
+      m = acc;
+    }
+  } else if (t < n) {
     const int64_t kb = base + (int64_t)t * kvw;
     double acc = 0;
     if (F16 && (d & 7)) {
@@ -734,8 +772,8 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
 #pragma unroll
           for (int c = 0; c < NP; c++)
             if (c < npair) {
-              a0[c] = a0[c] + p * (double)half_to_float(v[u][c] & 0xffffu);
-              a1[c] = a1[c] + p * (double)half_to_float(v[u][c] >> 16);
+              a0[c] = __builtin_fma(p, (double)half_to_float(v[u][c] & 0xffffu), a0[c]);
+              a1[c] = __builtin_fma(p, (double)half_to_float(v[u][c] >> 16), a1[c]);
             }
         }
       }
@@ -758,8 +796,8 @@ __device__ __forceinline__ void attention_part_t(const AttnArgs& a)
 #pragma unroll
           for (int c = 0; c < NP; c++)
             if (c < npair) {
-              a0[c] = a0[c] + p * (double)v[u][c].x;
-              a1[c] = a1[c] + p * (double)v[u][c].y;
+              a0[c] = __builtin_fma(p, (double)v[u][c].x, a0[c]);
+              a1[c] = __builtin_fma(p, (double)v[u][c].y, a1[c]);
             }
         }
       }
