@@ -172,9 +172,11 @@ int ihip_enqueue_linear_at(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
  * Q8 quantized activations of a multi-row call go to a fixed device array of
  * IHIP_STATIC_SCRATCH_BYTES per GPU instead of the context's growable
  * scratch: rows * (in + in / 8) must fit (else IHIP_E_NOMEM, nothing
- * enqueued). Every call on one GPU shares that array, so calls that overlap
- * on one GPU (two contexts' streams) race; one context's stream orders its
- * own calls. Same arguments and results as ihip_enqueue_linear_at. */
+ * enqueued). Every call on one GPU shares that array; one context's stream
+ * orders its own calls, so the first context to make a multi-row call holds
+ * the array until it is destroyed and a multi-row call of another context on
+ * that GPU is refused (IHIP_E_ARG, nothing enqueued). One-row calls use no
+ * array. Same arguments and results as ihip_enqueue_linear_at. */
 #define IHIP_STATIC_SCRATCH_BYTES (8u << 20)
 int ihip_enqueue_linear_at_static(ihip_ctx* ctx, uint64_t x, int64_t rows, int64_t in,
                                   int dtype, uint64_t w, int64_t out, uint64_t y,

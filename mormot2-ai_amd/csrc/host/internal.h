@@ -198,6 +198,8 @@ bool linear_ok(int dtype, int64_t in);
 uint64_t q8_row_bytes(int64_t in);
 // reads the device address of the static scratch array for the current device
 int static_scratch_init(ihip_ctx* c);
+// gives up a context's hold on the device array (ihip_destroy)
+void static_scratch_release(const ihip_ctx* c);
 // whether enqueue_linear runs a Q8 chunk of this weight type on the MFMA GEMM
 // (and takes grouped items of up to 64 slots)
 bool gemm_runs(const ihip_ctx* c, int dtype, int mode);

@@ -1127,6 +1127,12 @@ static int chunk(ihip_mctx* s, const int32_t* ids, const float* embeds, int64_t 
   int rc0 = part_start(s, ids ? ids[0] : -1, first);
   if (rc0) return rc0;
   std::vector<float> cs((size_t)n * d.head_dim), cs2((size_t)n * std::max<int64_t>(m->hd2, 1));
+  // declared after the host vectors, so destroyed before them: on every early
+  // return the queued copies from cs, cs2, ids and embeds have ended first
+  struct StreamWait {
+    hipStream_t st;
+    ~StreamWait() { (void)hipStreamSynchronize(st); }
+  } wait_copies{c->stream};
   rotary(d, s->length, n, cs.data());
   IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
   if (m->hd2) {
@@ -1605,10 +1611,14 @@ static int64_t usable(const ihip_mctx* s, const int32_t* prompt, int64_t count)
 // the draws of a request from a fresh TInferSampler: the model's sampler kept
 // when its settings are the request's (its stream restarted at the seed, the
 // decode graphs kept), else replaced (the graphs captured again)
+int model_sampling_locked(ihip_model* m, const ihip_sampling* s);
+
+// called with the device lock held, so a request's sampler cannot be swapped
+// or reseeded by another context's request before its decode has drawn
 static int request_sampler(ihip_model* m, const ihip_sampling* smp)
 {
   const bool greedy = !smp || !(smp->temperature > 0);
-  if (greedy) return m->sampler ? ihip_model_sampling(m, smp) : (smp ? ihip_model_sampling(m, smp) : 0);
+  if (greedy) return m->sampler || smp ? model_sampling_locked(m, smp) : 0;
   ihip_sampler* k = m->sampler;
   if (k && k->temperature == smp->temperature && k->top_k == smp->top_k && k->top_p == smp->top_p &&
       k->min_p == smp->min_p) {
@@ -1617,7 +1627,7 @@ static int request_sampler(ihip_model* m, const ihip_sampling* smp)
     IHIP_CHECK(hipStreamSynchronize(m->c->stream));
     return 0;
   }
-  return ihip_model_sampling(m, smp);
+  return model_sampling_locked(m, smp);
 }
 
 static int native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,
@@ -1638,9 +1648,11 @@ static int native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t
     if (prompt[i] < 0 || prompt[i] >= d.vocab) return fail(IHIP_E_ARG, "NativeDecode: token id outside the vocabulary");
   // token k is fed at position n + k - 1 only when another one follows
   if (max_new > limit - n + 1) max_new = limit - n + 1;
+  // one lock over the sampler's set-up and the whole decode: a request of
+  // another context of this model waits, so it cannot change this one's draws
+  std::lock_guard<std::mutex> g(m->c->lock);
   int rc = request_sampler(m, smp);
   if (rc) return rc;
-  std::lock_guard<std::mutex> g(m->c->lock);
   s->draw_ids = draw_ids > 0 && draw_ids < d.vocab ? draw_ids : 0;
   // the cached start of the prompt stays, the rest is computed
   const int64_t kept = usable(s, prompt, n - 1);
@@ -1684,6 +1696,30 @@ struct ihip_prompt_cache {
 };
 
 namespace ihip {
+}  // namespace ihip
+
+namespace ihip {
+// ihip_model_sampling with the device lock already held by the caller
+int model_sampling_locked(ihip_model* m, const ihip_sampling* s)
+{
+  ihip_sampler* k = nullptr;
+  if (s && s->temperature > 0) {
+    int rc = ihip_sampler_create(m->c, s, m->d.vocab, &k);
+    if (rc) return rc;
+  } else if (s) {
+    // greedy: the settings are still checked as TInferSampler.Create does
+    ihip_sampling chk = *s;
+    chk.temperature = 0;
+    ihip_sampler* probe = nullptr;
+    int rc = ihip_sampler_create(m->c, &chk, 1, &probe);
+    ihip_sampler_destroy(probe);
+    if (rc) return rc;
+  }
+  ihip_sampler_destroy(m->sampler);
+  m->sampler = k;
+  m->sampler_epoch++;  // every context's decode graph is captured again with it
+  return 0;
+}
 }  // namespace ihip
 
 using namespace ihip;
@@ -2035,23 +2071,7 @@ int ihip_model_sampling(ihip_model* m, const ihip_sampling* s)
 {
   if (!m) return fail(IHIP_E_ARG, "ihip_model_sampling");
   std::lock_guard<std::mutex> g(m->c->lock);
-  ihip_sampler* k = nullptr;
-  if (s && s->temperature > 0) {
-    int rc = ihip_sampler_create(m->c, s, m->d.vocab, &k);
-    if (rc) return rc;
-  } else if (s) {
-    // greedy: the settings are still checked as TInferSampler.Create does
-    ihip_sampling chk = *s;
-    chk.temperature = 0;
-    ihip_sampler* probe = nullptr;
-    int rc = ihip_sampler_create(m->c, &chk, 1, &probe);
-    ihip_sampler_destroy(probe);
-    if (rc) return rc;
-  }
-  ihip_sampler_destroy(m->sampler);
-  m->sampler = k;
-  m->sampler_epoch++;  // every context's decode graph is captured again with it
-  return 0;
+  return model_sampling_locked(m, s);
 }
 
 int ihip_native_decode(ihip_mctx* s, const int32_t* prompt, int64_t n, int64_t max_new,

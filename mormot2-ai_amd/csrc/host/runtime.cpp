@@ -221,6 +221,7 @@ void ihip_destroy(ihip_ctx* c)
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  static_scratch_release(c);
   for (int i = 0; i < 16; i++) {
     if (c->execs[i]) (void)hipGraphExecDestroy(c->execs[i]);
     if (c->graphs[i]) (void)hipGraphDestroy(c->graphs[i]);

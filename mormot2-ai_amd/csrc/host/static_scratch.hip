@@ -7,6 +7,9 @@
 // and take the array's device address as an argument.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
+
 #include "internal.h"
 
 // the whole of the quantized activations of one call: rows * (in + in / 8)
@@ -17,6 +20,30 @@
 static __device__ __align__(256) uint8_t scratch[IHIP_STATIC_SCRATCH_BYTES];
 
 namespace ihip {
+
+// the one context per device whose multi-row calls may use the array: the
+// first to make one, until it is destroyed. Another context's streams are not
+// ordered with its stream, so its calls would race on the array unseen.
+static std::mutex owners_mu;
+static std::map<int, const ihip_ctx*> owners;
+
+static bool claim(const ihip_ctx* c)
+{
+  std::lock_guard<std::mutex> g(owners_mu);
+  auto it = owners.find(c->device);
+  if (it == owners.end()) {
+    owners[c->device] = c;
+    return true;
+  }
+  return it->second == c;
+}
+
+void static_scratch_release(const ihip_ctx* c)
+{
+  std::lock_guard<std::mutex> g(owners_mu);
+  auto it = owners.find(c->device);
+  if (it != owners.end() && it->second == c) owners.erase(it);
+}
 
 int static_scratch_init(ihip_ctx* c)
 {
@@ -56,6 +83,10 @@ extern "C" int ihip_enqueue_linear_at_static(ihip_ctx* c, uint64_t x, int64_t ro
                                     " rows of " + std::to_string(in) + " need more than the " +
                                     std::to_string(IHIP_STATIC_SCRATCH_BYTES) +
                                     " bytes of static scratch");
+    if (!claim(c))
+      return fail(IHIP_E_ARG, "ihip_enqueue_linear_at_static: the static scratch of device " +
+                                  std::to_string(c->device) +
+                                  " belongs to another context (calls of two contexts would race)");
     int rc = enqueue_quantize(c, x, rows, in, kind, c->static_scratch);
     if (rc) return rc;
     k.xq = c->static_scratch;

@@ -594,11 +594,17 @@ __device__ __forceinline__ int xcd_head(unsigned x, int heads)
 }
 
 // the keys of one (head, row) cut into `splits` ranges of at most ATT_CHUNK
-// keys (flash-decoding): each block scores its range - every score the CPU's
-// sequential double dot product (CausalRows, backend.cpu.pas:1305-1354) -
-// then sums exp(score - range max) and the weighted values in double, and
-// writes them with the range's maximum and sum to part; attention_merge adds
-// the ranges (and the sink) as the CPU adds one softmax. Every load of a
+// keys (flash-decoding): each block scores its range in double, then sums
+// exp(score - range max) and the weighted values in double, and writes them
+// with the range's maximum and sum to part; attention_merge adds the ranges
+// (and the sink) as the CPU adds one softmax. Not the CPU's exact bits
+// (CausalRows, backend.cpu.pas:1305-1354): f16 keys of heads that are a
+// multiple of 16 are scored in another order of the double sum (two halves,
+// four chains each), and every value is added by a fused multiply-add of the
+// double weight p and the value (p * v is not exact in double, so one rounding
+// where the CPU has two). Both differ from the CPU in the last bits of a
+// double, far below the f32 rounding of the output (within 2 f32 ulp of the
+// oracle in the tests). Every load of a
 // range is issued before its first use: one thread per key reads the whole
 // key row at once, and each lane of the value pass holds a dimension pair of
 // all its keys, so a block waits for memory once per pass.

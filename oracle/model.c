@@ -305,8 +305,9 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       orc_fast_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, kvh, attn,
                          L->window, (const float*)L->sinks.data, m->threads);
     else
-      orc_causal_attention(q, n, d->heads, hd, m->keys[l], m->values[l], past, kvh,
-                           attn, L->window, (const float*)L->sinks.data, d->attention_scale);
+      orc_causal_attention_mt(q, n, d->heads, hd, m->keys[l], m->values[l], past, kvh,
+                              attn, L->window, (const float*)L->sinks.data, d->attention_scale,
+                              m->threads);
     if (L->output_gate) orc_gate_sigmoid(attn, gq, n * qw);
     err |= lin(m, attn, n, qw, L->o, 0, h, (const float*)L->o_bias.data, tmp);
     /* Gemma: the attention output normed before the residual */

@@ -70,50 +70,75 @@ void orc_rope(float* x, int64_t rows, int64_t heads, int64_t hd, const float* cs
 }
 
 /* backend.cpu.pas:1305-1354: the reference (double) rows of CausalRows */
+/* One head's rows; every (head, row) is computed on its own, so splitting the
+ * heads over threads changes no bit of the result. */
+static void causal_head(const float* q, int64_t rows, int64_t heads, int64_t d,
+                        const float* keys, const float* values, int64_t past, int64_t kvh,
+                        float* y, int64_t window, const float* sinks, double scale,
+                        int64_t h, double* sc, double* sums)
+{
+  int64_t kvw = kvh * d, qw = heads * d;
+  int64_t g = h / (heads / kvh);
+  for (int64_t r = 0; r < rows; r++) {
+    int64_t total = past + r + 1, first = 0;
+    if (window > 0 && total > window) first = total - window;
+    const float* qr = q + r * qw + h * d;
+    double m = 0;
+    for (int64_t j = first; j < total; j++) {
+      const float* k = keys + j * kvw + g * d;
+      double acc = 0;
+      for (int64_t t = 0; t < d; t++) acc = acc + (double)qr[t] * (double)k[t];
+      acc = acc * scale;
+      sc[j] = acc;
+      if (j == first || acc > m) m = acc;
+    }
+    if (sinks && sinks[h] > m) m = sinks[h];
+    double sum = 0;
+    for (int64_t j = first; j < total; j++) {
+      sc[j] = exp(sc[j] - m);
+      sum = sum + sc[j];
+    }
+    if (sinks) sum = sum + exp((double)sinks[h] - m);
+    for (int64_t t = 0; t < d; t++) sums[t] = 0;
+    for (int64_t j = first; j < total; j++) {
+      const float* v = values + j * kvw + g * d;
+      double a = sc[j];
+      for (int64_t t = 0; t < d; t++) sums[t] = sums[t] + a * (double)v[t];
+    }
+    sum = 1.0 / sum;
+    float* o = y + r * qw + h * d;
+    for (int64_t t = 0; t < d; t++) o[t] = (float)(sums[t] * sum);
+  }
+}
+
+void orc_causal_attention_mt(const float* q, int64_t rows, int64_t heads, int64_t d,
+                             const float* keys, const float* values, int64_t past,
+                             int64_t kvh, float* y, int64_t window, const float* sinks,
+                             double scale, int threads)
+{
+  int64_t total_max = past + rows;
+  if (!(scale > 0)) scale = 1.0 / sqrt((double)d);
+  if (threads < 1) threads = 1;
+#pragma omp parallel num_threads(threads)
+  {
+    double* sc = (double*)malloc(total_max * sizeof(double));
+    double* sums = (double*)malloc(d * sizeof(double));
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t h = 0; h < heads; h++)
+      causal_head(q, rows, heads, d, keys, values, past, kvh, y, window, sinks, scale, h, sc,
+                  sums);
+    free(sc);
+    free(sums);
+  }
+}
+
 void orc_causal_attention(const float* q, int64_t rows, int64_t heads, int64_t d,
                           const float* keys, const float* values, int64_t past,
                           int64_t kvh, float* y, int64_t window, const float* sinks,
                           double scale)
 {
-  int64_t kvw = kvh * d, qw = heads * d, total_max = past + rows;
-  if (!(scale > 0)) scale = 1.0 / sqrt((double)d);
-  double* sc = (double*)malloc(total_max * sizeof(double));
-  double* sums = (double*)malloc(d * sizeof(double));
-  for (int64_t h = 0; h < heads; h++) {
-    int64_t g = h / (heads / kvh);
-    for (int64_t r = 0; r < rows; r++) {
-      int64_t total = past + r + 1, first = 0;
-      if (window > 0 && total > window) first = total - window;
-      const float* qr = q + r * qw + h * d;
-      double m = 0;
-      for (int64_t j = first; j < total; j++) {
-        const float* k = keys + j * kvw + g * d;
-        double acc = 0;
-        for (int64_t t = 0; t < d; t++) acc = acc + (double)qr[t] * (double)k[t];
-        acc = acc * scale;
-        sc[j] = acc;
-        if (j == first || acc > m) m = acc;
-      }
-      if (sinks && sinks[h] > m) m = sinks[h];
-      double sum = 0;
-      for (int64_t j = first; j < total; j++) {
-        sc[j] = exp(sc[j] - m);
-        sum = sum + sc[j];
-      }
-      if (sinks) sum = sum + exp((double)sinks[h] - m);
-      for (int64_t t = 0; t < d; t++) sums[t] = 0;
-      for (int64_t j = first; j < total; j++) {
-        const float* v = values + j * kvw + g * d;
-        double a = sc[j];
-        for (int64_t t = 0; t < d; t++) sums[t] = sums[t] + a * (double)v[t];
-      }
-      sum = 1.0 / sum;
-      float* o = y + r * qw + h * d;
-      for (int64_t t = 0; t < d; t++) o[t] = (float)(sums[t] * sum);
-    }
-  }
-  free(sc);
-  free(sums);
+  orc_causal_attention_mt(q, rows, heads, d, keys, values, past, kvh, y, window, sinks, scale,
+                          1);
 }
 
 /* decoder.pas:2901-2949 TDecoderModel.Route */

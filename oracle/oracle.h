@@ -89,6 +89,11 @@ void orc_causal_attention(const float* q, int64_t rows, int64_t heads,
                           int64_t head_dim, const float* keys, const float* values,
                           int64_t past, int64_t kv_heads, float* y, int64_t window,
                           const float* sinks, double scale);
+/* the same, the heads split over `threads` OpenMP threads (bit-identical) */
+void orc_causal_attention_mt(const float* q, int64_t rows, int64_t heads, int64_t d,
+                             const float* keys, const float* values, int64_t past,
+                             int64_t kvh, float* y, int64_t window, const float* sinks,
+                             double scale, int threads);
 /* decoder.pas:2901-2949 TDecoderModel.Route (no expert scale, no tape) */
 void orc_route(const float* logits, int64_t experts, int64_t k, int norm_topk,
                int32_t* chosen, float* weights);

@@ -90,6 +90,41 @@ def test_native_decode_sampled_and_draw_ids(ctx, spec):
     c.close(); dev.close()
 
 
+def test_native_decode_two_threads_keep_their_settings(ctx, spec):
+    """Two requests with different sampling settings on two contexts of one
+    model, from two threads at once: each draws its own settings' tokens
+    (the sampler is set up and used under one hold of the device lock)."""
+    import threading
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, max_tokens=128)
+    prompt = np.random.default_rng(5).integers(0, spec.vocab, 10).astype(np.int32)
+    kws = [dict(temperature=0.8, top_k=40, top_p=0.95, seed=11),
+           dict(temperature=1.3, top_k=8, min_p=0.01, seed=5), None]
+    refs = [oracle_tokens(spec, prompt, 12, kw) for kw in kws]
+    ctxs = [dev.new_context() for _ in kws]
+    got = [[] for _ in kws]
+    errors = []
+
+    def run(i):
+        try:
+            for _ in range(4):
+                toks, _, _ = ctxs[i].native_decode(prompt, 12, kws[i])
+                got[i].append(list(toks))
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(len(kws))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    for c in ctxs:
+        c.close()
+    dev.close()
+    assert not errors, errors
+    for i, ref in enumerate(refs):
+        assert all(g == ref for g in got[i]), (i, got[i], ref)
+
+
 def test_native_decode_limits(ctx, spec):
     dev = H.Model(ctx, spec, mode=H.MODE_Q8, max_tokens=128)
     prompt = np.random.default_rng(3).integers(0, spec.vocab, 10).astype(np.int32)

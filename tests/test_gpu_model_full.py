@@ -22,6 +22,7 @@ the MoE models, the smallest gap between the k-th and (k+1)-th router logit
 of any row routed in that step: a near tie in either would be reported, not
 hidden behind a pass."""
 import gc
+import json
 import os
 
 import numpy as np
@@ -33,7 +34,8 @@ from infer_hip import models
 
 pytestmark = pytest.mark.gpu
 
-THREADS = min(16, os.cpu_count() or 1)
+THREADS = max(1, len(os.sched_getaffinity(0)))
+FIXTURES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "full_tokens")
 STEPS = 64
 
 
@@ -97,3 +99,45 @@ def test_full_shape_greedy_64(ctx, name, prompt_len):
     gc.collect()
     assert bad.size == 0, (f"first difference at step {bad[0]}", got[bad[0]], ref[bad[0]],
                            margins[bad[0]], gaps[bad[0]])
+
+
+WORKLOADS = ["qwen3-30b-a3b-q4_k_m", "gpt-oss-20b-mxfp4", "qwen3-0.6b-q4_k_m", "qwen3-0.6b-q8_0"]
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", WORKLOADS)
+def test_benchmark_workload_tokens(ctx, name):
+    """The decode the benchmark times, at its own prompt length (configs[3]:
+    1024 tokens, configs[4]: 2048 - two prompt chunks -, configs[2]: 512,
+    32), on the graph-replayed decode path: 64 greedy tokens equal
+    to the CPU oracle's, which tests/golden/make_full_tokens.py wrote from the
+    same seeded weights and prompt (the oracle takes most of an hour at these
+    lengths). The prompt's last-row logits of the oracle's 16 best ids agree
+    within 1e-5 relative. Every step's top-1/top-2 margin in the fixture is
+    far above the device's distance from the oracle (a few f32 ulps), so a
+    token difference is a real one, not a near tie."""
+    with open(os.path.join(FIXTURES, name + ".json")) as f:
+        fx = json.load(f)
+    margins = np.array(fx["margins"])
+    assert margins.min() > 1e-5, ("the fixture has a near tie at step", int(margins.argmin()))
+    spec = models.Spec(models.CONFIGS[name], seed=fx["seed"])
+    n = fx["prompt_len"]
+    prompt = np.random.default_rng(fx["prompt_seed"]).integers(0, spec.vocab, n).astype(np.int32)
+    print(f"\n[{name}] device: prompt {n}, greedy {fx['steps']}", flush=True)
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=fx["kv_f16"], max_tokens=n + fx["steps"] + 16)
+    lg = dev.forward(prompt)
+    top = fx["prompt_top16"]
+    got_top = lg[np.array(top["ids"])]
+    want_top = np.array(top["logits"], np.float32)
+    first = int(np.argmax(lg))
+    toks = np.concatenate([[first], dev.decode(first, fx["steps"] - 1)]).astype(np.int32)
+    dev.close()
+    del spec
+    gc.collect()
+    rel = float(np.abs(got_top - want_top).max() / np.abs(want_top).max())
+    print(f"[{name}] prompt top-16 logits rel {rel:.2e}; tokens {toks[:8].tolist()}", flush=True)
+    assert rel <= 1e-5, rel
+    ref = np.array(fx["tokens"], np.int32)
+    bad = np.nonzero(toks != ref)[0]
+    assert bad.size == 0, (f"first difference at step {bad[0]}", int(toks[bad[0]]), int(ref[bad[0]]),
+                           float(margins[bad[0]]))

@@ -121,7 +121,12 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     # 512 (Gemma 4's full layers: up to four pairs per lane)
     (44, 4, 1, 30, 3, 0, False, True), (44, 4, 2, 70, 2, 0, False, False),
     (320, 4, 2, 150, 2, 0, False, True), (512, 8, 1, 260, 3, 0, False, False),
-    (512, 4, 2, 40, 1, 0, True, True)])
+    (512, 4, 2, 40, 1, 0, True, True),
+    # heads of 256 (Qwen3.5, Gemma 4 sliding layers) with f16 keys: the paired
+    # key scoring and the fused value sums, one row and a few
+    (256, 8, 2, 300, 1, 0, True, True), (256, 16, 8, 1030, 1, 1024, True, False),
+    (256, 4, 1, 90, 3, 0, True, False), (512, 16, 2, 700, 1, 0, True, False),
+    (128, 32, 4, 1100, 1, 0, True, False)])
 def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     rng = np.random.default_rng(past + rows)
     T = past + rows

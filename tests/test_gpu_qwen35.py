@@ -209,6 +209,54 @@ def test_qwen35_restore_points(ctx):
     m.close()
 
 
+def test_qwen35_checkpoint_token_in_decode(ctx):
+    """The CheckpointId token fed by a decode (graph) step: its own part, so
+    an aligned context keeps the state before it (TDecoderModel.ForwardRows,
+    decoder.pas:3221-3240), and that restore point gives the logits of a
+    fresh pass. Drawn later in a decode, after steps that fed other tokens
+    (parts a fresh pass would not make, CheckPart :1083-1101), it adds none,
+    and the state goes on as a fresh pass of the same ids."""
+    s = spec("text-q8_0")
+    m = H.Model(ctx, s, max_tokens=96)
+    P = np.array([3, 11, 12, 13], np.int32)
+    T = 7
+    c = m.new_context()
+    c.set_checkpoints(T, 4)
+    c.forward(P)
+    d = c.decode(T, 3)  # feeds T, d[0], d[1]
+    assert c.checkpoints() == [len(P)]
+    c.truncate(len(P))
+    tail = np.array([T, 21, 22], np.int32)
+    got = c.forward(tail)
+    want = fresh_logits(m, np.concatenate([P, tail]))
+    assert rel(got, want) < 1e-6
+    assert rel(want, O.Model(s, 96).forward(np.concatenate([P, tail]))) < 1e-5
+    c.close()
+    # a token drawn mid-decode as the checkpoint id
+    probe = m.new_context()
+    x = int(np.argmax(probe.forward(P)))
+    g = probe.decode(x, 8).tolist()
+    probe.close()
+    fed = [x] + g
+    j = next((i for i in range(2, len(fed)) if fed[i] not in fed[:i] and fed[i] not in P), None)
+    if j is None:
+        pytest.skip(f"the greedy tokens {fed} hold no new id after two steps")
+    T2 = fed[j]
+    c2 = m.new_context()
+    c2.set_checkpoints(T2, 4)
+    c2.forward(P)
+    out = c2.decode(x, j + 2)  # feeds fed[0..j+1]: T2 at step j
+    assert out.tolist() == g[:j + 2]
+    assert c2.checkpoints() == []
+    more = np.array([T2, 5], np.int32)
+    got = c2.forward(more)
+    assert c2.checkpoints() == []
+    want = fresh_logits(m, np.concatenate([P, fed[:j + 2], more]).astype(np.int32))
+    assert rel(got, want) < 1e-6
+    c2.close()
+    m.close()
+
+
 def fresh_logits(m, ids):
     f = m.new_context()
     out = f.forward(ids)

@@ -3,7 +3,8 @@ quantized activations in a fixed device array) against
 ihip_enqueue_linear_at on the same inputs, through the C-ABI: bit-equal
 outputs on two calls in a row, the second with fewer rows (the array keeps
 the first call's bytes), on both sides of the GEMM threshold, and the
-refusal of a call that would not fit."""
+refusal of a call that would not fit, and of a multi-row call of a second
+context on the same GPU while the first holds the array."""
 import ctypes as C
 
 import numpy as np
@@ -14,7 +15,9 @@ import infer_hip as H
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
+# a context per test: the first context of a device to make a multi-row call
+# holds the array until it is destroyed
+@pytest.fixture()
 def ctx():
     c = H.Context(0)
     yield c
@@ -72,3 +75,38 @@ def test_static_refuses_beyond_its_size(ctx):
     H.check(H.lib().ihip_synchronize(ctx.h), "sync")
     xb.free()
     yb.free()
+
+
+def test_static_refuses_a_second_context():
+    """The array belongs to the first context of a device that makes a
+    multi-row call, until it is destroyed: a second context's multi-row call
+    is refused (their streams are not ordered), its one-row call is not."""
+    nin, out, dtype = 1024, 128, H.Q8_0
+    w = H.synth_normal(dtype, out, nin, 9, 0.05)
+    x = np.random.default_rng(4).standard_normal((16, nin)).astype(np.float32)
+    a, b = H.Context(0), H.Context(0)
+    try:
+        wa, wb = C.c_uint64(), C.c_uint64()
+        H.check(H.lib().ihip_weight(a.h, H._p(w), dtype, out, nin, 1, C.byref(wa)), "weight")
+        H.check(H.lib().ihip_weight(b.h, H._p(w), dtype, out, nin, 1, C.byref(wb)), "weight")
+        static = H.lib().ihip_enqueue_linear_at_static
+        ya = run(a, static, x, wa.value, dtype, out, 0, H.MODE_Q8)
+        xb = H.Buffer(b, x.nbytes)
+        yb = H.Buffer(b, 16 * out * 4)
+        rc = static(b.h, xb.ptr, 16, nin, dtype, wb.value, out, yb.ptr, 0, H.MODE_Q8)
+        assert rc == H.IHIP_E_ARG and b"another context" in H.lib().ihip_last_error()
+        xb.free()
+        yb.free()
+        y1 = run(b, static, x[:1], wb.value, dtype, out, 0, H.MODE_Q8)
+        assert np.array_equal(y1.view(np.uint32), ya[:1].view(np.uint32))
+        # the holder destroyed: the other context may take the array
+        H.lib().ihip_forget_weights(a.h, H._p(w), C.c_void_p(w.ctypes.data + w.nbytes))
+        a.close()
+        a = None
+        yb2 = run(b, static, x, wb.value, dtype, out, 0, H.MODE_Q8)
+        assert np.array_equal(yb2.view(np.uint32), ya.view(np.uint32))
+        H.lib().ihip_forget_weights(b.h, H._p(w), C.c_void_p(w.ctypes.data + w.nbytes))
+    finally:
+        if a is not None:
+            a.close()
+        b.close()
