@@ -440,14 +440,17 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        # the box's CPU share, and the reference's default pool size of it
+        # every core this process may run on (its affinity mask: the box's
+        # CPU share), and the reference's default pool size of it
         # ((cores * 2 + 2) / 3, backend.cpu.pas:1989)
-        cores = min(16, os.cpu_count() or 1)
+        cores = max(1, len(os.sched_getaffinity(0)))
+        nproc = os.cpu_count() or cores
         ref_threads = max(1, (cores * 2 + 2) // 3)
         t = time.time()
         cpu_prefill_s, rates = cpu_baseline(spec, prompt, 8, [cores, ref_threads])
         if rates:
             cpu = {"value": round(rates[cores], 3), "unit": "tok/s", "cores": cores, "kind": "port",
+                   "affinity_cores": cores, "host_cpus": nproc,
                    "variant": "avx2",
                    "value_ref_threads": round(rates[ref_threads], 3), "ref_threads": ref_threads,
                    "prefill_tok_s": round(len(prompt) / cpu_prefill_s, 1),
@@ -456,7 +459,9 @@ def main():
                              f"at {ref_threads} threads; TInferCpuFastBackend's default mode "
                              f"restated in C with AVX2/FMA (oracle/fast.c: tiles of 16 outputs "
                              f"over an OpenMP pool, exact K-quant sums, Q8DotF32x4x2 float "
-                             f"lanes, the fast attention) on {cpu_name()}"}
+                             f"lanes, the fast attention) on {cpu_name()}; {cores} threads = "
+                             f"every core of this process's affinity mask ({nproc} CPUs on "
+                             f"the host)"}
             log(f"cpu baseline {rates[cores]:.3f} tok/s ({cores} threads), "
                 f"{rates[ref_threads]:.3f} ({ref_threads} threads), prefill "
                 f"{cpu_prefill_s:.1f} s, in {time.time() - t:.1f}s")

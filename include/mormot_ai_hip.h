@@ -438,6 +438,16 @@ int ihip_model_sampling(ihip_model* m, const ihip_sampling* s);
 /* decode steps as one replayed HIP graph (on, the default) or as direct
  * launches (TQwen3Cuda.UseGraphs, model.qwen3.cuda.pas:253-262) */
 int ihip_model_use_graphs(ihip_model* m, int on);
+/* CheckRoute (TQwen3Cuda.CheckRoute, model.qwen3.cuda.pas:288-300), a
+ * diagnosis: with on, after every route the device forms for one row (the
+ * decode steps' experts) the step waits, reads the router logits and the
+ * choice back and compares them with TDecoderModel.Route on the same logits
+ * on the host; the decode runs without graphs meanwhile */
+int ihip_model_check_route(ihip_model* m, int on);
+/* CheckRoute's counts (RouteChecks, RouteMismatches, RouteMaxDiff): rows
+ * compared, rows whose ids differ, the largest weight difference of the rows
+ * with the same ids (1e30 for a NaN or an infinity) */
+int ihip_model_route_stats(ihip_model* m, int64_t* checks, int64_t* mismatches, double* max_diff);
 /* timings of the last greedy call: prefill and decode milliseconds */
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
 

@@ -546,7 +546,7 @@ struct DescBuilder {
   }
 
   // the settings common to the three architectures
-  void common(ihip_model_desc& d, bool qwen)
+  void common(ihip_model_desc& d, bool qwen, bool qwen2 = false)
   {
     const Tensor* emb = g->tensor("token_embd.weight");
     if (!emb) refuse("no tensor token_embd.weight in " + g->name);
@@ -557,7 +557,14 @@ struct DescBuilder {
     d.layers = count("block_count");
     d.heads = count("attention.head_count");
     d.kv_heads = count("attention.head_count_kv");
-    d.head_dim = count("attention.key_length");
+    // qwen2 files name no key length: hidden / heads (HeadDimOf)
+    if (!qwen2 || has("attention.key_length")) {
+      d.head_dim = count("attention.key_length");
+    } else {
+      if (d.heads <= 0 || d.hidden <= 0 || d.hidden % d.heads)
+        refuse(fmt("a hidden size of %d for %d heads", d.hidden, d.heads));
+      d.head_dim = d.hidden / d.heads;
+    }
     if (has("rope.dimension_count") && count("rope.dimension_count") != d.head_dim)
       refuse(fmt("RoPE over %d of %d dimensions not supported", count("rope.dimension_count"), d.head_dim));
     if (has("attention.value_length") && count("attention.value_length") != d.head_dim)
@@ -569,13 +576,15 @@ struct DescBuilder {
     (void)qwen;
   }
 
-  void qwen3(ihip_model_desc& d, bool moe)
+  // qwen3, qwen3moe and qwen2 (Qwen2 / Qwen2.5: a bias on Q, K and V in
+  // place of the head norms, TQwen2Model, model.qwen3.pas:128-139, :635-655)
+  void qwen3(ihip_model_desc& d, bool moe, bool qwen2 = false)
   {
     // a scaled RoPE or a sliding window would change the arithmetic: refused
     if (has("rope.scaling.type") && g->str(arch + ".rope.scaling.type") != "none")
       refuse("rope scaling \"" + g->str(arch + ".rope.scaling.type") + "\" not supported");
     if (has("attention.sliding_window")) refuse("sliding window attention not supported");
-    common(d, true);
+    common(d, true, qwen2);
     d.swiglu_alpha = 1.0f;
     d.swiglu_limit = 0.0f;
     if (moe) {
@@ -598,8 +607,14 @@ struct DescBuilder {
       L.k = matrix(b + "attn_k.weight", kvw, h);
       L.v = matrix(b + "attn_v.weight", kvw, h);
       L.o = matrix(b + "attn_output.weight", h, qw);
-      L.q_norm = weight(b + "attn_q_norm.weight", {hd});
-      L.k_norm = weight(b + "attn_k_norm.weight", {hd});
+      if (qwen2) {
+        L.q_bias = weight(b + "attn_q.bias", {qw});
+        L.k_bias = weight(b + "attn_k.bias", {kvw});
+        L.v_bias = weight(b + "attn_v.bias", {kvw});
+      } else {
+        L.q_norm = weight(b + "attn_q_norm.weight", {hd});
+        L.k_norm = weight(b + "attn_k_norm.weight", {hd});
+      }
       L.input_norm = weight(b + "attn_norm.weight", {h});
       L.post_norm = weight(b + "ffn_norm.weight", {h});
       // qwen3moe: a layer with a router has experts, the others are dense
@@ -971,6 +986,8 @@ struct DescBuilder {
       qwen3(d, false);
     } else if (arch == "qwen3moe") {
       qwen3(d, true);
+    } else if (arch == "qwen2") {
+      qwen3(d, false, true);
     } else if (arch == "gpt-oss") {
       gptoss(d);
     } else if (arch == "qwen35") {
@@ -978,7 +995,7 @@ struct DescBuilder {
     } else if (arch == "gemma4") {
       gemma4(d);
     } else {
-      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, gpt-oss, qwen35, gemma4)");
+      refuse("architecture \"" + arch + "\" is not supported (qwen3, qwen3moe, qwen2, gpt-oss, qwen35, gemma4)");
     }
     // an unknown tensor means a model this path does not understand
     const int64_t expect = trunk >= 0 ? trunk : (int64_t)g->tensors.size();

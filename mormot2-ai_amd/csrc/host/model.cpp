@@ -129,6 +129,11 @@ struct ihip_model {
   ihip_sampler* sampler = nullptr;  // null: the argmax
   int sampler_epoch = 0;            // bumped by ihip_model_sampling (graphs captured again)
   bool use_graphs = true;  // TQwen3Cuda.UseGraphs (model.qwen3.cuda.pas:253-262)
+  // CheckRoute (model.qwen3.cuda.pas:288-300): after every one-row route on
+  // the device the step waits and compares the choice with the host's Route
+  bool check_route = false;
+  int64_t route_checks = 0, route_mismatches = 0;
+  double route_max_diff = 0;
   int64_t chunk_rows = ihip::CHUNK;  // prompt rows per chunk (ihip_model_chunk), at most CHUNK
   int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
   ihip_mctx* def = nullptr;  // the context of the ihip_model_* calls
@@ -444,6 +449,75 @@ static bool one_row_fused(const ihip_model* m)
   return true;
 }
 
+// CheckDeviceRoute (model.qwen3.cuda.pas:1207-1256): the router logits, the
+// picks and the weights the device wrote for one row, read back after the
+// route, against TDecoderModel.Route (decoder.pas:2901-2949) on the same
+// logits on the host: softmax in double, the k highest (the lower id on a
+// tie), NormTopK, the expert scales, then the picks sorted by id as the
+// device writes them. Counts rows, rows whose ids differ and the largest
+// weight difference of the others (1e30 for a NaN or infinity).
+static int check_device_route(ihip_mctx* s, int l)
+{
+  ihip_model* m = s->m;
+  const ihip_model_desc& d = m->d;
+  const int64_t E = d.experts, K = d.experts_used;
+  ihip_ctx* c = m->c;
+  std::vector<float> lg((size_t)E), kw((size_t)K), scale;
+  std::vector<int32_t> kid((size_t)K);
+  IHIP_CHECK(hipMemcpyDtoHAsync(lg.data(), (hipDeviceptr_t)s->route, E * 4, c->stream));
+  IHIP_CHECK(hipMemcpyDtoHAsync(kid.data(), (hipDeviceptr_t)s->ids_dev, K * 4, c->stream));
+  IHIP_CHECK(hipMemcpyDtoHAsync(kw.data(), (hipDeviceptr_t)s->rw, K * 4, c->stream));
+  if (m->L[l].expert_scale) {
+    scale.resize((size_t)E);
+    IHIP_CHECK(hipMemcpyDtoHAsync(scale.data(), (hipDeviceptr_t)m->L[l].expert_scale, E * 4, c->stream));
+  }
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  double mx = lg[0], sum = 0, picked = 0;
+  for (int64_t i = 1; i < E; i++)
+    if (lg[i] > mx) mx = lg[i];
+  for (int64_t i = 0; i < E; i++) sum = sum + std::exp((double)lg[i] - mx);
+  std::vector<int32_t> ch((size_t)K);
+  std::vector<float> cw((size_t)K);
+  for (int64_t j = 0; j < K; j++) {
+    int64_t best = -1;
+    for (int64_t i = 0; i < E; i++) {
+      bool taken = false;
+      for (int64_t t = 0; t < j; t++) taken = taken || ch[t] == i;
+      if (!taken && (best < 0 || lg[i] > lg[best])) best = i;
+    }
+    ch[j] = (int32_t)best;
+    cw[j] = (float)(std::exp((double)lg[best] - mx) / sum);
+    picked = picked + cw[j];
+  }
+  if (d.norm_topk)
+    for (int64_t j = 0; j < K; j++) cw[j] = (float)(cw[j] / picked);
+  if (!scale.empty())
+    for (int64_t j = 0; j < K; j++) cw[j] = cw[j] * scale[ch[j]];
+  for (int64_t j = 1; j < K; j++) {  // by id, as the device writes them
+    const int32_t id = ch[j];
+    const float v = cw[j];
+    int64_t t = j;
+    for (; t > 0 && ch[t - 1] > id; t--) {
+      ch[t] = ch[t - 1];
+      cw[t] = cw[t - 1];
+    }
+    ch[t] = id;
+    cw[t] = v;
+  }
+  m->route_checks++;
+  for (int64_t j = 0; j < K; j++)
+    if (ch[j] != kid[j]) {
+      m->route_mismatches++;
+      return 0;
+    }
+  for (int64_t j = 0; j < K; j++) {
+    double dd = std::fabs((double)cw[j] - (double)kw[j]);
+    if (!(dd <= 1)) dd = 1e30;
+    if (dd > m->route_max_diff) m->route_max_diff = dd;
+  }
+  return 0;
+}
+
 // one row through the layers, x holding its embedding: every RMSNorm is
 // computed by the GEMVs that read it (their staging), the residual adds by
 // the GEMVs that produce them (o projection, FFN down, the experts'
@@ -593,6 +667,7 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
       k.rl = s->route; k.rw = s->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
     }
     if ((rc = enqueue_linear(m->c, k))) return rc;
+    if (m->check_route && !m->c->capturing && (rc = check_device_route(s, l))) return rc;
     LinearCall dn;
     dn.x = s->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
     dn.y = s->x; dn.res = s->x; dn.cw = s->rw; dn.mode = m->mode; dn.ids = s->ids_dev;
@@ -866,6 +941,7 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
           k.rscale = L.expert_scale;
         }
         if ((rc = enqueue_linear(m->c, k))) return rc;
+        if (n == 1 && m->check_route && !m->c->capturing && (rc = check_device_route(s, l))) return rc;
         LinearCall dn;
         dn.x = s->gate; dn.rows = K; dn.in = FI; dn.dtype = L.edd; dn.w = L.ed; dn.out = H;
         dn.y = s->eout; dn.mode = m->mode; dn.ids = s->ids_dev; dn.stride = L.ed_stride;
@@ -1366,7 +1442,8 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   if (rc) return rc;
   // a graph holds this context's cache and ranges: captured again when the
   // cache grew or the sampler changed since
-  if (m->use_graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
+  const bool graphs = m->use_graphs && !m->check_route;
+  if (graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
                         s->graph_sampler != m->sampler_epoch || s->graph_draw != s->draw_ids) &&
       (rc = decode_graph(s)))
     return rc;
@@ -1385,7 +1462,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, &tok, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->pos, &pos, 4, c->stream));
     IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
-    if (m->use_graphs) {
+    if (graphs) {
       IHIP_CHECK(hipGraphLaunch(s->exec, c->stream));
     } else if ((rc = decode_body(s))) {
       return rc;
@@ -2207,6 +2284,24 @@ int ihip_model_use_graphs(ihip_model* m, int on)
 {
   if (!m) return fail(IHIP_E_ARG, "ihip_model_use_graphs");
   m->use_graphs = on != 0;
+  return 0;
+}
+
+int ihip_model_check_route(ihip_model* m, int on)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_check_route");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  m->check_route = on != 0;
+  return 0;
+}
+
+int ihip_model_route_stats(ihip_model* m, int64_t* checks, int64_t* mismatches, double* max_diff)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_route_stats");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  if (checks) *checks = m->route_checks;
+  if (mismatches) *mismatches = m->route_mismatches;
+  if (max_diff) *max_diff = m->route_max_diff;
   return 0;
 }
 

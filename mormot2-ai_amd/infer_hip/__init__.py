@@ -128,6 +128,8 @@ def lib():
             "ihip_model_greedy": (i32, [vp, vp, i64, i64, vp]),
             "ihip_model_decode": (i32, [vp, C.c_int32, i64, vp]),
             "ihip_model_use_graphs": (i32, [vp, i32]),
+            "ihip_model_check_route": (i32, [vp, i32]),
+            "ihip_model_route_stats": (i32, [vp, vp, vp, vp]),
             "ihip_model_chunk": (i32, [vp, i64]),
             "ihip_enqueue_stream_read": (i32, [vp, u64, u64, u64]),
             "ihip_model_rotary": (i32, [vp, i64, i64, vp]),
@@ -446,6 +448,17 @@ class Model:
         out = np.empty(steps, np.int32)
         check(lib().ihip_model_decode(self.h, int(first), steps, _p(out)), "decode")
         return out
+
+    def check_route(self, on):
+        """CheckRoute: compare every one-row device route with the host's
+        TDecoderModel.Route (decode without graphs meanwhile)."""
+        check(lib().ihip_model_check_route(self.h, int(on)), "check_route")
+
+    def route_stats(self):
+        """(RouteChecks, RouteMismatches, RouteMaxDiff)."""
+        a, b, d = C.c_int64(), C.c_int64(), C.c_double()
+        check(lib().ihip_model_route_stats(self.h, C.byref(a), C.byref(b), C.byref(d)), "route_stats")
+        return a.value, b.value, d.value
 
     def timing(self):
         a, b = C.c_double(), C.c_double()

@@ -14,10 +14,13 @@ converter and ggml's reference quantizers, and by transformers in float32):
   tests of the DeltaNet (tests/test.infer.cuda.pas);
 - tiny-gemma4/gguf/{bf16,q8_0,dense-bf16,dense-q8_0,rope44,bad-*}.gguf: the
   gemma4 files of TTestInferGemma4 (tests/test.infer.gemma4.pas);
+- tiny-qwen2/gguf/{q8_0,bad-nobias}.gguf: the qwen2 (Qwen2.5) files of
+  TTestInferQwen3's Qwen2 cases (the decoder with q/k/v biases and no head
+  norms);
 - the case ids, logits, greedy tokens and margins of tiny-qwen3,
   tiny-qwen3/untied, tiny-qwen3moe, tiny-gpt-oss/mxfp4, tiny-qwen35 and
   tiny-qwen35/text (with the one-token-at-a-time logits and the first layer's
-  mixer output of the last two), tiny-gemma4 and tiny-gemma4/dense
+  mixer output of the last two), tiny-gemma4, tiny-gemma4/dense and tiny-qwen2
   (tensors.bin, described by manifest.json),
   gathered into expected.npz.
 
@@ -75,7 +78,7 @@ def main(ref):
     copy_dir(os.path.join(root, "tiny-gguf"), ["model.gguf"], OUT, {})
     sets = [("tiny-qwen3-gguf", "qwen3"), (os.path.join("tiny-qwen3moe", "gguf"), "qwen3moe"),
             (os.path.join("tiny-gpt-oss", "gguf"), "gpt-oss"), (os.path.join("tiny-qwen35", "gguf"), "qwen35"),
-            (os.path.join("tiny-gemma4", "gguf"), "gemma4")]
+            (os.path.join("tiny-gemma4", "gguf"), "gemma4"), (os.path.join("tiny-qwen2", "gguf"), "qwen2")]
     for folder, tag in sets:
         src = os.path.join(root, folder)
         files = json.load(open(os.path.join(src, "manifest.json"))).get("files", {})
@@ -89,7 +92,8 @@ def main(ref):
     for folder, tag in [("tiny-qwen3", "qwen3"), (os.path.join("tiny-qwen3", "untied"), "qwen3-untied"),
                         ("tiny-qwen3moe", "qwen3moe"), (os.path.join("tiny-gpt-oss", "mxfp4"), "gpt-oss"),
                         ("tiny-qwen35", "qwen35"), (os.path.join("tiny-qwen35", "text"), "qwen35-text"),
-                        ("tiny-gemma4", "gemma4"), (os.path.join("tiny-gemma4", "dense"), "gemma4-dense")]:
+                        ("tiny-gemma4", "gemma4"), (os.path.join("tiny-gemma4", "dense"), "gemma4-dense"),
+                        ("tiny-qwen2", "qwen2")]:
         for k, v in cases(os.path.join(root, folder)).items():
             expected[f"{tag}/{k}"] = v
     np.savez_compressed(os.path.join(OUT, "expected.npz"), **expected)

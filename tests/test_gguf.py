@@ -196,6 +196,21 @@ def test_qwen3_settings_of_the_file():
     assert su.struct.head.data and su.struct.head.dtype == H.F16
 
 
+def test_qwen2_settings_of_the_file():
+    # tiny-qwen2 as llama.cpp writes a qwen2 file (TTestInferQwen3.
+    # TinyQwen2MatchesReference, tests/test.infer.qwen3.pas:2532-2606): no
+    # attention.key_length, so head_dim = hidden / heads = 16; F32 biases on
+    # q, k and v, no head norm
+    s = H.GgufSpec(os.path.join(GG, "qwen2", "q8_0.gguf"))
+    d = s.struct
+    assert (d.vocab, d.hidden, d.layers, d.heads, d.kv_heads, d.head_dim, d.ffn) == \
+        (96, 64, 2, 4, 2, 16, 160)
+    assert d.head.data is None  # tied
+    for L in s.layers:
+        assert L.q_bias.data and L.k_bias.data and L.v_bias.data and not L.o_bias.data
+        assert not L.q_norm.data and not L.k_norm.data and L.q.dtype == H.Q8_0
+
+
 def test_qwen3moe_and_gptoss_settings():
     s = H.GgufSpec(os.path.join(GG, "qwen3moe", "q8_0.gguf"))
     d = s.struct
@@ -224,7 +239,7 @@ def test_qwen3moe_and_gptoss_settings():
     ("gpt-oss", "bad-arch", "architecture"), ("gpt-oss", "bad-rope", "rope scaling"),
     ("gpt-oss", "bad-yarn", "attention factor"), ("gpt-oss", "bad-tied", "tied embeddings"),
     ("gpt-oss", "bad-missing", "attn_sinks"), ("gpt-oss", "bad-extra", "understood"),
-    ("gpt-oss", "bad-scale", "beyond the range")])
+    ("gpt-oss", "bad-scale", "beyond the range"), ("qwen2", "bad-nobias", "attn_k.bias")])
 def test_model_refuses_damaged_files(arch, name, why):
     with pytest.raises(H.FormatError, match=why):
         H.GgufSpec(os.path.join(GG, "bad", arch, name + ".gguf"))
@@ -232,7 +247,7 @@ def test_model_refuses_damaged_files(arch, name, why):
 
 def test_reader_accepts_every_damaged_model_file():
     # the damage is in the model, not in the file format
-    for arch in ("qwen3", "qwen3moe", "gpt-oss"):
+    for arch in ("qwen3", "qwen3moe", "gpt-oss", "qwen2"):
         for n in os.listdir(os.path.join(GG, "bad", arch)):
             H.Gguf(os.path.join(GG, "bad", arch, n)).close()
 
@@ -253,7 +268,9 @@ def expected(tag):
     ("qwen3/q8_0.gguf", "qwen3", "q8", 0.999),
     ("qwen3/q8_0.gguf", "qwen3", "f32", 0.999),
     ("qwen3moe/q8_0.gguf", "qwen3moe", "q8", 0.999),
-    ("qwen3moe/q8_0.gguf", "qwen3moe", "f32", 0.999)])
+    ("qwen3moe/q8_0.gguf", "qwen3moe", "f32", 0.999),
+    ("qwen2/q8_0.gguf", "qwen2", "q8", 0.999),
+    ("qwen2/q8_0.gguf", "qwen2", "f32", 0.999)])
 def test_oracle_q8_0_file_vs_transformers(file, tag, mode, min_cos):
     # Q8_0 weights against the float32 logits of the BF16 checkpoint: within
     # the Q8_0 error (the reference's own bound, test.infer.qwen3.pas:1527)

@@ -160,3 +160,18 @@ def test_gemma4_real_widths(ctx):
     print("min margin", float(margins.min()), flush=True)
     assert np.array_equal(got, ref)
     dev.close()
+
+
+def test_gemma4_check_route(ctx):
+    # the experts' route formed inside the gate/up launch with Gemma 4's
+    # expert scales, against TDecoderModel.Route with the scales on the host
+    s = spec("q8_0")
+    c = cases("gemma4")[0]
+    dev = H.Model(ctx, s, mode=H.MODE_Q8, max_tokens=96)
+    dev.check_route(True)
+    dev.greedy(c["ids"], 8)
+    checks, mismatches, max_diff = dev.route_stats()
+    dev.close()
+    moe_layers = sum(1 for L in s.layers if L.moe)
+    assert checks == 8 * moe_layers and mismatches == 0 and max_diff <= 1e-6, \
+        (checks, mismatches, max_diff)

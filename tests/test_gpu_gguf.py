@@ -1,6 +1,7 @@
 """The device decoder over llama.cpp GGUF files (the model files of the
-reference's tests, tests/golden/gguf/): every file of qwen3, qwen3moe and
-gpt-oss against the CPU oracle on the same mapped bytes (tier 2: logits within
+reference's tests, tests/golden/gguf/): every file of qwen3, qwen3moe,
+qwen2 (Qwen2.5: q/k/v biases, no head norm; the reference's device test is
+tests/test.infer.cuda.pas:2240-2330) and gpt-oss against the CPU oracle on the same mapped bytes (tier 2: logits within
 1e-5 relative; tier 3: greedy token-identical), and against the float32 logits
 transformers wrote for the same weights, as the reference's device tests do
 (tests/test.infer.cuda.pas:1560-1640, :1950-2010)."""
@@ -43,7 +44,7 @@ def cos(a, b):
 FILES = [("qwen3/q8_0.gguf", "qwen3"), ("qwen3/q4_0.gguf", "qwen3"),
          ("qwen3/untied-f16.gguf", "qwen3-untied"), ("qwen3moe/q8_0.gguf", "qwen3moe"),
          ("qwen3moe/q4_0.gguf", "qwen3moe"), ("gpt-oss/bf16.gguf", "gpt-oss"),
-         ("gpt-oss/q8_0.gguf", "gpt-oss")]
+         ("gpt-oss/q8_0.gguf", "gpt-oss"), ("qwen2/q8_0.gguf", "qwen2")]
 
 
 @pytest.mark.parametrize("kv_f16", [False, True])
@@ -69,7 +70,8 @@ def test_gguf_device_matches_oracle(ctx, file, tag, kv_f16):
 
 
 @pytest.mark.parametrize("file,tag", [("qwen3/q8_0.gguf", "qwen3"),
-                                      ("qwen3moe/q8_0.gguf", "qwen3moe")])
+                                      ("qwen3moe/q8_0.gguf", "qwen3moe"),
+                                      ("qwen2/q8_0.gguf", "qwen2")])
 def test_gguf_device_q8_0_vs_transformers(ctx, file, tag):
     # the Q8_0 file against the float32 logits of the BF16 checkpoint: within
     # the Q8_0 error, as the reference's device test bounds it (cosine 0.999)

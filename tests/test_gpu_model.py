@@ -108,3 +108,26 @@ def test_tiny_greedy_long_context(ctx, name, over, chunk):
     assert np.array_equal(got, ref), (got, ref, margins)
     dev.close()
     cpu.close()
+
+
+@pytest.mark.parametrize("name,over", [TINY[2], TINY[3]])
+def test_check_route_counts(ctx, name, over):
+    """CheckRoute (model.qwen3.cuda.pas:288-300, :1207-1256): every decode
+    step's on-device route of every MoE layer is read back and compared with
+    TDecoderModel.Route on the host: the same ids, weights within 1e-6, the
+    tokens those of a decode without the check (graphs on)."""
+    spec = models.Spec(models.tiny(name, **over), seed=33)
+    prompt = np.random.default_rng(5).integers(0, spec.vocab, 12).astype(np.int32)
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, max_tokens=64)
+    want = dev.greedy(prompt, 10)
+    dev.close()
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, max_tokens=64)
+    dev.check_route(True)
+    got = dev.greedy(prompt, 10)
+    checks, mismatches, max_diff = dev.route_stats()
+    dev.close()
+    assert np.array_equal(got, want)
+    # the 10 decode steps after the prompt (Greedy feeds its last token too),
+    # every layer routed
+    assert checks == 10 * over["layers"], checks
+    assert mismatches == 0 and max_diff <= 1e-6, (mismatches, max_diff)
