@@ -448,6 +448,19 @@ int ihip_model_check_route(ihip_model* m, int on);
  * compared, rows whose ids differ, the largest weight difference of the rows
  * with the same ids (1e30 for a NaN or an infinity) */
 int ihip_model_route_stats(ihip_model* m, int64_t* checks, int64_t* mismatches, double* max_diff);
+/* TDecoderRouteTape in replay mode (decoder.pas:2955-3035; the reference's
+ * device tests hand the CPU's expert choice to the device this way,
+ * tests/test.infer.cuda.pas:2162-2200): ids / weights [rows][experts_used],
+ * the picks (by id) and weights of every routed row of another run, given in
+ * turn to the rows this model routes from now on (prompt rows and decode
+ * steps, without graphs) in place of its own choice, which is compared with
+ * them; rows 0: off. A row past the tape is refused. */
+int ihip_model_route_tape(ihip_model* m, const int32_t* ids, const float* weights, int64_t rows);
+/* the tape's counts: rows replayed, rows where the device's own choice
+ * differed, the largest router gap (k-th chosen minus the best left out, in
+ * the device's logits) of those rows, rows not yet replayed */
+int ihip_model_route_tape_stats(ihip_model* m, int64_t* routes, int64_t* differs, double* gap,
+                                int64_t* pending);
 /* timings of the last greedy call: prefill and decode milliseconds */
 int ihip_model_timing(ihip_model* m, double* prefill_ms, double* decode_ms);
 

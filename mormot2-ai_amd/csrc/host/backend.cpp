@@ -481,6 +481,22 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
               (int32_t)k.out, ksplit};
       return launch(c, "gemm_split_sum", dim3((unsigned)((n + 255) / 256)), dim3(256), &sa);
     }
+    if (k.dtype == DT_MXFP4 && q8 && c->gemm_f8 && !k.no_alloc && !c->capturing) {
+      // the e4m3 planes of the quantized rows, then the f8f6f4 GEMM on them
+      const int64_t G = k.in / 32;
+      const int64_t nx = k.items ? (k.x_per_slot ? (k.rows + k.x_per_slot - 1) / k.x_per_slot : 1) : k.rows;
+      int rc = scratch(c, c->scratch_planes, c->scratch_planes_bytes, (uint64_t)nx * 68 * G);
+      if (rc) return rc;
+      struct {
+        const uint8_t* xq;
+        uint8_t* planes;
+        int32_t rows, in;
+      } pa = {(const uint8_t*)xq, (uint8_t*)c->scratch_planes, (int32_t)nx, (int32_t)k.in};
+      if ((rc = launch(c, "f8_planes", dim3((unsigned)((G + 255) / 256), (unsigned)nx), dim3(256), &pa)))
+        return rc;
+      g.xq = (const uint8_t*)c->scratch_planes;
+      return launch(c, "gemm_mxfp4_f8", dim3(gx, gy), dim3(256), &g);
+    }
     return launch(c, gname, dim3(gx, gy), dim3(256), &g);
   }
   if (k.nw && (batch || k.in > 4096 || xq))

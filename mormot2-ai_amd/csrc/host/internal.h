@@ -80,6 +80,9 @@ struct ihip_ctx {
   int gemv_blocks_per_cu = 2;  // one-row GEMV launches: blocks per CU at least (IHIP_GEMV_BLOCKS_PER_CU)
   int gemv_hold = 1;  // one-row GEMV launches: at most this many rounds of resident blocks (IHIP_GEMV_HOLD)
   bool use_gemm8 = true;  // 2..79 quantized rows on the int8 matrix cores, gemm8 (IHIP_GEMM8=0: the VALU gemv_rows)
+  // MXFP4 prefill GEMMs on the scaled f8f6f4 matrix cores (IHIP_GEMM_F8=1)
+  // rather than the int8 ones
+  bool gemm_f8 = false;
   bool gemm_split = true;  // float-weight GEMMs of few tiles split over the sum (IHIP_GEMM_SPLIT=0: off)
   bool attn_mfma = true;  // prompt attention ranges on the f64 matrix cores (IHIP_ATTN_MFMA=0: VALU tiles of 8 rows)
   hipStream_t stream = nullptr;
@@ -97,6 +100,7 @@ struct ihip_ctx {
   uint64_t scratch_split = 0, scratch_split_bytes = 0;  // split sums of the float-weight GEMM
   uint64_t scratch_argmax = 0;  // [ARGMAX_PARTS] block results of argmax_part
   uint64_t scratch_attn = 0, scratch_attn_bytes = 0;
+  uint64_t scratch_planes = 0, scratch_planes_bytes = 0;  // e4m3 activation planes (gemm_mxfp4_f8)
   // the device address of static_scratch.hip's array on this device
   // (ihip_enqueue_linear_at_static), read once at ihip_create
   uint64_t static_scratch = 0;

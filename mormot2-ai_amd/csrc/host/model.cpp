@@ -134,6 +134,14 @@ struct ihip_model {
   bool check_route = false;
   int64_t route_checks = 0, route_mismatches = 0;
   double route_max_diff = 0;
+  // TDecoderRouteTape replayed (decoder.pas:2993-3035): the picks and
+  // weights of another run (the CPU's), given to every routed row in turn in
+  // place of the device's own; the device's own choice counted where it
+  // differs, with the largest router gap of such a row
+  std::vector<int32_t> tape_ids;
+  std::vector<float> tape_w;
+  int64_t tape_rows = 0, tape_pos = 0, tape_routes = 0, tape_differs = 0;
+  double tape_gap = 0;
   int64_t chunk_rows = ihip::CHUNK;  // prompt rows per chunk (ihip_model_chunk), at most CHUNK
   int item_rows = 8;  // slots per grouped-expert work item: 64 when the experts run on the GEMM
   ihip_mctx* def = nullptr;  // the context of the ihip_model_* calls
@@ -449,6 +457,55 @@ static bool one_row_fused(const ihip_model* m)
   return true;
 }
 
+// TDecoderRouteTape.Take (decoder.pas:2993-3035) for the n rows the device
+// just routed (their picks in ids_dev, by id, and weights in rw): each row's
+// own choice compared with the tape's, then the tape's picks and weights
+// written in their place for the experts that follow
+static int tape_route(ihip_mctx* s, int64_t n)
+{
+  ihip_model* m = s->m;
+  const int64_t E = m->d.experts, K = m->d.experts_used;
+  if (m->tape_pos + n > m->tape_rows)
+    return fail(IHIP_E_ARG, "route tape: no recorded choice left (" + std::to_string(m->tape_routes) +
+                                " replayed)");
+  ihip_ctx* c = m->c;
+  std::vector<float> lg((size_t)(n * E));
+  std::vector<int32_t> ids((size_t)(n * K));
+  IHIP_CHECK(hipMemcpyDtoHAsync(lg.data(), (hipDeviceptr_t)s->route, n * E * 4, c->stream));
+  IHIP_CHECK(hipMemcpyDtoHAsync(ids.data(), (hipDeviceptr_t)s->ids_dev, n * K * 4, c->stream));
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  const int32_t* tid = m->tape_ids.data() + m->tape_pos * K;
+  const float* tw = m->tape_w.data() + m->tape_pos * K;
+  for (int64_t r = 0; r < n; r++) {
+    const int32_t* mine = ids.data() + r * K;
+    bool same = true;
+    for (int64_t j = 0; j < K && same; j++) {
+      bool found = false;
+      for (int64_t i = 0; i < K; i++) found = found || tid[r * K + i] == mine[j];
+      same = found;
+    }
+    if (!same) {
+      // the k-th highest logit of the device's choice and the highest it left out
+      const float* l = lg.data() + r * E;
+      double kth = INFINITY, best = -1e38;
+      for (int64_t j = 0; j < K; j++) kth = std::min(kth, (double)l[mine[j]]);
+      for (int64_t i = 0; i < E; i++) {
+        bool picked = false;
+        for (int64_t j = 0; j < K; j++) picked = picked || mine[j] == i;
+        if (!picked && l[i] > best) best = l[i];
+      }
+      m->tape_differs++;
+      m->tape_gap = std::max(m->tape_gap, kth - best);
+    }
+  }
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->ids_dev, (void*)tid, n * K * 4, c->stream));
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->rw, (void*)tw, n * K * 4, c->stream));
+  IHIP_CHECK(hipStreamSynchronize(c->stream));
+  m->tape_pos += n;
+  m->tape_routes += n;
+  return 0;
+}
+
 // CheckDeviceRoute (model.qwen3.cuda.pas:1207-1256): the router logits, the
 // picks and the weights the device wrote for one row, read back after the
 // route, against TDecoderModel.Route (decoder.pas:2901-2949) on the same
@@ -646,7 +703,8 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
     // the route (TDecoderModel.Route) inside the gate/up launch: each block
     // ranks the logits for its slot's expert, one writes the picks and
     // weights for the down launch (up to 256 experts); else its own launch
-    const bool self_route = E <= 256 && K <= E && K <= 8;
+    const bool taped = m->tape_rows > 0 && !m->c->capturing;
+    const bool self_route = E <= 256 && K <= E && K <= 8 && !taped;
     if (!self_route) {
       struct {
         const float* logits;
@@ -657,6 +715,7 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
       } ra = {(const float*)s->route, (int*)s->ids_dev, (float*)s->rw, (int32_t)E, (int32_t)K,
               d.norm_topk, 1};
       if ((rc = launch(m->c, "route", dim3(1), dim3(256), &ra))) return rc;
+      if (taped && (rc = tape_route(s, 1))) return rc;
     }
     LinearCall k;
     k.x = s->x; k.rows = K; k.in = H; k.dtype = L.egd; k.w = L.eg; k.out = FI;
@@ -917,8 +976,10 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
               d.norm_topk, (int32_t)n, (const float*)L.expert_scale};
       // one row beside the dense block: the route formed in the experts'
       // gate/up launch (route_wave, the expert scales applied as route does)
-      const bool self_route = staged && E <= 256 && K <= E && K <= 8;
+      const bool taped = m->tape_rows > 0 && !m->c->capturing;
+      const bool self_route = staged && E <= 256 && K <= E && K <= 8 && !taped;
       if (!self_route && (rc = launch(m->c, "route", dim3((unsigned)n), dim3(256), &ra))) return rc;
+      if (taped && (rc = tape_route(s, n))) return rc;
       QCache qe{s->xq0, s->xqk};
       if (beside && !staged) {
         if ((rc = norm(s->x, L.moe_in_norm, s->h))) return rc;
@@ -1442,7 +1503,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   if (rc) return rc;
   // a graph holds this context's cache and ranges: captured again when the
   // cache grew or the sampler changed since
-  const bool graphs = m->use_graphs && !m->check_route;
+  const bool graphs = m->use_graphs && !m->check_route && m->tape_rows == 0;
   if (graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
                         s->graph_sampler != m->sampler_epoch || s->graph_draw != s->draw_ids) &&
       (rc = decode_graph(s)))
@@ -2302,6 +2363,34 @@ int ihip_model_route_stats(ihip_model* m, int64_t* checks, int64_t* mismatches, 
   if (checks) *checks = m->route_checks;
   if (mismatches) *mismatches = m->route_mismatches;
   if (max_diff) *max_diff = m->route_max_diff;
+  return 0;
+}
+
+int ihip_model_route_tape(ihip_model* m, const int32_t* ids, const float* weights, int64_t rows)
+{
+  if (!m || rows < 0 || (rows > 0 && (!ids || !weights))) return fail(IHIP_E_ARG, "ihip_model_route_tape");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  const int64_t K = m->d.experts_used;
+  if (rows > 0 && K < 1) return fail(IHIP_E_ARG, "ihip_model_route_tape: the model has no experts");
+  for (int64_t i = 0; i < rows * K; i++)
+    if (ids[i] < 0 || ids[i] >= m->d.experts) return fail(IHIP_E_ARG, "ihip_model_route_tape: an expert id out of range");
+  m->tape_ids.assign(ids, ids + rows * K);
+  m->tape_w.assign(weights, weights + rows * K);
+  m->tape_rows = rows;
+  m->tape_pos = m->tape_routes = m->tape_differs = 0;
+  m->tape_gap = 0;
+  return 0;
+}
+
+int ihip_model_route_tape_stats(ihip_model* m, int64_t* routes, int64_t* differs, double* gap,
+                                int64_t* pending)
+{
+  if (!m) return fail(IHIP_E_ARG, "ihip_model_route_tape_stats");
+  std::lock_guard<std::mutex> g(m->c->lock);
+  if (routes) *routes = m->tape_routes;
+  if (differs) *differs = m->tape_differs;
+  if (gap) *gap = m->tape_gap;
+  if (pending) *pending = m->tape_rows - m->tape_pos;
   return 0;
 }
 

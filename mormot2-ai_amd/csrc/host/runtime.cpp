@@ -176,6 +176,7 @@ int ihip_create(int device, ihip_ctx** out)
   if (const char* v = getenv("IHIP_ATTN_MFMA")) c->attn_mfma = atoi(v) != 0;
   if (const char* v = getenv("IHIP_GEMM8")) c->use_gemm8 = atoi(v) != 0;
   if (const char* v = getenv("IHIP_GEMM_SPLIT")) c->gemm_split = atoi(v) != 0;
+  if (const char* v = getenv("IHIP_GEMM_F8")) c->gemm_f8 = atoi(v) != 0;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -229,7 +230,7 @@ void ihip_destroy(ihip_ctx* c)
   for (auto& w : c->weights) (void)hipFree((void*)w.dev);
   for (auto a : c->allocations) (void)hipFree((void*)a);
   for (uint64_t b : {c->scratch_x, c->scratch_y, c->scratch_q, c->scratch_bad, c->scratch_attn,
-                     c->scratch_argmax, c->scratch_split})
+                     c->scratch_argmax, c->scratch_split, c->scratch_planes})
     if (b) (void)hipFree((void*)b);
   for (auto ev : c->events)
     if (ev) (void)hipEventDestroy(ev);

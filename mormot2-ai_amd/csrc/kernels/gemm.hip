@@ -149,7 +149,10 @@ struct ChunkRegs {
   Raw wr[2];      // weight groups: column t / 8 (+ 32), group t % 8
   v4u32 xc[4];    // activation codes: row t / 4, groups 2 (t % 4) and 2 (t % 4) + 1
   float dx[2];    // and their scales
+  v4u32 xp[4];    // F8: the second half of the groups' 64-byte e4m3 planes
 };
+
+
 
 template <int F>
 __device__ __forceinline__ void chunk_load(const GemmArgs& a, const uint8_t* wb, const Regions& rg,
@@ -202,6 +205,222 @@ __device__ __forceinline__ void chunk_store(const ChunkRegs& cr, uint32_t* sw, u
       sbs[j * GBM + row] = sm;
     }
   }
+}
+
+// ------------------------------------------- MXFP4 on the scaled f8f6f4 MFMA
+// v_mfma_scale_f32_32x32x64_f8f6f4 with B the group's e2m1 codes as they are
+// stored (no decode) and A the activation codes split q = 16 hi + lo (hi, lo
+// in [-8, 8]): A's first 32 k are e4m3(16 hi) and its last 32 e4m3(lo), B's
+// two 32-k blocks both the group's 32 codes, every block scale 1. Each
+// product is exact (e4m3 x e2m1) and every partial sum a multiple of 1/2
+// below 2^23, so the f32 result is the exact group dot sum q w over the e2m1
+// values, half the doubled-table integer sum of the int8 path: the CPU's
+// group sum, as exact. One instruction per 32-value group, like the int8
+// MFMA, without the e2m1 -> int8 decode of the weights.
+//
+// Operand layout (probed on gfx950): byte j of an 8-bit operand in lane half
+// h holds k = 16 h + j (j < 16) or 32 + 16 h + (j - 16); nibble j of a 4-bit
+// operand in lane half h holds k = 32 h + j. The k order is free as long as A
+// and B agree: B's block position p is nibble p of the 16 stored code bytes,
+// value v(p) = p / 2 + 16 (p % 2) (byte j: value j low, value j + 16 high), so
+// A's positions take q[v(p)]. A row's planes per group (f8_planes): for h =
+// 0, 1 the 32 bytes e4m3(16 hi[v(16h + j)]) j < 16, e4m3(lo[v(16h + j)]) j
+// < 16 - lane half h reads bytes 32h..32h+31 of the group.
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+// e4m3 of an integer in [-8, 8] (times 16 when x16: the exponent + 4)
+__device__ __forceinline__ uint32_t e4m3_small(int v, bool x16)
+{
+  const int a = v < 0 ? -v : v;
+  // 0, 1 .. 8: 0x00 0x38 0x40 0x44 0x48 0x4A 0x4C 0x4E 0x50
+  const uint32_t lo4 = 0x44403800u, hi4 = 0x4E4C4A48u;
+  uint32_t m = a == 8 ? 0x50u : (a < 4 ? (lo4 >> (8 * a)) & 255u : (hi4 >> (8 * (a - 4))) & 255u);
+  if (x16 && a) m += 0x20u;
+  return v < 0 ? (m | 0x80u) : m;
+}
+
+template <int F>
+__device__ __forceinline__ void chunk_load8(const GemmArgs& a, const uint8_t* wb, const Regions& rg,
+                                            int col0, const int* sxr, int64_t xstride, int G, int gc,
+                                            ChunkRegs& cr)
+{
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int64_t o = min(col0 + (t >> 3) + 32 * p, a.out - 1);
+    load_group<F>(wb, rg, o, G, min(gc + (t & 7), G - 1), a.in, cr.wr[p]);
+  }
+  const uint8_t* xr = a.xq + (int64_t)sxr[t >> 2] * xstride;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int g = min(gc + 2 * (t & 3) + k, G - 1);
+    const v4u32* q = (const v4u32*)(xr + (int64_t)g * 64);
+    cr.xc[2 * k] = q[0];
+    cr.xc[2 * k + 1] = q[1];
+    cr.xp[2 * k] = q[2];
+    cr.xp[2 * k + 1] = q[3];
+    cr.dx[k] = ((const float*)(xr + (int64_t)G * 64))[g];
+  }
+}
+
+constexpr int GSA8 = GKC * 16 + 4;  // LDS dwords per activation row of planes
+
+template <int F>
+__device__ __forceinline__ void chunk_store8(const ChunkRegs& cr, uint32_t* sw, uint32_t* sa, double* sdx)
+{
+  const int t = threadIdx.x;
+  constexpr int WS = GKC * raw_dwords<F>() + 1;
+#pragma unroll
+  for (int p = 0; p < 2; p++) raw_put<F>(sw + ((t >> 3) + 32 * p) * WS + (t & 7), GKC, cr.wr[p]);
+  const int row = t >> 2;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int j = 2 * (t & 3) + k;
+    uint32_t* d = sa + row * GSA8 + j * 16;
+    *(v4u32*)d = cr.xc[2 * k];
+    *(v4u32*)(d + 4) = cr.xc[2 * k + 1];
+    *(v4u32*)(d + 8) = cr.xp[2 * k];
+    *(v4u32*)(d + 12) = cr.xp[2 * k + 1];
+    sdx[j * GBM + row] = (double)cr.dx[k];
+  }
+}
+
+// the MXFP4 GEMM on the f8f6f4 matrix cores: gemm's tiles, chunks and
+// double scaling; A from the planes of f8_planes
+__device__ __forceinline__ void gemm_mxfp4_f8(const GemmArgs& a)
+{
+  constexpr int F = DT_MXFP4;
+  __shared__ uint32_t sw_[GBN * GSW];
+  __shared__ __align__(16) uint32_t sa_[GBM * GSA8];
+  __shared__ __align__(16) double sdx_[GKC * GBM];
+  __shared__ int sxr[GBM], syr[GBM];
+  const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5;
+  const int wm = w & 1, wn = w >> 1;
+  const int G = a.in >> 5;
+  const int64_t xstride = 68 * (int64_t)G;
+  const uint8_t* wb = a.w;
+  const float* bias = a.bias;
+  int nrows;
+  if (a.items) {
+    const int4 it = a.items[blockIdx.y];
+    if (it.z <= 0) return;
+    wb += (int64_t)it.x * a.stride;
+    if (bias) bias += (int64_t)it.x * a.out;
+    nrows = min(GBM, it.z);
+    if (t < GBM) {
+      const int sl = a.perm[it.y + min(t, nrows - 1)];
+      sxr[t] = a.x_per_slot ? sl / a.x_per_slot : 0;
+      syr[t] = sl;
+    }
+  } else {
+    const int r0 = blockIdx.y * GBM;
+    nrows = min(GBM, a.rows - r0);
+    if (t < GBM) sxr[t] = syr[t] = r0 + min(t, nrows - 1);
+  }
+  __syncthreads();
+  const Regions rg = regions(F, a.out, a.in);
+  const int col0 = blockIdx.x * GBN;
+  const int o_real = col0 + 32 * wn + (l & 31);
+  const int64_t o = min(o_real, a.out - 1);
+  const int rb = 32 * wm + 4 * h;
+  constexpr int WS = GKC * raw_dwords<F>() + 1;
+  const uint32_t* myw = sw_ + (32 * wn + (l & 31)) * WS;
+  const uint32_t* mya = sa_ + (32 * wm + (l & 31)) * GSA8 + 8 * h;
+  double acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.0;
+  const int nch = (G + GKC - 1) / GKC;
+  ChunkRegs cr;
+  chunk_load8<F>(a, wb, rg, col0, sxr, xstride, G, 0, cr);
+  chunk_store8<F>(cr, sw_, sa_, sdx_);
+  chunk_load8<F>(a, wb, rg, col0, sxr, xstride, G, GKC, cr);
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    const int gc = c * GKC;
+#pragma unroll
+    for (int j = 0; j < GKC; j++) {
+      const int g = gc + j;
+      if (g < G) {
+        const Raw r = raw_get<F>(myw + j, GKC);
+        const v4u32 a0 = *(const v4u32*)(mya + j * 16), a1 = *(const v4u32*)(mya + j * 16 + 4);
+        const v8i_t av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+        const v8i_t bv = {(int)r.q0.x, (int)r.q0.y, (int)r.q0.z, (int)r.q0.w, 0, 0, 0, 0};
+        const v16f_t z = {};
+        // formats: A e4m3 (0), B e2m1 (4); every block scale E8M0 127 (1.0)
+        const v16f_t cf = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, z, 0, 4, 0, 0x7F7F7F7F, 0,
+                                                                           0x7F7F7F7F);
+        const double dw = mxfp4_q8_scale(r.a);
+        double2 dq[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) dq[q] = *(const double2*)&sdx_[j * GBM + rb + 8 * (q >> 1) + 2 * (q & 1)];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const double2 d2 = dq[i >> 1];
+          const double dx = (i & 1) ? d2.y : d2.x;
+          // 2 cf: the doubled-table integer group sum of the CPU, exact
+          acc[i] = __builtin_fma(2.0 * (double)cf[i], dw * dx, acc[i]);
+        }
+      }
+    }
+    __syncthreads();
+    chunk_store8<F>(cr, sw_, sa_, sdx_);
+    chunk_load8<F>(a, wb, rg, col0, sxr, xstride, G, gc + 2 * GKC, cr);
+    __syncthreads();
+  }
+  if (o_real >= a.out) return;
+  const double b = bias ? (double)bias[o] : 0.0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int rt = rb + 8 * (i >> 2) + (i & 3);
+    if (rt < nrows) {
+      double v = acc[i];
+      if (bias) v = b + v;
+      a.y[(int64_t)syr[rt] * a.out + o] = (float)v;
+    }
+  }
+}
+
+// the e4m3 planes of quantized activation rows for gemm_mxfp4_f8: row r of
+// xq (codes [in], then dx [G]) into row r of planes (64 bytes per group as
+// above, then the same dx [G]); one thread per group
+struct PlanesArgs {
+  const uint8_t* xq;
+  uint8_t* planes;
+  int32_t rows, in;
+};
+__device__ __forceinline__ void f8_planes(const PlanesArgs& a)
+{
+  const int G = a.in >> 5;
+  const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int row = blockIdx.y;
+  if (gi >= G) return;
+  const uint8_t* src = a.xq + (int64_t)row * ((int64_t)a.in + 4 * G);
+  uint8_t* dst = a.planes + (int64_t)row * 68 * G;
+  const v4u32 c0 = *(const v4u32*)(src + gi * 32), c1 = *(const v4u32*)(src + gi * 32 + 16);
+  const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  uint32_t outw[16];
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      uint32_t whi = 0, wlo = 0;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const int p = 16 * hh + 4 * jj + b;
+        const int v = (p >> 1) + 16 * (p & 1);
+        const int q = (int)(int8_t)((cw[v >> 2] >> (8 * (v & 3))) & 255u);
+        const int hi = (q + 8) >> 4, lo = q - 16 * hi;
+        whi |= e4m3_small(hi, true) << (8 * b);
+        wlo |= e4m3_small(lo, false) << (8 * b);
+      }
+      outw[8 * hh + jj] = whi;
+      outw[8 * hh + 4 + jj] = wlo;
+    }
+  v4u32* d = (v4u32*)(dst + gi * 64);
+#pragma unroll
+  for (int k = 0; k < 4; k++) d[k] = v4u32{outw[4 * k], outw[4 * k + 1], outw[4 * k + 2], outw[4 * k + 3]};
+  ((float*)(dst + (int64_t)G * 64))[gi] = ((const float*)(src + a.in))[gi];
 }
 
 template <int F>
@@ -800,6 +1019,8 @@ IHIP_GEMM_FLT(f16, ihip::DT_F16)
 IHIP_GEMM(q4_0, ihip::DT_Q4_0)
 #endif
 #ifdef IHIP_ONLY_FMT_MXFP4
+extern "C" __global__ __launch_bounds__(256) void gemm_mxfp4_f8(ihip::GemmArgs a) { ihip::gemm_mxfp4_f8(a); }
+extern "C" __global__ __launch_bounds__(256) void f8_planes(ihip::PlanesArgs a) { ihip::f8_planes(a); }
 IHIP_GEMM(mxfp4, ihip::DT_MXFP4)
 #endif
 #ifdef IHIP_ONLY_FMT_Q5_0

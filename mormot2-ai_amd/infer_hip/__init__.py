@@ -130,6 +130,8 @@ def lib():
             "ihip_model_use_graphs": (i32, [vp, i32]),
             "ihip_model_check_route": (i32, [vp, i32]),
             "ihip_model_route_stats": (i32, [vp, vp, vp, vp]),
+            "ihip_model_route_tape": (i32, [vp, vp, vp, i64]),
+            "ihip_model_route_tape_stats": (i32, [vp, vp, vp, vp, vp]),
             "ihip_model_chunk": (i32, [vp, i64]),
             "ihip_enqueue_stream_read": (i32, [vp, u64, u64, u64]),
             "ihip_model_rotary": (i32, [vp, i64, i64, vp]),
@@ -459,6 +461,25 @@ class Model:
         a, b, d = C.c_int64(), C.c_int64(), C.c_double()
         check(lib().ihip_model_route_stats(self.h, C.byref(a), C.byref(b), C.byref(d)), "route_stats")
         return a.value, b.value, d.value
+
+    def route_tape(self, ids=None, weights=None):
+        """TDecoderRouteTape replay: the rows routed from now on take these
+        picks and weights [rows, experts_used] in turn (None: off)."""
+        if ids is None:
+            check(lib().ihip_model_route_tape(self.h, None, None, 0), "route_tape")
+            return
+        self._tape = (np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(weights, np.float32))
+        check(lib().ihip_model_route_tape(self.h, _p(self._tape[0]), _p(self._tape[1]),
+                                          self._tape[0].shape[0]), "route_tape")
+
+    def route_tape_stats(self):
+        """(routes replayed, rows the device chose otherwise, the largest
+        router gap of those, rows pending)."""
+        a, b, p = C.c_int64(), C.c_int64(), C.c_int64()
+        g = C.c_double()
+        check(lib().ihip_model_route_tape_stats(self.h, C.byref(a), C.byref(b), C.byref(g),
+                                                C.byref(p)), "route_tape_stats")
+        return a.value, b.value, g.value, p.value
 
     def timing(self):
         a, b = C.c_double(), C.c_double()

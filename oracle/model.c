@@ -18,6 +18,11 @@ struct orc_model {
    * routed row since the last orc_model_route_gap (a near tie there could
    * pick another expert on another arithmetic) */
   double route_gap;
+  /* TDecoderRouteTape in drmRecord (decoder.pas:2955-2990): every routed
+   * row's k picks (by id) and weights appended here, up to rec_cap rows */
+  int32_t* rec_ids;
+  float* rec_w;
+  int64_t rec_cap, rec_rows;
   float** keys;
   float** values;
   /* per DeltaNet layer: the last conv - 1 inputs of every channel and the
@@ -83,6 +88,16 @@ int orc_model_truncate(orc_model* m, int64_t length)
   m->length = length;
   return 0;
 }
+
+void orc_model_route_record(orc_model* m, int32_t* ids, float* w, int64_t cap)
+{
+  m->rec_ids = ids;
+  m->rec_w = w;
+  m->rec_cap = ids && w ? cap : 0;
+  m->rec_rows = 0;
+}
+
+int64_t orc_model_route_recorded(orc_model* m) { return m->rec_rows; }
 
 double orc_model_route_gap(orc_model* m)
 {
@@ -349,6 +364,11 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
         }
         if (escale)
           for (int64_t j = 0; j < K; j++) cw[r * K + j] = cw[r * K + j] * escale[chosen[r * K + j]];
+        if (m->rec_rows < m->rec_cap) {
+          memcpy(m->rec_ids + m->rec_rows * K, chosen + r * K, K * 4);
+          memcpy(m->rec_w + m->rec_rows * K, cw + r * K, K * 4);
+          m->rec_rows++;
+        }
       }
       memset(dst, 0, n * h * 4);
       /* gate and up of an expert: two tensors, or one [E, 2 fi, h] with the

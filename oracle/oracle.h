@@ -150,6 +150,10 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
 int orc_model_truncate(orc_model* m, int64_t length);
 /* the smallest k-th vs (k+1)-th router logit gap since the last call (then reset) */
 double orc_model_route_gap(orc_model* m);
+/* TDecoderRouteTape recording: the k picks (by id) and weights of every
+ * routed row from now on appended to ids / w [cap][k] (NULL: off) */
+void orc_model_route_record(orc_model* m, int32_t* ids, float* w, int64_t cap);
+int64_t orc_model_route_recorded(orc_model* m);
 int orc_model_forward(orc_model* m, const int32_t* ids, int64_t count,
                       float* logits, int all_logits);
 /* decoder.pas:3390-3426 Greedy; margins[i] = top1 - top2 logit of step i */

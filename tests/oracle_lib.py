@@ -80,6 +80,10 @@ def lib():
         L.orc_fast_attention.restype = None
         L.orc_model_route_gap.restype = C.c_double
         L.orc_model_route_gap.argtypes = [vp]
+        L.orc_model_route_record.argtypes = [vp, vp, vp, i64]
+        L.orc_model_route_record.restype = None
+        L.orc_model_route_recorded.argtypes = [vp]
+        L.orc_model_route_recorded.restype = i64
         L.orc_model_forward.argtypes = [vp, vp, i64, vp, C.c_int]
         L.orc_model_greedy.argtypes = [vp, vp, i64, i64, vp, vp]
         L.orc_splitmix_next.restype = C.c_double
@@ -339,6 +343,17 @@ class Model:
         """The smallest k-th vs (k+1)-th router logit gap of the rows routed
         since the last call (inf for a dense model)."""
         return float(lib().orc_model_route_gap(self.h))
+
+    def record_routes(self, rows, k):
+        """TDecoderRouteTape in record mode: keep the picks (by id) and
+        weights of up to `rows` routed rows from now on; routes() returns
+        those recorded so far."""
+        self._rec = (np.zeros((rows, k), np.int32), np.zeros((rows, k), np.float32))
+        lib().orc_model_route_record(self.h, _p(self._rec[0]), _p(self._rec[1]), rows)
+
+    def routes(self):
+        n = int(lib().orc_model_route_recorded(self.h))
+        return self._rec[0][:n].copy(), self._rec[1][:n].copy()
 
     def greedy(self, prompt, max_new):
         p = np.ascontiguousarray(prompt, np.int32)

@@ -379,3 +379,37 @@ def test_two_models_at_reused_addresses(ctx):
         del spec
         assert np.abs(outs[-1] - ref).max() <= 1e-5 * np.abs(ref).max()
     assert np.array_equal(outs[0], outs[2]) and not np.array_equal(outs[0], outs[1])
+
+
+@pytest.fixture(scope="module")
+def f8_ctx():
+    # MXFP4 chunks of 16 rows or more on the scaled f8f6f4 matrix cores
+    saved = {k: os.environ.get(k) for k in ("IHIP_GEMM_MIN_ROWS", "IHIP_GEMM", "IHIP_GEMM_F8")}
+    os.environ.update(IHIP_GEMM_MIN_ROWS="16", IHIP_GEMM="1", IHIP_GEMM_F8="1")
+    try:
+        c = H.Context(0)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    yield c
+    c.close()
+
+
+def test_gemm_mxfp4_f8f6f4_bits_of_int8(f8_ctx, gemm_ctx):
+    # the MXFP4 GEMM on v_mfma_scale_f32_32x32x64_f8f6f4 (e2m1 codes as
+    # stored, the activation split q = 16 hi + lo into e4m3 planes) gives the
+    # exact group sums the int8 MFMA gives: every output the same bits, and
+    # the oracle's to 1 ulp
+    rng = np.random.default_rng(31)
+    for rows, cols, out in GEMM_SHAPES + [(512, 2880, 2880), (100, 1024, 3000)]:
+        w = weights(H.MXFP4, out, cols, rows + cols + out)
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        b = rng.standard_normal(out).astype(np.float32)
+        a = f8_ctx.linear(x, w, H.MXFP4, out, b, mode=H.MODE_Q8)
+        c = gemm_ctx.linear(x, w, H.MXFP4, out, b, mode=H.MODE_Q8)
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), (rows, cols, out)
+        if rows <= 200:
+            assert ulp_diff(a, O.linear(x, w, H.MXFP4, out, b)).max() <= 1

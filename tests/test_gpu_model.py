@@ -131,3 +131,27 @@ def test_check_route_counts(ctx, name, over):
     # every layer routed
     assert checks == 10 * over["layers"], checks
     assert mismatches == 0 and max_diff <= 1e-6, (mismatches, max_diff)
+
+
+def test_gptoss_f8f6f4_experts_greedy(ctx):
+    """A gpt-oss-shaped model whose MXFP4 expert GEMMs (grouped items of the
+    prompt) run on the scaled f8f6f4 matrix cores: the oracle's tokens."""
+    import os
+    name, over = TINY[3]
+    spec = models.Spec(models.tiny(name, **over), seed=41)
+    prompt = np.random.default_rng(9).integers(0, spec.vocab, 200).astype(np.int32)
+    saved = os.environ.get("IHIP_GEMM_F8")
+    os.environ["IHIP_GEMM_F8"] = "1"
+    try:
+        c = H.Context(0)
+    finally:
+        if saved is None:
+            os.environ.pop("IHIP_GEMM_F8", None)
+        else:
+            os.environ["IHIP_GEMM_F8"] = saved
+    dev = H.Model(c, spec, mode=H.MODE_Q8, max_tokens=256)
+    got = dev.greedy(prompt, 16)
+    dev.close()
+    c.close()
+    ref, margins = O.Model(spec, 256).greedy(prompt, 16)
+    assert np.array_equal(got, ref), (got, ref, margins)

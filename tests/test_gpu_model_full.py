@@ -125,12 +125,30 @@ def test_benchmark_workload_tokens(ctx, name):
     prompt = np.random.default_rng(fx["prompt_seed"]).integers(0, spec.vocab, n).astype(np.int32)
     print(f"\n[{name}] device: prompt {n}, greedy {fx['steps']}", flush=True)
     dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=fx["kv_f16"], max_tokens=n + fx["steps"] + 16)
+    dev.chunk(1024)  # the prompt chunks whose routed rows the tape holds in order
+    tape = os.path.join(FIXTURES, name + ".routes.npz")
+    if os.path.exists(tape):
+        # the CPU's expert choice handed to the device (TDecoderRouteTape, as
+        # the reference's device test does, tests/test.infer.cuda.pas:
+        # 2162-2200): at a near tie of the router (a gap of a few ulps among
+        # the tens of thousands of prompt routes) the two arithmetics may
+        # pick other experts for a row; with the choice given, the logits
+        # differ by arithmetic only. The device's own choice is compared.
+        t = np.load(tape)
+        dev.route_tape(t["ids"].astype(np.int32), t["weights"])
     lg = dev.forward(prompt)
     top = fx["prompt_top16"]
     got_top = lg[np.array(top["ids"])]
     want_top = np.array(top["logits"], np.float32)
     first = int(np.argmax(lg))
     toks = np.concatenate([[first], dev.decode(first, fx["steps"] - 1)]).astype(np.int32)
+    if os.path.exists(tape):
+        routes, differs, gap, pending = dev.route_tape_stats()
+        print(f"[{name}] route tape: {routes} rows replayed, the device chose otherwise for "
+              f"{differs} (largest router gap {gap:.2e}), {pending} pending", flush=True)
+        assert pending == 0 and routes == t["ids"].shape[0]
+        # only near ties: a routing error gives gaps of whole units
+        assert differs * 100 <= routes and gap <= 1e-4, (differs, routes, gap)
     dev.close()
     del spec
     gc.collect()
