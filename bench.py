@@ -178,10 +178,12 @@ def decode_kernels(ctx, model, spec, first, steps, past):
     if moe:
         E, K, FI = c["experts"], c["experts_used"], c["expert_ffn"]
         gt = L0.exp_gate.dtype
-        # both matrices of K experts, the residual row and its norm weights,
+        # both matrices of K experts, the normed row as the router's launch
+        # quantized it (Q8_K or Q8_0 codes and a float scale per 32 values),
         # the router logits, the K x FI outputs, the picks and their weights
         wb = 2 * K * FI * H.row_bytes(gt, Hd)
-        nb = wb + 2 * Hd * 4 + E * 4 + K * FI * 4 + K * 8
+        xrow = 2 * Hd * 4 if c.get("family") == "gemma4" else Hd + 4 * (Hd // 32)
+        nb = wb + xrow + E * 4 + K * FI * 4 + K * 8
         if L0.exp_gate_bias.data:
             nb += 2 * K * FI * 4
         what = f"gate+up+{act} of {K} routed experts ({FI}x{Hd}, {H.NAMES[gt]}), route in-launch"
@@ -190,7 +192,8 @@ def decode_kernels(ctx, model, spec, first, steps, past):
         wb = 2 * FI * H.row_bytes(gt, Hd)
         nb = wb + 2 * Hd * 4 + FI * 4
         what = f"FFN gate+up+{act} ({FI}x{Hd}, {H.NAMES[gt]})"
-    dom_name = f"gemv_{H.NAMES[gt].lower()}_q8_norm_glu"
+    # (the MoE experts read the router launch's quantized row: no norm of their own)
+    dom_name = f"gemv_{H.NAMES[gt].lower()}_q8_{'' if moe and c.get('family') != 'gemma4' else 'norm_'}glu"
     kvw = c["kv_heads"] * hd
     out = {}
     model.use_graphs(False)

@@ -456,6 +456,13 @@ int ihip_model_route_stats(ihip_model* m, int64_t* checks, int64_t* mismatches, 
  * steps, without graphs) in place of its own choice, which is compared with
  * them; rows 0: off. A row past the tape is refused. */
 int ihip_model_route_tape(ihip_model* m, const int32_t* ids, const float* weights, int64_t rows);
+/* A test hook (no counterpart in the reference): after each later chunk,
+ * the residual rows [rows, hidden] after layer `layer` (0-based; -1: every
+ * layer, [layers, rows, hidden]) copied to `rows` (host memory the caller
+ * keeps alive; NULL turns it off). One-row decode steps on the fused path
+ * are not captured. */
+int ihip_model_debug_layer(ihip_model* m, int layer, float* rows);
+
 /* the tape's counts: rows replayed, rows where the device's own choice
  * differed, the largest router gap (k-th chosen minus the best left out, in
  * the device's logits) of those rows, rows not yet replayed */

@@ -409,6 +409,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     float* rw;
     int32_t rexp, rk, rnorm, rpad;
     const float* rscale;
+    uint8_t* xq_out;
+    int32_t xq_k8, xq_pad;
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
@@ -420,10 +422,10 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          {(float*)k.yseg[0], (float*)k.yseg[1], (float*)k.yseg[2]},
          {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]},
          k.dtype2 ? k.nseg1 : k.nseg, (const float*)k.rl, (float*)k.rw, (int32_t)k.rexp,
-         (int32_t)k.rk, (int32_t)k.rnorm, 0, (const float*)k.rscale};
-  if (k.rl && (!k.ids || !k.rw || !k.w2 || !k.nw || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
+         (int32_t)k.rk, (int32_t)k.rnorm, 0, (const float*)k.rscale, (uint8_t*)k.xq_out, k.xq_k8, 0};
+  if (k.rl && (!k.ids || !k.rw || !k.w2 || !(k.nw || xq) || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
                k.rk > std::min<int64_t>(k.rexp, 8) || k.rk != k.rows))
-    return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts, gate/up with a norm");
+    return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts, gate/up with a norm or a quantized row");
   if (k.w2 && batch) return fail(IHIP_E_ARG, "EnqueueLinear: the fused SwiGLU takes one row per block");
   // a chunk of rows in the Q8 arithmetic: the MFMA GEMM (64 x 64 tiles)
   // (float weights in the Q8 arithmetic: the float activations as they are,
@@ -534,9 +536,13 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
       }
       const int64_t hold = (int64_t)c->cus * resident_blocks(c, name, 256) * c->gemv_hold;
       const int64_t wgs = std::max<int64_t>(1, std::min((rows + 3) / 4, hold));
-      return launch(c, name, dim3((unsigned)wgs), dim3(256), &a);
+      if (k.xq_out && (!k.nw || (k.xq_k8 && k.in % 256)))
+        return fail(IHIP_E_ARG, "EnqueueLinear: the quantized row out takes a normed row (Q8_K: whole super-blocks)");
+      // (the quantized row out: one block more, which takes no rows)
+      return launch(c, name, dim3((unsigned)(wgs + (k.xq_out ? 1 : 0))), dim3(256), &a);
     }
   }
+  if (k.xq_out) return fail(IHIP_E_ARG, "EnqueueLinear: the quantized row out takes a normed one-row float GEMV");
   // a small batch of quantized rows on the int8 matrix cores: 8 rows (or an
   // item of at most 8 slots) x 128 outputs per block, the weights read once
   // per 8 rows (gemm8), when its tiles fill the chip (a block walks the
@@ -1136,15 +1142,34 @@ int enqueue_attention_one(ihip_ctx* c, const AttnOne& o)
     double scale, eps;
     int32_t heads, kvh, hd, past, window, splits;
     int* done;
+    int32_t place, pad;
   } a = {(const float*)o.q, (const float*)o.k, (const float*)o.v, (const float*)o.qn,
          (const float*)o.kn, (const float*)o.cs, (void*)o.kc, (void*)o.vc, (float*)o.y,
          (const float*)o.sinks, (const int*)o.pastp, (double*)o.part,
          o.scale > 0 ? o.scale : 1.0 / std::sqrt((double)o.hd), o.eps, (int32_t)o.heads,
          (int32_t)o.kvh, (int32_t)o.hd, (int32_t)o.past, (int32_t)o.window, o.splits,
-         (int*)o.done};
+         (int*)o.done, 1, 0};
   char name[32];
   snprintf(name, sizeof name, "attention_one_%s_%d", o.f16 ? "f16" : "f32", (int)o.hd);
-  int rc = launch(c, name, dim3((unsigned)o.heads, 1, (unsigned)o.splits), dim3(256), &a);
+  int rc;
+  if (o.f16) {
+    // one block per (head, range) in a 1-D grid laid out over the XCDs by KV
+    // group (ops.hip attn_one_block): with 8 / kvh XCDs a group, the ranges
+    // rounded up to a multiple of that (a range past the keys is empty)
+    static const int place = [] {
+      const char* v = getenv("IHIP_ATTN_PLACE");
+      return v ? atoi(v) : 1;
+    }();
+    a.place = place;
+    if (place == 1 && o.heads % 8 == 0 && o.kvh <= 8 && 8 % o.kvh == 0) {
+      const int X = 8 / (int)o.kvh;
+      a.splits = (o.splits + X - 1) / X * X;
+      if (a.splits > MAX_SPLITS) return fail(IHIP_E_ARG, "attention_one: heads / splits");
+    }
+    rc = launch(c, name, dim3((unsigned)(o.heads * a.splits)), dim3(256), &a);
+  } else {
+    rc = launch(c, name, dim3((unsigned)o.heads, 1, (unsigned)o.splits), dim3(256), &a);
+  }
   if (rc || o.done) return rc;
   struct {
     const float* q;
@@ -1157,7 +1182,7 @@ int enqueue_attention_one(ihip_ctx* c, const AttnOne& o)
     double scale;
     int32_t rows, heads, kvh, hd, past, window, f16, splits;
   } mg = {nullptr, nullptr, nullptr, (float*)o.y, (const float*)o.sinks, nullptr, (double*)o.part,
-          0.0, 1, (int32_t)o.heads, (int32_t)o.kvh, (int32_t)o.hd, 0, 0, o.f16, o.splits};
+          0.0, 1, (int32_t)o.heads, (int32_t)o.kvh, (int32_t)o.hd, 0, 0, o.f16, a.splits};
   return launch(c, "attention_merge", dim3((unsigned)o.heads, 1), dim3(128), &mg);
 }
 

@@ -186,6 +186,10 @@ struct LinearCall {
   // one block writes the picks (by id) to ids and their weights to rw
   uint64_t rl = 0, rw = 0;
   int rexp = 0, rk = 0, rnorm = 0;
+  // a normed one-row float GEMV (the router) also writes its normed row
+  // quantized here (Q8_K when xq_k8, else Q8_0), for the next launch
+  uint64_t xq_out = 0;
+  int xq_k8 = 0;
   // [rexp] per-expert weight scales (Gemma 4), or 0
   uint64_t rscale = 0;
   // the caller cannot allocate (ihip_enqueue_linear_at_static): no path

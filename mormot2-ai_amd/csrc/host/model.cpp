@@ -132,6 +132,9 @@ struct ihip_model {
   // CheckRoute (model.qwen3.cuda.pas:288-300): after every one-row route on
   // the device the step waits and compares the choice with the host's Route
   bool check_route = false;
+  // a test's capture of the residual rows after one layer of a chunk
+  float* dbg_host = nullptr;
+  int dbg_layer = -1;
   int64_t route_checks = 0, route_mismatches = 0;
   double route_max_diff = 0;
   // TDecoderRouteTape replayed (decoder.pas:2993-3035): the picks and
@@ -498,8 +501,23 @@ static int tape_route(ihip_mctx* s, int64_t n)
       m->tape_gap = std::max(m->tape_gap, kth - best);
     }
   }
-  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->ids_dev, (void*)tid, n * K * 4, c->stream));
-  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->rw, (void*)tw, n * K * 4, c->stream));
+  // the tape holds each row's picks in pick order (TDecoderModel.Route's
+  // ranking); the device's slots hold them by id, as its own route writes
+  // them and as TDecoderModel.Experts adds the experts (id order)
+  std::vector<int32_t> sid((size_t)(n * K));
+  std::vector<float> sw((size_t)(n * K));
+  for (int64_t r = 0; r < n; r++) {
+    std::vector<int64_t> ord((size_t)K);
+    for (int64_t j = 0; j < K; j++) ord[j] = j;
+    std::stable_sort(ord.begin(), ord.end(),
+                     [&](int64_t a, int64_t b) { return tid[r * K + a] < tid[r * K + b]; });
+    for (int64_t j = 0; j < K; j++) {
+      sid[r * K + j] = tid[r * K + ord[j]];
+      sw[r * K + j] = tw[r * K + ord[j]];
+    }
+  }
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->ids_dev, (void*)sid.data(), n * K * 4, c->stream));
+  IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->rw, (void*)sw.data(), n * K * 4, c->stream));
   IHIP_CHECK(hipStreamSynchronize(c->stream));
   m->tape_pos += n;
   m->tape_routes += n;
@@ -699,7 +717,24 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
     }
     // MoeBlock (decoder.pas:3037-3053), the experts chosen on the device
     const int64_t E = d.experts, K = d.experts_used, FI = d.expert_ffn;
-    if ((rc = normed(L.post_norm, L.rd, L.router, E, L.router_b, s->route))) return rc;
+    // the router's launch also writes the normed row quantized for the
+    // experts' gate/up (float router weights, the Q8 arithmetic): the same
+    // rmsnorm and quantization as the experts' own staging would form, once
+    const int xk = q8_kind(L.egd);
+    const bool xq_pass = (m->mode & 1) == IHIP_MODE_Q8 && xk >= 0 &&
+                         (L.rd == DT_F32 || L.rd == DT_BF16 || L.rd == DT_F16) && H <= 4096 &&
+                         (xk == 0 || H % 256 == 0);
+    const uint64_t xqr = xk == 1 ? s->xqk : s->xq0;
+    {
+      LinearCall k;
+      k.x = s->x; k.rows = 1; k.in = H; k.dtype = L.rd; k.w = L.router; k.out = E; k.bias = L.router_b;
+      k.y = s->route; k.mode = m->mode; k.nw = L.post_norm; k.eps = d.rms_eps;
+      if (xq_pass) {
+        k.xq_out = xqr;
+        k.xq_k8 = xk == 1;
+      }
+      if ((rc = enqueue_linear(m->c, k))) return rc;
+    }
     // the route (TDecoderModel.Route) inside the gate/up launch: each block
     // ranks the logits for its slot's expert, one writes the picks and
     // weights for the down launch (up to 256 experts); else its own launch
@@ -722,6 +757,10 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
     k.y = s->gate; k.mode = m->mode; k.ids = s->ids_dev; k.stride = L.eg_stride; k.x_per_slot = 0;
     k.nexp = (int)E; k.bias = L.egb; k.w2 = L.eu; k.bias2 = L.eub; k.alpha = d.swiglu_alpha;
     k.limit = d.swiglu_limit; k.nw = L.post_norm; k.eps = d.rms_eps;
+    if (xq_pass) {
+      // the router's quantized normed row (the norm is not formed again)
+      k.x = xqr; k.nw = 0; k.mode = m->mode | IHIP_MODE_XQ;
+    }
     if (self_route) {
       k.rl = s->route; k.rw = s->rw; k.rexp = (int)E; k.rk = (int)K; k.rnorm = d.norm_topk;
     }
@@ -863,7 +902,16 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
   auto norm = [&](uint64_t x, uint64_t w, uint64_t y) { return ihip_enqueue_rmsnorm(m->c, x, w, y, n, H, d.rms_eps); };
   int rc = norm(s->x, m->L[0].input_norm, s->h);
   if (rc) return rc;
+  // a test's capture of the residual rows after layer dbg_layer (a chunk)
+  auto capture = [&](int l) -> int {
+    if (!m->dbg_host || (m->dbg_layer >= 0 && l != m->dbg_layer)) return 0;
+    float* dst = m->dbg_host + (m->dbg_layer < 0 ? (size_t)l * n * H : 0);
+    IHIP_CHECK(hipMemcpyDtoHAsync(dst, (hipDeviceptr_t)s->x, (size_t)n * H * 4, m->c->stream));
+    IHIP_CHECK(hipStreamSynchronize(m->c->stream));
+    return 0;
+  };
   for (int l = 0; l < d.layers; l++) {
+    if (l > 0 && (rc = capture(l - 1))) return rc;
     const DevLayer& L = m->L[l];
     const int64_t hd = L.hd, qw = (int64_t)d.heads * hd, kvw = L.kvh * hd;
     QCache qh{s->xq0, s->xqk};
@@ -1096,6 +1144,7 @@ static int layers(ihip_mctx* s, int64_t n, int64_t past, bool graph)
     }
     if (rc) return rc;
   }
+  if ((rc = capture(d.layers - 1))) return rc;
   return 0;
 }
 
@@ -1401,7 +1450,10 @@ static const uint64_t ATTN_PART_MAX = 1ull << 30;
 
 static uint64_t part_bytes(const ihip_model* m, int64_t rows, int64_t keys)
 {
-  return (uint64_t)m->d.heads * rows * attention_splits(keys) * (m->max_hd + 2) * 8;
+  // one row (the decode step): the ranges rounded up to a multiple of 8 at
+  // most, as enqueue_attention_one lays them over the XCDs
+  const int64_t splits = attention_splits(keys);
+  return (uint64_t)m->d.heads * rows * (rows == 1 ? (splits + 7) / 8 * 8 : splits) * (m->max_hd + 2) * 8;
 }
 
 // rows of the next chunk after `past` cached tokens, at most `want`
@@ -2379,6 +2431,14 @@ int ihip_model_route_tape(ihip_model* m, const int32_t* ids, const float* weight
   m->tape_rows = rows;
   m->tape_pos = m->tape_routes = m->tape_differs = 0;
   m->tape_gap = 0;
+  return 0;
+}
+
+int ihip_model_debug_layer(ihip_model* m, int layer, float* rows)
+{
+  if (!m || (rows && (layer < -1 || layer >= m->d.layers))) return fail(IHIP_E_ARG, "ihip_model_debug_layer");
+  m->dbg_host = rows;
+  m->dbg_layer = layer;
   return 0;
 }
 

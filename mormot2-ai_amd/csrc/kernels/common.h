@@ -9,20 +9,38 @@
 #include "../layout.h"
 
 // IHIP_STAMP(i): with IHIP_TRACE defined (a timing build that defines
-// ihip_trace), thread 0 of a block records the 100 MHz clock at phase i of
-// an instrumented kernel; compiled out otherwise
+// ihip_trace), the 100 MHz clock at phase i of an instrumented kernel, held
+// in registers and written by thread 0 of the block when the function that
+// opened IHIP_STAMP_SCOPE returns (a store per stamp would make the
+// compiler wait for the vector memory counter at the next stamp); compiled
+// out otherwise
 #ifdef IHIP_TRACE
 // the stamp buffer of a timing build ([blocks][8] clocks), set by
 // ihip_trace_buffer through hipModuleGetGlobal
-__device__ uint64_t* ihip_trace;
-#define IHIP_STAMP(i)                                                                            \
-  do {                                                                                           \
-    if (threadIdx.x == 0)                                                                        \
-      if (ihip_trace)                                                                            \
-        ihip_trace[(((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8 + \
-                   (i)] = __builtin_amdgcn_s_memrealtime();                                      \
+__constant__ uint64_t* ihip_trace;  // scalar loads
+struct IhipStamps {
+  uint64_t t[8];
+  uint32_t mask = 0;
+  __device__ ~IhipStamps()
+  {
+    if (threadIdx.x == 0 && ihip_trace) {
+      uint64_t* p = ihip_trace + (((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (mask & (1u << i)) p[i] = t[i];
+    }
+  }
+};
+#define IHIP_STAMP_SCOPE IhipStamps ihip_st
+#define IHIP_STAMP(i)                                   \
+  do {                                                  \
+    ihip_st.t[i] = __builtin_amdgcn_s_memrealtime();    \
+    ihip_st.mask |= 1u << (i);                          \
   } while (0)
 #else
+#define IHIP_STAMP_SCOPE \
+  do {                   \
+  } while (0)
 #define IHIP_STAMP(i) \
   do {                \
   } while (0)

@@ -83,6 +83,11 @@ struct LinArgs {
   int32_t rexp, rk, rnorm, rpad;
   // each written weight times its expert's scale (Gemma 4), or null
   const float* rscale;
+  // a normed one-row float GEMV (gemv_flt) also writes its normed row
+  // quantized (Q8_K when xq_k8, else Q8_0) to xq_out [in] codes then [in / 32]
+  // floats: the next launch over the same normed row takes it as given
+  uint8_t* xq_out;
+  int32_t xq_k8, xq_pad;
 };
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
@@ -510,6 +515,67 @@ __device__ __forceinline__ void unpack8(const float4& a, const float4& b, float*
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// the Q8 quantization of quarter q (8 consecutive values) of a row:
+// InferQuantizeRowQ8_0 with 4 lanes a group (K8 false: the group's largest
+// magnitude / 127, dx the scale rounded to half) or InferQuantizeRowQ8_K with
+// 32 lanes a super-block (K8: the super-block's first value of the largest
+// magnitude m, codes rint(-127 / m * v) at most 127, dx its inverse). The
+// lanes of a group / super-block are aligned neighbours of one wave, all
+// calling it.
+template <bool K8>
+__device__ __forceinline__ void quant_quarter(const float (&v)[8], int q, uint32_t& c0, uint32_t& c1,
+                                              float& dx, bool& nonfinite)
+{
+  nonfinite = false;
+  float amax = 0.f, m = 0.f;
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
+    float f = fabsf(v[j]);
+    if (f > amax) {
+      amax = f;
+      m = v[j];
+      idx = 8 * q + j;
+    }
+  }
+  c0 = c1 = 0;
+  dx = 0.f;
+  if constexpr (!K8) {
+    amax = fmaxf(amax, xpart<1>(amax));
+    amax = fmaxf(amax, xpart<2>(amax));
+    float d = amax / 127.0f;
+    if (!(d < 2.9387359e-39f)) {
+      float id = 1.0f / d;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        uint32_t c = (uint32_t)(int)__builtin_rintf(v[j] * id) & 255u;
+        if (j < 4) c0 |= c << (8 * j);
+        else c1 |= c << (8 * (j - 4));
+      }
+    }
+    dx = half_to_float(float_to_half(d));
+  } else {
+    first_max<1>(amax, m, idx);
+    first_max<2>(amax, m, idx);
+    first_max<4>(amax, m, idx);
+    first_max<8>(amax, m, idx);
+    first_max<16>(amax, m, idx);
+    if (!(amax < 3.7320437e-37f)) {
+      float iscale = -127.0f / m;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        int ci = (int)__builtin_rintf(iscale * v[j]);
+        if (ci > 127) ci = 127;
+        uint32_t c = (uint32_t)ci & 255u;
+        if (j < 4) c0 |= c << (8 * j);
+        else c1 |= c << (8 * (j - 4));
+      }
+      dx = 1.0f / iscale;
+    }
+  }
+}
+
 // phase 2: into LDS (codes / dx, or floats at xs), normed first with NORM
 // (one row of n values), quantized on the way when no quantized row was given
 // - the arithmetic of quantize_q8_0 / quantize_q8_k (InferQuantizeRowQ8_0,
@@ -568,56 +634,11 @@ __device__ __forceinline__ void stage_store(const XStage& s, bool quantized, int
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) v[j] = has ? vv[8 * k + j] : 0.f;
-      bool nonfinite = false;
-      float amax = 0.f, m = 0.f;
-      int idx = 0x7fffffff;
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        nonfinite |= (float_bits(v[j]) & 0x7f800000u) == 0x7f800000u;
-        float f = fabsf(v[j]);
-        if (f > amax) {
-          amax = f;
-          m = v[j];
-          idx = 8 * q + j;
-        }
-      }
+      bool nonfinite;
+      uint32_t c0, c1;
+      float dx;
+      quant_quarter<is_k_quant(F)>(v, q, c0, c1, dx, nonfinite);
       if (nonfinite && bad) bad[0] = badrow;
-      uint32_t c0 = 0, c1 = 0;
-      float dx = 0.f;
-      if constexpr (!is_k_quant(F)) {
-        amax = fmaxf(amax, xpart<1>(amax));
-        amax = fmaxf(amax, xpart<2>(amax));
-        float d = amax / 127.0f;
-        if (!(d < 2.9387359e-39f)) {
-          float id = 1.0f / d;
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            uint32_t c = (uint32_t)(int)__builtin_rintf(v[j] * id) & 255u;
-            if (j < 4) c0 |= c << (8 * j);
-            else c1 |= c << (8 * (j - 4));
-          }
-        }
-        dx = half_to_float(float_to_half(d));
-      } else {
-        // the super-block's first value of the largest magnitude: 32 lanes
-        first_max<1>(amax, m, idx);
-        first_max<2>(amax, m, idx);
-        first_max<4>(amax, m, idx);
-        first_max<8>(amax, m, idx);
-        first_max<16>(amax, m, idx);
-        if (!(amax < 3.7320437e-37f)) {
-          float iscale = -127.0f / m;
-#pragma unroll
-          for (int j = 0; j < 8; j++) {
-            int ci = (int)__builtin_rintf(iscale * v[j]);
-            if (ci > 127) ci = 127;
-            uint32_t c = (uint32_t)ci & 255u;
-            if (j < 4) c0 |= c << (8 * j);
-            else c1 |= c << (8 * (j - 4));
-          }
-          dx = 1.0f / iscale;
-        }
-      }
       if (has) {
         ((uint2*)xs)[q] = make_uint2(c0, c1);
         if ((q & 3) == 0) dxs[q >> 2] = dx;
@@ -690,6 +711,7 @@ __device__ __forceinline__ void load_tiles(const uint8_t* w, const uint8_t* w2, 
 template <int F, int MODE, int U, int R, bool GLU, bool NORM>
 __device__ __forceinline__ void gemv(const LinArgs& a)
 {
+  IHIP_STAMP_SCOPE;
   const int lane = threadIdx.x & 63;
   const int lpr = a.lpr;
   const int lr = lane & (lpr - 1);
@@ -714,7 +736,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     nrows = min(R, it.z);
     xrow0 = yrow0 = 0;
   } else if (a.ids) {
-    const bool routed = R == 1 && GLU && NORM && a.rl != nullptr;
+    const bool routed = R == 1 && GLU && a.rl != nullptr;
     // a self-routed token: row 0 of the launch forms the route, row 1 + s
     // computes slot s
     const int slot = routed ? (int)blockIdx.y - 1 : (int)blockIdx.y;
@@ -791,14 +813,14 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     // a self-routed token: the router logits first (the route needs them
     // before any weight address is known)
     float rlg[4];
-    if (GLU && NORM && a.ids && a.rl) route_logits(a.rl, a.rexp, rlg);
+    if (GLU && a.ids && a.rl) route_logits(a.rl, a.rexp, rlg);
     XStage st;
     const bool quantized = !NORM && stage_q8<F, MODE>() && a.xq != nullptr;
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
                               quantized ? a.xq + xrow0 * (int64_t)(a.in + 4 * G) : nullptr, a.in,
                               a.nw, st);
     IHIP_STAMP(6);
-    if (GLU && NORM && a.ids && a.rl) {
+    if (GLU && a.ids && a.rl) {
       // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
       // of this block's slot; the launch's extra row writes the picks and
       // weights for the down launch
@@ -1324,10 +1346,13 @@ __device__ __forceinline__ void gemv_flt(const LinArgs& a)
   const int NC = a.in / VPC;  // chunks per row: at most 64 NJ
   const int nj = (NC + 63) / 64;
   const int64_t rb = (int64_t)a.in * ES;  // row bytes
-  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
+  // with xq_out the launch's last block quantizes the normed row and takes
+  // no rows (beside the row blocks, off their path)
+  const bool qblock = NORM && a.xq_out && blockIdx.x == gridDim.x - 1;
+  const int64_t nw = (int64_t)(gridDim.x - (NORM && a.xq_out ? 1 : 0)) * (NT >> 6);
   const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
   __shared__ __align__(16) float xs[XN];
-  if ((int64_t)blockIdx.x * (NT >> 6) >= total) return;  // the whole block: no rows
+  if (!qblock && (int64_t)blockIdx.x * (NT >> 6) >= total) return;  // the whole block: no rows
   // (selected, not indexed: an index into the argument block would move it
   // to scratch memory)
   auto wrow = [&](int64_t g, int& sg, int& o) -> const uint8_t* {
@@ -1354,6 +1379,32 @@ __device__ __forceinline__ void gemv_flt(const LinArgs& a)
   load(g, wv);
   stage_store<F, 1, NORM>(st, false, a.in, a.eps, (uint8_t*)xs, nullptr, a.bad, 1);
   __syncthreads();
+  if constexpr (NORM) {
+    // the normed row quantized for the next launch: wave w of the last block
+    // takes 64 quarters (2 super-blocks, 16 groups) at a time, from quarter
+    // 64 w on
+    if (qblock) {
+      const int nq = a.in >> 3;
+      for (int q0 = (int)(threadIdx.x >> 6) * 64; q0 < nq; q0 += 256) {
+        const int q = q0 + lane;
+        float v[8];
+        const float4 u0 = ((const float4*)xs)[2 * min(q, nq - 1)], u1 = ((const float4*)xs)[2 * min(q, nq - 1) + 1];
+        v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+        v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+        uint32_t c0, c1;
+        float dx;
+        bool nonfinite;
+        if (a.xq_k8) quant_quarter<true>(v, q, c0, c1, dx, nonfinite);
+        else quant_quarter<false>(v, q, c0, c1, dx, nonfinite);
+        if (q < nq) {
+          ((uint2*)a.xq_out)[q] = make_uint2(c0, c1);
+          if ((q & 3) == 0) ((float*)(a.xq_out + a.in))[q >> 2] = dx;
+          if (nonfinite && a.bad) a.bad[0] = 1;
+        }
+      }
+      return;
+    }
+  }
   while (g < total) {
     // the next row's weights in flight during this row's sums
     const int64_t gn = g + nw;

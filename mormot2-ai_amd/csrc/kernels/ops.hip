@@ -1354,7 +1354,7 @@ struct AttnOneArgs {
   // launches, or null: with them the last
   // range block of a head to finish merges the head's ranges (and sets its
   // counter back to zero), else attention_merge does
-  int* done;
+  int* done;  int32_t place, pad;  // f16 one-row launch: 0 blocks by head, 1 by KV group over the XCDs
 };
 
 // the sums of two values over a block of 256 (wave sums, then 4 waves)
@@ -1375,6 +1375,7 @@ __device__ __forceinline__ void block_sum2(double& a, double& b, double* red)
 template <bool F16, int HD>
 __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
 {
+  IHIP_STAMP_SCOPE;
   __shared__ double qd[HD];
   __shared__ float nq[HD], nk[HD];
   __shared__ float knew[HD], vnew[HD];
@@ -1651,15 +1652,304 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   }
 }
 
+// ---------------------------------------------- the f16 decode attention
+// The f16-cache decode step of attention_one_t, its arithmetic bit for bit,
+// with the launch laid out for the chip:
+//  - blocks by KV group: the 1-D grid's block lin runs on XCD lin % 8, and
+//    XCD c takes KV group c / X (X = 8 / kvh XCDs a group) over every X-th
+//    key range, all heads of the group: each key and value tile is fetched
+//    into one L2 (by head, a group's heads spanned two XCDs and both L2s
+//    fetched its tiles);
+//  - the range's keys and values through buffer loads bounded by the range's
+//    rows (a row past them, and the new key's row not yet written, reads 0):
+//    no per-load 64-bit address or clamp, no per-key select;
+//  - the head norms and RoPE in wave 0 alone (a lane holds the pairs of its
+//    dimensions: no block reduction), while the tiles are on their way.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded(const void* p, uint32_t bytes)
+{
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// block lin of heads * splits: its head, its range, and whether every range
+// block of the head runs on one XCD (its partials then meet in that L2)
+__device__ __forceinline__ void attn_one_block(int lin, int heads, int kvh, int splits, int& h,
+                                               int& s, bool& xcd, int place)
+{
+  if (place == 0 && (heads & 7) == 0) {
+    // by head: XCD c takes heads c * heads / 8 .. over every range
+    h = xcd_head((unsigned)(lin % heads), heads);
+    s = lin / heads;
+    xcd = true;
+  } else if ((heads & 7) == 0 && kvh <= 8 && (8 % kvh) == 0) {
+    const int X = 8 / kvh, hpg = heads / kvh;  // the host rounds splits to a multiple of X
+    const int c = lin & 7, r = lin >> 3;
+    h = (c / X) * hpg + r % hpg;
+    s = (r / hpg) * X + c % X;
+    xcd = X == 1;
+  } else {
+    h = lin % heads;
+    s = lin / heads;
+    xcd = false;
+  }
+  (void)splits;
+}
+
+template <int HD>
+__device__ __forceinline__ void attention_one_f16(const AttnOneArgs& a)
+{
+  IHIP_STAMP_SCOPE;
+  constexpr int d = HD, half = HD / 2;
+  constexpr int QPL = HD / 64;                  // dimensions of the head per lane of wave 0
+  constexpr int KROW = HD * 2 / 16;             // 16-byte words of a key row
+  constexpr int KLD = ATT_CHUNK * KROW / 256;   // key words per thread
+  constexpr int KPAD = KROW + 1;                // odd row pitch: the per-key reads hit distinct banks
+  constexpr int lpk = HD / 2;                   // value pass: lanes per key (a dimension pair each)
+  constexpr int kpw = 64 / lpk;                 // keys side by side in a wave
+  constexpr int step = 4 * kpw;
+  constexpr int VB = ATT_CHUNK / step;          // a lane's keys
+  __shared__ double qd[HD];
+  __shared__ double sc[ATT_CHUNK];
+  __shared__ double red[8];
+  __shared__ double accs[4][HD];
+  __shared__ uint4 ks[ATT_CHUNK * KPAD];
+  const int t = threadIdx.x, w = t >> 6, l = t & 63;
+  int h, s;
+  bool xcd;
+  attn_one_block(blockIdx.x, a.heads, a.kvh, a.splits, h, s, xcd, a.place);
+  IHIP_STAMP(0);
+  const int kvw = a.kvh * d;
+  const uint32_t rowb = (uint32_t)kvw * 2u;  // bytes of a cache row
+  const int g = h / (a.heads / a.kvh);
+  const int past = a.pastp ? *a.pastp : a.past;
+  const int total = past + 1;
+  const int first = (a.window > 0 && total > a.window) ? total - a.window : 0;
+  const int cnt = total - first;
+  const int j0 = min(cnt, s * ATT_CHUNK), j1 = min(cnt, j0 + ATT_CHUNK);
+  const int n = j1 - j0;
+  const bool hasnew = n > 0 && j1 == cnt;  // the range holds the new key, its last row
+  const int jn = n - 1;
+  const int nload = hasnew ? n - 1 : n;    // rows already in the cache
+  double* out = a.part + ((int64_t)h * a.splits + s) * (d + 2);
+  const int64_t rbase = (int64_t)(first + j0) * kvw + (int64_t)g * d;  // halves
+  const auto kr = bounded((const uint16_t*)a.kc + rbase, (uint32_t)nload * rowb);
+  const auto vr = bounded((const uint16_t*)a.vc + rbase, (uint32_t)nload * rowb);
+  const int lane_key = l / lpk, pair = l % lpk;
+  const int jb0 = w * kpw + lane_key;  // value pass: key jb0 + u * step
+
+  // ---- every load first: wave 0 the head's q (and the new key), every
+  // thread its key words and value pairs
+  float qv[QPL], qw[QPL], kv[QPL], kw[QPL], cv[QPL], sv[QPL];
+  if (w == 0) {
+#pragma unroll
+    for (int i = 0; i < QPL; i++) {
+      const int e = l + 64 * i, p = e % half;
+      qv[i] = a.q[(int64_t)h * d + e];
+      qw[i] = a.qn ? a.qn[e] : 1.f;
+      kv[i] = hasnew ? a.k[(int64_t)g * d + e] : 0.f;
+      kw[i] = (hasnew && a.kn) ? a.kn[e] : 1.f;
+      cv[i] = a.cs[p];
+      sv[i] = a.cs[half + p];
+    }
+  }
+  uint4 kt[KLD];
+  const uint32_t koff = (uint32_t)(t / KROW) * rowb + (uint32_t)(t % KROW) * 16u;
+#pragma unroll
+  for (int r = 0; r < KLD; r++)
+    kt[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          kr, (int)(koff + (uint32_t)r * (256u / KROW) * rowb), 0, 0));
+  uint32_t vv[VB];
+  const uint32_t voff = (uint32_t)jb0 * rowb + (uint32_t)pair * 4u;
+#pragma unroll
+  for (int u = 0; u < VB; u++)
+    vv[u] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)(voff + (uint32_t)(u * step) * rowb), 0, 0);
+  // the new value (its f16 bits, as the cache holds it) for the wave and
+  // lanes whose chain holds the new key
+  const bool vlane = hasnew && w == (jn % step) / kpw && lane_key == (jn % kpw);
+  float vn0 = 0.f, vn1 = 0.f;
+  if (vlane) {
+    const float2 x = *(const float2*)(a.v + (int64_t)g * d + 2 * pair);
+    const uint16_t h0 = float_to_half(x.x), h1 = float_to_half(x.y);
+    vn0 = half_to_float(h0);
+    vn1 = half_to_float(h1);
+    ((uint32_t*)a.vc)[((int64_t)past * kvw + (int64_t)g * d) / 2 + pair] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+  }
+  IHIP_STAMP(1);
+
+  // ---- wave 0: the head norms (qkrope's arithmetic: the sums of squares
+  // of dimensions 0..63 and 64..127 as the two waves of a block formed
+  // them) and RoPE of q and the new key
+  if (w == 0) {
+    double sqa = (double)qv[0] * (double)qv[0], ska = (double)kv[0] * (double)kv[0];
+    double sq = wave_sum(sqa, 64), sk = wave_sum(ska, 64);
+    if constexpr (QPL == 2) {
+      const double sqb = (double)qv[1] * (double)qv[1], skb = (double)kv[1] * (double)kv[1];
+      sq = sq + wave_sum(sqb, 64);
+      sk = sk + wave_sum(skb, 64);
+    }
+    float xq[QPL], xk[QPL];
+#pragma unroll
+    for (int i = 0; i < QPL; i++) {
+      xq[i] = qv[i];
+      xk[i] = kv[i];
+      if (a.qn) xq[i] = qw[i] * (float)((double)qv[i] * (1.0 / sqrt(sq / (double)d + a.eps)));
+      if (hasnew && a.kn) xk[i] = kw[i] * (float)((double)kv[i] * (1.0 / sqrt(sk / (double)d + a.eps)));
+    }
+    // the pair (p, p + half): in one lane (HD 128), in lanes l and l ^ 32 (HD 64)
+    double x0, x1, k0, k1;
+    if constexpr (QPL == 2) {
+      x0 = xq[0]; x1 = xq[1]; k0 = xk[0]; k1 = xk[1];
+    } else {
+      const float pq = xpart<32>(xq[0]), pk = xpart<32>(xk[0]);
+      const bool lo = l < half;
+      x0 = lo ? xq[0] : pq; x1 = lo ? pq : xq[0];
+      k0 = lo ? xk[0] : pk; k1 = lo ? pk : xk[0];
+    }
+    const double c = cv[0], sn = sv[0];
+    const double r0 = (double)(float)(x0 * c - x1 * sn), r1 = (double)(float)(x1 * c + x0 * sn);
+    const float o0 = (float)(k0 * c - k1 * sn), o1 = (float)(k1 * c + k0 * sn);
+    uint16_t* knew = (uint16_t*)&ks[jn * KPAD];
+    const int64_t dst = (int64_t)past * kvw + (int64_t)g * d;
+    if constexpr (QPL == 2) {
+      qd[l] = r0;
+      qd[l + 64] = r1;
+      if (hasnew) {
+        const uint16_t h0 = float_to_half(o0), h1 = float_to_half(o1);
+        ((uint16_t*)a.kc)[dst + l] = h0;
+        ((uint16_t*)a.kc)[dst + l + 64] = h1;
+        knew[l] = h0;
+        knew[l + 64] = h1;
+      }
+    } else {
+      const bool lo = l < half;
+      qd[l] = lo ? r0 : r1;
+      if (hasnew) {
+        const uint16_t hk = float_to_half(lo ? o0 : o1);
+        ((uint16_t*)a.kc)[dst + l] = hk;
+        knew[l] = hk;
+      }
+    }
+  }
+  // the key words into LDS (the new key's row is wave 0's)
+#pragma unroll
+  for (int r = 0; r < KLD; r++) {
+    const int q = t + 256 * r, row = q / KROW;
+    if (!(hasnew && row == jn)) ks[row * KPAD + q % KROW] = kt[r];
+  }
+  __syncthreads();
+
+  // ---- scores (attention_one_t's): two threads a key, four chains each
+  IHIP_STAMP(2);
+  double m = -1.0e308;
+  {
+    const int kk = t >> 1, hh = t & 1;
+    double c4[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < KROW / 2; k++) {
+      const int kw2 = hh * (KROW / 2) + k;
+      const uint4 kw4 = ks[kk * KPAD + kw2];
+      const uint32_t wv[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = 8 * kw2 + 2 * j;
+        c4[(2 * j) & 3] = __builtin_fma(qd[i], (double)half_to_float(wv[j] & 0xffffu), c4[(2 * j) & 3]);
+        c4[(2 * j + 1) & 3] =
+            __builtin_fma(qd[i + 1], (double)half_to_float(wv[j] >> 16), c4[(2 * j + 1) & 3]);
+      }
+    }
+    const double part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+    double acc = part + xpart<1>(part);
+    acc = acc * a.scale;
+    if (kk < n) {
+      if (hh == 0) sc[kk] = acc;
+      m = acc;
+    }
+  }
+  __syncthreads();
+  m = wave_max(m);
+  if (l == 0) red[w] = m;
+  __syncthreads();
+  m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+  double e = 0;
+  if (t < n) {
+    e = exp(sc[t] - m);
+    sc[t] = e;
+  } else if (t < ATT_CHUNK) {
+    sc[t] = 0.0;
+  }
+  e = wave_sum(e, 64);
+  __syncthreads();
+  if (l == 0) red[4 + w] = e;
+
+  // ---- the weighted values: even and odd key slots in two chains per
+  // dimension; a row past the range read 0 (weight 0), the new key's value
+  // added after its chain's last nonzero term, where its slot puts it
+  IHIP_STAMP(3);
+  double a0e = 0, a1e = 0, a0o = 0, a1o = 0;
+#pragma unroll
+  for (int u = 0; u < VB; u++) {
+    const double p = sc[jb0 + u * step];
+    const double x0 = half_to_float(vv[u] & 0xffffu), x1 = half_to_float(vv[u] >> 16);
+    if (u & 1) {
+      a0o = __builtin_fma(p, x0, a0o);
+      a1o = __builtin_fma(p, x1, a1o);
+    } else {
+      a0e = __builtin_fma(p, x0, a0e);
+      a1e = __builtin_fma(p, x1, a1e);
+    }
+  }
+  if (vlane) {
+    const double p = sc[jn];
+    if ((jn / step) & 1) {
+      a0o = __builtin_fma(p, (double)vn0, a0o);
+      a1o = __builtin_fma(p, (double)vn1, a1o);
+    } else {
+      a0e = __builtin_fma(p, (double)vn0, a0e);
+      a1e = __builtin_fma(p, (double)vn1, a1e);
+    }
+  }
+  double a0 = a0e + a0o, a1 = a1e + a1o;
+  if constexpr (lpk == 32) {
+    a0 = a0 + xpart<32>(a0);
+    a1 = a1 + xpart<32>(a1);
+  }
+  if (lane_key == 0) {
+    accs[w][2 * pair] = a0;
+    accs[w][2 * pair + 1] = a1;
+  }
+  __syncthreads();
+  IHIP_STAMP(4);
+  auto put = [&](double* p, double v) {
+    if (xcd) *p = v;
+    else store_agent(p, v);
+  };
+  if (n > 0) {
+    for (int i = t; i < d; i += 256) put(out + i, (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]));
+    if (t == 0) {
+      put(out + d, m);
+      put(out + d + 1, (red[4] + red[5]) + (red[6] + red[7]));
+    }
+  } else if (t == 0) {
+    put(out + d, -1.0e308);
+    put(out + d + 1, 0.0);
+  }
+  if (a.done && last_block(a.done + h * 32, a.splits, xcd)) {
+    IHIP_STAMP(5);
+    merge_ranges<true>(a.part + (int64_t)h * a.splits * (d + 2), a.splits, d,
+                       a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d, xcd);
+    IHIP_STAMP(6);
+    if (t == 0) a.done[h * 32] = 0;
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_64(AttnOneArgs a)
 {
   ihip::touch_kernargs<sizeof(AttnOneArgs)>();
-  attention_one_t<true, 64>(a);
+  attention_one_f16<64>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f16_128(AttnOneArgs a)
 {
   ihip::touch_kernargs<sizeof(AttnOneArgs)>();
-  attention_one_t<true, 128>(a);
+  attention_one_f16<128>(a);
 }
 extern "C" __global__ __launch_bounds__(256, 1) void attention_one_f32_64(AttnOneArgs a)
 {
@@ -2273,6 +2563,7 @@ extern "C" __global__ __launch_bounds__(1024) void sample_pick(SampleArgs a)
   __shared__ uint32_t cnt[SBK];
   __shared__ uint64_t mass[SBK];
   const int t = threadIdx.x;
+  IHIP_STAMP_SCOPE;
   IHIP_STAMP(0);
   const int best = *a.best;
   __syncthreads();  // every thread has read best before it may be overwritten

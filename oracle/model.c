@@ -30,6 +30,9 @@ struct orc_model {
   float** conv;
   float** state;
   int recurrent;
+  /* a test's capture of the residual rows after layer dbg_layer */
+  float* dbg;
+  int64_t dbg_layer;
 };
 
 static uint64_t row_bytes(int t, int64_t cols)
@@ -98,6 +101,12 @@ void orc_model_route_record(orc_model* m, int32_t* ids, float* w, int64_t cap)
 }
 
 int64_t orc_model_route_recorded(orc_model* m) { return m->rec_rows; }
+
+void orc_model_debug_layer(orc_model* m, int64_t layer, float* rows)
+{
+  m->dbg = rows;
+  m->dbg_layer = layer;
+}
 
 double orc_model_route_gap(orc_model* m)
 {
@@ -420,6 +429,8 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       const float sc = *(const float*)L->scalar.data;
       for (int64_t i = 0; i < n * h; i++) x[i] = x[i] * sc;
     }
+    if (m->dbg && (m->dbg_layer < 0 || l == m->dbg_layer))
+      memcpy(m->dbg + (m->dbg_layer < 0 ? (size_t)l * n * h : 0), x, (size_t)(n * h) * 4);
   }
   if (!err) {
     m->length = past + n;

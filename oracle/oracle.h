@@ -154,6 +154,8 @@ double orc_model_route_gap(orc_model* m);
  * routed row from now on appended to ids / w [cap][k] (NULL: off) */
 void orc_model_route_record(orc_model* m, int32_t* ids, float* w, int64_t cap);
 int64_t orc_model_route_recorded(orc_model* m);
+/* a test hook: the residual rows after layer `layer` (-1: every layer, one after another) of each later forward copied to rows (NULL: off) */
+void orc_model_debug_layer(orc_model* m, int64_t layer, float* rows);
 int orc_model_forward(orc_model* m, const int32_t* ids, int64_t count,
                       float* logits, int all_logits);
 /* decoder.pas:3390-3426 Greedy; margins[i] = top1 - top2 logit of step i */
