@@ -237,7 +237,7 @@ def decode_kernels(ctx, model, spec, first, steps, past):
 
 
 PROFILED = {  # roofline kernel -> its committed counter profile
-    "gemv_q4_k_q8_norm_glu": "gemv_q4_k_q8_norm_glu_route_8x768x2048_traffic.txt",
+    "gemv_q4_k_q8_glu": "gemv_q4_k_q8_glu_route_8x768x2048_traffic.txt",
 }
 
 
