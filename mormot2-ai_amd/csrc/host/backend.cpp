@@ -271,14 +271,15 @@ bool linear_ok(int t, int64_t in)
 // equal choices: narrow rows (more groups per lane: a row's lane sums and its
 // addressing are paid once per U groups) when the matrix still gives every CU
 // four tiles of them, else wide rows (more waves for a short matrix)
-static void pick_lpr_order(int64_t G, const int (&order)[4], int& lpr, int& U)
+static void pick_lpr_order(int64_t G, const int (&order)[4], int& lpr, int& U, int ulimit = 4)
 {
   // at most this many groups per lane (IHIP_GEMV_UMAX, 1..4: fewer give
   // wider rows, shorter per-lane work, more waves)
-  static const int umax = [] {
+  static const int umax_env = [] {
     const char* v = getenv("IHIP_GEMV_UMAX");
     return v ? std::min(4, std::max(1, atoi(v))) : 4;
   }();
+  const int umax = std::min(umax_env, ulimit);
   int best = -1;
   for (int l : order) {
     int u = (int)((G + l - 1) / l);
@@ -291,6 +292,8 @@ static void pick_lpr_order(int64_t G, const int (&order)[4], int& lpr, int& U)
     }
   }
 }
+
+static const int glu_order[4] = {8, 16, 32, 64};
 
 static void pick_lpr(int64_t G, int64_t out, int cus, int& lpr, int& U)
 {
@@ -360,6 +363,17 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
   // decide between narrow and wide rows
   if (k.ids && !k.cw && !k.items) out_max *= std::max<int64_t>(1, k.rows);
   pick_lpr(G, out_max, c->cus, lpr, U);
+  // a token's experts through the fused gate/up: at most 2 groups a lane (rows
+  // of more lanes, twice the blocks of 4 groups a lane, each with half the
+  // bytes: measured faster for these short matrices)
+  if (k.w2 && k.ids && !k.items && U > 2) {
+    int l2 = lpr, u2 = U;
+    pick_lpr_order(G, glu_order, l2, u2, 2);
+    if ((int64_t)l2 * u2 == G) {  // (when no lane idles for it)
+      lpr = l2;
+      U = u2;
+    }
+  }
   uint64_t xq = k.xq;
   const int mode = k.mode & 1;
   const bool q8 = mode == IHIP_MODE_Q8 && q8_kind(k.dtype) >= 0;
