@@ -425,6 +425,7 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     const float* rscale;
     uint8_t* xq_out;
     int32_t xq_k8, xq_pad;
+    int32_t bstart[4];
   } a = {(const uint8_t*)k.w, (const float*)k.x, (const uint8_t*)xq, (const float*)k.bias,
          (float*)k.y, (const int*)k.ids, k.stride, (int32_t)k.out, (int32_t)k.in,
          (int32_t)k.rows, lpr, k.x_per_slot, k.nexp, (const void*)k.items, (const int*)k.perm,
@@ -436,7 +437,8 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
          {(float*)k.yseg[0], (float*)k.yseg[1], (float*)k.yseg[2]},
          {(int32_t)k.oseg[0], (int32_t)k.oseg[1], (int32_t)k.oseg[2]},
          k.dtype2 ? k.nseg1 : k.nseg, (const float*)k.rl, (float*)k.rw, (int32_t)k.rexp,
-         (int32_t)k.rk, (int32_t)k.rnorm, 0, (const float*)k.rscale, (uint8_t*)k.xq_out, k.xq_k8, 0};
+         (int32_t)k.rk, (int32_t)k.rnorm, 0, (const float*)k.rscale, (uint8_t*)k.xq_out, k.xq_k8, 0,
+         {0, 0, 0, 0}};
   if (k.rl && (!k.ids || !k.rw || !k.w2 || !(k.nw || xq) || k.batch_rows() || k.rexp < 1 || k.rexp > 256 || k.rk < 1 ||
                k.rk > std::min<int64_t>(k.rexp, 8) || k.rk != k.rows))
     return fail(IHIP_E_ARG, "EnqueueLinear: self-routing takes one token's <= 8 slots of <= 256 experts, gate/up with a norm or a quantized row");
@@ -638,6 +640,24 @@ int enqueue_linear(ihip_ctx* c, const LinearCall& k)
     // rest of the rows, each block stages its row once
     const int64_t hold = ((int64_t)c->cus * resident_blocks(c, name, 256) * c->gemv_hold + share - 1) / share;
     wgs = std::max<int64_t>(1, std::min(wgs, hold));
+    static const bool seg1d = [] {
+      const char* v = getenv("IHIP_GEMV_SEG1D");
+      return !v || atoi(v) != 0;
+    }();
+    if (k.nseg > 1 && seg1d) {
+      // one index space: each matrix its own blocks, sized as above for its
+      // own rows, none idle
+      int64_t start = 0;
+      for (int i = 0; i < k.nseg; i++) {
+        const int64_t ti = (k.oseg[i] + rpw - 1) / rpw;
+        const int64_t bi = std::max<int64_t>(1, std::min(wgs, (ti + 4 * T - 1) / (4 * T)));
+        a.bstart[i] = (int32_t)start;
+        start += bi;
+      }
+      a.bstart[k.nseg] = (int32_t)start;
+      if (k.nseg == 2) a.bstart[3] = (int32_t)start;
+      return launch(c, name, dim3((unsigned)start, 1), dim3(256), &a);
+    }
   }
   return launch(c, name, dim3((unsigned)wgs, gy), dim3(256), &a);
 }

@@ -88,7 +88,21 @@ struct LinArgs {
   // floats: the next launch over the same normed row takes it as given
   uint8_t* xq_out;
   int32_t xq_k8, xq_pad;
+  // matrices of one launch in one index space of blocks (bstart[1] > 0):
+  // blocks [bstart[s], bstart[s + 1]) take matrix s, so the blocks of every
+  // matrix are dispatched in the first round (by blockIdx.y, the blocks of
+  // a short matrix came after every block of the long one)
+  int32_t bstart[4];
 };
+
+// the matrix of a block of a several-matrix launch (blockIdx.y, or its place
+// in the one index space)
+__device__ __forceinline__ int seg_of(const LinArgs& a)
+{
+  if (a.bstart[1] <= 0) return (int)blockIdx.y;
+  const int b = (int)blockIdx.x;
+  return (b >= a.bstart[1] ? 1 : 0) + (a.nseg > 2 && b >= a.bstart[2] ? 1 : 0);
+}
 
 // F32 mode: the group's contribution to the row sum. x: the 32 activations,
 // sx their sum. Every code is turned into its exact value (signed, offset
@@ -722,6 +736,7 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   const float* bias = a.bias;
   int out = a.out;
   float* yp = a.y;
+  int bx = (int)blockIdx.x, gx = (int)gridDim.x;  // the block among its matrix's
   int64_t xrow0, yrow0;
   int nrows;
   int pstart = -1;  // grouped: the first entry of perm
@@ -783,8 +798,12 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     yrow0 = slot;
     nrows = 1;
   } else if (R == 1 && a.nseg > 1) {
-    // several matrices of this type over the same row: blockIdx.y = matrix
-    const int sg = blockIdx.y;
+    // several matrices of this type over the same row
+    const int sg = seg_of(a);
+    if (a.bstart[1] > 0) {
+      bx -= a.bstart[sg];
+      gx = a.bstart[sg + 1] - a.bstart[sg];
+    }
     w = a.wseg[sg];
     bias = a.bseg[sg];
     out = a.oseg[sg];
@@ -798,12 +817,12 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
   }
   const Regions rg = regions(F, out, a.in);
   const int64_t tiles = ((int64_t)out + rpw - 1) / rpw;
-  const int64_t nw = (int64_t)gridDim.x * (NT >> 6);
-  const int64_t wid = (int64_t)blockIdx.x * (NT >> 6) + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gx * (NT >> 6);
+  const int64_t wid = (int64_t)bx * (NT >> 6) + (threadIdx.x >> 6);
 
   if constexpr (R == 1) {
     IHIP_STAMP(0);
-    if ((int64_t)blockIdx.x * (NT >> 6) >= tiles) return;  // the whole block: no tile
+    if ((int64_t)bx * (NT >> 6) >= tiles) return;  // the whole block: no tile
     // T tiles per wave step, their weight loads issued together (and the
     // first ones before the activation row is read), so a wave keeps several
     // 16-byte loads per lane in flight
@@ -1688,7 +1707,7 @@ __device__ __forceinline__ void dequant(const DeqArgs& a)
   extern "C" __global__ __launch_bounds__(256) void NAME(ihip::LinArgs a)               \
   {                                                                                    \
     ihip::touch_kernargs<sizeof(ihip::LinArgs)>();                                     \
-    if ((int)blockIdx.y < a.nseg1) ihip::gemv<F, M, U, 1, false, true>(a);             \
+    if (ihip::seg_of(a) < a.nseg1) ihip::gemv<F, M, U, 1, false, true>(a);             \
     else ihip::gemv<F2, M, U, 1, false, true>(a);                                      \
   }
 #define IHIP_GEMV_MIX_U(PFX, F, F2, M) \
