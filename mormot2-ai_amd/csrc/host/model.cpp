@@ -75,6 +75,14 @@ struct ihip_mctx {
   uint64_t qkv = 0, z = 0, beta = 0, decay = 0, core = 0, qg = 0, gq = 0;
   // Gemma 4: the second rotary set's cos/sin, the experts' sum of a row
   uint64_t cs2 = 0, moe = 0;
+  // the rotary rows of positions 0 .. cs_rows - 1 (cs_cap allocated), and the
+  // second set's: the decode graph's last launch takes the next position's
+  // rows from them
+  uint64_t cs_tab = 0, cs2_tab = 0;
+  int64_t cs_rows = 0, cs_cap = 0;
+  // pinned staging of the ids of a pipelined decode
+  int32_t* ids_pinned = nullptr;
+  int64_t ids_pinned_n = 0;
   // the restore points of the DeltaNet states (TDecoderContext.CheckpointId,
   // MaxCheckpoints, decoder.pas:466-620, :1049-1230): the states before the
   // CheckpointId tokens of aligned parts, the oldest first; each in a slot of
@@ -1169,6 +1177,7 @@ static int head(ihip_mctx* s, int64_t n, bool all, uint64_t y)
 // decoder.pas:996-1230)
 
 static int dalloc_ctx(ihip_mctx* s, uint64_t bytes, uint64_t& p);
+static void free_owned(ihip_mctx* s, uint64_t& p);
 
 static bool ckpt_on(const ihip_mctx* s) { return s->m->recurrent && s->ckpt_id >= 0 && s->ckpt_max > 0; }
 
@@ -1380,7 +1389,59 @@ static int decode_body(ihip_mctx* s)
   if (!rc) rc = head(s, 1, false, s->logits);
   if (!rc) rc = softcap(s, 1, s->logits);
   if (!rc) rc = next_token(s);
+  if (!rc && c->capturing && s->cs_tab) {
+    // the next step's token, position and rotary rows (a pipelined decode
+    // enqueues the steps without reading the ids back in between)
+    struct {
+      const int* next;
+      int* tok;
+      int* pos;
+      float* cs;
+      const float* tab;
+      float* cs2;
+      const float* tab2;
+      int32_t rs, rs2, rows, pad;
+    } aa = {(const int*)s->next, (int*)s->tok, (int*)s->pos, (float*)s->cs, (const float*)s->cs_tab,
+            m->hd2 ? (float*)s->cs2 : nullptr, m->hd2 ? (const float*)s->cs2_tab : nullptr,
+            (int32_t)m->d.head_dim, (int32_t)std::max<int64_t>(m->hd2, 0), (int32_t)s->cs_cap, 0};
+    rc = launch(c, "decode_advance", dim3(1), dim3(256), &aa);
+  }
   return rc;
+}
+
+// the rotary table rows of positions [0, upto) (grown to the context's
+// capacity + 1 rows; rows already there are kept)
+static int cs_table(ihip_mctx* s, int64_t upto)
+{
+  ihip_model* m = s->m;
+  ihip_ctx* c = m->c;
+  const int64_t rs = m->d.head_dim, rs2 = m->hd2;
+  const int64_t cap = s->capacity + 1;
+  if (s->cs_cap < cap) {
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    free_owned(s, s->cs_tab);
+    free_owned(s, s->cs2_tab);
+    s->cs_rows = s->cs_cap = 0;
+    int rc = dalloc_ctx(s, (uint64_t)cap * rs * 4, s->cs_tab);
+    if (!rc && rs2 > 0) rc = dalloc_ctx(s, (uint64_t)cap * rs2 * 4, s->cs2_tab);
+    if (rc) return rc;
+    s->cs_cap = cap;
+    s->graph_ready = false;  // the graph holds the table's address
+  }
+  upto = std::min(upto, s->cs_cap);
+  if (upto <= s->cs_rows) return 0;
+  const int64_t n = upto - s->cs_rows;
+  std::vector<float> t((size_t)(n * rs), 0.f), t2((size_t)std::max<int64_t>(n * rs2, 1), 0.f);
+  for (int64_t r = 0; r < n; r++) {
+    rotary(m->d, s->cs_rows + r, 1, t.data() + r * rs);
+    if (rs2 > 0) rotary2(m->d, rs2, s->cs_rows + r, 1, t2.data() + r * rs2);
+  }
+  IHIP_CHECK(hipMemcpyHtoD((hipDeviceptr_t)(s->cs_tab + (uint64_t)s->cs_rows * rs * 4), t.data(), t.size() * 4));
+  if (rs2 > 0)
+    IHIP_CHECK(hipMemcpyHtoD((hipDeviceptr_t)(s->cs2_tab + (uint64_t)s->cs_rows * rs2 * 4), t2.data(),
+                             t2.size() * 4));
+  s->cs_rows = upto;
+  return 0;
 }
 
 // the context's decode graph, captured for its capacity (the attention's
@@ -1556,12 +1617,53 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
   // a graph holds this context's cache and ranges: captured again when the
   // cache grew or the sampler changed since
   const bool graphs = m->use_graphs && !m->check_route && m->tape_rows == 0;
+  // the graph's last launch advances token, position and rotary rows: the
+  // steps of a model without a recurrent state (whose restore points need
+  // each id on the host) go out back to back, the ids read once at the end
+  static const bool pipeline_on = [] {
+    const char* v = getenv("IHIP_DECODE_PIPELINE");
+    return !v || atoi(v) != 0;
+  }();
+  const bool pipelined = pipeline_on && graphs && !m->recurrent && steps > 1;
+  if (graphs && (rc = cs_table(s, s->length + steps + 1))) return rc;
   if (graphs && (!s->graph_ready || s->graph_capacity != s->capacity ||
                         s->graph_sampler != m->sampler_epoch || s->graph_draw != s->draw_ids) &&
       (rc = decode_graph(s)))
     return rc;
   std::vector<float> cs(m->d.head_dim), cs2(std::max<int64_t>(m->hd2, 1));
   int32_t tok = first;
+  if (pipelined) {
+    if (s->ids_pinned_n < steps) {
+      IHIP_CHECK(hipStreamSynchronize(c->stream));
+      if (s->ids_pinned) (void)hipHostFree(s->ids_pinned);
+      s->ids_pinned = nullptr;
+      s->ids_pinned_n = 0;
+      IHIP_CHECK(hipHostMalloc((void**)&s->ids_pinned, (size_t)steps * 4, hipHostMallocDefault));
+      s->ids_pinned_n = steps;
+    }
+    const int32_t pos = (int32_t)s->length;
+    if (m->hd2) {
+      rotary2(m->d, m->hd2, pos, 1, cs2.data());
+      IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs2, cs2.data(), cs2.size() * 4, c->stream));
+    }
+    rotary(m->d, pos, 1, cs.data());
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->tok, &tok, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->pos, &pos, 4, c->stream));
+    IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs, cs.data(), cs.size() * 4, c->stream));
+    for (int64_t i = 0; i < steps; i++) {
+      IHIP_CHECK(hipGraphLaunch(s->exec, c->stream));
+      IHIP_CHECK(hipMemcpyDtoHAsync(s->ids_pinned + i, (hipDeviceptr_t)s->next, 4, c->stream));
+    }
+    IHIP_CHECK(hipStreamSynchronize(c->stream));
+    for (int64_t i = 0; i < steps; i++) {
+      out_ids[i] = s->ids_pinned[i];
+      s->ids[s->length] = tok;
+      s->length++;
+      tok = out_ids[i];
+    }
+    s->state_ok = true;
+    return 0;
+  }
   for (int64_t i = 0; i < steps; i++) {
     int32_t pos = (int32_t)s->length;
     if (pos == 0 && m->recurrent && (rc = reset_states(s))) return rc;
@@ -1595,6 +1697,7 @@ static void context_free(ihip_mctx* s)
   if (!s) return;
   ihip_ctx* c = s->m->c;
   (void)hipStreamSynchronize(c->stream);
+  if (s->ids_pinned) (void)hipHostFree(s->ids_pinned);
   if (s->exec) (void)hipGraphExecDestroy(s->exec);
   if (s->graph) (void)hipGraphDestroy(s->graph);
   for (auto p : s->owned) (void)hipFree((void*)p);

@@ -2715,6 +2715,36 @@ extern "C" __global__ __launch_bounds__(256) void stream_read(StreamArgs a)
   if (acc == 0x9E3779B9u) a.out[0] = acc;
 }
 
+// ---------------------------------------------- the next decode step's inputs
+// The last launch of a decode step's graph: the step's sampled id becomes the
+// next step's token, the position advances, and the next position's rotary
+// rows (cos, sin) come from the context's table of positions, so the host
+// can enqueue the following steps without waiting for this one.
+struct AdvanceArgs {
+  const int* next;   // the id this step chose
+  int* tok;          // the next step's token
+  int* pos;          // the position, advanced by one
+  float* cs;         // the rotary row of a position [rs] (cos then sin)
+  const float* tab;  // [rows, rs]: the rows of positions 0 .. rows - 1
+  float* cs2;        // a second rotary set [rs2], or null
+  const float* tab2;
+  int32_t rs, rs2, rows, pad;
+};
+extern "C" __global__ __launch_bounds__(256) void decode_advance(AdvanceArgs a)
+{
+  const int p = *a.pos + 1;
+  if (p < a.rows) {
+    for (int i = threadIdx.x; i < a.rs; i += 256) a.cs[i] = a.tab[(int64_t)p * a.rs + i];
+    if (a.cs2)
+      for (int i = threadIdx.x; i < a.rs2; i += 256) a.cs2[i] = a.tab2[(int64_t)p * a.rs2 + i];
+  }
+  __syncthreads();  // every read of the position before it moves
+  if (threadIdx.x == 0) {
+    *a.tok = *a.next;
+    *a.pos = p;
+  }
+}
+
 // ------------------------------------------------------- MoE prompt plan
 struct PlanArgs {
   const int* ids;  // [slots] expert of each slot (route, sorted per token)
