@@ -992,8 +992,10 @@ __device__ __forceinline__ void gemm_flt(const GemmArgs& a)
 
 }  // namespace ihip
 
+// (three blocks a CU: the registers fit in 168, no spill; a b512 6144 x 2048
+// launch's 768 blocks then run in one round instead of one and a half)
 #define IHIP_GEMM(NAME, F)                                                                      \
-  extern "C" __global__ __launch_bounds__(256) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm<F>(a); } \
+  extern "C" __global__ __launch_bounds__(256, 3) void gemm_##NAME(ihip::GemmArgs a) { ihip::gemm<F>(a); } \
   extern "C" __global__ __launch_bounds__(256) void gemm8_##NAME(ihip::GemmArgs a)                    \
   {                                                                                                 \
     ihip::touch_kernargs<sizeof(ihip::GemmArgs)>();                                                 \
