@@ -420,6 +420,24 @@ __device__ __forceinline__ double row_value(const uint8_t* w, const Raw (&rawin)
     if (lpr > 16) tot = tot + xpart<16>(tot);
     if (lpr > 32) tot = tot + xpart<32>(tot);
     return tot;
+  } else if constexpr (!is_float_type(F)) {
+    // every group is formed (a group past the row reads clamped codes and a
+    // zeroed activation) and its term kept or dropped by a select, with no
+    // branch a group: adding +0.0 leaves a sum that starts at +0.0 as it is
+    float accf = 0.f;
+    double accd = 0.0;
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      const int g = lr + k * lpr;
+      const bool ok = valid && g < G;
+      float af = 0.f;
+      double ad = 0.0;
+      int isum = 0, msum = 0;
+      group_term<F, MODE>(w, raw[k], o, g, in, xg[k], af, ad, isum, msum);
+      accf += ok ? af : 0.f;
+      accd += ok ? ad : 0.0;
+    }
+    return row_total<F, MODE>(lpr, raw[0], 0.f, false, accf, accd, 0, 0, 0);
   } else {
     float accf = 0.f;
     double accd = 0.0;
