@@ -337,7 +337,9 @@ typedef struct {
   int32_t rope_set;        /* 0: the first rotary set, 1: the second (Rope2) */
   int32_t exp_gate_up;     /* 1: exp_gate is [E, 2 fi, h], per expert its gate
                               rows then its up rows; exp_up unused */
-  int32_t reserved1;
+  int32_t no_rope;         /* 1: no rotary positions on q and k in this layer
+                              (NoPE, TDecoderLayerSpec.NoRope, decoder.pas:139;
+                              SmolLM3's no_rope_layers, model.qwen3.pas:28-33) */
   ihip_tensor attn_out_norm; /* [h] F32: the attention output normed before
                                 the residual (SandwichNorm), or NULL */
   ihip_tensor ffn_out_norm;  /* [h] F32: the feed-forward output normed

@@ -47,6 +47,7 @@ struct DevLayer {
   // and the layer scalar (0: none)
   int64_t hd = 0, kvh = 0;
   int k_is_v = 0, rope_set = 0;
+  int no_rope = 0;  // no rotary positions on q and k (NoPE): the kernels get no rotary table
   uint64_t attn_out_norm = 0, ffn_out_norm = 0, dense_out_norm = 0, moe_in_norm = 0, moe_out_norm = 0;
   uint64_t router_norm = 0, expert_scale = 0, scalar = 0;
 };
@@ -351,7 +352,7 @@ static int rope_attn(ihip_mctx* s, int l, int64_t n, int64_t past, bool graph)
   } ra = {(float*)s->q, (const float*)s->k,
           // K=V: the values are the raw keys (normed by ValueNorm, not rotated)
           (const float*)(L.k_is_v ? s->k : s->v), (const float*)L.qn, (const float*)L.kn,
-          (const float*)(L.rope_set ? s->cs2 : s->cs), (void*)s->kc[l], (void*)s->vc[l],
+          (const float*)(L.no_rope ? 0 : L.rope_set ? s->cs2 : s->cs), (void*)s->kc[l], (void*)s->vc[l],
           graph ? (const int*)s->pos : nullptr, (double)d.rms_eps, (int32_t)n, d.heads, (int32_t)kvh,
           (int32_t)hd, (int32_t)past, m->kv_f16,
           // the second set: every pair of the head (those beyond its share
@@ -683,7 +684,7 @@ static int layers_one(ihip_mctx* s, int64_t past, bool graph)
     if ((hd == 64 || hd == 128) && rope_dims(d) == hd) {
       // head norms, RoPE, cache store and the ranges in one launch, then the merge
       AttnOne o;
-      o.q = s->q; o.k = s->k; o.v = s->v; o.qn = L.qn; o.kn = L.kn; o.cs = s->cs;
+      o.q = s->q; o.k = s->k; o.v = s->v; o.qn = L.qn; o.kn = L.kn; o.cs = L.no_rope ? 0 : s->cs;
       o.kc = s->kc[l]; o.vc = s->vc[l]; o.y = s->attn; o.sinks = L.sinks; o.pastp = graph ? s->pos : 0;
       o.part = s->attn_part; o.scale = 1.0 / std::sqrt((double)hd);
       o.eps = d.rms_eps; o.heads = d.heads; o.kvh = d.kv_heads; o.hd = hd; o.past = past;
@@ -2073,6 +2074,7 @@ int ihip_model_create(ihip_ctx* c, const ihip_model_desc* desc, int mode, int kv
     L.kvh = kvh;
     L.k_is_v = s.k_is_v != 0;
     L.rope_set = s.rope_set != 0;
+    L.no_rope = s.no_rope != 0;
     if (kvh < 1 || d.heads % kvh || (hd & 1) || hd < 2 || hd > 512)
       return bad(fail(IHIP_E_ARG, "model: layer " + std::to_string(l) + " has heads of " + std::to_string(hd) +
                                       " with " + std::to_string(kvh) + " KV heads (even, up to 512)"));

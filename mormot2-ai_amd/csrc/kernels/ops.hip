@@ -444,7 +444,8 @@ struct RopeArgs {
   const float* v;
   const float* qn;  // [hd] or null: no per-head norm
   const float* kn;
-  const float* cs;  // [rows, hd/2] cos, then [rows, hd/2] sin
+  const float* cs;  // [rows, hd/2] cos, then [rows, hd/2] sin; null: no rotary
+                    // positions (a NoPE layer, TDecoderLayerSpec.NoRope)
   void* kc;         // cache [*, kvh * hd] float or half
   void* vc;
   const int* pastp;  // device position of row 0 (graph replay), or null: past
@@ -466,7 +467,8 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
   constexpr int NV = 8, NR = 4;
   __shared__ float nv[512];
   int hh = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
-  int d = a.hd, half = (a.rot > 0 ? a.rot : d) >> 1;
+  // (a NoPE layer: no rotating part, every value normed and stored as it is)
+  int d = a.hd, half = a.cs ? (a.rot > 0 ? a.rot : d) >> 1 : 0;
   const int past = a.pastp ? *a.pastp : a.past;
   bool isq = hh < a.heads;
   int h = isq ? hh : hh - a.heads;
@@ -486,8 +488,8 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
 #pragma unroll
   for (int j = 0; j < NR; j++) {
     const int ii = min(t + 64 * j, max(half - 1, 0));
-    cv[j] = cr[ii];
-    sv[j] = sr[ii];
+    cv[j] = a.cs ? cr[ii] : 1.f;
+    sv[j] = a.cs ? sr[ii] : 0.f;
   }
   if (nw) {
     double s = 0;
@@ -1341,7 +1343,7 @@ struct AttnOneArgs {
   const float* v;
   const float* qn;  // head norms [hd] or null
   const float* kn;
-  const float* cs;  // cos [hd / 2] then sin [hd / 2]
+  const float* cs;  // cos [hd / 2] then sin [hd / 2], or null: a NoPE layer
   void* kc;
   void* vc;
   float* y;         // [heads * hd]
@@ -1415,7 +1417,8 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   float kv = a.k[(int64_t)g * d + tc];
   const float vv = a.v[(int64_t)g * d + tc];
   const float kw = a.kn ? a.kn[tc] : 1.f;
-  const float cv = a.cs[th], sv = a.cs[half + th];
+  const bool rope = a.cs != nullptr;  // (null: a NoPE layer, q and k as normed)
+  const float cv = rope ? a.cs[th] : 1.f, sv = rope ? a.cs[half + th] : 0.f;
   if (t >= d) qv = kv = 0.f;
   // the range's rows (an empty range reads row 0 of the cache)
   const int64_t rbase = n > 0 ? base : (int64_t)g * d;
@@ -1478,11 +1481,12 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
     __syncthreads();
     if (t < half) {
       double x0 = nq[t], x1 = nq[t + half], c = cv, sn = sv;
-      qd[t] = (double)(float)(x0 * c - x1 * sn);
-      qd[t + half] = (double)(float)(x1 * c + x0 * sn);
+      qd[t] = rope ? (double)(float)(x0 * c - x1 * sn) : x0;
+      qd[t + half] = rope ? (double)(float)(x1 * c + x0 * sn) : x1;
       if (hasnew) {
         double k0 = nk[t], k1 = nk[t + half];
-        float o0 = (float)(k0 * c - k1 * sn), o1 = (float)(k1 * c + k0 * sn);
+        float o0 = rope ? (float)(k0 * c - k1 * sn) : (float)k0;
+        float o1 = rope ? (float)(k1 * c + k0 * sn) : (float)k1;
         const int64_t dst = (int64_t)past * kvw + (int64_t)g * d;
         if constexpr (F16) {
           uint16_t h0 = float_to_half(o0), h1 = float_to_half(o1);
@@ -1747,8 +1751,8 @@ __device__ __forceinline__ void attention_one_f16(const AttnOneArgs& a)
       qw[i] = a.qn ? a.qn[e] : 1.f;
       kv[i] = hasnew ? a.k[(int64_t)g * d + e] : 0.f;
       kw[i] = (hasnew && a.kn) ? a.kn[e] : 1.f;
-      cv[i] = a.cs[p];
-      sv[i] = a.cs[half + p];
+      cv[i] = a.cs ? a.cs[p] : 1.f;  // (null: a NoPE layer)
+      sv[i] = a.cs ? a.cs[half + p] : 0.f;
     }
   }
   uint4 kt[KLD];
@@ -1805,8 +1809,11 @@ __device__ __forceinline__ void attention_one_f16(const AttnOneArgs& a)
       k0 = lo ? xk[0] : pk; k1 = lo ? pk : xk[0];
     }
     const double c = cv[0], sn = sv[0];
-    const double r0 = (double)(float)(x0 * c - x1 * sn), r1 = (double)(float)(x1 * c + x0 * sn);
-    const float o0 = (float)(k0 * c - k1 * sn), o1 = (float)(k1 * c + k0 * sn);
+    const bool rope = a.cs != nullptr;  // (a NoPE layer: q and the new key as normed)
+    const double r0 = rope ? (double)(float)(x0 * c - x1 * sn) : x0;
+    const double r1 = rope ? (double)(float)(x1 * c + x0 * sn) : x1;
+    const float o0 = rope ? (float)(k0 * c - k1 * sn) : (float)k0;
+    const float o1 = rope ? (float)(k1 * c + k0 * sn) : (float)k1;
     uint16_t* knew = (uint16_t*)&ks[jn * KPAD];
     const int64_t dst = (int64_t)past * kvw + (int64_t)g * d;
     if constexpr (QPL == 2) {

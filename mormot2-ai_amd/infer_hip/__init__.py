@@ -377,7 +377,7 @@ class LayerDesc(C.Structure):
         ("window", C.c_int32), ("moe", C.c_int32), ("mixer", C.c_int32),
         ("output_gate", C.c_int32)] + [(n, Tensor) for n in _LIN_TENSORS] + [
         (n, C.c_int32) for n in ("head_dim", "kv_heads", "k_is_v", "rope_set", "exp_gate_up",
-                                 "reserved1")] + [(n, Tensor) for n in _GEMMA_TENSORS]
+                                 "no_rope")] + [(n, Tensor) for n in _GEMMA_TENSORS]
 
 
 class ModelDesc(C.Structure):

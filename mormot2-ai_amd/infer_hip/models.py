@@ -137,6 +137,10 @@ class Spec:
                 L.sinks = self.vec(c["heads"], 1.0)
             if c.get("window") and li % 2 == 0:
                 L.window = c["window"]
+            # SmolLM3's NoPE layers: every no_rope_interval-th layer without
+            # rotary positions (no_rope_layer_interval, model.qwen3.pas:28-33)
+            if c.get("no_rope_interval") and (li + 1) % c["no_rope_interval"] == 0:
+                L.no_rope = 1
             if moe:
                 L.moe = 1
                 rt = BF16 if q == "gptoss" else F32

@@ -311,7 +311,9 @@ int orc_model_forward_rows(orc_model* m, const int32_t* ids, const float* embeds
       orc_rmsnorm(k, n * kvh, hd, (const float*)L->k_norm.data, d->rms_eps, k);
     }
     if (d->value_norm) orc_rmsnorm(v, n * kvh, hd, ones, d->rms_eps, v);
-    if (L->rope_set) {
+    if (L->no_rope) {
+      /* a NoPE layer (decoder.pas:139, NoRope): q and k as they are */
+    } else if (L->rope_set) {
       /* the second set: every pair of the head, frequency 0 beyond its share */
       orc_rope(q, n, d->heads, hd, cs2, cs2 + n * (hd / 2), 0);
       orc_rope(k, n, kvh, hd, cs2, cs2 + n * (hd / 2), 0);

@@ -30,6 +30,12 @@ TINY = [
     ("gpt-oss-20b-mxfp4", dict(layers=4, vocab=2048, hidden=512, heads=8, kv_heads=2,
                                head_dim=64, experts=8, experts_used=2, expert_ffn=512,
                                window=8)),
+    # SmolLM3-like: no head norms, every second layer without rotary
+    # positions (NoPE), heads of 128 and of 64
+    ("qwen3-0.6b-q8_0", dict(layers=4, vocab=2048, hidden=512, heads=4, kv_heads=2, head_dim=128,
+                             ffn=768, qk_norm=False, no_rope_interval=2)),
+    ("qwen3-0.6b-q4_k_m", dict(layers=4, vocab=2048, hidden=512, heads=8, kv_heads=4, head_dim=64,
+                               ffn=768, qk_norm=False, no_rope_interval=2)),
 ]
 
 
@@ -77,6 +83,23 @@ def test_baseline_shape_greedy_64(ctx, name, prompt_len):
     ref, margins = cpu.greedy(prompt, 64)
     print(name, "min margin", float(margins.min()), "tokens", got[:8], flush=True)
     assert np.array_equal(got, ref), (np.nonzero(got != ref)[0][:5], margins)
+    dev.close()
+    cpu.close()
+
+
+def test_nope_prompt_on_the_matrix_cores(ctx):
+    # NoPE layers through a 96-row prefill (the GEMM and the prompt attention
+    # on the f64 matrix cores) and the graph-replayed decode
+    spec = models.Spec(models.tiny("qwen3-0.6b-q8_0", layers=4, vocab=2048, hidden=512, heads=4,
+                                   kv_heads=2, head_dim=128, ffn=768, qk_norm=False,
+                                   no_rope_interval=2), seed=9)
+    prompt = np.random.default_rng(12).integers(0, spec.vocab, 96).astype(np.int32)
+    dev = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=True, max_tokens=160)
+    cpu = O.Model(spec, 160, kv_f16=True)
+    got = dev.greedy(prompt, 32)
+    ref, margins = cpu.greedy(prompt, 32)
+    print("nope min margin", float(margins.min()), flush=True)
+    assert np.array_equal(got, ref), (got, ref, margins)
     dev.close()
     cpu.close()
 
