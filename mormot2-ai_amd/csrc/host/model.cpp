@@ -1632,7 +1632,13 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
       (rc = decode_graph(s)))
     return rc;
   std::vector<float> cs(m->d.head_dim), cs2(std::max<int64_t>(m->hd2, 1));
-  int32_t tok = first;
+  int32_t tok = first, pos = 0;
+  // destroyed before cs, cs2, tok and pos: on an early return the copies
+  // queued from them have ended first
+  struct StreamWait {
+    hipStream_t st;
+    ~StreamWait() { (void)hipStreamSynchronize(st); }
+  } wait_copies{c->stream};
   if (pipelined) {
     if (s->ids_pinned_n < steps) {
       IHIP_CHECK(hipStreamSynchronize(c->stream));
@@ -1642,7 +1648,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
       IHIP_CHECK(hipHostMalloc((void**)&s->ids_pinned, (size_t)steps * 4, hipHostMallocDefault));
       s->ids_pinned_n = steps;
     }
-    const int32_t pos = (int32_t)s->length;
+    pos = (int32_t)s->length;
     if (m->hd2) {
       rotary2(m->d, m->hd2, pos, 1, cs2.data());
       IHIP_CHECK(hipMemcpyHtoDAsync((hipDeviceptr_t)s->cs2, cs2.data(), cs2.size() * 4, c->stream));
@@ -1666,7 +1672,7 @@ static int decode_steps(ihip_mctx* s, int32_t first, int64_t steps, int32_t* out
     return 0;
   }
   for (int64_t i = 0; i < steps; i++) {
-    int32_t pos = (int32_t)s->length;
+    pos = (int32_t)s->length;
     if (pos == 0 && m->recurrent && (rc = reset_states(s))) return rc;
     // each step is a forward of one token: its own part
     if ((rc = part_start(s, tok, true))) return rc;

@@ -475,8 +475,8 @@ extern "C" __global__ __launch_bounds__(64) void qkrope(RopeArgs a)
   int64_t src = isq ? ((int64_t)r * a.heads + h) * d : ((int64_t)r * a.kvh + h) * d;
   const float* in = isq ? a.q + src : a.k + src;
   const float* nw = isq ? a.qn : a.kn;
-  const float* cr = a.cs + (int64_t)r * half;
-  const float* sr = a.cs + (int64_t)a.rows * half + (int64_t)r * half;
+  const float* cr = a.cs ? a.cs + (int64_t)r * half : nullptr;
+  const float* sr = a.cs ? a.cs + (int64_t)a.rows * half + (int64_t)r * half : nullptr;
   float xin[NV], wv[NV], vin[NV], cv[NR], sv[NR];
 #pragma unroll
   for (int i = 0; i < NV; i++) {
