@@ -1359,6 +1359,29 @@ struct AttnOneArgs {
   int* done;  int32_t place, pad;  // f16 one-row launch: 0 blocks by head, 1 by KV group over the XCDs
 };
 
+// a head whose keys all fall in one range (cnt <= the range size): its range
+// block writes the output itself, no partials, no counter, no merge; the
+// arithmetic is merge_ranges' for one non-empty range (its weight exp(m - M)
+// with the sink in M, the denominator fma(e, l, 0) plus the sink's term, each
+// value 0 + e p, times 1 / den), so the bits are those of the merged path.
+// m: the range's maximum score, l: its sum of weights, p(i): its weighted
+// value sum of dimension i.
+template <typename P>
+__device__ __forceinline__ void finish_one_range(double m, double l, P p, int d, const float* sink,
+                                                 float* y)
+{
+  double M = m;
+  if (sink && (double)*sink > M) M = *sink;
+  const double e = m > -1.0e308 ? exp(m - M) : 0.0;
+  double den = __builtin_fma(e, l, 0.0);
+  if (sink) den = den + exp((double)*sink - M);
+  const double inv = 1.0 / den;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) {
+    const double acc = 0.0 + e * p(i);
+    y[i] = (float)(acc * inv);
+  }
+}
+
 // the sums of two values over a block of 256 (wave sums, then 4 waves)
 __device__ __forceinline__ void block_sum2(double& a, double& b, double* red)
 {
@@ -1398,6 +1421,10 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   const int n = j1 - j0;
   const int jn = cnt - 1 - j0;  // the new key within the range (valid when hasnew)
   const bool hasnew = n > 0 && j1 == cnt;
+  // every key in range 0 (a short context, a window): that block finishes the
+  // head alone (finish_one_range), the other ranges have nothing to add
+  const bool whole = a.done && cnt <= ATT_CHUNK;
+  if (whole && s > 0) return;
   double* out = a.part + ((int64_t)h * a.splits + s) * (d + 2);
   const int64_t base = (int64_t)(first + j0) * kvw + (int64_t)g * d;
   const int w = t >> 6, l = t & 63;
@@ -1628,6 +1655,12 @@ __device__ __forceinline__ void attention_one_t(const AttnOneArgs& a)
   }
   __syncthreads();
   IHIP_STAMP(4);
+  if (whole) {
+    finish_one_range(n > 0 ? m : -1.0e308, (red[4] + red[5]) + (red[6] + red[7]),
+                     [&](int i) { return (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]); }, d,
+                     a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d);
+    return;
+  }
   // the head's last range block may read these: with a multiple of 8 heads
   // every range block of head h runs on one XCD (launch-order ids h' + heads
   // * s, xcd_head), so plain stores meet in that XCD's L2; else agent-scope
@@ -1733,6 +1766,10 @@ __device__ __forceinline__ void attention_one_f16(const AttnOneArgs& a)
   const bool hasnew = n > 0 && j1 == cnt;  // the range holds the new key, its last row
   const int jn = n - 1;
   const int nload = hasnew ? n - 1 : n;    // rows already in the cache
+  // every key in range 0 (a short context, a window): that block finishes the
+  // head alone (finish_one_range), the other ranges have nothing to add
+  const bool whole = a.done && cnt <= ATT_CHUNK;
+  if (whole && s > 0) return;
   double* out = a.part + ((int64_t)h * a.splits + s) * (d + 2);
   const int64_t rbase = (int64_t)(first + j0) * kvw + (int64_t)g * d;  // halves
   const auto kr = bounded((const uint16_t*)a.kc + rbase, (uint32_t)nload * rowb);
@@ -1925,6 +1962,12 @@ __device__ __forceinline__ void attention_one_f16(const AttnOneArgs& a)
   }
   __syncthreads();
   IHIP_STAMP(4);
+  if (whole) {
+    finish_one_range(n > 0 ? m : -1.0e308, (red[4] + red[5]) + (red[6] + red[7]),
+                     [&](int i) { return (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]); }, d,
+                     a.sinks ? a.sinks + h : nullptr, a.y + (int64_t)h * d);
+    return;
+  }
   auto put = [&](double* p, double v) {
     if (xcd) *p = v;
     else store_agent(p, v);
