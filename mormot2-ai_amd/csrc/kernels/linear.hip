@@ -849,8 +849,14 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
     // loads, so the row is staged while the weights are on their way
     // a self-routed token: the router logits first (the route needs them
     // before any weight address is known)
+    // (more than 64 experts: wave 0 alone, the other waves take its pick
+    // from LDS - every wave of every block loading the same logit lines
+    // queued them at the L2; with fewer, the barrier costs more than the
+    // shared lines)
     float rlg[4];
-    if (GLU && a.ids && a.rl) route_logits(a.rl, a.rexp, rlg);
+    const bool shared_pick = a.rexp > 64;
+    const bool route0 = !shared_pick || threadIdx.x < 64;
+    if (GLU && a.ids && a.rl && route0) route_logits(a.rl, a.rexp, rlg);
     XStage st;
     const bool quantized = !NORM && stage_q8<F, MODE>() && a.xq != nullptr;
     stage_load<F, MODE, NORM>(a.x + xrow0 * a.in,
@@ -861,15 +867,25 @@ __device__ __forceinline__ void gemv(const LinArgs& a)
       // self-routed (TDecoderModel.Route in the wave, route_wave): the expert
       // of this block's slot; the launch's extra row writes the picks and
       // weights for the down launch
-      int sid[8];
-      float sw[8];
-      if (a.rexp <= 64) route_wave<1, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
-      else if (a.rexp <= 128) route_wave<2, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
-      else route_wave<4, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
-      IHIP_STAMP(7);
+      __shared__ int spick;
       int e = -1;
+      if (route0) {
+        int sid[8];
+        float sw[8];
+        if (a.rexp <= 64) route_wave<1, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
+        else if (a.rexp <= 128) route_wave<2, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
+        else route_wave<4, false>(rlg, a.rexp, a.rk, a.rnorm, sid, sw);
+        int e0 = -1;
 #pragma unroll
-      for (int s = 0; s < 8; s++) e = s == (int)yrow0 ? sid[s] : e;
+        for (int s = 0; s < 8; s++) e0 = s == (int)yrow0 ? sid[s] : e0;
+        if (threadIdx.x == 0) spick = e0;
+        if (!shared_pick) e = e0;
+      }
+      if (shared_pick) {
+        __syncthreads();
+        e = spick;
+      }
+      IHIP_STAMP(7);
       if (e < 0 || (a.nexp > 0 && e >= a.nexp)) {
         for (int64_t o = (int64_t)(blockIdx.x * NT + threadIdx.x); o < a.out;
              o += (int64_t)gridDim.x * NT)
