@@ -1532,9 +1532,12 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
   float* dxs = (float*)(cmb_xs + n);
   // the activation rows need no expert id: their loads go first (the first
   // XN values; more, gpt-oss's 4 x 2880, in further chunks below)
+  IHIP_STAMP_SCOPE;
+  IHIP_STAMP(0);
   const int nc0 = min(XN, n);
   XStage st0;
   stage_load<F, MODE, false>(a.x, nullptr, nc0, nullptr, st0);
+  IHIP_STAMP(6);
   // this wave's slots and their experts (a bad id adds nothing)
   const uint8_t* wi[2];
   bool ok[2];
@@ -1565,6 +1568,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
     er = a.res ? a.res[o] : 0.f;
   };
   load(t);
+  IHIP_STAMP(1);
   stage_store<F, MODE, false>(st0, false, nc0, 0.0, cmb_xs, dxs, a.bad, 1);
   for (int c0 = XN; c0 < n; c0 += XN) {
     XStage st;
@@ -1574,6 +1578,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
                          cmb_xs + (stage_q8<F, MODE>() ? c0 : 4 * c0), dxs + c0 / 32, a.bad, 1);
   }
   __syncthreads();
+  IHIP_STAMP(2);
   while (t < tiles) {
     const int64_t o = t * rpw + rsub;
     const bool valid = o < a.out;
@@ -1600,6 +1605,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
       }
     }
     __syncthreads();
+    IHIP_STAMP(4);
     const float res = er;  // this tile's residual, before the next tile's loads
     const int64_t tn = t + gridDim.x;
     if (tn < tiles) load(tn);
@@ -1614,6 +1620,7 @@ __device__ __forceinline__ void gemv_cmb(const LinArgs& a)
     __syncthreads();
     t = tn;
   }
+  IHIP_STAMP(5);
 }
 
 // ------------------------------------------------------------ dequant/embed

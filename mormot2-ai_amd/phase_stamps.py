@@ -14,7 +14,10 @@ Phases of the one-row GEMV (linear.hip gemv, R = 1): 0 block start, 6 the
 activation row's loads issued (self-routed experts: after the router logits),
 7 the block's expert picked (self-routed only), 1 the first weight loads
 issued, 2 the row staged in LDS, 3 the row's groups in registers, 4 after
-each wave step's sums, 5 the block's last store. Of the decode attention
+each wave step's sums, 5 the block's last store. Of the expert down+combine
+(linear.hip gemv_cmb): 0 start, 6 the slot rows' loads issued, 1 the first
+weight loads issued (after the expert ids), 2 the rows staged in LDS, 4 after
+each tile's combine, 5 the block's end. Of the decode attention
 (ops.hip attention_one): 0 start, 1 every load issued, 2 head norms, RoPE and
 the cache store done, 3 the softmax done, 4 the weighted values in LDS, 5 the
 merge started (the head's last range block), 6 the merge done.
