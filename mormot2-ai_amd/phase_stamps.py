@@ -8,7 +8,12 @@ graph), traces every launch of each kernel name prefix over a few decode
 steps, and prints per phase the median / 10th / 90th percentile over blocks
 and launches of the time since the launch's earliest block started (us).
 
-  python mormot2-ai_amd/phase_stamps.py [config] [prefix,prefix,...] [prompt]
+  python mormot2-ai_amd/phase_stamps.py [config] [prefix,prefix,...] [prompt] [group]
+
+With a group size, the medians and 90th percentiles of phases 0, 1, 2, 4 and
+5 are also printed for every group of that many consecutive blocks (in
+dispatch order: the matrices of a several-matrix launch, an expert slot's
+blocks, the key ranges of the decode attention).
 
 Phases of the one-row GEMV (linear.hip gemv, R = 1): 0 block start, 6 the
 activation row's loads issued (self-routed experts: after the router logits),
@@ -43,6 +48,7 @@ def main():
                 ["gemv_q4_k_q8_norm_glu", "attention_one", "gemv_q4_k_q6_k_q8_norm",
                  "gemv_q4_k_q8_u4", "gemv_f32_q8_norm_rows"])
     plen = int(sys.argv[3]) if len(sys.argv) > 3 else 1024
+    group = int(sys.argv[4]) if len(sys.argv) > 4 else 0
     ctx = H.Context(0)
     spec = models.Spec(models.CONFIGS[cfg], seed=1)
     m = H.Model(ctx, spec, mode=H.MODE_Q8, kv_f16=True, max_tokens=plen + 64)
@@ -84,6 +90,18 @@ def main():
                       f"  p90 {np.percentile(col, 90):6.2f}  max {col.max():6.2f}  blocks {col.size}")
         print(f"  last stamp of a launch: median {np.median([np.nanmax(r) for r in rows]):.2f} us",
               flush=True)
+        if group > 0:
+            R = np.stack(rows)  # launches x blocks x 8
+            for g0 in range(0, R.shape[1], group):
+                part = R[:, g0:g0 + group, :]
+                cols = []
+                for i in (0, 1, 2, 4, 5):
+                    v = part[:, :, i]
+                    v = v[~np.isnan(v)]
+                    cols.append(f"p{i} {np.median(v):5.2f}/{np.percentile(v, 90):5.2f}" if v.size
+                                else f"p{i}   -  /  -  ")
+                print(f"  blocks {g0:4d}-{min(R.shape[1], g0 + group) - 1:4d}: " + "  ".join(cols),
+                      flush=True)
     m.close()
     ctx.close()
     sys.stdout.flush()
