@@ -126,7 +126,14 @@ def test_qkrope_and_cache(ctx, hd, heads, kvh, norm, f16):
     # key scoring and the fused value sums, one row and a few
     (256, 8, 2, 300, 1, 0, True, True), (256, 16, 8, 1030, 1, 1024, True, False),
     (256, 4, 1, 90, 3, 0, True, False), (512, 16, 2, 700, 1, 0, True, False),
-    (128, 32, 4, 1100, 1, 0, True, False)])
+    (128, 32, 4, 1100, 1, 0, True, False),
+    # one row whose keys fit one 128-key range: sinks with half-float keys,
+    # a window with float keys and sinks, exactly 128 keys, a window of 128
+    # past 128 keys (the decode step's own one-row kernel, which finishes
+    # such a head in its range block, runs in the model tests: prompts of 12
+    # and 16 tokens decode at most 128 keys)
+    (64, 8, 2, 90, 1, 0, True, True), (128, 8, 2, 60, 1, 40, True, False),
+    (128, 32, 4, 127, 1, 0, True, True), (64, 16, 4, 400, 1, 128, False, True)])
 def test_attention(ctx, hd, heads, kvh, past, rows, window, sinks, f16):
     rng = np.random.default_rng(past + rows)
     T = past + rows
